@@ -1,0 +1,232 @@
+/*
+ * pe_hip.h: C ABI of the MI355X tree-verification pass (libpe_hip.so).
+ *
+ * Every entry point takes plain device pointers and sizes, launches on the
+ * HIP stream it is given (`stream`, a hipStream_t passed as void*), never
+ * allocates device memory, and returns a PE_* status (PE_OK == 0). Errors
+ * that depend on device data (a non-topological tree, a token id out of the
+ * vocabulary, a dense bias that is not a tree mask) are written to a
+ * caller-provided device int32 `status` word with atomicOr of the PE_ERR_*
+ * bit; the host reads it after the stream synchronises.
+ *
+ * Scratch buffers (`workspace`) are caller-owned; their counters region must
+ * be zero when first used and is left zero by every call.
+ *
+ * The reference implements this pass in Python over transformers/torch/
+ * bitsandbytes; each entry point below names the reference function it
+ * replaces (file:line in puneethgv/parallel_eagle, "HF:" = transformers 5.x).
+ */
+#ifndef PE_HIP_H
+#define PE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes (bit flags so device-side errors can be OR-ed) */
+#define PE_OK 0
+#define PE_ERR_ARG 1       /* invalid argument: null pointer, shape, unsupported size */
+#define PE_ERR_LAUNCH 2    /* a kernel launch failed */
+#define PE_ERR_TREE 4      /* parents not topological / out of range, tree too large */
+#define PE_ERR_CAPACITY 8  /* KV cache capacity exceeded / position out of table */
+#define PE_ERR_MASK 16     /* dense bias is not a prefix+ancestor tree mask */
+#define PE_ERR_TOKEN 32    /* token id outside the vocabulary */
+#define PE_ERR_INDEX 64    /* keep index not strictly increasing / out of range */
+#define PE_ERR_WORKSPACE 128 /* workspace too small */
+
+/* element types */
+#define PE_DTYPE_F32 0
+#define PE_DTYPE_BF16 1
+#define PE_DTYPE_F16 2
+
+/* linear-weight storage formats */
+#define PE_WFMT_DENSE 0 /* dtype weights, MFMA-tiled (16-bit) or row-major (fp32) */
+#define PE_WFMT_NF4 1   /* NF4 codes + fp16 absmax per 64 along K, MFMA-tiled */
+
+/* GEMM epilogues */
+#define PE_EPI_STORE 0    /* out = round(acc + bias) */
+#define PE_EPI_RESIDUAL 1 /* out = round(resid + round(acc)); out may alias resid */
+#define PE_EPI_SWIGLU 2   /* columns interleaved by 32 (gate tile, up tile):
+                             out = round(round(silu(round(g))) * round(u)) */
+
+/* attention masks */
+#define PE_MASK_TREE 0   /* rows are tree nodes: whole prefix + ancestor bits */
+#define PE_MASK_CAUSAL 1 /* rows are consecutive tokens: key j allowed iff j <= P + row */
+
+#define PE_TREE_MAX_WORDS 4 /* ancestor bitmask words per node: T <= 256 */
+
+const char* pe_status_string(int status);
+int pe_version(void);
+
+/* ---------------------------------------------------------------- synthetic data */
+/* Counter-based normal(0, std) fill (splitmix64 hash -> 4x16-bit Irwin-Hall sum),
+ * bit-identical to the numpy generator used for fixtures. No reference
+ * counterpart: the reference loads hub checkpoints (src/pe/target.py:32-38). */
+int pe_fill_normal(void* out, int64_t n, int dtype, uint64_t seed, uint64_t stream_id, double std_,
+                   void* stream);
+int pe_fill_uniform_int(int64_t* out, int64_t n, int64_t hi, uint64_t seed, uint64_t stream_id,
+                        void* stream);
+
+/* ---------------------------------------------------------------- NF4 format */
+/* Blockwise NF4 quantisation of fp32 W[N][K] (block 64 along K) into the logical
+ * bitsandbytes layout: packed[N*K/2] (element 2j in the high nibble of byte j),
+ * absmax[N*K/64] fp16. Nearest code, lowest index on ties. Stands in for the
+ * pre-quantized checkpoint the reference loads (src/pe/target.py:32-38). */
+int pe_nf4_quantize(const float* w, int64_t N, int64_t K, uint8_t* packed, uint16_t* absmax,
+                    void* stream);
+/* Logical NF4 -> MFMA-tiled layout read by pe_nf4_gemm. */
+int pe_nf4_repack(const uint8_t* packed, const uint16_t* absmax, int64_t N, int64_t K,
+                  uint8_t* tiled, uint16_t* tiled_absmax, void* stream);
+/* Tiled NF4 -> logical bf16 W[N][K]: bf16_rne(NF4[c] * float(absmax)). Replaces
+ * bitsandbytes dequantize_4bit (src/pe/target.py:55-62). */
+int pe_nf4_dequant(const uint8_t* tiled, const uint16_t* tiled_absmax, int64_t N, int64_t K,
+                   uint16_t* out, void* stream);
+/* Row-major 16-bit W[N][K] -> MFMA-tiled layout read by pe_dense_gemm (copy for fp32). */
+int pe_dense_repack(const void* w, int64_t N, int64_t K, int dtype, void* tiled, void* stream);
+
+/* ---------------------------------------------------------------- GEMMs */
+/* Bytes of workspace a GEMM of this shape needs (split-K partials + counters). */
+int64_t pe_gemm_workspace_bytes(int M, int N, int K, int wfmt, int dtype, int epilogue);
+/* Y[M][N] = X[M][K] . deq(W)^T with fp32 accumulation, then the epilogue.
+ * Replaces bitsandbytes Linear4bit.forward (dequantize then F.linear) at
+ * src/pe/target.py:32-38 / HF modeling_llama.py:175,254-256,280.
+ * K % 128 == 0, N % 32 == 0 (N % 64 for PE_EPI_SWIGLU). */
+int pe_nf4_gemm(const void* x, int64_t ldx, int M, int K, const uint8_t* w_tiled,
+                const uint16_t* absmax_tiled, int N, int epilogue, const void* bias,
+                const void* resid, int64_t ld_resid, void* out, int64_t ld_out, void* workspace,
+                int64_t workspace_bytes, void* stream);
+/* Dense linear in dtype (bf16/fp16 MFMA on tiled weights, fp32 VALU on row-major).
+ * Replaces F.linear in HF modeling_llama.py:175,254-256,280,480. */
+int pe_dense_gemm(const void* x, int64_t ldx, int M, int K, const void* w, int dtype, int N,
+                  int epilogue, const void* bias, const void* resid, int64_t ld_resid, void* out,
+                  int64_t ld_out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- elementwise */
+/* out[m][:] = table[ids[m]][:]. HF modeling_llama.py:381 (embed_tokens). */
+int pe_embed(const int64_t* ids, int M, const void* table, int64_t V, int H, int dtype, void* out,
+             int64_t ld_out, int32_t* status, void* stream);
+/* HF LlamaRMSNorm (modeling_llama.py:62-67): w * round(x * rsqrt(mean(x^2) + eps)). */
+int pe_rmsnorm(const void* x, int64_t ldx, int M, int H, const void* w, float eps, int dtype,
+               void* out, int64_t ld_out, void* stream);
+/* RoPE at the given positions on q and k of a fused qkv row block, HF
+ * apply_rotary_pos_emb (modeling_llama.py:130-160); writes roped q to q_out
+ * [M][nh][hd] and appends k, v at cache rows [row0, row0 + M) in place of
+ * DynamicLayer.update's torch.cat (HF cache_utils.py:127-146).
+ * cos_sin: [max_pos][hd] cos followed by [max_pos][hd] sin, in dtype. */
+int pe_rope_qkv(const void* qkv, int64_t ld_qkv, int M, int nh, int nkv, int hd,
+                const int64_t* positions, const void* cos_sin, int64_t max_pos, int dtype,
+                void* q_out, void* k_cache, void* v_cache, int64_t cache_cap, int64_t row0,
+                int32_t* status, void* stream);
+/* dst[m][0:H] = src[m][0:H] (feature capture, src/pe/target.py:161-162). */
+int pe_copy_rows(const void* src, int64_t ld_src, int M, int64_t row_bytes, void* dst,
+                 int64_t ld_dst, void* stream);
+
+/* ---------------------------------------------------------------- tree masks */
+/* Per-node ancestor bitmask (bits[t][w], bit u set iff node u is t or an
+ * ancestor of t), depth and position P + depth. Replaces tree_depths /
+ * tree_allow_mask / tree_position_ids (src/pe/masks.py:118-156). */
+int pe_tree_masks(const int32_t* parents, int T, int64_t P, uint64_t* bits, int words,
+                  int64_t* positions, int32_t* depths, int32_t* status, void* stream);
+/* Dense bool allow matrix (P+T)^2 from the bitmasks (masks.py:127-147). */
+int pe_tree_allow_dense(const uint64_t* bits, int T, int words, int64_t P, uint8_t* allow,
+                        void* stream);
+/* Additive bias (T rows of a (.., T, P+T) mask, to_additive_bias masks.py:29-33)
+ * back to bitmasks; PE_ERR_MASK if a prefix column is masked or a value is
+ * neither 0 nor <= finfo(dtype).min / 2. */
+int pe_bias_to_bits(const void* bias, int64_t ld_bias, int dtype, int T, int64_t P,
+                    uint64_t* bits, int words, int32_t* status, void* stream);
+
+/* ---------------------------------------------------------------- attention */
+int64_t pe_attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_len, int dtype);
+/* softmax(q k^T * scale + mask) v over cache rows [0, P + T) of one layer,
+ * replacing HF sdpa_attention_forward (integrations/sdpa_attention.py:79-154)
+ * with the tree bias of masks.py:127-147. q [T][nh][hd], caches [nkv][cap][hd],
+ * out [T][ld_out] with head h at columns [h*hd, (h+1)*hd). */
+int pe_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
+                      int nh, int nkv, int hd, int T, int64_t P, int mask_mode,
+                      const uint64_t* bits, int words, float scale, int dtype, void* out,
+                      int64_t ld_out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- acceptance */
+/* Row argmax (first index among equal maxima; NaN counts as the maximum). */
+int pe_argmax_rows(const void* x, int64_t ld, int rows, int64_t V, int dtype, int32_t* out_idx,
+                   void* stream);
+/* Greedy tree walk of accept_tree_cached (src/pe/decode/verify.py:104-125):
+ * out[0] = |path|, out[1] = bonus token, out[2 + i] = path node i.
+ * scratch: T + 1 int32. */
+int pe_accept_tree(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V,
+                   int dtype, const int64_t* node_tokens, const int32_t* parents, int32_t* out,
+                   int32_t* scratch, void* stream);
+/* Move accepted rows P + path[i] -> P + i in every layer's K and V, in place;
+ * path read from a pe_accept_tree result on the device. Replaces
+ * TargetModel.gather_cache (src/pe/target.py:194-201) for the keep index
+ * serve.py:308-309 builds. Caches [L][nkv][cap][hd]. */
+int pe_kv_compact(void* k_cache, void* v_cache, int L, int nkv, int64_t cap, int hd, int dtype,
+                  int64_t P, const int32_t* accept_out, void* stream);
+/* General in-place gather of rows keep[0..n) (strictly increasing) on the
+ * sequence axis, gather_cache with an arbitrary keep index. */
+int pe_kv_gather(void* k_cache, void* v_cache, int L, int nkv, int64_t cap, int hd, int dtype,
+                 const int64_t* keep, int64_t n_keep, int32_t* status, void* stream);
+
+/* ---------------------------------------------------------------- whole pass */
+typedef struct pe_model_desc {
+  int32_t num_layers, hidden, num_heads, num_kv_heads, head_dim, intermediate, vocab;
+  int32_t intermediate_padded; /* intermediate rounded up to 32 */
+  int32_t dtype;               /* activations, norms, embeddings, lm_head, KV */
+  int32_t weight_format;       /* PE_WFMT_* of the per-layer linears */
+  float rms_eps;
+  int64_t max_positions;
+  const void* embed;        /* [V][H] */
+  const void* final_norm;   /* [H] */
+  const void* lm_head;      /* dense [V][H], tiled for 16-bit dtypes */
+  const void* rope_cos_sin; /* [max_pos][hd] cos, then [max_pos][hd] sin */
+  /* arrays of num_layers pointers */
+  const void* const* attn_norm;
+  const void* const* mlp_norm;
+  const void* const* w_qkv; /* N = (nh + 2 nkv) * hd */
+  const void* const* a_qkv; /* NF4 absmax (NULL entries for dense) */
+  const void* const* b_qkv; /* bias [N] or NULL entries */
+  const void* const* w_o;
+  const void* const* a_o;
+  const void* const* w_gu; /* gate/up interleaved by 32 rows, N = 2 * intermediate_padded */
+  const void* const* a_gu;
+  const void* const* w_down; /* K = intermediate_padded */
+  const void* const* a_down;
+} pe_model_desc;
+
+typedef struct pe_pass_args {
+  const int64_t* input_ids; /* [M] */
+  const int64_t* positions; /* [M] */
+  int32_t M;                /* rows of this pass (tree nodes or tokens) */
+  int32_t mask_mode;        /* PE_MASK_TREE | PE_MASK_CAUSAL */
+  int64_t prefix_len;       /* P: new K/V rows land at [P, P + M) */
+  const uint64_t* tree_bits;
+  int32_t bits_words;
+  int32_t num_features;     /* hidden-state slots to fuse (0..4) */
+  int32_t feature_layers[4];/* 0 = embeddings, i < L = after layer i, L = final norm */
+  int32_t _pad;
+  void* k_cache;
+  void* v_cache;
+  int64_t cache_capacity;
+  void* logits; /* [M][V] or NULL */
+  void* fused;  /* [M][num_features * H] or NULL */
+  void* workspace;
+  int64_t workspace_bytes;
+  int32_t* status;
+} pe_pass_args;
+
+/* Workspace for pe_forward with up to M rows and kv_len = P + M keys. */
+int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int64_t kv_len);
+/* The masked verification forward TargetModel.forward_cached
+ * (src/pe/target.py:203-224 -> HF LlamaForCausalLM / Qwen2ForCausalLM forward,
+ * modeling_llama.py:347-490): embeddings, L decoder layers with in-place KV
+ * append, final norm, lm_head over all M rows, fused features. */
+int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PE_HIP_H */

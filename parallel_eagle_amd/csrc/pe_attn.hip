@@ -1,0 +1,372 @@
+// Tree-masked GQA attention over the KV cache (split-KV flash decoding).
+//
+// Query rows are the T tree nodes (x G query heads per KV head); keys are the
+// P cached prefix rows followed by the T node rows appended by pe_rope_qkv.
+// A node attends to the whole prefix and to the node rows of its ancestor set,
+// read from a per-node bitmask (bit u of bits[t] <=> node u is t or an
+// ancestor of t), which is the (T, P+T) additive bias of the reference
+// (src/pe/masks.py:127-147 + to_additive_bias :29-33) without materialising it.
+//
+// 16-bit path (hd = 128): one wave per (KV head, key split, 32-row tile).
+//   S^T = K Q^T with v_mfma_f32_32x32x16 (A = 32 keys x 16 dims of K straight
+//   from the cache, B = Q^T held in registers), so every lane owns one query
+//   row (column) and 16 of the 32 keys: the online-softmax max/sum of a row is
+//   a 16-value in-lane reduction plus one exchange with lane^32.
+//   O^T += V^T P^T (A = V^T from a wave-private LDS transpose of the 32-key V
+//   block, B = P^T taken directly from the S^T accumulator registers rounded to
+//   the compute dtype), so the per-row rescale is a per-lane scalar.
+//   Partial (O, max, sum) per split are merged by attn_combine_kernel.
+// Softmax is fp32; exp(s - m) is summed in fp32 and rounded to the compute
+// dtype for the PV product, as torch's CPU flash attention does for reduced
+// precision inputs.
+//
+// fp32 path: one block per (row, query head), scores in LDS, VALU arithmetic.
+
+#include "pe_common.h"
+
+namespace {
+
+constexpr float kMaskedScore = -3.0e38f;
+constexpr float kInitMax = -2.0e38f;
+
+__device__ __forceinline__ bool key_allowed(int64_t key, int64_t P, int t, int mask_mode, const uint64_t* nb) {
+  if (mask_mode == PE_MASK_CAUSAL) return key <= P + t;
+  if (key < P) return true;
+  const int u = (int)(key - P);
+  return (nb[u >> 6] >> (u & 63)) & 1ull;
+}
+
+template <int DT>
+__global__ __launch_bounds__(64) void attn_mfma_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
+    int nh, int nkv, int T, int64_t P, int mask_mode, const uint64_t* __restrict__ bits, int words, float scale,
+    int keys_per_split, int splits, int rows_pad, float* __restrict__ opart, float* __restrict__ mlpart) {
+  constexpr int HD = 128;
+  const int kvh = blockIdx.x, split = blockIdx.y, rt = blockIdx.z;
+  const int G = nh / nkv, rows = T * G;
+  const int lane = threadIdx.x, ln = lane & 31, g = lane >> 5;
+  const int64_t S = P + T;
+  const int64_t j0 = (int64_t)split * keys_per_split;
+  const int64_t j1 = min(S, j0 + keys_per_split);
+
+  const int r = rt * 32 + ln;
+  const bool rvalid = r < rows;
+  const int t = rvalid ? r / G : 0;
+  const int hq = kvh * G + (rvalid ? r % G : 0);
+
+  uint64_t nb[PE_TREE_MAX_WORDS];
+#pragma unroll
+  for (int w = 0; w < PE_TREE_MAX_WORDS; ++w)
+    nb[w] = (mask_mode == PE_MASK_TREE && w < words && rvalid) ? bits[(int64_t)t * words + w] : 0ull;
+
+  const u32x4_t zero4 = {0u, 0u, 0u, 0u};
+  u32x4_t qf[8];
+  const uint16_t* qp = q + ((int64_t)t * nh + hq) * HD;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) qf[j] = rvalid ? *(const u32x4_t*)(qp + 16 * j + 8 * g) : zero4;
+
+  f32x16_t o[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
+  float m = kInitMax, l = 0.f;
+
+  __shared__ uint16_t vt[HD][32 + 8];
+  const uint16_t* kbase = kc + (int64_t)kvh * cap * HD;
+  const uint16_t* vbase = vc + (int64_t)kvh * cap * HD;
+
+  for (int64_t jb = j0; jb < j1; jb += 32) {
+    // ---- S^T = K Q^T over hd
+    const int64_t key = jb + ln;
+    const bool kvalid = key < j1;
+    const uint16_t* kp = kbase + (kvalid ? key : jb) * HD + 8 * g;
+    u32x4_t kf[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kf[j] = kvalid ? *(const u32x4_t*)(kp + 16 * j) : zero4;
+    // V block -> LDS transposed: vt[d][key offset]
+    u32x4_t vf[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int chunk = c * 64 + lane;  // 32 keys x 16 chunks of 8 dims
+      const int koff = chunk >> 4, dc = chunk & 15;
+      const int64_t vk = jb + koff;
+      vf[c] = (vk < j1) ? *(const u32x4_t*)(vbase + vk * HD + dc * 8) : zero4;
+    }
+    f32x16_t s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (DT == PE_DTYPE_F16)
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[j]),
+                                                   __builtin_bit_cast(f16x8_t, qf[j]), s, 0, 0, 0);
+      else
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[j]),
+                                                    __builtin_bit_cast(bf16x8_t, qf[j]), s, 0, 0, 0);
+    }
+    // ---- scale + mask, block max (s[i] holds key jb + 8*(i/4) + 4*g + (i%4) of row ln)
+    float bmax = kInitMax;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t kj = jb + 8 * (i >> 2) + 4 * g + (i & 3);
+      const bool ok = rvalid && kj < j1 && key_allowed(kj, P, t, mask_mode, nb);
+      s[i] = ok ? s[i] * scale : kMaskedScore;
+      bmax = fmaxf(bmax, s[i]);
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    const float mnew = fmaxf(m, bmax);
+    const float alpha = expf(m - mnew);
+    float psum = 0.f;
+    uint32_t pb[8];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = expf(s[i] - mnew), p1 = expf(s[i + 1] - mnew);
+      psum += p0 + p1;
+      pb[i >> 1] = (DT == PE_DTYPE_F16) ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
+                                        : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
+    }
+    psum += __shfl_xor(psum, 32, 64);
+    l = l * alpha + psum;
+    m = mnew;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[h][i] *= alpha;
+
+    // ---- V^T into LDS
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int chunk = c * 64 + lane;
+      const int koff = chunk >> 4, dc = chunk & 15;
+      const uint16_t* ve = (const uint16_t*)&vf[c];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt[dc * 8 + e][koff] = ve[e];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- O^T += V^T P^T: two 16-key halves c; lane group g holds keys 16c+4g+{0..3}, 16c+8+4g+{0..3}
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      u32x4_t b;
+      b[0] = pb[4 * c + 0];
+      b[1] = pb[4 * c + 1];
+      b[2] = pb[4 * c + 2];
+      b[3] = pb[4 * c + 3];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int d = h * 32 + ln;
+        const uint2 lo = *(const uint2*)&vt[d][16 * c + 4 * g];
+        const uint2 hi = *(const uint2*)&vt[d][16 * c + 8 + 4 * g];
+        u32x4_t a;
+        a[0] = lo.x;
+        a[1] = lo.y;
+        a[2] = hi.x;
+        a[3] = hi.y;
+        if constexpr (DT == PE_DTYPE_F16)
+          o[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                        __builtin_bit_cast(f16x8_t, b), o[h], 0, 0, 0);
+        else
+          o[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                         __builtin_bit_cast(bf16x8_t, b), o[h], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  if (!rvalid) return;
+  const int64_t pidx = ((int64_t)kvh * splits + split) * rows_pad + r;
+  float* op = opart + pidx * HD;
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) op[h * 32 + 8 * (i >> 2) + 4 * g + (i & 3)] = o[h][i];
+  if (g == 0) {
+    mlpart[pidx * 2 + 0] = m;
+    mlpart[pidx * 2 + 1] = l;
+  }
+}
+
+// out[t][hq*hd + d] = sum_s e^{m_s - M} O_s[d] / sum_s e^{m_s - M} l_s
+template <int DT>
+__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ opart,
+                                                           const float* __restrict__ mlpart, int nh, int nkv, int T,
+                                                           int hd, int splits, int rows_pad,
+                                                           typename Elem<DT>::T* __restrict__ out, int64_t ld_out) {
+  const int r = blockIdx.x, kvh = blockIdx.y;
+  const int G = nh / nkv;
+  const int t = r / G, hq = kvh * G + r % G;
+  float M = kInitMax;
+  for (int s = 0; s < splits; ++s) M = fmaxf(M, mlpart[(((int64_t)kvh * splits + s) * rows_pad + r) * 2]);
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < splits; ++s) {
+      const int64_t pidx = ((int64_t)kvh * splits + s) * rows_pad + r;
+      const float w = expf(mlpart[pidx * 2] - M);
+      den += w * mlpart[pidx * 2 + 1];
+      num += w * opart[pidx * hd + d];
+    }
+    Elem<DT>::store(out, (int64_t)t * ld_out + (int64_t)hq * hd + d, num / den);
+  }
+}
+
+// Generic path (fp32, any hd <= 256): one block per (row t, query head), all keys.
+template <int DT>
+__global__ __launch_bounds__(128) void attn_generic_kernel(
+    const typename Elem<DT>::T* __restrict__ q, const typename Elem<DT>::T* __restrict__ kc,
+    const typename Elem<DT>::T* __restrict__ vc, int64_t cap, int nh, int nkv, int hd, int T, int64_t P,
+    int mask_mode, const uint64_t* __restrict__ bits, int words, float scale, typename Elem<DT>::T* __restrict__ out,
+    int64_t ld_out, float* __restrict__ scores /* [T*nh][P+T] */) {
+  typedef Elem<DT> E;
+  const int t = blockIdx.x, hq = blockIdx.y;
+  const int G = nh / nkv, kvh = hq / G;
+  const int64_t S = P + T;
+  uint64_t nb[PE_TREE_MAX_WORDS];
+  for (int w = 0; w < PE_TREE_MAX_WORDS; ++w)
+    nb[w] = (mask_mode == PE_MASK_TREE && w < words) ? bits[(int64_t)t * words + w] : 0ull;
+  const typename E::T* qr = q + ((int64_t)t * nh + hq) * hd;
+  float* sc = scores + ((int64_t)t * nh + hq) * S;
+  __shared__ float red[2];
+  float lmax = kInitMax;
+  for (int64_t j = threadIdx.x; j < S; j += blockDim.x) {
+    float v = kMaskedScore;
+    if (key_allowed(j, P, t, mask_mode, nb)) {
+      const typename E::T* kr = kc + ((int64_t)kvh * cap + j) * hd;
+      float acc = 0.f;
+      for (int d = 0; d < hd; ++d) acc = fmaf(E::load(qr, d), E::load(kr, d), acc);
+      v = acc * scale;
+    }
+    sc[j] = v;
+    lmax = fmaxf(lmax, v);
+  }
+  lmax = wave_max(lmax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = lmax;
+  __syncthreads();
+  const float M = fmaxf(red[0], red[1]);
+  __syncthreads();
+  float lsum = 0.f;
+  for (int64_t j = threadIdx.x; j < S; j += blockDim.x) {
+    const float p = expf(sc[j] - M);
+    sc[j] = p;
+    lsum += p;
+  }
+  lsum = wave_sum(lsum);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = lsum;
+  __syncthreads();
+  const float L = red[0] + red[1];
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    float acc = 0.f;
+    for (int64_t j = 0; j < S; ++j) {
+      const float p = sc[j];
+      if (p != 0.f) acc = fmaf(E::round(p), E::load(vc + ((int64_t)kvh * cap + j) * hd, d), acc);
+    }
+    E::store(out, (int64_t)t * ld_out + (int64_t)hq * hd + d, acc / L);
+  }
+}
+
+struct AttnPlan {
+  int splits, keys_per_split, row_tiles, rows_pad;
+  int64_t opart_bytes, ml_bytes;
+};
+
+AttnPlan attn_plan(int T, int nh, int nkv, int64_t S) {
+  AttnPlan p;
+  const int rows = T * (nh / nkv);
+  p.row_tiles = (rows + 31) / 32;
+  p.rows_pad = p.row_tiles * 32;
+  // aim for ~512 waves; at least 64 keys per split
+  int64_t want = (512 + (int64_t)nkv * p.row_tiles - 1) / ((int64_t)nkv * p.row_tiles);
+  int64_t maxsplit = (S + 63) / 64;
+  if (want > maxsplit) want = maxsplit;
+  if (want < 1) want = 1;
+  int64_t kps = (S + want - 1) / want;
+  kps = ((kps + 31) / 32) * 32;
+  p.keys_per_split = (int)kps;
+  p.splits = (int)((S + kps - 1) / kps);
+  p.opart_bytes = (int64_t)nkv * p.splits * p.rows_pad * 128 * 4;
+  p.ml_bytes = (int64_t)nkv * p.splits * p.rows_pad * 2 * 4;
+  return p;
+}
+
+}  // namespace
+
+extern "C" int64_t pe_attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_len, int dtype) {
+  if (T <= 0 || nh <= 0 || nkv <= 0 || kv_len <= 0) return 0;
+  if (dtype != PE_DTYPE_F32 && hd == 128) {
+    AttnPlan p = attn_plan(T, nh, nkv, kv_len);
+    return p.opart_bytes + p.ml_bytes;
+  }
+  return (int64_t)T * nh * kv_len * 4;
+}
+
+extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap, int nh,
+                                 int nkv, int hd, int T, int64_t P, int mask_mode, const uint64_t* bits, int words,
+                                 float scale, int dtype, void* out, int64_t ld_out, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  if (!q || !k_cache || !v_cache || !out || !workspace) return PE_ERR_ARG;
+  if (T <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || hd <= 0 || hd > 256 || P < 0) return PE_ERR_ARG;
+  if (P + T > cache_cap) return PE_ERR_CAPACITY;
+  if (mask_mode != PE_MASK_TREE && mask_mode != PE_MASK_CAUSAL) return PE_ERR_ARG;
+  if (mask_mode == PE_MASK_TREE && (!bits || words <= 0 || words > PE_TREE_MAX_WORDS || T > 64 * words))
+    return PE_ERR_TREE;
+  const int64_t S = P + T;
+  if (workspace_bytes < pe_attention_workspace_bytes(T, nh, nkv, hd, S, dtype)) return PE_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype != PE_DTYPE_F32 && hd == 128) {
+    AttnPlan p = attn_plan(T, nh, nkv, S);
+    float* opart = (float*)workspace;
+    float* ml = (float*)((char*)workspace + p.opart_bytes);
+    dim3 grid(nkv, p.splits, p.row_tiles);
+    dim3 cgrid(T * (nh / nkv), nkv);
+    if (dtype == PE_DTYPE_BF16) {
+      attn_mfma_kernel<PE_DTYPE_BF16><<<grid, 64, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
+                                                           (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
+                                                           mask_mode, bits, words, scale, p.keys_per_split,
+                                                           p.splits, p.rows_pad, opart, ml);
+      PE_CHECK_LAUNCH();
+      attn_combine_kernel<PE_DTYPE_BF16><<<cgrid, 128, 0, st>>>(opart, ml, nh, nkv, T, hd, p.splits, p.rows_pad,
+                                                                (uint16_t*)out, ld_out);
+    } else if (dtype == PE_DTYPE_F16) {
+      attn_mfma_kernel<PE_DTYPE_F16><<<grid, 64, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
+                                                          (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
+                                                          mask_mode, bits, words, scale, p.keys_per_split, p.splits,
+                                                          p.rows_pad, opart, ml);
+      PE_CHECK_LAUNCH();
+      attn_combine_kernel<PE_DTYPE_F16><<<cgrid, 128, 0, st>>>(opart, ml, nh, nkv, T, hd, p.splits, p.rows_pad,
+                                                               (uint16_t*)out, ld_out);
+    } else {
+      return PE_ERR_ARG;
+    }
+    PE_CHECK_LAUNCH();
+    return PE_OK;
+  }
+  dim3 grid(T, nh);
+  float* scores = (float*)workspace;
+  switch (dtype) {
+    case PE_DTYPE_F32:
+      attn_generic_kernel<PE_DTYPE_F32><<<grid, 128, 0, st>>>((const float*)q, (const float*)k_cache,
+                                                              (const float*)v_cache, cache_cap, nh, nkv, hd, T, P,
+                                                              mask_mode, bits, words, scale, (float*)out, ld_out,
+                                                              scores);
+      break;
+    case PE_DTYPE_BF16:
+      attn_generic_kernel<PE_DTYPE_BF16><<<grid, 128, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
+                                                               (const uint16_t*)v_cache, cache_cap, nh, nkv, hd, T,
+                                                               P, mask_mode, bits, words, scale, (uint16_t*)out,
+                                                               ld_out, scores);
+      break;
+    case PE_DTYPE_F16:
+      attn_generic_kernel<PE_DTYPE_F16><<<grid, 128, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
+                                                              (const uint16_t*)v_cache, cache_cap, nh, nkv, hd, T, P,
+                                                              mask_mode, bits, words, scale, (uint16_t*)out, ld_out,
+                                                              scores);
+      break;
+    default:
+      return PE_ERR_ARG;
+  }
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}

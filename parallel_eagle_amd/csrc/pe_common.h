@@ -1,0 +1,82 @@
+// Shared device helpers for the verification-pass kernels (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/pe_hip.h"
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+
+#define PE_WAVE 64
+
+// ---------------------------------------------------------------------------
+// Scalar conversions. Rounding is round-to-nearest-even everywhere, which is
+// what torch's float -> bfloat16 / float16 casts do.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  __bf16 h = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+// Element access by storage type: dtype codes follow PE_DTYPE_* in pe_hip.h.
+template <int DT> struct Elem;
+template <> struct Elem<PE_DTYPE_F32> {
+  typedef float T;
+  static __device__ __forceinline__ float load(const T* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(T* p, int64_t i, float v) { p[i] = v; }
+  static __device__ __forceinline__ float round(float v) { return v; }
+};
+template <> struct Elem<PE_DTYPE_BF16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float load(const T* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+  static __device__ __forceinline__ void store(T* p, int64_t i, float v) { p[i] = f32_to_bf16_bits(v); }
+  static __device__ __forceinline__ float round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+};
+template <> struct Elem<PE_DTYPE_F16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float load(const T* p, int64_t i) { return f16_bits_to_f32(p[i]); }
+  static __device__ __forceinline__ void store(T* p, int64_t i, float v) { p[i] = f32_to_f16_bits(v); }
+  static __device__ __forceinline__ float round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
+};
+
+// The published NF4 code book (QLoRA / bitsandbytes), fp32. Code 7 is 0.
+__device__ __constant__ static const float kNF4[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+
+// Wave-level reductions (wave64) through DPP-free shuffles.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+#define PE_CHECK_LAUNCH()                                   \
+  do {                                                      \
+    hipError_t _e = hipGetLastError();                      \
+    if (_e != hipSuccess) return PE_ERR_LAUNCH;             \
+  } while (0)
+
+static inline int pe_cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }

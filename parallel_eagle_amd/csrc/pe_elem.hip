@@ -1,0 +1,177 @@
+// Row-wise ops of the decoder layer: token embedding, RMSNorm, RoPE with the
+// in-place KV append, and row copies for the fused features.
+//
+// Rounding mirrors HF Llama/Qwen2 in the compute dtype: RMSNorm statistics in
+// fp32, the normalised row rounded to the dtype before the weight multiply
+// (HF modeling_llama.py:62-67); RoPE as round(round(q*cos) + round(rot(q)*sin))
+// (modeling_llama.py:130-160). fp32 arithmetic uses __fmul_rn/__fadd_rn so no
+// multiply-add is contracted where torch rounds between the two.
+
+#include "pe_common.h"
+
+namespace {
+
+template <int DT>
+__global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ ids, const typename Elem<DT>::T* __restrict__ table,
+                                                    int64_t V, int H, typename Elem<DT>::T* __restrict__ out,
+                                                    int64_t ld_out, int32_t* status) {
+  const int m = blockIdx.x;
+  const int64_t id = ids[m];
+  const bool ok = id >= 0 && id < V;
+  if (!ok && threadIdx.x == 0 && status) atomicOr(status, PE_ERR_TOKEN);
+  for (int c = threadIdx.x; c < H; c += blockDim.x)
+    out[(int64_t)m * ld_out + c] = ok ? table[id * H + c] : (typename Elem<DT>::T)0;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t ldx, int H,
+                                                      const typename Elem<DT>::T* __restrict__ w, float eps,
+                                                      typename Elem<DT>::T* __restrict__ out, int64_t ld_out) {
+  typedef Elem<DT> E;
+  const int m = blockIdx.x;
+  const typename E::T* xr = x + (int64_t)m * ldx;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < H; c += blockDim.x) {
+    const float v = E::load(xr, c);
+    ss = __fadd_rn(ss, __fmul_rn(v, v));
+  }
+  __shared__ float part[4];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const int nw = blockDim.x >> 6;
+  float tot = 0.f;
+  for (int i = 0; i < nw; ++i) tot += part[i];
+  const float var = tot / (float)H;
+  const float inv = 1.0f / sqrtf(var + eps);
+  typename E::T* orow = out + (int64_t)m * ld_out;
+  for (int c = threadIdx.x; c < H; c += blockDim.x) {
+    const float y = E::round(__fmul_rn(E::load(xr, c), inv));
+    E::store(orow, c, __fmul_rn(E::load(w, c), y));
+  }
+}
+
+// One block per row m; threads over (head, d < hd/2) pairs of q and k, then v copies.
+template <int DT>
+__global__ __launch_bounds__(256) void rope_qkv_kernel(const typename Elem<DT>::T* __restrict__ qkv, int64_t ld_qkv, int nh,
+                                                       int nkv, int hd, const int64_t* __restrict__ pos,
+                                                       const typename Elem<DT>::T* __restrict__ cs, int64_t max_pos,
+                                                       typename Elem<DT>::T* __restrict__ q_out,
+                                                       typename Elem<DT>::T* __restrict__ kc,
+                                                       typename Elem<DT>::T* __restrict__ vc, int64_t cap,
+                                                       int64_t row0, int32_t* status) {
+  typedef Elem<DT> E;
+  const int m = blockIdx.x;
+  const int64_t p = pos[m];
+  const bool ok = p >= 0 && p < max_pos;
+  if (!ok) {
+    if (threadIdx.x == 0 && status) atomicOr(status, PE_ERR_CAPACITY);
+    return;
+  }
+  const int half = hd >> 1;
+  const typename E::T* cosr = cs + p * hd;
+  const typename E::T* sinr = cs + (max_pos + p) * hd;
+  const typename E::T* row = qkv + (int64_t)m * ld_qkv;
+  const int64_t dst_row = row0 + m;
+  const int nq = nh * half, nk = nkv * half;
+  for (int i = threadIdx.x; i < nq + nk; i += blockDim.x) {
+    const bool is_q = i < nq;
+    const int ii = is_q ? i : i - nq;
+    const int h = ii / half, d = ii % half;
+    const typename E::T* src = row + (is_q ? h * hd : nh * hd + h * hd);
+    const float x1 = E::load(src, d), x2 = E::load(src, d + half);
+    const float c1 = E::load(cosr, d), s1 = E::load(sinr, d);
+    const float c2 = E::load(cosr, d + half), s2 = E::load(sinr, d + half);
+    const float o1 = __fadd_rn(E::round(__fmul_rn(x1, c1)), E::round(__fmul_rn(-x2, s1)));
+    const float o2 = __fadd_rn(E::round(__fmul_rn(x2, c2)), E::round(__fmul_rn(x1, s2)));
+    if (is_q) {
+      typename E::T* dst = q_out + ((int64_t)m * nh + h) * hd;
+      E::store(dst, d, o1);
+      E::store(dst, d + half, o2);
+    } else {
+      typename E::T* dst = kc + ((int64_t)h * cap + dst_row) * hd;
+      E::store(dst, d, o1);
+      E::store(dst, d + half, o2);
+    }
+  }
+  const typename E::T* vsrc = row + (nh + nkv) * hd;
+  for (int i = threadIdx.x; i < nkv * hd; i += blockDim.x) {
+    const int h = i / hd, d = i % hd;
+    vc[((int64_t)h * cap + dst_row) * hd + d] = vsrc[h * hd + d];
+  }
+}
+
+__global__ void copy_rows_kernel(const uint8_t* __restrict__ src, int64_t ld_src, int64_t row_bytes,
+                                 uint8_t* __restrict__ dst, int64_t ld_dst) {
+  const int m = blockIdx.x;
+  const uint8_t* s = src + (int64_t)m * ld_src;
+  uint8_t* d = dst + (int64_t)m * ld_dst;
+  if ((row_bytes & 3) == 0 && (((uintptr_t)s | (uintptr_t)d) & 3) == 0) {
+    for (int64_t i = threadIdx.x; i < row_bytes / 4; i += blockDim.x)
+      ((uint32_t*)d)[i] = ((const uint32_t*)s)[i];
+  } else {
+    for (int64_t i = threadIdx.x; i < row_bytes; i += blockDim.x) d[i] = s[i];
+  }
+}
+
+}  // namespace
+
+#define PE_DISPATCH_DT(dtype, ...)                               \
+  switch (dtype) {                                               \
+    case PE_DTYPE_F32: { constexpr int DT = PE_DTYPE_F32; __VA_ARGS__; } break;  \
+    case PE_DTYPE_BF16: { constexpr int DT = PE_DTYPE_BF16; __VA_ARGS__; } break; \
+    case PE_DTYPE_F16: { constexpr int DT = PE_DTYPE_F16; __VA_ARGS__; } break;   \
+    default: return PE_ERR_ARG;                                  \
+  }
+
+extern "C" int pe_embed(const int64_t* ids, int M, const void* table, int64_t V, int H, int dtype, void* out,
+                        int64_t ld_out, int32_t* status, void* stream) {
+  if (!ids || !table || !out || M <= 0 || V <= 0 || H <= 0) return PE_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  PE_DISPATCH_DT(dtype, {
+    typedef typename Elem<DT>::T T;
+    embed_kernel<DT><<<M, 256, 0, st>>>(ids, (const T*)table, V, H, (T*)out, ld_out, status);
+  });
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+extern "C" int pe_rmsnorm(const void* x, int64_t ldx, int M, int H, const void* w, float eps, int dtype,
+                          void* out, int64_t ld_out, void* stream) {
+  if (!x || !w || !out || M <= 0 || H <= 0) return PE_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  PE_DISPATCH_DT(dtype, {
+    typedef typename Elem<DT>::T T;
+    rmsnorm_kernel<DT><<<M, 256, 0, st>>>((const T*)x, ldx, H, (const T*)w, eps, (T*)out, ld_out);
+  });
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+extern "C" int pe_rope_qkv(const void* qkv, int64_t ld_qkv, int M, int nh, int nkv, int hd,
+                           const int64_t* positions, const void* cos_sin, int64_t max_pos, int dtype,
+                           void* q_out, void* k_cache, void* v_cache, int64_t cache_cap, int64_t row0,
+                           int32_t* status, void* stream) {
+  if (!qkv || !positions || !cos_sin || !q_out || !k_cache || !v_cache) return PE_ERR_ARG;
+  if (M <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || hd <= 0 || hd % 2 || row0 < 0) return PE_ERR_ARG;
+  if (row0 + M > cache_cap) return PE_ERR_CAPACITY;
+  hipStream_t st = (hipStream_t)stream;
+  PE_DISPATCH_DT(dtype, {
+    typedef typename Elem<DT>::T T;
+    rope_qkv_kernel<DT><<<M, 256, 0, st>>>((const T*)qkv, ld_qkv, nh, nkv, hd, positions, (const T*)cos_sin,
+                                           max_pos, (T*)q_out, (T*)k_cache, (T*)v_cache, cache_cap, row0,
+                                           status);
+  });
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+extern "C" int pe_copy_rows(const void* src, int64_t ld_src, int M, int64_t row_bytes, void* dst, int64_t ld_dst,
+                            void* stream) {
+  if (!src || !dst || M < 0 || row_bytes < 0) return PE_ERR_ARG;
+  if (M == 0 || row_bytes == 0) return PE_OK;
+  copy_rows_kernel<<<M, 256, 0, (hipStream_t)stream>>>((const uint8_t*)src, ld_src, row_bytes, (uint8_t*)dst,
+                                                       ld_dst);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}

@@ -1,0 +1,177 @@
+// Whole verification pass: the decoder forward of TargetModel.forward_cached
+// (src/pe/target.py:203-224 -> HF modeling_llama.py:367-480), launched from
+// C++ as one sequence of kernels on the caller's stream so a host loop over
+// layers never sits between launches (and the sequence can be captured in a
+// HIP graph by the caller).
+//
+// Per layer:
+//   rmsnorm -> qkv linear (+bias) -> RoPE + in-place K/V append -> tree attention
+//   -> o linear (+residual) -> rmsnorm -> gate/up linear (SwiGLU epilogue)
+//   -> down linear (+residual)
+// then final rmsnorm and lm_head over all rows. Hidden-state slots for the fused
+// features follow HF's output_hidden_states tuple: slot 0 = embeddings, slot
+// i in [1, L) = residual stream after layer i, slot L = final-norm output
+// (HF utils/output_capturing.py:269-277; src/pe/target.py:161-162).
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+
+#include "../../include/pe_hip.h"
+
+namespace {
+
+constexpr int64_t kAlign = 256;
+constexpr int64_t kCounterBytes = 32768;
+
+int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+int esize(int dtype) { return dtype == PE_DTYPE_F32 ? 4 : 2; }
+
+struct Layout {
+  int64_t gemm;  // counters + partials (must start with the zeroed counters)
+  int64_t gemm_bytes;
+  int64_t h, xn, qkv, q, attn, act, attn_ws, attn_ws_bytes, total;
+};
+
+int64_t gemm_ws(const pe_model_desc* m, int M, int N, int K, int epi) {
+  const int wf = m->weight_format;
+  return pe_gemm_workspace_bytes(M, N, K, wf, m->dtype, epi);
+}
+
+Layout make_layout(const pe_model_desc* m, int M, int64_t kv_len) {
+  Layout L;
+  const int es = esize(m->dtype);
+  const int H = m->hidden, qd = m->num_heads * m->head_dim, kvd = m->num_kv_heads * m->head_dim;
+  const int nqkv = qd + 2 * kvd, ip = m->intermediate_padded;
+  int64_t g = kCounterBytes;
+  int64_t cand[5] = {gemm_ws(m, M, nqkv, H, PE_EPI_STORE), gemm_ws(m, M, H, qd, PE_EPI_RESIDUAL),
+                     gemm_ws(m, M, 2 * ip, H, PE_EPI_SWIGLU), gemm_ws(m, M, H, ip, PE_EPI_RESIDUAL),
+                     pe_gemm_workspace_bytes(M, m->vocab, H, PE_WFMT_DENSE, m->dtype, PE_EPI_STORE)};
+  for (int i = 0; i < 5; ++i)
+    if (cand[i] > g) g = cand[i];
+  int64_t off = 0;
+  L.gemm = off;
+  L.gemm_bytes = align_up(g);
+  off += L.gemm_bytes;
+  L.h = off; off += align_up((int64_t)M * H * es);
+  const int xw = H > ip ? H : ip;
+  L.xn = off; off += align_up((int64_t)M * (xw > qd ? xw : qd) * es);
+  L.qkv = off; off += align_up((int64_t)M * nqkv * es);
+  L.q = off; off += align_up((int64_t)M * qd * es);
+  L.attn = off; off += align_up((int64_t)M * qd * es);
+  L.act = off; off += align_up((int64_t)M * ip * es);
+  L.attn_ws = off;
+  L.attn_ws_bytes = align_up(pe_attention_workspace_bytes(M, m->num_heads, m->num_kv_heads, m->head_dim, kv_len,
+                                                          m->dtype));
+  off += L.attn_ws_bytes;
+  L.total = off;
+  return L;
+}
+
+int linear(const pe_model_desc* m, const void* x, int64_t ldx, int M, int K, const void* w, const void* a, int N,
+           int epi, const void* bias, const void* resid, int64_t ldr, void* out, int64_t ldo, void* ws, int64_t wsb,
+           hipStream_t st) {
+  if (m->weight_format == PE_WFMT_NF4)
+    return pe_nf4_gemm(x, ldx, M, K, (const uint8_t*)w, (const uint16_t*)a, N, epi, bias, resid, ldr, out, ldo, ws,
+                       wsb, st);
+  return pe_dense_gemm(x, ldx, M, K, w, m->dtype, N, epi, bias, resid, ldr, out, ldo, ws, wsb, st);
+}
+
+}  // namespace
+
+extern "C" const char* pe_status_string(int status) {
+  if (status == PE_OK) return "ok";
+  if (status & PE_ERR_ARG) return "invalid argument";
+  if (status & PE_ERR_LAUNCH) return "kernel launch failed";
+  if (status & PE_ERR_TREE) return "parents are not a topologically ordered tree (or tree too large)";
+  if (status & PE_ERR_CAPACITY) return "KV cache capacity or position table exceeded";
+  if (status & PE_ERR_MASK) return "attention bias is not a prefix + ancestor tree mask";
+  if (status & PE_ERR_TOKEN) return "token id outside the vocabulary";
+  if (status & PE_ERR_INDEX) return "keep index not strictly increasing or out of range";
+  if (status & PE_ERR_WORKSPACE) return "workspace too small";
+  return "unknown error";
+}
+
+extern "C" int pe_version(void) { return 1; }
+
+extern "C" int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int64_t kv_len) {
+  if (!m || M <= 0 || kv_len <= 0) return 0;
+  return make_layout(m, M, kv_len).total;
+}
+
+extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* stream) {
+  if (!m || !a) return PE_ERR_ARG;
+  const int M = a->M;
+  if (M <= 0 || !a->input_ids || !a->positions || !a->k_cache || !a->v_cache || !a->workspace) return PE_ERR_ARG;
+  if (a->prefix_len < 0 || a->prefix_len + M > a->cache_capacity) return PE_ERR_CAPACITY;
+  if (a->num_features < 0 || a->num_features > 4) return PE_ERR_ARG;
+  if (a->mask_mode == PE_MASK_TREE && !a->tree_bits) return PE_ERR_ARG;
+  if (m->intermediate_padded % 32 || m->intermediate_padded < m->intermediate) return PE_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t kv_len = a->prefix_len + M;
+  const Layout Lo = make_layout(m, M, kv_len);
+  if (a->workspace_bytes < Lo.total) return PE_ERR_WORKSPACE;
+  char* ws = (char*)a->workspace;
+  void* gws = ws + Lo.gemm;
+  const int64_t gwsb = Lo.gemm_bytes;
+  const int es = esize(m->dtype);
+  const int H = m->hidden, nh = m->num_heads, nkv = m->num_kv_heads, hd = m->head_dim;
+  const int qd = nh * hd, kvd = nkv * hd, nqkv = qd + 2 * kvd, ip = m->intermediate_padded;
+  void* h = ws + Lo.h;
+  void* xn = ws + Lo.xn;
+  void* qkv = ws + Lo.qkv;
+  void* q = ws + Lo.q;
+  void* attn = ws + Lo.attn;
+  void* act = ws + Lo.act;
+  void* aws = ws + Lo.attn_ws;
+  const float scale = (float)(1.0 / std::sqrt((double)hd));
+  const int64_t layer_stride = (int64_t)nkv * a->cache_capacity * hd * es;
+  const int64_t fused_ld = (int64_t)a->num_features * H * es;
+  int rc;
+#define PE_TRY(expr)            \
+  do {                          \
+    rc = (expr);                \
+    if (rc != PE_OK) return rc; \
+  } while (0)
+
+  auto capture = [&](int slot_layer, const void* src) -> int {
+    if (!a->fused) return PE_OK;
+    for (int f = 0; f < a->num_features; ++f) {
+      if (a->feature_layers[f] != slot_layer) continue;
+      int r = pe_copy_rows(src, (int64_t)H * es, M, (int64_t)H * es, (char*)a->fused + (int64_t)f * H * es, fused_ld,
+                           st);
+      if (r != PE_OK) return r;
+    }
+    return PE_OK;
+  };
+
+  PE_TRY(pe_embed(a->input_ids, M, m->embed, m->vocab, H, m->dtype, h, H, a->status, st));
+  PE_TRY(capture(0, h));
+  for (int l = 0; l < m->num_layers; ++l) {
+    void* kc = (char*)a->k_cache + l * layer_stride;
+    void* vc = (char*)a->v_cache + l * layer_stride;
+    PE_TRY(pe_rmsnorm(h, H, M, H, m->attn_norm[l], m->rms_eps, m->dtype, xn, H, st));
+    PE_TRY(linear(m, xn, H, M, H, m->w_qkv[l], m->a_qkv ? m->a_qkv[l] : nullptr, nqkv, PE_EPI_STORE,
+                  m->b_qkv ? m->b_qkv[l] : nullptr, nullptr, 0, qkv, nqkv, gws, gwsb, st));
+    PE_TRY(pe_rope_qkv(qkv, nqkv, M, nh, nkv, hd, a->positions, m->rope_cos_sin, m->max_positions, m->dtype, q, kc, vc,
+                       a->cache_capacity, a->prefix_len, a->status, st));
+    PE_TRY(pe_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode, a->tree_bits,
+                             a->bits_words, scale, m->dtype, attn, qd, aws, Lo.attn_ws_bytes, st));
+    PE_TRY(linear(m, attn, qd, M, qd, m->w_o[l], m->a_o ? m->a_o[l] : nullptr, H, PE_EPI_RESIDUAL, nullptr, h, H, h,
+                  H, gws, gwsb, st));
+    PE_TRY(pe_rmsnorm(h, H, M, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, H, st));
+    PE_TRY(linear(m, xn, H, M, H, m->w_gu[l], m->a_gu ? m->a_gu[l] : nullptr, 2 * ip, PE_EPI_SWIGLU, nullptr,
+                  nullptr, 0, act, ip, gws, gwsb, st));
+    PE_TRY(linear(m, act, ip, M, ip, m->w_down[l], m->a_down ? m->a_down[l] : nullptr, H, PE_EPI_RESIDUAL, nullptr,
+                  h, H, h, H, gws, gwsb, st));
+    if (l + 1 < m->num_layers) PE_TRY(capture(l + 1, h));
+  }
+  PE_TRY(pe_rmsnorm(h, H, M, H, m->final_norm, m->rms_eps, m->dtype, xn, H, st));
+  PE_TRY(capture(m->num_layers, xn));
+  if (a->logits)
+    PE_TRY(pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
+                         m->vocab, gws, gwsb, st));
+#undef PE_TRY
+  return PE_OK;
+}

@@ -1,0 +1,292 @@
+"""Thin torch-tensor wrappers over the C ABI of libpe_hip.so.
+
+Every function takes device tensors, validates shapes and dtypes on the host,
+launches on torch's current HIP stream and raises ``PEError`` on a non-zero
+status. They are registered as torch custom ops under the ``pe`` namespace
+(``torch.ops.pe.*``) where a functional form exists; in-place cache updates
+stay plain functions. There is no CPU implementation behind any of them.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+from ._lib import check
+
+DTYPE_CODE = {torch.float32: _lib.PE_DTYPE_F32, torch.bfloat16: _lib.PE_DTYPE_BF16, torch.float16: _lib.PE_DTYPE_F16}
+
+
+def lib():
+    return _lib.load()
+
+
+def stream_ptr() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("parallel_eagle_amd kernels take HIP device tensors")
+    return t.data_ptr()
+
+
+def dcode(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODE[dtype]
+    except KeyError as e:
+        raise TypeError(f"unsupported dtype {dtype}") from e
+
+
+def _req(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+# ------------------------------------------------------------------ synthetic / formats
+def fill_normal(out: torch.Tensor, seed: int, stream_id: int, std: float) -> torch.Tensor:
+    _req(out.is_contiguous(), "out must be contiguous")
+    check(lib().pe_fill_normal(ptr(out), out.numel(), dcode(out.dtype), seed, stream_id, std, stream_ptr()),
+          "pe_fill_normal")
+    return out
+
+
+def fill_uniform_int(out: torch.Tensor, hi: int, seed: int, stream_id: int) -> torch.Tensor:
+    _req(out.dtype == torch.int64 and out.is_contiguous(), "out must be contiguous int64")
+    check(lib().pe_fill_uniform_int(ptr(out), out.numel(), hi, seed, stream_id, stream_ptr()), "pe_fill_uniform_int")
+    return out
+
+
+def nf4_quantize(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    _req(w.dtype == torch.float32 and w.dim() == 2 and w.is_contiguous(), "w must be contiguous fp32 [N][K]")
+    n, k = w.shape
+    _req(k % 64 == 0, "K must be a multiple of 64")
+    packed = torch.empty((n, k // 2), dtype=torch.uint8, device=w.device)
+    absmax = torch.empty((n, k // 64), dtype=torch.float16, device=w.device)
+    check(lib().pe_nf4_quantize(ptr(w), n, k, ptr(packed), ptr(absmax), stream_ptr()), "pe_nf4_quantize")
+    return packed, absmax
+
+
+def nf4_repack(packed: torch.Tensor, absmax: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    n, kh = packed.shape
+    k = kh * 2
+    _req(packed.dtype == torch.uint8 and packed.is_contiguous(), "packed must be contiguous uint8 [N][K/2]")
+    _req(absmax.dtype == torch.float16 and absmax.shape == (n, k // 64) and absmax.is_contiguous(),
+         "absmax must be contiguous fp16 [N][K/64]")
+    _req(n % 32 == 0 and k % 128 == 0, "N % 32 == 0 and K % 128 == 0 required")
+    tiled = torch.empty(n * k // 2, dtype=torch.uint8, device=packed.device)
+    tabs = torch.empty(n * k // 64, dtype=torch.float16, device=packed.device)
+    check(lib().pe_nf4_repack(ptr(packed), ptr(absmax), n, k, ptr(tiled), ptr(tabs), stream_ptr()), "pe_nf4_repack")
+    return tiled, tabs
+
+
+def nf4_dequant(tiled: torch.Tensor, tabs: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=tiled.device)
+    check(lib().pe_nf4_dequant(ptr(tiled), ptr(tabs), n, k, ptr(out), stream_ptr()), "pe_nf4_dequant")
+    return out
+
+
+def dense_repack(w: torch.Tensor) -> torch.Tensor:
+    _req(w.dim() == 2 and w.is_contiguous(), "w must be contiguous [N][K]")
+    n, k = w.shape
+    out = torch.empty(n * k, dtype=w.dtype, device=w.device)
+    check(lib().pe_dense_repack(ptr(w), n, k, dcode(w.dtype), ptr(out), stream_ptr()), "pe_dense_repack")
+    return out
+
+
+# ------------------------------------------------------------------ GEMMs
+def gemm_workspace_bytes(m: int, n: int, k: int, nf4: bool, dtype: torch.dtype, epilogue: int) -> int:
+    return int(lib().pe_gemm_workspace_bytes(m, n, k, _lib.PE_WFMT_NF4 if nf4 else _lib.PE_WFMT_DENSE,
+                                             dcode(dtype), epilogue))
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+
+def linear(x: torch.Tensor, n: int, *, nf4: tuple | None = None, dense: torch.Tensor | None = None,
+           epilogue: int = _lib.PE_EPI_STORE, bias: torch.Tensor | None = None, resid: torch.Tensor | None = None,
+           out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Y = X . W^T with W given as nf4=(tiled, tabs) or dense (tiled/row-major)."""
+    _req(x.dim() == 2 and x.stride(1) == 1, "x must be [M][K] with unit column stride")
+    m, k = x.shape
+    n_out = n // 2 if epilogue == _lib.PE_EPI_SWIGLU else n
+    if out is None:
+        out = torch.empty((m, n_out), dtype=x.dtype, device=x.device)
+    _req(out.shape == (m, n_out) and out.stride(1) == 1 and out.dtype == x.dtype, "bad out")
+    if resid is not None:
+        _req(resid.shape == (m, n_out) and resid.dtype == x.dtype, "bad resid")
+    if workspace is None:
+        workspace = _workspace(gemm_workspace_bytes(m, n, k, nf4 is not None, x.dtype, epilogue), x.device)
+    L = lib()
+    if nf4 is not None:
+        _req(x.dtype == torch.bfloat16, "NF4 linears compute in bf16")
+        rc = L.pe_nf4_gemm(ptr(x), x.stride(0), m, k, ptr(nf4[0]), ptr(nf4[1]), n, epilogue, ptr(bias), ptr(resid),
+                           resid.stride(0) if resid is not None else 0, ptr(out), out.stride(0), ptr(workspace),
+                           workspace.numel(), stream_ptr())
+    else:
+        rc = L.pe_dense_gemm(ptr(x), x.stride(0), m, k, ptr(dense), dcode(x.dtype), n, epilogue, ptr(bias),
+                             ptr(resid), resid.stride(0) if resid is not None else 0, ptr(out), out.stride(0),
+                             ptr(workspace), workspace.numel(), stream_ptr())
+    check(rc, "linear")
+    return out
+
+
+# ------------------------------------------------------------------ elementwise
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    _req(x.dim() == 2 and x.stride(1) == 1 and w.dtype == x.dtype, "bad rmsnorm args")
+    out = torch.empty_like(x)
+    check(lib().pe_rmsnorm(ptr(x), x.stride(0), x.shape[0], x.shape[1], ptr(w), eps, dcode(x.dtype), ptr(out),
+                           out.stride(0), stream_ptr()), "pe_rmsnorm")
+    return out
+
+
+def embed(ids: torch.Tensor, table: torch.Tensor, status: torch.Tensor) -> torch.Tensor:
+    m = ids.numel()
+    v, h = table.shape
+    out = torch.empty((m, h), dtype=table.dtype, device=table.device)
+    check(lib().pe_embed(ptr(ids), m, ptr(table), v, h, dcode(table.dtype), ptr(out), h, ptr(status),
+                         stream_ptr()), "pe_embed")
+    return out
+
+
+def rope_qkv(qkv, nh, nkv, hd, positions, cos_sin, k_cache, v_cache, row0, status):
+    m = qkv.shape[0]
+    q = torch.empty((m, nh, hd), dtype=qkv.dtype, device=qkv.device)
+    check(lib().pe_rope_qkv(ptr(qkv), qkv.stride(0), m, nh, nkv, hd, ptr(positions), ptr(cos_sin),
+                            cos_sin.shape[1], dcode(qkv.dtype), ptr(q), ptr(k_cache), ptr(v_cache), k_cache.shape[1],
+                            row0, ptr(status), stream_ptr()), "pe_rope_qkv")
+    return q
+
+
+# ------------------------------------------------------------------ masks
+def tree_masks(parents: torch.Tensor, prefix_len: int, words: int, status: torch.Tensor):
+    """parents int32 device [T] -> (bits u64 [T][words] as int64, positions int64 [T], depths int32 [T])."""
+    t = parents.numel()
+    bits = torch.empty((t, words), dtype=torch.int64, device=parents.device)
+    pos = torch.empty(t, dtype=torch.int64, device=parents.device)
+    dep = torch.empty(t, dtype=torch.int32, device=parents.device)
+    check(lib().pe_tree_masks(ptr(parents), t, prefix_len, ptr(bits), words, ptr(pos), ptr(dep), ptr(status),
+                              stream_ptr()), "pe_tree_masks")
+    return bits, pos, dep
+
+
+def tree_allow_dense(bits: torch.Tensor, prefix_len: int) -> torch.Tensor:
+    t, words = bits.shape
+    n = prefix_len + t
+    allow = torch.empty((n, n), dtype=torch.bool, device=bits.device)
+    check(lib().pe_tree_allow_dense(ptr(bits), t, words, prefix_len, ptr(allow), stream_ptr()), "pe_tree_allow_dense")
+    return allow
+
+
+def bias_to_bits(bias: torch.Tensor, prefix_len: int, words: int, status: torch.Tensor) -> torch.Tensor:
+    _req(bias.dim() == 2 and bias.stride(1) == 1, "bias must be [T][P+T] with unit column stride")
+    t = bias.shape[0]
+    bits = torch.empty((t, words), dtype=torch.int64, device=bias.device)
+    check(lib().pe_bias_to_bits(ptr(bias), bias.stride(0), dcode(bias.dtype), t, prefix_len, ptr(bits), words,
+                                ptr(status), stream_ptr()), "pe_bias_to_bits")
+    return bits
+
+
+# ------------------------------------------------------------------ attention
+def tree_attention(q, k_cache, v_cache, prefix_len, mask_mode, bits, scale, workspace=None):
+    """q [T][nh][hd]; caches [nkv][cap][hd] (one layer)."""
+    t, nh, hd = q.shape
+    nkv, cap, _ = k_cache.shape
+    words = bits.shape[1] if bits is not None else 0
+    need = int(lib().pe_attention_workspace_bytes(t, nh, nkv, hd, prefix_len + t, dcode(q.dtype)))
+    if workspace is None:
+        workspace = _workspace(need, q.device)
+    out = torch.empty((t, nh * hd), dtype=q.dtype, device=q.device)
+    check(lib().pe_tree_attention(ptr(q), ptr(k_cache), ptr(v_cache), cap, nh, nkv, hd, t, prefix_len, mask_mode,
+                                  ptr(bits), words, scale, dcode(q.dtype), ptr(out), out.stride(0), ptr(workspace),
+                                  workspace.numel(), stream_ptr()), "pe_tree_attention")
+    return out
+
+
+# ------------------------------------------------------------------ acceptance / cache
+def argmax_rows(x: torch.Tensor) -> torch.Tensor:
+    _req(x.dim() == 2 and x.stride(1) == 1, "x must be [rows][V]")
+    out = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)
+    check(lib().pe_argmax_rows(ptr(x), x.stride(0), x.shape[0], x.shape[1], dcode(x.dtype), ptr(out), stream_ptr()),
+          "pe_argmax_rows")
+    return out
+
+
+def accept_tree(root_logit: torch.Tensor, node_logits: torch.Tensor, node_tokens: torch.Tensor,
+                parents: torch.Tensor, out: torch.Tensor | None = None, scratch: torch.Tensor | None = None):
+    """Device result int32 [2 + T]: (|path|, bonus, path...)."""
+    t = node_tokens.numel()
+    v = root_logit.shape[-1]
+    _req(root_logit.stride(-1) == 1 and (t == 0 or node_logits.stride(1) == 1), "logit rows must be contiguous")
+    if out is None:
+        out = torch.empty(2 + max(t, 1), dtype=torch.int32, device=root_logit.device)
+    if scratch is None:
+        scratch = torch.empty(t + 1, dtype=torch.int32, device=root_logit.device)
+    ld = node_logits.stride(0) if t > 0 else v
+    check(lib().pe_accept_tree(ptr(root_logit), ptr(node_logits) if t > 0 else None, ld, t, v,
+                               dcode(root_logit.dtype), ptr(node_tokens) if t > 0 else None,
+                               ptr(parents) if t > 0 else None, ptr(out), ptr(scratch), stream_ptr()), "pe_accept_tree")
+    return out
+
+
+def kv_compact(k_cache, v_cache, prefix_len: int, accept_out: torch.Tensor) -> None:
+    """Caches [L][nkv][cap][hd]."""
+    L, nkv, cap, hd = k_cache.shape
+    check(lib().pe_kv_compact(ptr(k_cache), ptr(v_cache), L, nkv, cap, hd, dcode(k_cache.dtype), prefix_len,
+                              ptr(accept_out), stream_ptr()), "pe_kv_compact")
+
+
+def kv_gather(k_cache, v_cache, keep: torch.Tensor, status4: torch.Tensor) -> None:
+    L, nkv, cap, hd = k_cache.shape
+    _req(keep.dtype == torch.int64 and keep.is_contiguous(), "keep must be contiguous int64")
+    _req(status4.dtype == torch.int32 and status4.numel() >= 4, "status must be int32[4]")
+    check(lib().pe_kv_gather(ptr(k_cache), ptr(v_cache), L, nkv, cap, hd, dcode(k_cache.dtype), ptr(keep),
+                             keep.numel(), ptr(status4), stream_ptr()), "pe_kv_gather")
+
+
+def read_status(status: torch.Tensor, where: str) -> None:
+    s = int(status[0].item())
+    if s:
+        status.zero_()
+        raise _lib.PEError(s, where)
+
+
+# ------------------------------------------------------------------ torch custom ops
+_REGISTERED = False
+
+
+def register_torch_ops() -> None:
+    """Expose the functional kernels as torch.ops.pe.* custom ops."""
+    global _REGISTERED
+    if _REGISTERED:
+        return
+
+    @torch.library.custom_op("pe::rmsnorm", mutates_args=())
+    def _rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+        return rmsnorm(x, w, eps)
+
+    @torch.library.custom_op("pe::argmax_rows", mutates_args=())
+    def _argmax(x: torch.Tensor) -> torch.Tensor:
+        return argmax_rows(x)
+
+    @torch.library.custom_op("pe::nf4_linear", mutates_args=())
+    def _nf4_linear(x: torch.Tensor, tiled: torch.Tensor, tabs: torch.Tensor, n: int) -> torch.Tensor:
+        return linear(x, n, nf4=(tiled, tabs))
+
+    @torch.library.custom_op("pe::dense_linear", mutates_args=())
+    def _dense_linear(x: torch.Tensor, w: torch.Tensor, n: int) -> torch.Tensor:
+        return linear(x, n, dense=w)
+
+    @torch.library.custom_op("pe::accept_tree", mutates_args=())
+    def _accept(root: torch.Tensor, nodes: torch.Tensor, tokens: torch.Tensor, parents: torch.Tensor) -> torch.Tensor:
+        return accept_tree(root, nodes, tokens, parents)
+
+    _REGISTERED = True
+
+
+_ = C  # ctypes kept importable for callers building descriptors

@@ -1,0 +1,65 @@
+"""The C ABI library (CPU checks, no kernel launches): it loads, exports every
+function include/pe_hip.h declares, binds to a single HIP runtime, and its host-
+side argument validation rejects bad calls before launching anything."""
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from parallel_eagle_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "pe_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pe_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libpe_hip.so not built")
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = declared_functions()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(lib, n), f"{n} missing from libpe_hip.so"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_single_hip_runtime(lib):
+    maps = _lib.hip_runtime_mappings()
+    assert len(maps) == 1, maps
+
+
+def test_version_and_status_strings(lib):
+    assert lib.pe_version() == 1
+    assert lib.pe_status_string(0) == b"ok"
+    assert b"topolog" in lib.pe_status_string(_lib.PE_ERR_TREE)
+
+
+def test_host_validation_rejects_bad_arguments(lib):
+    # null pointers and impossible shapes are refused before any launch
+    assert lib.pe_nf4_gemm(None, 0, 26, 4096, None, None, 4096, 0, None, None, 0, None, 0, None, 0, None) \
+        == _lib.PE_ERR_ARG
+    assert lib.pe_nf4_repack(C.c_void_p(8), C.c_void_p(8), 32, 100, C.c_void_p(8), C.c_void_p(8), None) \
+        == _lib.PE_ERR_ARG  # K not a multiple of 128
+    assert lib.pe_tree_masks(C.c_void_p(8), 300, 0, C.c_void_p(8), 4, None, None, None, None) == _lib.PE_ERR_TREE
+    assert lib.pe_tree_attention(C.c_void_p(8), C.c_void_p(8), C.c_void_p(8), 10, 4, 4, 128, 8, 5, 0,
+                                 C.c_void_p(8), 1, 0.1, 1, C.c_void_p(8), 512, C.c_void_p(8), 1 << 20, None) \
+        == _lib.PE_ERR_CAPACITY  # P + T > capacity
+    assert lib.pe_rope_qkv(C.c_void_p(8), 0, 4, 6, 4, 128, C.c_void_p(8), C.c_void_p(8), 100, 1, C.c_void_p(8),
+                           C.c_void_p(8), C.c_void_p(8), 10, 8, None, None) == _lib.PE_ERR_ARG  # nh % nkv
+    assert lib.pe_dense_gemm(C.c_void_p(8), 0, 26, 4096, C.c_void_p(8), 1, 96, 2, None, None, 0,
+                             C.c_void_p(8), 0, None, 0, None) == _lib.PE_ERR_ARG  # SwiGLU needs N % 64
+    # a split-K shape without workspace is refused, not launched
+    assert lib.pe_dense_gemm(C.c_void_p(8), 0, 26, 4096, C.c_void_p(8), 1, 4096, 2, None, None, 0,
+                             C.c_void_p(8), 0, None, 0, None) == _lib.PE_ERR_WORKSPACE

@@ -1,0 +1,283 @@
+"""Kernel-level parity on the GPU: every HIP kernel against the CPU oracle.
+
+Integer / byte / index work is compared bit for bit; floating-point kernels
+within the stated tolerance (fp32 1e-4, bf16/fp16 2e-2 on values of O(1)).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import masks as om
+from oracle import nf4 as onf4
+from oracle import verify as ov
+from parallel_eagle_amd import _lib, ops, synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _status():
+    return torch.zeros(4, dtype=torch.int32, device=DEV)
+
+
+# ------------------------------------------------------------------ RNG
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_fill_normal_bit_exact_with_host_generator(dtype):
+    n = 100_003
+    out = ops.fill_normal(torch.empty(n, dtype=dtype, device=DEV), seed=11, stream_id=77, std=0.02)
+    ref = torch.from_numpy(synth.normal(11, 77, n, 0.02)).to(dtype)
+    assert torch.equal(out.cpu().view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       ref.view(torch.int16 if dtype != torch.float32 else torch.int32))
+
+
+def test_fill_uniform_int_bit_exact():
+    out = ops.fill_uniform_int(torch.empty(5000, dtype=torch.int64, device=DEV), 32000, 3, 9)
+    assert np.array_equal(out.cpu().numpy(), synth.uniform_int(3, 9, 5000, 32000))
+
+
+# ------------------------------------------------------------------ NF4
+def test_nf4_quantize_bit_exact():
+    w = torch.from_numpy(synth.normal(5, 123, 96 * 256, 0.02).reshape(96, 256))
+    p, a = ops.nf4_quantize(w.to(DEV))
+    rp, ra = onf4.quantize(w.numpy())
+    assert np.array_equal(p.cpu().numpy(), rp)
+    assert np.array_equal(a.cpu().numpy().view(np.uint16), ra.view(np.uint16))
+
+
+@pytest.mark.parametrize("n,k", [(32, 128), (96, 384), (4096 // 8, 1024)])
+def test_nf4_repack_dequant_bit_exact(n, k):
+    w = synth.normal(8, 5, n * k, 0.02).reshape(n, k)
+    rp, ra = onf4.quantize(w)
+    tiled, tabs = ops.nf4_repack(torch.from_numpy(rp).to(DEV), torch.from_numpy(ra).to(DEV))
+    deq = ops.nf4_dequant(tiled, tabs, n, k)
+    ref = onf4.dequantize(rp, ra)
+    assert np.array_equal(deq.cpu().view(torch.int16).numpy().view(np.uint16), ref)
+
+
+# ------------------------------------------------------------------ GEMMs
+def _nf4_weight(n, k, seed):
+    w = synth.normal(seed, 31, n * k, 0.02).reshape(n, k)
+    p, a = onf4.quantize(w)
+    tiled, tabs = ops.nf4_repack(torch.from_numpy(p).to(DEV), torch.from_numpy(a).to(DEV))
+    wdq = onf4.dequantize_torch(p, a)  # bf16 [N][K]
+    return (tiled, tabs), wdq
+
+
+@pytest.mark.parametrize("m", [1, 26, 33, 64, 130])
+@pytest.mark.parametrize("n,k", [(256, 1024), (4096, 512), (96, 4096)])
+def test_nf4_linear_matches_dequant_then_linear(m, n, k):
+    (tiled, tabs), wdq = _nf4_weight(n, k, seed=m + n)
+    x = torch.from_numpy(synth.normal(m, 32, m * k, 1.0).reshape(m, k)).to(torch.bfloat16)
+    y = ops.linear(x.to(DEV), n, nf4=(tiled, tabs)).cpu()
+    ref32 = x.float() @ wdq.float().t()  # fp32 product of the exact dequantised operands
+    ref = torch.nn.functional.linear(x, wdq)  # the reference's bf16 path on CPU
+    assert torch.allclose(y.float(), ref32, rtol=1e-2, atol=1e-2), (y.float() - ref32).abs().max()
+    assert torch.allclose(y.float(), ref.float(), rtol=2e-2, atol=2e-2)
+
+
+def test_nf4_linear_deterministic_and_batch_invariant():
+    n, k = 4096, 4096
+    (tiled, tabs), _ = _nf4_weight(n, k, seed=3)
+    x = torch.from_numpy(synth.normal(4, 33, 26 * k, 1.0).reshape(26, k)).to(torch.bfloat16).to(DEV)
+    y1 = ops.linear(x, n, nf4=(tiled, tabs))
+    y2 = ops.linear(x, n, nf4=(tiled, tabs))
+    y_row = ops.linear(x[5:6].contiguous(), n, nf4=(tiled, tabs))
+    assert torch.equal(y1, y2)
+    assert torch.equal(y1[5:6], y_row)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("epi", ["store", "bias", "residual", "swiglu"])
+def test_dense_linear_epilogues(dtype, epi):
+    m, n, k = 26, 512, 1024
+    w = torch.from_numpy(synth.normal(1, 40, n * k, 0.02).reshape(n, k)).to(dtype)
+    x = torch.from_numpy(synth.normal(2, 41, m * k, 1.0).reshape(m, k)).to(dtype)
+    wt = ops.dense_repack(w.to(DEV))
+    bias = torch.from_numpy(synth.normal(3, 42, n, 0.1)).to(dtype)
+    resid = torch.from_numpy(synth.normal(4, 43, m * n, 1.0).reshape(m, n)).to(dtype)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    lin = torch.nn.functional.linear
+    if epi == "store":
+        y = ops.linear(x.to(DEV), n, dense=wt).cpu()
+        ref = lin(x, w)
+    elif epi == "bias":
+        y = ops.linear(x.to(DEV), n, dense=wt, bias=bias.to(DEV)).cpu()
+        ref = lin(x, w, bias)
+    elif epi == "residual":
+        y = ops.linear(x.to(DEV), n, dense=wt, epilogue=_lib.PE_EPI_RESIDUAL, resid=resid.to(DEV)).cpu()
+        ref = resid + lin(x, w)
+    else:
+        # gate/up interleaved by 32 rows
+        g, u = w[: n // 2], w[n // 2:]
+        inter = torch.stack([g.view(-1, 32, k), u.view(-1, 32, k)], 1).reshape(n, k).contiguous()
+        y = ops.linear(x.to(DEV), n, dense=ops.dense_repack(inter.to(DEV)), epilogue=_lib.PE_EPI_SWIGLU).cpu()
+        ref = torch.nn.functional.silu(lin(x, g)) * lin(x, u)
+    assert torch.allclose(y.float(), ref.float(), rtol=tol, atol=tol), (y.float() - ref.float()).abs().max()
+
+
+# ------------------------------------------------------------------ masks
+TREES = [
+    [-1, 0, -1],
+    [-1, -1, 0, 0, 1, 2, 2, 5],
+    [-1] + list(range(0, 63)),  # chain of 64
+    [-1, -1, -1, -1] + [i % 4 for i in range(22)],
+]
+
+
+@pytest.mark.parametrize("parents", TREES)
+@pytest.mark.parametrize("P", [0, 2, 37])
+def test_tree_masks_match_oracle(parents, P):
+    t = len(parents)
+    words = (t + 63) // 64
+    st = _status()
+    bits, pos, dep = ops.tree_masks(torch.tensor(parents, dtype=torch.int32, device=DEV), P, words, st)
+    assert int(st[0]) == 0
+    ref_bits = om.ancestor_bits(parents)
+    got = bits.cpu().numpy().view(np.uint64)
+    for i in range(t):
+        val = sum(int(got[i, w]) << (64 * w) for w in range(words))
+        assert val == ref_bits[i]
+    assert pos.cpu().tolist() == om.tree_position_ids(parents, P)[P:]
+    assert dep.cpu().tolist() == om.tree_depths(parents)
+    allow = ops.tree_allow_dense(bits, P).cpu().numpy()
+    assert np.array_equal(allow, om.tree_allow_mask(parents, P))
+
+
+def test_tree_masks_reject_non_topological():
+    st = _status()
+    ops.tree_masks(torch.tensor([-1, 2, 0], dtype=torch.int32, device=DEV), 4, 1, st)
+    assert int(st[0]) & _lib.PE_ERR_TREE
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_bias_to_bits_round_trip(dtype):
+    parents, P = TREES[1], 5
+    allow = om.tree_allow_mask(parents, P)[P:, :]
+    bias = om.to_additive_bias(allow, dtype)[0, 0].to(DEV).contiguous()
+    st = _status()
+    bits = ops.bias_to_bits(bias, P, 1, st)
+    assert int(st[0]) == 0
+    assert bits.cpu().numpy().view(np.uint64)[:, 0].tolist() == om.ancestor_bits(parents)
+    bad = bias.clone()
+    bad[2, 1] = torch.finfo(dtype).min  # masks a prefix column: not a tree mask
+    ops.bias_to_bits(bad, P, 1, st)
+    assert int(st[0]) & _lib.PE_ERR_MASK
+
+
+# ------------------------------------------------------------------ attention
+def _attn_ref(q, k, v, P, parents, causal, scale, dtype):
+    """q [T][nh][hd], k/v [nkv][S][hd] -> [T][nh*hd] via the oracle's SDPA path."""
+    T, nh, hd = q.shape
+    nkv, S, _ = k.shape
+    if causal:
+        allow = torch.arange(T)[:, None] + P >= torch.arange(S)[None, :]
+    else:
+        allow = torch.from_numpy(om.tree_allow_mask(parents, P)[P:, :])
+    bias = om.to_additive_bias(allow.numpy(), dtype)
+    from oracle.model import repeat_kv
+
+    qq = q.permute(1, 0, 2).unsqueeze(0)
+    kk = repeat_kv(k.unsqueeze(0), nh // nkv)
+    vv = repeat_kv(v.unsqueeze(0), nh // nkv)
+    o = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, attn_mask=bias, scale=scale)
+    return o[0].permute(1, 0, 2).reshape(T, nh * hd)
+
+
+@pytest.mark.parametrize("dtype,hd", [(torch.bfloat16, 128), (torch.float16, 128), (torch.float32, 64)])
+@pytest.mark.parametrize("nh,nkv", [(4, 4), (10, 2)])
+@pytest.mark.parametrize("P,parents,causal", [
+    (0, [-1, -1, 0, 0, 1, 2, 2, 5], False),
+    (77, TREES[3], False),
+    (300, [-1, 0, 1, 2, 3], False),
+    (50, None, True),
+])
+def test_tree_attention_matches_sdpa(dtype, hd, nh, nkv, P, parents, causal):
+    T = 6 if causal else len(parents)
+    S = P + T
+    cap = S + 3
+    q = torch.from_numpy(synth.normal(1, 50, T * nh * hd).reshape(T, nh, hd)).to(dtype)
+    k = torch.from_numpy(synth.normal(2, 51, nkv * S * hd).reshape(nkv, S, hd)).to(dtype)
+    v = torch.from_numpy(synth.normal(3, 52, nkv * S * hd).reshape(nkv, S, hd)).to(dtype)
+    kc = torch.zeros((nkv, cap, hd), dtype=dtype)
+    vc = torch.zeros((nkv, cap, hd), dtype=dtype)
+    kc[:, :S], vc[:, :S] = k, v
+    scale = hd ** -0.5
+    if causal:
+        bits, mode = None, _lib.PE_MASK_CAUSAL
+    else:
+        st = _status()
+        bits, _, _ = ops.tree_masks(torch.tensor(parents, dtype=torch.int32, device=DEV), P, (T + 63) // 64, st)
+        mode = _lib.PE_MASK_TREE
+    out = ops.tree_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), P, mode, bits, scale).cpu()
+    ref = _attn_ref(q, k, v, P, parents, causal, scale, dtype)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert torch.allclose(out.float(), ref.float(), rtol=tol, atol=tol), (out.float() - ref.float()).abs().max()
+
+
+# ------------------------------------------------------------------ acceptance and compaction
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("seed", range(6))
+def test_accept_tree_matches_oracle(dtype, seed):
+    rng = np.random.default_rng(seed)
+    V, T = 50, 12
+    parents = [-1]
+    for t in range(1, T):
+        parents.append(int(rng.integers(-1, t)))
+    # coarse values so ties are common; plant matches along a random chain
+    logits = torch.from_numpy(rng.integers(0, 4, size=(T + 1, V)).astype(np.float32)).to(dtype)
+    tokens = [int(x) for x in rng.integers(0, V, size=T)]
+    amax = [ov.first_argmax(logits[r]) for r in range(T + 1)]
+    cur, row = -1, 0
+    for _ in range(3):
+        kids = [t for t in range(T) if parents[t] == cur]
+        if not kids:
+            break
+        c = kids[int(rng.integers(0, len(kids)))]
+        tokens[c] = amax[row]
+        cur, row = c, 1 + c
+    ref = ov.accept_tree_cached(logits[0], logits[1:], tokens, parents)
+    out = ops.accept_tree(logits[0].to(DEV), logits[1:].to(DEV), torch.tensor(tokens, device=DEV),
+                          torch.tensor(parents, dtype=torch.int32, device=DEV)).cpu().tolist()
+    assert (out[2: 2 + out[0]], out[1]) == ref
+
+
+def test_argmax_rows_first_index_and_nan():
+    x = torch.zeros((3, 1000), dtype=torch.float32)
+    x[0, 7] = 5.0
+    x[0, 900] = 5.0
+    x[1, 300] = float("nan")
+    x[1, 10] = float("nan")
+    x[2, :] = -1.0
+    got = ops.argmax_rows(x.to(DEV)).cpu().tolist()
+    assert got == [7, 10, 0]
+
+
+@pytest.mark.parametrize("path", [[], [0], [1, 3, 7], [0, 1, 2, 3, 4]])
+def test_kv_compact_matches_gather_semantics(path):
+    L, nkv, cap, hd, P, T = 3, 2, 64, 128, 20, 9
+    k = torch.from_numpy(synth.normal(1, 60, L * nkv * cap * hd).reshape(L, nkv, cap, hd)).to(torch.bfloat16)
+    v = torch.from_numpy(synth.normal(2, 61, L * nkv * cap * hd).reshape(L, nkv, cap, hd)).to(torch.bfloat16)
+    res = torch.tensor([len(path), 0] + path + [0] * (T - len(path)), dtype=torch.int32)
+    kd, vd = k.to(DEV), v.to(DEV)
+    ops.kv_compact(kd, vd, P, res.to(DEV))
+    n = P + len(path)
+    ref_k = ov.compact_rows(k[:, :, : P + T].float().numpy(), P, path)
+    ref_v = ov.compact_rows(v[:, :, : P + T].float().numpy(), P, path)
+    assert np.array_equal(kd[:, :, :n].cpu().float().numpy(), ref_k)
+    assert np.array_equal(vd[:, :, :n].cpu().float().numpy(), ref_v)
+
+
+def test_kv_gather_general_keep_and_rejects_unsorted():
+    L, nkv, cap, hd = 2, 2, 40, 64
+    k = torch.from_numpy(synth.normal(3, 62, L * nkv * cap * hd).reshape(L, nkv, cap, hd))
+    v = torch.from_numpy(synth.normal(4, 63, L * nkv * cap * hd).reshape(L, nkv, cap, hd))
+    keep = [0, 1, 2, 5, 6, 9, 20, 21, 33]
+    kd, vd = k.to(DEV), v.to(DEV)
+    st = _status()
+    ops.kv_gather(kd, vd, torch.tensor(keep, device=DEV), st)
+    assert int(st[0]) == 0
+    assert torch.equal(kd[:, :, : len(keep)].cpu(), k[:, :, keep])
+    assert torch.equal(vd[:, :, : len(keep)].cpu(), v[:, :, keep])
+    ops.kv_gather(kd, vd, torch.tensor([0, 3, 2], device=DEV), st)
+    assert int(st[0]) & _lib.PE_ERR_INDEX
