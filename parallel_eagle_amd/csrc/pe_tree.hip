@@ -180,7 +180,7 @@ __global__ void kv_compact_kernel(uint8_t* __restrict__ kc, uint8_t* __restrict_
   const int64_t nchunk = row_bytes / 16;
   for (int i = 0; i < len; ++i) {
     const int src = res[2 + i];
-    if (src == i) continue;
+    if (src == i || src < 0 || P + src >= cap || P + i >= cap) continue;
     const uint4* s = (const uint4*)(base + (P + src) * row_bytes);
     uint4* d = (uint4*)(base + (P + i) * row_bytes);
     for (int64_t c = threadIdx.x; c < nchunk; c += blockDim.x) d[c] = s[c];

@@ -15,11 +15,14 @@ row is below the measured logit error, and is reported), and the compacted
 cache equal to the oracle's gather of the GPU's own K/V rows.
 """
 
+from dataclasses import replace
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import masks as om
+from oracle import nf4 as onf4
 from oracle import verify as ov
 from oracle.model import OracleTarget
 from parallel_eagle_amd import synth
@@ -45,6 +48,32 @@ def _plant(orc, cache, prompt_logit, tokens, parents, a, vocab, P):
     return tokens
 
 
+def _close(a: torch.Tensor, b: torch.Tensor, tol: float, ref32: torch.Tensor | None = None,
+           min_frac: float = 0.95) -> tuple[bool, float]:
+    """Parity of a GPU tensor ``a`` with the oracle's ``b``; returns (ok, max |a - b|).
+
+    fp32 (``ref32`` None): every element within rtol = atol = tol.
+    bf16/fp16: the oracle itself deviates from an fp32 evaluation of the same
+    weights by more than 2e-2 on some logits (its own rounding: torch's CPU
+    flash attention uses its own approximate exp, so no other implementation
+    reproduces its bf16 roundings), so the check is (i) at least ``min_frac`` of
+    the elements within rtol = atol = tol and (ii) the GPU no farther from the
+    fp32 evaluation than the oracle is (relative L2, 10% slack)."""
+    a, b = a.float().cpu(), b.float().cpu()
+    d = (a - b).abs()
+    inside = (d <= tol + tol * b.abs()).float().mean().item()
+    if ref32 is None:
+        return inside == 1.0, float(d.max())
+    r = ref32.float().cpu()
+    e_gpu = ((a - r).norm() / r.norm()).item()
+    e_orc = ((b - r).norm() / r.norm()).item()
+    ok = inside >= min_frac and e_gpu <= 1.1 * e_orc + 1e-6
+    if not ok:
+        print(f"parity: inside {inside:.5f} (need {min_frac}), relL2 gpu-vs-fp32 {e_gpu:.4g}, "
+              f"oracle-vs-fp32 {e_orc:.4g}, max|gpu-oracle| {float(d.max()):.4g}")
+    return ok, float(d.max())
+
+
 def _margin(row: torch.Tensor) -> float:
     v = row.float().topk(2).values
     return float(v[0] - v[1])
@@ -65,14 +94,31 @@ def _check_acceptance(gpu, ref, o_root, o_nodes, tokens, parents, tol):
     return f"near-tie at depth {i} (margin {m:.3g})"
 
 
+def _fp32_oracle(shape, host_weights):
+    """The same model evaluated in fp32 (NF4 weights dequantised to the bf16 operands
+    the reference multiplies, then upcast): the yardstick for bf16/fp16 rounding."""
+    def up(x):
+        if isinstance(x, tuple):
+            return onf4.dequantize_torch(x[1], x[2]).float()
+        return x.float()
+
+    hw32 = {"embed": up(host_weights["embed"]), "final_norm": up(host_weights["final_norm"]),
+            "lm_head": up(host_weights["lm_head"]),
+            "layers": [{k: up(v) for k, v in lw.items()} for lw in host_weights["layers"]]}
+    return OracleTarget(replace(shape, dtype="float32", weight_format="dense"), hw32)
+
+
 def _run_case(shape, seed, P, depth, widths, top_k, plant, tol, random_kv=False):
     torch.manual_seed(0)
     tm = TargetModel.synthetic(shape, seed=seed, device=DEV, keep_logical=True, norm_noise=0.1,
                                cache_capacity=P + 128)
-    orc = OracleTarget(shape, tm.model.host_weights())
+    hw = tm.model.host_weights()
+    orc = OracleTarget(shape, hw)
     orc.cache_dequant = True  # dequantise each NF4 matrix once; values are the same every call
+    o32 = _fp32_oracle(shape, hw) if shape.dtype != "float32" else None
     V = shape.vocab
     cache = tm.make_cache()
+    c32 = None
     if random_kv:
         # identical random prefix K/V for both paths
         g = torch.Generator().manual_seed(seed)
@@ -82,18 +128,25 @@ def _run_case(shape, seed, P, depth, widths, top_k, plant, tol, random_kv=False)
         cache.v[:, :, :P] = vv.to(DEV)
         cache.seq_len = P
         o_cache = [(kk[li].unsqueeze(0), vv[li].unsqueeze(0)) for li in range(shape.num_layers)]
+        if o32 is not None:
+            c32 = [(a.float(), b.float()) for a, b in o_cache]
         last = int(synth.uniform_int(seed, synth.STREAM_PROMPT, 1, V)[0])
-        # root logit: one causal token on both sides at position P - 1 is not defined here;
-        # use a 1-token continuation from the random prefix instead
+        # the root logit comes from a 1-token continuation of the random prefix
         root_g, _, cache = tm.forward_cached(torch.tensor([[last]]), cache, torch.tensor([[P]]))
         root_o, _, o_cache = orc.forward([last], [P], o_cache, None)
+        root32 = None
+        if o32 is not None:
+            root32, _, c32 = o32.forward([last], [P], c32, None)
         P = P + 1
     else:
         prompt = synth.uniform_int(seed, synth.STREAM_PROMPT, P, V).tolist()
         root_g, _, cache = tm.forward_cached(torch.tensor([prompt]), cache, torch.arange(P).unsqueeze(0))
         root_o, _, o_cache = orc.forward(prompt, list(range(P)), None, None)
-    perr = (root_g[0, -1].float().cpu() - root_o[0, -1].float()).abs().max().item()
-    assert perr <= tol, f"prefix logits differ by {perr}"
+        root32 = None
+        if o32 is not None:
+            root32, _, c32 = o32.forward(prompt, list(range(P)), None, None)
+    ok, perr = _close(root_g[0, -1], root_o[0, -1], tol, None if root32 is None else root32[0, -1])
+    assert ok, f"prefix logits differ by {perr}"
     # the oracle continues from its own prefix cache; the GPU from its own
     tokens, parents = synth.tree_for_seed(seed, V, depth, widths, top_k)
     a = plant(seed)
@@ -101,17 +154,24 @@ def _run_case(shape, seed, P, depth, widths, top_k, plant, tol, random_kv=False)
     pos = [P + d for d in om.tree_depths(parents)]
     bias_o = om.to_additive_bias(om.tree_allow_mask(parents, P)[P:, :], orc.dtype)
     o_lg, o_fu, o_cache2 = orc.forward(tokens, pos, o_cache, bias_o)
+    r_lg = r_fu = r_cache = None
+    if o32 is not None:
+        bias32 = om.to_additive_bias(om.tree_allow_mask(parents, P)[P:, :], torch.float32)
+        r_lg, r_fu, r_cache = o32.forward(tokens, pos, c32, bias32)
     lg, fu, cache = tm.forward_cached(torch.tensor([tokens]), cache, torch.tensor([pos]), parents=parents)
-    lerr = (lg.float().cpu() - o_lg.float()).abs().max().item()
-    ferr = (fu.float().cpu() - o_fu.float()).abs().max().item()
-    assert lerr <= tol and ferr <= tol, f"logits {lerr:.3g} / features {ferr:.3g} exceed {tol}"
+    ok_l, lerr = _close(lg, o_lg, tol, r_lg)
+    ok_f, ferr = _close(fu, o_fu, tol, r_fu)
+    assert ok_l and ok_f, f"logits {lerr:.3g} / features {ferr:.3g} outside the parity bound (tol {tol})"
     # node K/V rows written by the pass
     for li in range(shape.num_layers):
-        kerr = (cache.k[li, :, P:P + len(tokens)].float().cpu() - o_cache2[li][0][0, :, P:].float()).abs().max()
-        assert kerr.item() <= tol
+        rk = None if r_cache is None else r_cache[li][0][0, :, P:]
+        rv = None if r_cache is None else r_cache[li][1][0, :, P:]
+        ok_k, kerr = _close(cache.k[li, :, P:P + len(tokens)], o_cache2[li][0][0, :, P:], tol, rk)
+        ok_v, verr = _close(cache.v[li, :, P:P + len(tokens)], o_cache2[li][1][0, :, P:], tol, rv)
+        assert ok_k and ok_v, f"layer {li} K/V rows differ: {kerr:.3g} / {verr:.3g}"
     gpu = accept_tree_cached(root_g[0, -1], lg[0], tokens, parents)
     ref = ov.accept_tree_cached(root_o[0, -1], o_lg[0], tokens, parents)
-    verdict = _check_acceptance(gpu, ref, root_o[0, -1], o_lg[0], tokens, parents, lerr)
+    verdict = _check_acceptance(gpu, ref, root_o[0, -1], o_lg[0], tokens, parents, max(lerr, perr))
     # the acceptance kernel on the oracle's own logits must be bit-exact
     same = accept_tree_cached(root_o[0, -1].to(DEV), o_lg[0].to(DEV), tokens, parents)
     assert same == ref
