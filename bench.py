@@ -1,0 +1,339 @@
+#!/usr/bin/env python3
+"""Tree-verification pass benchmark on one MI355X.
+
+One step is one verification pass of a drafted tree against the KV cache,
+entirely on the device and captured in a HIP graph: ancestor bitmasks and
+positions from the parent list, the masked forward over the cache (embeddings,
+every decoder layer with the in-place K/V append, final norm, lm_head over all
+tree rows, fused features), the greedy acceptance walk and the in-place
+compaction of the accepted rows. The default workload is the Llama-2-7B shape
+with NF4 linears (block 64, fp16 absmax, bf16 compute), a 26-node depth-5 tree
+over a 2048-token bf16 KV prefix, batch 1. Weights and the KV prefix are
+synthetic (counter-based N(0, 0.02) weights, N(0, 1) K/V), resident in HBM
+before timing starts.
+
+Printed (one JSON line): ``value`` = algorithmic HBM bytes of one pass divided
+by the measured pass time (GB/s), ``ms_per_step`` = pass latency, plus
+
+- ``roofline``: the NF4 dequant-GEMM (every q/k/v, o, gate/up and down launch
+  of one pass, in pass order, replayed from a HIP graph with HIP events on its
+  stream), algorithmic bytes per launch over the mean launch time, against the
+  8 TB/s HBM peak;
+- ``cpu_baseline``: the CPU restatement of the reference path (per-call NF4
+  dequantise, bf16 matmuls, masked SDPA, acceptance walk, index_select commit)
+  timed on the host cores on a 2-layer slice of the same shape and scaled to
+  the full layer count.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload NAME] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "tree-verify pass latency + HBM GB/s (% peak), 7B-int4 T=26 KV=2048 bs=1"
+DEFAULT_WORKLOAD = "llama2-7b-nf4-T26-P2048"
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", default=DEFAULT_WORKLOAD)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--gemm-reps", type=int, default=10, help="replays of the per-pass NF4 GEMM sequence")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-layers", type=int, default=2, help="layers of the CPU-path sample")
+    p.add_argument("--cpu-runs", type=int, default=3)
+    return p.parse_args(argv)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- device pass
+def build_step(wl, seed):
+    import torch
+
+    from parallel_eagle_amd import ops, synth
+    from parallel_eagle_amd.target import TargetModel
+
+    shape, P, T = wl.model, wl.prefix_len, wl.tree_nodes
+    t0 = time.perf_counter()
+    tm = TargetModel.synthetic(shape, seed=seed, device="cuda:0", cache_capacity=P + T)
+    torch.cuda.synchronize()
+    log(f"model {shape.name}: {tm.model.weight_bytes() / 1e9:.2f} GB of repacked layer weights "
+        f"in {time.perf_counter() - t0:.1f} s")
+    cache = tm.make_cache(P + T)
+    ops.fill_normal(cache.k, seed, synth.STREAM_KV, 1.0)
+    ops.fill_normal(cache.v, seed, synth.STREAM_KV_V, 1.0)
+    # the root logit: a 1-token continuation that writes prefix row P - 1
+    cache.seq_len = P - 1
+    last = int(synth.uniform_int(seed, synth.STREAM_PROMPT, 1, shape.vocab)[0])
+    root, _, cache = tm.forward_cached(torch.tensor([[last]]), cache, torch.tensor([[P - 1]]))
+    root = root[0, -1].clone()
+    tokens, parents = synth.tree_for_seed(seed, shape.vocab, wl.depth, wl.widths, wl.top_k)
+    step = tm.verify_step(cache, T)
+    # plant the device's own greedy chain along the deepest first branch, so the
+    # timed pass accepts a full-depth path and compacts it
+    chain = synth.chain_nodes(parents, synth.deepest_first_leaf(parents))
+    row = root
+    for node in chain:
+        synth.set_token(tokens, parents, node, int(row.float().argmax()), shape.vocab)
+        step.load_tree(tokens, parents, root)
+        step.run()
+        row = step.logits[node].clone()
+    step.load_tree(tokens, parents, root)
+    step.run()
+    path, bonus = step.result()
+    log(f"tree T={T} depth={wl.depth} widths={list(wl.widths)}: accepted {len(path)} nodes {path}, bonus {bonus}")
+    return tm, cache, step, (tokens, parents, path, bonus)
+
+
+def time_pass(step, steps: int, warmup: int):
+    import torch
+
+    step.capture()
+    for _ in range(warmup):
+        step.run()
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    evs[0].record()
+    for i in range(steps):
+        step.run()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
+    total_ms = evs[0].elapsed_time(evs[-1])
+    return total_ms / steps, statistics.median(per), wall
+
+
+def nf4_gemm_roofline(tm, wl, reps: int):
+    """Mean duration and algorithmic bytes per launch of the NF4 dequant-GEMM
+    over one pass's 4 * L launches (same shapes, weights and epilogues as
+    pe_forward issues), replayed from a HIP graph."""
+    import ctypes as C
+
+    import torch
+
+    from parallel_eagle_amd import _lib, ops
+
+    L = _lib.load()
+    m, s = tm.model, tm.shape
+    M, H, ip = wl.tree_nodes * wl.batch, s.hidden, m.ipad
+    qd, kvd = s.q_dim, s.kv_dim
+    nqkv = qd + 2 * kvd
+    dev = tm.device
+    bf = torch.bfloat16
+    xn = torch.randn((M, H), device=dev).to(bf)
+    attn = torch.randn((M, qd), device=dev).to(bf)
+    act = (0.1 * torch.randn((M, ip), device=dev)).to(bf)
+    qkv = torch.empty((M, nqkv), dtype=bf, device=dev)
+    h = torch.randn((M, H), device=dev).to(bf)
+    gu_out = torch.empty((M, ip), dtype=bf, device=dev)
+    ws_bytes = max(ops.gemm_workspace_bytes(M, n, k, True, bf, e) for n, k, e in
+                   [(nqkv, H, 0), (H, qd, 1), (2 * ip, H, 2), (H, ip, 1)])
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    st = ops.stream_ptr
+
+    def seq():
+        for ly in m.layers:
+            for (x, K, w, a, N, epi, res, out, ldo) in (
+                    (xn, H, ly["w_qkv"], ly["a_qkv"], nqkv, _lib.PE_EPI_STORE, None, qkv, nqkv),
+                    (attn, qd, ly["w_o"], ly["a_o"], H, _lib.PE_EPI_RESIDUAL, h, h, H),
+                    (xn, H, ly["w_gu"], ly["a_gu"], 2 * ip, _lib.PE_EPI_SWIGLU, None, gu_out, ip),
+                    (act, ip, ly["w_down"], ly["a_down"], H, _lib.PE_EPI_RESIDUAL, h, h, H)):
+                _lib.check(L.pe_nf4_gemm(x.data_ptr(), K, M, K, w.data_ptr(), a.data_ptr(), N, epi, None,
+                                         res.data_ptr() if res is not None else None, H, out.data_ptr(), ldo,
+                                         ws.data_ptr(), ws.numel(), st()), "pe_nf4_gemm")
+
+    seq()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        seq()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    launches = 4 * s.num_layers
+    mean_us = e0.elapsed_time(e1) * 1e3 / (reps * launches)
+    # algorithmic bytes: NF4 codes (0.5 B) + fp16 absmax (2 B / 64) + X once + output once
+    # (+ the residual read of the residual epilogues)
+    def nf4_bytes(n, k):
+        return n * k // 2 + (n * k // 64) * 2
+
+    per_layer = (nf4_bytes(nqkv, H) + 2 * M * H + 2 * M * nqkv
+                 + nf4_bytes(H, qd) + 2 * M * qd + 2 * 2 * M * H
+                 + nf4_bytes(2 * s.intermediate, H) + 2 * M * H + 2 * M * s.intermediate
+                 + nf4_bytes(H, s.intermediate) + 2 * M * s.intermediate + 2 * 2 * M * H)
+    bytes_per_launch = per_layer * s.num_layers / launches
+    gbs = bytes_per_launch / (mean_us * 1e-6) / 1e9
+    _ = C
+    return {"kernel": "mfma_gemm_kernel<NF4> (q/k/v, o, gate/up+SwiGLU, down; all launches of one pass)",
+            "mean_launch_us": round(mean_us, 3), "bytes_per_launch": int(bytes_per_launch),
+            "achieved": round(gbs, 1)}
+
+
+# ---------------------------------------------------------------- CPU path
+def cpu_baseline(wl, seed, n_layers: int, runs: int):
+    """The reference path on the host cores (the oracle restatement, timed):
+    tree mask + additive bias, forward with per-call NF4 dequantise, bf16
+    matmuls and masked SDPA, the acceptance walk, and the index_select commit
+    over every layer's cache, on an ``n_layers`` slice of the shape at full
+    width, P and T. Per-layer time is scaled to the full layer count; the
+    embedding/lm_head/mask/walk part is counted once."""
+    import torch
+
+    from oracle import masks as om
+    from oracle import verify as ov
+    from oracle.model import OracleTarget
+    from parallel_eagle_amd import synth
+    from parallel_eagle_amd.config import algorithmic_bytes
+    from parallel_eagle_amd.model import DeviceModel
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    full = wl.model
+    fl = tuple(min(f, n_layers) for f in (1, n_layers, n_layers))
+    shape = full.reduced(n_layers, feature_layers=fl)
+    dm = DeviceModel.synthetic(shape, seed, "cuda:0", keep_logical=True)
+    hw = dm.host_weights()
+    del dm
+    torch.cuda.empty_cache()
+    orc = OracleTarget(shape, hw)
+    P, T = wl.prefix_len, wl.tree_nodes
+    dt = orc.dtype
+    g = torch.Generator().manual_seed(seed)
+    kv = [(torch.randn((1, full.num_kv_heads, P, full.head_dim), generator=g).to(dt),
+           torch.randn((1, full.num_kv_heads, P, full.head_dim), generator=g).to(dt)) for _ in range(n_layers)]
+    root = torch.randn(full.vocab, generator=g).to(dt)
+    tokens, parents = synth.tree_for_seed(seed, full.vocab, wl.depth, wl.widths, wl.top_k)
+
+    def one():
+        t0 = time.perf_counter()
+        allow = om.tree_allow_mask(parents, P)
+        bias = om.to_additive_bias(allow[P:, :], dt)
+        pos = om.tree_position_ids(parents, P)[P:]
+        t_mask = time.perf_counter() - t0
+        t1 = time.perf_counter()
+        lg, _, cache = orc.forward(tokens, pos, kv, bias)
+        t_fwd = time.perf_counter() - t1
+        t2 = time.perf_counter()
+        path, _ = ov.accept_tree_cached(root, lg[0], tokens, parents)
+        keep = torch.tensor(list(range(P)) + [P + t for t in path])
+        for k_, v_ in cache:
+            k_.index_select(2, keep).contiguous()
+            v_.index_select(2, keep).contiguous()
+        t_walk = time.perf_counter() - t2
+        return t_mask, t_fwd, t_walk
+
+    one()  # warm-up
+    samples = [one() for _ in range(runs)]
+    t_mask = statistics.median(s[0] for s in samples)
+    t_fwd = statistics.median(s[1] for s in samples)
+    t_walk = statistics.median(s[2] for s in samples)
+    # lm_head + final norm + embedding, timed alone, is the per-pass fixed part of the forward
+    x = torch.randn((1, T, full.hidden)).to(dt)
+    lm = hw["lm_head"]
+    fixed = []
+    for _ in range(runs + 1):
+        t0 = time.perf_counter()
+        torch.nn.functional.linear(x, lm)
+        fixed.append(time.perf_counter() - t0)
+    t_head = statistics.median(fixed[1:])
+    per_layer_fwd = max(0.0, t_fwd - t_head) / n_layers
+    # compaction cost scales with the layer count too
+    t_pass = t_mask + t_head + per_layer_fwd * full.num_layers + t_walk * full.num_layers / n_layers
+    pass_bytes = algorithmic_bytes(full, [P] * wl.batch, T)
+    return {"value": round(pass_bytes / t_pass / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "ms_per_pass": round(t_pass * 1e3, 1),
+            "sample": (f"oracle forward of a {n_layers}-layer slice at full width (H={full.hidden}, "
+                       f"I={full.intermediate}, V={full.vocab}, P={P}, T={T}; per-call NF4 dequantise in torch), "
+                       f"median of {runs} runs after 1 warm-up, per-layer part scaled x{full.num_layers / n_layers:g}; "
+                       f"torch threads = {cores}")}
+
+
+# ---------------------------------------------------------------- main
+def main(argv=None) -> int:
+    a = parse_args(argv)
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: the verification pass runs on a single device and no multi-GPU "
+              f"path is built (asked for --gpus {a.gpus})", file=sys.stderr)
+        return 2
+    import torch
+
+    from parallel_eagle_amd.config import WORKLOADS, algorithmic_bytes
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    wl = WORKLOADS[a.workload]
+    if wl.batch != 1:
+        print(f"workload {wl.name} is batched; the bench measures the batch-1 pass", file=sys.stderr)
+        return 2
+    tm, cache, step, (tokens, parents, path, bonus) = build_step(wl, a.seed)
+    pass_bytes = algorithmic_bytes(wl.model, [wl.prefix_len], wl.tree_nodes)
+    ms, med_ms, wall = time_pass(step, a.steps, a.warmup)
+    path2, bonus2 = step.result()
+    if (path2, bonus2) != (path, bonus):
+        log(f"WARNING: graph replay accepted {path2}/{bonus2}, eager pass {path}/{bonus}")
+    gbs = pass_bytes / (ms * 1e-3) / 1e9
+    log(f"pass: {ms:.4f} ms mean, {med_ms:.4f} ms median over {a.steps} steps "
+        f"({pass_bytes / 1e9:.3f} GB algorithmic -> {gbs:.0f} GB/s, {gbs / HBM_PEAK_GBS:.1%} of peak)")
+    roof = None
+    if wl.model.weight_format == "nf4":
+        r = nf4_gemm_roofline(tm, wl, a.gemm_reps)
+        log(f"NF4 GEMM: {r['mean_launch_us']} us per launch, {r['bytes_per_launch'] / 1e6:.2f} MB -> "
+            f"{r['achieved']} GB/s")
+        roof = {"bound": "hbm", "achieved": r["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": r["kernel"],
+                "mean_launch_us": r["mean_launch_us"], "bytes_per_launch": r["bytes_per_launch"]}
+    cpu = None
+    if not a.no_cpu_baseline:
+        del step
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(wl, a.seed, a.cpu_layers, a.cpu_runs)
+        log(f"CPU path: {cpu['ms_per_pass']} ms per pass on {cpu['cores']} threads "
+            f"({time.perf_counter() - t0:.1f} s of sampling)")
+    out = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": wl.name, "layers": wl.model.num_layers, "hidden": wl.model.hidden,
+                   "heads": f"{wl.model.num_heads}/{wl.model.num_kv_heads}", "intermediate": wl.model.intermediate,
+                   "vocab": wl.model.vocab, "weights": wl.model.weight_format, "tree_nodes": wl.tree_nodes,
+                   "tree_depth": wl.depth, "prefix_len": wl.prefix_len, "batch": wl.batch,
+                   "pass_bytes": pass_bytes, "hip_graph": True},
+        "latency_ms_median": round(med_ms, 4),
+        "pass_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "accepted": len(path),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

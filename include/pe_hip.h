@@ -52,6 +52,13 @@ extern "C" {
 #define PE_EPI_SWIGLU 2   /* columns interleaved by 32 (gate tile, up tile):
                              out = round(round(silu(round(g))) * round(u)) */
 
+/* row order of the fused q/k/v weight */
+#define PE_QKV_PLAIN 0       /* q heads, k heads, v heads; head dims in order */
+#define PE_QKV_ROPE_PAIRED 1 /* same heads, dims of each head in 32-row tiles ordered
+                                [0,32) [hd/2, hd/2+32) [32,64) [hd/2+32, hd/2+64) ...:
+                                the two halves a RoPE pair needs share a GEMM column
+                                group; bias stays in plain order (16-bit, hd == 128) */
+
 /* attention masks */
 #define PE_MASK_TREE 0   /* rows are tree nodes: whole prefix + ancestor bits */
 #define PE_MASK_CAUSAL 1 /* rows are consecutive tokens: key j allowed iff j <= P + row */
@@ -177,6 +184,7 @@ typedef struct pe_model_desc {
   int32_t intermediate_padded; /* intermediate rounded up to 32 */
   int32_t dtype;               /* activations, norms, embeddings, lm_head, KV */
   int32_t weight_format;       /* PE_WFMT_* of the per-layer linears */
+  int32_t qkv_layout;          /* PE_QKV_* row order of w_qkv */
   float rms_eps;
   int64_t max_positions;
   const void* embed;        /* [V][H] */

@@ -80,5 +80,16 @@ def dequantize(packed: np.ndarray, absmax: np.ndarray) -> np.ndarray:
     return f32_to_bf16_bits(vals.reshape(n, k).astype(np.float32))
 
 
+_TABLE_T = torch.from_numpy(NF4_TABLE)
+
+
 def dequantize_torch(packed: np.ndarray, absmax: np.ndarray) -> torch.Tensor:
-    return torch.from_numpy(dequantize(packed, absmax).view(np.int16)).view(torch.bfloat16)
+    """The same dequantisation as ``dequantize`` in torch ops (multi-threaded on the
+    host cores) -> bf16 tensor [N][K]. Bit-identical to ``dequantize``: one fp32
+    product per element, then one round-to-nearest-even cast."""
+    p = torch.from_numpy(np.ascontiguousarray(packed, dtype=np.uint8))
+    n, kh = p.shape
+    codes = torch.stack([p >> 4, p & 15], dim=-1).reshape(n, kh * 2).long()
+    scale = torch.from_numpy(np.ascontiguousarray(absmax)).float().unsqueeze(-1)
+    vals = _TABLE_T[codes].view(n, kh * 2 // 64, 64) * scale
+    return vals.view(n, kh * 2).to(torch.bfloat16)

@@ -29,6 +29,7 @@ PE_DTYPE_F32, PE_DTYPE_BF16, PE_DTYPE_F16 = 0, 1, 2
 PE_WFMT_DENSE, PE_WFMT_NF4 = 0, 1
 PE_EPI_STORE, PE_EPI_RESIDUAL, PE_EPI_SWIGLU = 0, 1, 2
 PE_MASK_TREE, PE_MASK_CAUSAL = 0, 1
+PE_QKV_PLAIN, PE_QKV_ROPE_PAIRED = 0, 1
 PE_TREE_MAX_WORDS = 4
 
 _ERR_NAMES = {
@@ -62,7 +63,7 @@ class ModelDesc(C.Structure):
     _fields_ = [
         ("num_layers", i32), ("hidden", i32), ("num_heads", i32), ("num_kv_heads", i32),
         ("head_dim", i32), ("intermediate", i32), ("vocab", i32), ("intermediate_padded", i32),
-        ("dtype", i32), ("weight_format", i32), ("rms_eps", f32), ("max_positions", i64),
+        ("dtype", i32), ("weight_format", i32), ("qkv_layout", i32), ("rms_eps", f32), ("max_positions", i64),
         ("embed", vp), ("final_norm", vp), ("lm_head", vp), ("rope_cos_sin", vp),
         ("attn_norm", C.POINTER(vp)), ("mlp_norm", C.POINTER(vp)),
         ("w_qkv", C.POINTER(vp)), ("a_qkv", C.POINTER(vp)), ("b_qkv", C.POINTER(vp)),

@@ -36,28 +36,46 @@ __device__ __forceinline__ bool key_allowed(int64_t key, int64_t P, int t, int m
   return (nb[u >> 6] >> (u & 63)) & 1ull;
 }
 
+// One workgroup = 4 waves = one (KV head, key split, 32-row tile). Each wave
+// takes a contiguous run of the split's 32-key blocks; the next block's K and
+// V fragments are loaded as soon as the current ones are consumed (K after the
+// S MFMAs, V after its LDS transpose), so the loads overlap softmax and PV.
+// Loads are clamped to the wave's last valid key (those scores are masked and
+// their probabilities are exactly zero), so no uninitialised cache row is read.
+// At the end the 4 waves' (m, l, O) are merged in LDS in wave order and one
+// partial per workgroup is written for attn_combine_kernel.
+constexpr int kAttnWaves = 4;
+
 template <int DT>
-__global__ __launch_bounds__(64) void attn_mfma_kernel(
+__global__ __launch_bounds__(64 * kAttnWaves) void attn_wg_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
     int nh, int nkv, int T, int64_t P, int mask_mode, const uint64_t* __restrict__ bits, int words, float scale,
     int keys_per_split, int splits, int rows_pad, float* __restrict__ opart, float* __restrict__ mlpart) {
   constexpr int HD = 128;
+  constexpr int kVtBytes = HD * (32 + 8) * 2;
+  constexpr int kCmbBytes = (kAttnWaves - 1) * 32 * (HD + 2) * 4;
+  constexpr int kSmem = (kAttnWaves * kVtBytes > kCmbBytes) ? kAttnWaves * kVtBytes : kCmbBytes;
+  __shared__ __align__(16) uint8_t smem[kSmem];
   const int kvh = blockIdx.x, split = blockIdx.y, rt = blockIdx.z;
   const int G = nh / nkv, rows = T * G;
-  const int lane = threadIdx.x, ln = lane & 31, g = lane >> 5;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 31, g = lane >> 5;
   const int64_t S = P + T;
-  const int64_t j0 = (int64_t)split * keys_per_split;
-  const int64_t j1 = min(S, j0 + keys_per_split);
+  const int64_t ks0 = (int64_t)split * keys_per_split;
+  const int64_t ks1 = min(S, ks0 + keys_per_split);
+  const int nb = (int)((ks1 - ks0 + 31) / 32);
+  const int b0 = (nb * wave) / kAttnWaves, b1 = (nb * (wave + 1)) / kAttnWaves;
+  const int64_t j1 = min(ks1, ks0 + 32 * (int64_t)b1);  // end of this wave's keys
+  uint16_t(*vt)[32 + 8] = (uint16_t(*)[32 + 8])(smem + wave * kVtBytes);
 
   const int r = rt * 32 + ln;
   const bool rvalid = r < rows;
   const int t = rvalid ? r / G : 0;
   const int hq = kvh * G + (rvalid ? r % G : 0);
 
-  uint64_t nb[PE_TREE_MAX_WORDS];
+  uint64_t nbits[PE_TREE_MAX_WORDS];
 #pragma unroll
   for (int w = 0; w < PE_TREE_MAX_WORDS; ++w)
-    nb[w] = (mask_mode == PE_MASK_TREE && w < words && rvalid) ? bits[(int64_t)t * words + w] : 0ull;
+    nbits[w] = (mask_mode == PE_MASK_TREE && w < words && rvalid) ? bits[(int64_t)t * words + w] : 0ull;
 
   const u32x4_t zero4 = {0u, 0u, 0u, 0u};
   u32x4_t qf[8];
@@ -72,47 +90,61 @@ __global__ __launch_bounds__(64) void attn_mfma_kernel(
     for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
   float m = kInitMax, l = 0.f;
 
-  __shared__ uint16_t vt[HD][32 + 8];
   const uint16_t* kbase = kc + (int64_t)kvh * cap * HD;
   const uint16_t* vbase = vc + (int64_t)kvh * cap * HD;
-
-  for (int64_t jb = j0; jb < j1; jb += 32) {
-    // ---- S^T = K Q^T over hd
-    const int64_t key = jb + ln;
-    const bool kvalid = key < j1;
-    const uint16_t* kp = kbase + (kvalid ? key : jb) * HD + 8 * g;
-    u32x4_t kf[8];
+  const int64_t jlast = j1 - 1;
+  u32x4_t kf[8], vf[8];
+  auto load_k = [&](int64_t jb) {
+    const uint16_t* kp = kbase + min(jb + ln, jlast) * HD + 8 * g;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) kf[j] = kvalid ? *(const u32x4_t*)(kp + 16 * j) : zero4;
-    // V block -> LDS transposed: vt[d][key offset]
-    u32x4_t vf[8];
+    for (int j = 0; j < 8; ++j) kf[j] = *(const u32x4_t*)(kp + 16 * j);
+  };
+  auto load_v = [&](int64_t jb) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const int chunk = c * 64 + lane;  // 32 keys x 16 chunks of 8 dims
       const int koff = chunk >> 4, dc = chunk & 15;
-      const int64_t vk = jb + koff;
-      vf[c] = (vk < j1) ? *(const u32x4_t*)(vbase + vk * HD + dc * 8) : zero4;
+      vf[c] = *(const u32x4_t*)(vbase + min(jb + koff, jlast) * HD + dc * 8);
     }
-    f32x16_t s;
+  };
+  if (b0 < b1) {
+    load_k(ks0 + 32 * (int64_t)b0);
+    load_v(ks0 + 32 * (int64_t)b0);
+  }
+  for (int b = b0; b < b1; ++b) {
+    const int64_t jb = ks0 + 32 * (int64_t)b;
+    const int64_t jnext = ks0 + 32 * (int64_t)min(b + 1, b1 - 1);
+    // ---- S^T = K Q^T over hd
+    f32x16_t sc;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+    for (int i = 0; i < 16; ++i) sc[i] = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if constexpr (DT == PE_DTYPE_F16)
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[j]),
-                                                   __builtin_bit_cast(f16x8_t, qf[j]), s, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[j]),
+                                                    __builtin_bit_cast(f16x8_t, qf[j]), sc, 0, 0, 0);
       else
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[j]),
-                                                    __builtin_bit_cast(bf16x8_t, qf[j]), s, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[j]),
+                                                     __builtin_bit_cast(bf16x8_t, qf[j]), sc, 0, 0, 0);
     }
-    // ---- scale + mask, block max (s[i] holds key jb + 8*(i/4) + 4*g + (i%4) of row ln)
+    load_k(jnext);
+    // ---- scale + mask, block max (sc[i] holds key jb + 8*(i/4) + 4*g + (i%4) of row ln)
     float bmax = kInitMax;
+    if (jb + 32 <= min(P, j1) && (mask_mode == PE_MASK_TREE || jb + 32 <= P + 1)) {
+      // a whole block of prefix keys: every key is visible to every node
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t kj = jb + 8 * (i >> 2) + 4 * g + (i & 3);
-      const bool ok = rvalid && kj < j1 && key_allowed(kj, P, t, mask_mode, nb);
-      s[i] = ok ? s[i] * scale : kMaskedScore;
-      bmax = fmaxf(bmax, s[i]);
+      for (int i = 0; i < 16; ++i) {
+        sc[i] = rvalid ? sc[i] * scale : kMaskedScore;
+        bmax = fmaxf(bmax, sc[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t kj = jb + 8 * (i >> 2) + 4 * g + (i & 3);
+        const bool ok = rvalid && kj < j1 && key_allowed(kj, P, t, mask_mode, nbits);
+        sc[i] = ok ? sc[i] * scale : kMaskedScore;
+        bmax = fmaxf(bmax, sc[i]);
+      }
     }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
     const float mnew = fmaxf(m, bmax);
@@ -121,20 +153,24 @@ __global__ __launch_bounds__(64) void attn_mfma_kernel(
     uint32_t pb[8];
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
-      const float p0 = expf(s[i] - mnew), p1 = expf(s[i + 1] - mnew);
+      const float p0 = expf(sc[i] - mnew), p1 = expf(sc[i + 1] - mnew);
       psum += p0 + p1;
       pb[i >> 1] = (DT == PE_DTYPE_F16) ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
                                         : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
     }
     psum += __shfl_xor(psum, 32, 64);
     l = l * alpha + psum;
+    // rescale O only if some row's running max moved (alpha == 1 leaves O as is)
+    const bool rescale = __builtin_amdgcn_ballot_w64(mnew != m) != 0ull;
     m = mnew;
+    if (rescale) {
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
+      for (int h = 0; h < 4; ++h)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[h][i] *= alpha;
+        for (int i = 0; i < 16; ++i) o[h][i] *= alpha;
+    }
 
-    // ---- V^T into LDS
+    // ---- V^T into LDS, then the next block's V
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const int chunk = c * 64 + lane;
@@ -143,17 +179,18 @@ __global__ __launch_bounds__(64) void attn_mfma_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) vt[dc * 8 + e][koff] = ve[e];
     }
+    load_v(jnext);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // ---- O^T += V^T P^T: two 16-key halves c; lane group g holds keys 16c+4g+{0..3}, 16c+8+4g+{0..3}
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      u32x4_t b;
-      b[0] = pb[4 * c + 0];
-      b[1] = pb[4 * c + 1];
-      b[2] = pb[4 * c + 2];
-      b[3] = pb[4 * c + 3];
+      u32x4_t bp;
+      bp[0] = pb[4 * c + 0];
+      bp[1] = pb[4 * c + 1];
+      bp[2] = pb[4 * c + 2];
+      bp[3] = pb[4 * c + 3];
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
         const int d = h * 32 + ln;
@@ -166,10 +203,10 @@ __global__ __launch_bounds__(64) void attn_mfma_kernel(
         a[3] = hi.y;
         if constexpr (DT == PE_DTYPE_F16)
           o[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
-                                                        __builtin_bit_cast(f16x8_t, b), o[h], 0, 0, 0);
+                                                        __builtin_bit_cast(f16x8_t, bp), o[h], 0, 0, 0);
         else
           o[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                         __builtin_bit_cast(bf16x8_t, b), o[h], 0, 0, 0);
+                                                         __builtin_bit_cast(bf16x8_t, bp), o[h], 0, 0, 0);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -177,16 +214,52 @@ __global__ __launch_bounds__(64) void attn_mfma_kernel(
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
-  if (!rvalid) return;
+  // ---- merge the waves: (m, l, O) of waves 1..3 through LDS, wave 0 sums in wave order
+  __syncthreads();
+  float* cmb = (float*)smem;
+  if (wave > 0) {
+    float* cw = cmb + (int64_t)(wave - 1) * 32 * (HD + 2);
+    if (g == 0) {
+      cw[ln * (HD + 2) + HD] = m;
+      cw[ln * (HD + 2) + HD + 1] = l;
+    }
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) cw[ln * (HD + 2) + h * 32 + 8 * (i >> 2) + 4 * g + (i & 3)] = o[h][i];
+  }
+  __syncthreads();
+  if (wave != 0 || !rvalid) return;
+  float mw[kAttnWaves], wt[kAttnWaves];
+  mw[0] = m;
+  float M = m;
+#pragma unroll
+  for (int w = 1; w < kAttnWaves; ++w) {
+    mw[w] = cmb[(int64_t)(w - 1) * 32 * (HD + 2) + ln * (HD + 2) + HD];
+    M = fmaxf(M, mw[w]);
+  }
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) {
+    wt[w] = expf(mw[w] - M);
+    const float lw = (w == 0) ? l : cmb[(int64_t)(w - 1) * 32 * (HD + 2) + ln * (HD + 2) + HD + 1];
+    L += wt[w] * lw;
+  }
   const int64_t pidx = ((int64_t)kvh * splits + split) * rows_pad + r;
   float* op = opart + pidx * HD;
 #pragma unroll
   for (int h = 0; h < 4; ++h)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) op[h * 32 + 8 * (i >> 2) + 4 * g + (i & 3)] = o[h][i];
+    for (int i = 0; i < 16; ++i) {
+      const int d = h * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+      float v = wt[0] * o[h][i];
+#pragma unroll
+      for (int w = 1; w < kAttnWaves; ++w) v += wt[w] * cmb[(int64_t)(w - 1) * 32 * (HD + 2) + ln * (HD + 2) + d];
+      op[d] = v;
+    }
   if (g == 0) {
-    mlpart[pidx * 2 + 0] = m;
-    mlpart[pidx * 2 + 1] = l;
+    mlpart[pidx * 2 + 0] = M;
+    mlpart[pidx * 2 + 1] = L;
   }
 }
 
@@ -277,9 +350,9 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S) {
   const int rows = T * (nh / nkv);
   p.row_tiles = (rows + 31) / 32;
   p.rows_pad = p.row_tiles * 32;
-  // aim for ~512 waves; at least 64 keys per split
-  int64_t want = (512 + (int64_t)nkv * p.row_tiles - 1) / ((int64_t)nkv * p.row_tiles);
-  int64_t maxsplit = (S + 63) / 64;
+  // about one workgroup per CU, each with at least two 32-key blocks per wave
+  int64_t want = (256 + (int64_t)nkv * p.row_tiles - 1) / ((int64_t)nkv * p.row_tiles);
+  int64_t maxsplit = (S + 32 * 2 * kAttnWaves - 1) / (32 * 2 * kAttnWaves);
   if (want > maxsplit) want = maxsplit;
   if (want < 1) want = 1;
   int64_t kps = (S + want - 1) / want;
@@ -322,7 +395,7 @@ extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void*
     dim3 grid(nkv, p.splits, p.row_tiles);
     dim3 cgrid(T * (nh / nkv), nkv);
     if (dtype == PE_DTYPE_BF16) {
-      attn_mfma_kernel<PE_DTYPE_BF16><<<grid, 64, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
+      attn_wg_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
                                                            (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
                                                            mask_mode, bits, words, scale, p.keys_per_split,
                                                            p.splits, p.rows_pad, opart, ml);
@@ -330,7 +403,7 @@ extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void*
       attn_combine_kernel<PE_DTYPE_BF16><<<cgrid, 128, 0, st>>>(opart, ml, nh, nkv, T, hd, p.splits, p.rows_pad,
                                                                 (uint16_t*)out, ld_out);
     } else if (dtype == PE_DTYPE_F16) {
-      attn_mfma_kernel<PE_DTYPE_F16><<<grid, 64, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
+      attn_wg_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
                                                           (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
                                                           mask_mode, bits, words, scale, p.keys_per_split, p.splits,
                                                           p.rows_pad, opart, ml);

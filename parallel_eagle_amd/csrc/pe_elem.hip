@@ -8,6 +8,7 @@
 // multiply-add is contracted where torch rounds between the two.
 
 #include "pe_common.h"
+#include "pe_internal.h"
 
 namespace {
 
@@ -101,6 +102,84 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(const typename Elem<DT>::
   }
 }
 
+// One block per row: the residual add of a split-K projection (partials summed
+// in split order, HF modeling_llama.py:317,323) fused with the RMSNorm that
+// follows it (modeling_llama.py:62-67) and the hidden-state captures. Each
+// thread owns up to kNormChunks chunks of 4 columns and issues all of its
+// partial loads before summing, so the row costs one memory round trip.
+constexpr int kNormThreads = 1024;
+constexpr int kNormChunks = 2;    // H <= 4 * 1024 * 2
+constexpr int kNormMaxSplits = 16;
+
+template <int DT>
+__global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
+    const float* __restrict__ partial, int S, int M, typename Elem<DT>::T* __restrict__ h, int H,
+    const typename Elem<DT>::T* __restrict__ w, float eps, typename Elem<DT>::T* __restrict__ xn,
+    typename Elem<DT>::T* __restrict__ cap_h, int64_t ld_cap_h, typename Elem<DT>::T* __restrict__ cap_xn,
+    int64_t ld_cap_xn) {
+  typedef Elem<DT> E;
+  typedef typename E::T T;
+  const int m = blockIdx.x;
+  T* hr = h + (int64_t)m * H;
+  const int nchunk = H >> 2;
+  float v[kNormChunks][4];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNormChunks; ++k) {
+    const int c = threadIdx.x + k * kNormThreads;
+    if (c >= nchunk) continue;
+    float4 pv[kNormMaxSplits];
+#pragma unroll
+    for (int sp = 0; sp < kNormMaxSplits; ++sp)
+      if (sp < S) pv[sp] = *(const float4*)(partial + ((int64_t)sp * M + m) * H + 4 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[k][e] = E::load(hr, 4 * c + e);
+    if (S > 0) {
+      float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sp = 0; sp < kNormMaxSplits; ++sp) {
+        if (sp < S) {
+          a[0] += pv[sp].x;
+          a[1] += pv[sp].y;
+          a[2] += pv[sp].z;
+          a[3] += pv[sp].w;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[k][e] = E::round(__fadd_rn(v[k][e], E::round(a[e])));
+        E::store(hr, 4 * c + e, v[k][e]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (cap_h) E::store(cap_h + (int64_t)m * ld_cap_h, 4 * c + e, v[k][e]);
+      ss = __fadd_rn(ss, __fmul_rn(v[k][e], v[k][e]));
+    }
+  }
+  __shared__ float part[kNormThreads / 64];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += part[i];
+  const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+  T* orow = xn + (int64_t)m * H;
+#pragma unroll
+  for (int k = 0; k < kNormChunks; ++k) {
+    const int c = threadIdx.x + k * kNormThreads;
+    if (c >= nchunk) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float y = E::round(__fmul_rn(v[k][e], inv));
+      const float o = __fmul_rn(E::load(w, 4 * c + e), y);
+      E::store(orow, 4 * c + e, o);
+      if (cap_xn) E::store(cap_xn + (int64_t)m * ld_cap_xn, 4 * c + e, o);
+    }
+  }
+}
+
 __global__ void copy_rows_kernel(const uint8_t* __restrict__ src, int64_t ld_src, int64_t row_bytes,
                                  uint8_t* __restrict__ dst, int64_t ld_dst) {
   const int m = blockIdx.x;
@@ -172,6 +251,20 @@ extern "C" int pe_copy_rows(const void* src, int64_t ld_src, int M, int64_t row_
   if (M == 0 || row_bytes == 0) return PE_OK;
   copy_rows_kernel<<<M, 256, 0, (hipStream_t)stream>>>((const uint8_t*)src, ld_src, row_bytes, (uint8_t*)dst,
                                                        ld_dst);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, int H, const void* w, float eps,
+                                 int dtype, void* xn, void* cap_h, int64_t ld_cap_h, void* cap_xn, int64_t ld_cap_xn,
+                                 hipStream_t st) {
+  if (!h || !w || !xn || M <= 0 || H <= 0 || S < 0 || (S > 0 && !partial)) return PE_ERR_ARG;
+  if (H % 4 || H > 4 * kNormThreads * kNormChunks || S > kNormMaxSplits) return PE_ERR_ARG;
+  PE_DISPATCH_DT(dtype, {
+    typedef typename Elem<DT>::T T;
+    residual_rmsnorm_kernel<DT><<<M, kNormThreads, 0, st>>>(partial, S, M, (T*)h, H, (const T*)w, eps, (T*)xn,
+                                                            (T*)cap_h, ld_cap_h, (T*)cap_xn, ld_cap_xn);
+  });
   PE_CHECK_LAUNCH();
   return PE_OK;
 }

@@ -19,6 +19,7 @@
 #include <cstring>
 
 #include "../../include/pe_hip.h"
+#include "pe_internal.h"
 
 namespace {
 
@@ -29,10 +30,16 @@ int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 int esize(int dtype) { return dtype == PE_DTYPE_F32 ? 4 : 2; }
 
 struct Layout {
-  int64_t gemm;  // counters + partials (must start with the zeroed counters)
+  int64_t gemm;  // split-K partials of the standalone GEMMs / fp32 partials of the layer GEMMs
   int64_t gemm_bytes;
   int64_t h, xn, qkv, q, attn, act, attn_ws, attn_ws_bytes, total;
 };
+
+// The 16-bit pass with fused epilogues (see pe_forward) needs the q/k/v rows
+// in RoPE-paired order and hd == 128 attention.
+bool fused_path(const pe_model_desc* m, int M) {
+  return m->dtype != PE_DTYPE_F32 && m->qkv_layout == PE_QKV_ROPE_PAIRED && m->head_dim == 128 && M <= 64;
+}
 
 int64_t gemm_ws(const pe_model_desc* m, int M, int N, int K, int epi) {
   const int wf = m->weight_format;
@@ -45,10 +52,14 @@ Layout make_layout(const pe_model_desc* m, int M, int64_t kv_len) {
   const int H = m->hidden, qd = m->num_heads * m->head_dim, kvd = m->num_kv_heads * m->head_dim;
   const int nqkv = qd + 2 * kvd, ip = m->intermediate_padded;
   int64_t g = kCounterBytes;
-  int64_t cand[5] = {gemm_ws(m, M, nqkv, H, PE_EPI_STORE), gemm_ws(m, M, H, qd, PE_EPI_RESIDUAL),
+  int64_t cand[7] = {gemm_ws(m, M, nqkv, H, PE_EPI_STORE), gemm_ws(m, M, H, qd, PE_EPI_RESIDUAL),
                      gemm_ws(m, M, 2 * ip, H, PE_EPI_SWIGLU), gemm_ws(m, M, H, ip, PE_EPI_RESIDUAL),
-                     pe_gemm_workspace_bytes(M, m->vocab, H, PE_WFMT_DENSE, m->dtype, PE_EPI_STORE)};
-  for (int i = 0; i < 5; ++i)
+                     pe_gemm_workspace_bytes(M, m->vocab, H, PE_WFMT_DENSE, m->dtype, PE_EPI_STORE), 0, 0};
+  if (fused_path(m, M)) {
+    cand[5] = pe_internal_gemm_partial_bytes(M, H, qd, m->weight_format);
+    cand[6] = pe_internal_gemm_partial_bytes(M, H, ip, m->weight_format);
+  }
+  for (int i = 0; i < 7; ++i)
     if (cand[i] > g) g = cand[i];
   int64_t off = 0;
   L.gemm = off;
@@ -95,9 +106,99 @@ extern "C" const char* pe_status_string(int status) {
 
 extern "C" int pe_version(void) { return 1; }
 
+constexpr int kFusedChunk = 64;  // rows per fused pass (causal passes are chunked)
+
 extern "C" int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int64_t kv_len) {
   if (!m || M <= 0 || kv_len <= 0) return 0;
+  if (m->qkv_layout == PE_QKV_ROPE_PAIRED && M > kFusedChunk) M = kFusedChunk;
   return make_layout(m, M, kv_len).total;
+}
+
+// The 16-bit pass: per layer
+//   q/k/v GEMM with bias + RoPE + in-place K/V append in its epilogue
+//   -> tree attention (split-KV) -> combine
+//   -> o GEMM (fp32 split partials) -> residual add + post-attention RMSNorm
+//   -> gate/up GEMM with SwiGLU epilogue
+//   -> down GEMM (fp32 split partials) -> residual add + next RMSNorm
+// The RMSNorm after the down projection is the next layer's input norm, or the
+// final norm after the last layer; hidden-state captures ride on it.
+int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& Lo, hipStream_t st) {
+  const int M = a->M;
+  char* ws = (char*)a->workspace;
+  float* part = (float*)(ws + Lo.gemm);
+  const int64_t part_bytes = Lo.gemm_bytes;
+  const int es = esize(m->dtype);
+  const int H = m->hidden, nh = m->num_heads, nkv = m->num_kv_heads, hd = m->head_dim;
+  const int qd = nh * hd, ip = m->intermediate_padded, L = m->num_layers, wf = m->weight_format;
+  void* h = ws + Lo.h;
+  void* xn = ws + Lo.xn;
+  void* q = ws + Lo.q;
+  void* attn = ws + Lo.attn;
+  void* act = ws + Lo.act;
+  void* aws = ws + Lo.attn_ws;
+  const float scale = (float)(1.0 / std::sqrt((double)hd));
+  const int64_t layer_stride = (int64_t)nkv * a->cache_capacity * hd * es;
+  const int64_t fused_ld = (int64_t)a->num_features * H;  // elements
+  int rc;
+#define PE_TRY(expr)            \
+  do {                          \
+    rc = (expr);                \
+    if (rc != PE_OK) return rc; \
+  } while (0)
+  // first fused-feature slot capturing `layer` (or -1), and extra copies for repeated layers
+  auto slot_of = [&](int layer) -> int {
+    if (!a->fused) return -1;
+    for (int f = 0; f < a->num_features; ++f)
+      if (a->feature_layers[f] == layer) return f;
+    return -1;
+  };
+  auto slot_ptr = [&](int f) -> void* { return f < 0 ? nullptr : (char*)a->fused + (int64_t)f * H * es; };
+  auto copy_repeats = [&](int layer, int first) -> int {
+    if (first < 0) return PE_OK;
+    for (int f = first + 1; f < a->num_features; ++f) {
+      if (a->feature_layers[f] != layer) continue;
+      int r = pe_copy_rows(slot_ptr(first), fused_ld * es, M, (int64_t)H * es, slot_ptr(f), fused_ld * es, st);
+      if (r != PE_OK) return r;
+    }
+    return PE_OK;
+  };
+
+  PE_TRY(pe_embed(a->input_ids, M, m->embed, m->vocab, H, m->dtype, h, H, a->status, st));
+  {
+    const int f0 = slot_of(0);
+    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->attn_norm[0], m->rms_eps, m->dtype, xn, slot_ptr(f0),
+                                        fused_ld, nullptr, 0, st));
+    PE_TRY(copy_repeats(0, f0));
+  }
+  for (int l = 0; l < L; ++l) {
+    void* kc = (char*)a->k_cache + l * layer_stride;
+    void* vc = (char*)a->v_cache + l * layer_stride;
+    int S = 1;
+    PE_TRY(pe_internal_gemm_rope_kv(wf, m->dtype, xn, H, M, H, m->w_qkv[l], (const uint16_t*)(m->a_qkv ? m->a_qkv[l] : nullptr),
+                                    nh, nkv, hd, m->b_qkv ? m->b_qkv[l] : nullptr, a->positions, m->rope_cos_sin,
+                                    m->max_positions, q, kc, vc, a->cache_capacity, a->prefix_len, a->status, st));
+    PE_TRY(pe_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode, a->tree_bits,
+                             a->bits_words, scale, m->dtype, attn, qd, aws, Lo.attn_ws_bytes, st));
+    PE_TRY(pe_internal_gemm_partials(wf, m->dtype, attn, qd, M, qd, m->w_o[l], (const uint16_t*)(m->a_o ? m->a_o[l] : nullptr),
+                                     H, part, part_bytes, &S, st));
+    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, nullptr, 0,
+                                        nullptr, 0, st));
+    PE_TRY(pe_internal_gemm_epilogue(wf, m->dtype, xn, H, M, H, m->w_gu[l], (const uint16_t*)(m->a_gu ? m->a_gu[l] : nullptr),
+                                     2 * ip, PE_EPI_SWIGLU, nullptr, nullptr, 0, act, ip, st));
+    PE_TRY(pe_internal_gemm_partials(wf, m->dtype, act, ip, M, ip, m->w_down[l],
+                                     (const uint16_t*)(m->a_down ? m->a_down[l] : nullptr), H, part, part_bytes, &S, st));
+    const bool last = l + 1 == L;
+    const int fh = last ? -1 : slot_of(l + 1);
+    const int fx = last ? slot_of(L) : -1;
+    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, last ? m->final_norm : m->attn_norm[l + 1], m->rms_eps,
+                                        m->dtype, xn, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
+    PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
+  }
+  if (a->logits)
+    PE_TRY(pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
+                         m->vocab, part, part_bytes, st));
+#undef PE_TRY
+  return PE_OK;
 }
 
 extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* stream) {
@@ -111,7 +212,30 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
   hipStream_t st = (hipStream_t)stream;
   const int64_t kv_len = a->prefix_len + M;
   const Layout Lo = make_layout(m, M, kv_len);
+  if (m->qkv_layout == PE_QKV_ROPE_PAIRED) {
+    // 16-bit hd-128 models only; a tree pass must fit one chunk (its nodes see
+    // ancestors only, so it cannot be split into causal continuations).
+    if (m->dtype == PE_DTYPE_F32 || m->head_dim != 128) return PE_ERR_ARG;
+    if (a->mask_mode == PE_MASK_TREE && M > kFusedChunk) return PE_ERR_TREE;
+    const int64_t vocab_bytes = (int64_t)m->vocab * esize(m->dtype);
+    const int64_t fused_bytes = (int64_t)a->num_features * m->hidden * esize(m->dtype);
+    for (int c0 = 0; c0 < M; c0 += kFusedChunk) {
+      pe_pass_args b = *a;
+      b.M = (M - c0 < kFusedChunk) ? M - c0 : kFusedChunk;
+      b.input_ids = a->input_ids + c0;
+      b.positions = a->positions + c0;
+      b.prefix_len = a->prefix_len + c0;
+      b.logits = a->logits ? (char*)a->logits + c0 * vocab_bytes : nullptr;
+      b.fused = a->fused ? (char*)a->fused + c0 * fused_bytes : nullptr;
+      const Layout Lc = make_layout(m, b.M, b.prefix_len + b.M);
+      if (a->workspace_bytes < Lc.total) return PE_ERR_WORKSPACE;
+      const int rc = forward_fused(m, &b, Lc, st);
+      if (rc != PE_OK) return rc;
+    }
+    return PE_OK;
+  }
   if (a->workspace_bytes < Lo.total) return PE_ERR_WORKSPACE;
+  if (m->qkv_layout != PE_QKV_PLAIN) return PE_ERR_ARG;
   char* ws = (char*)a->workspace;
   void* gws = ws + Lo.gemm;
   const int64_t gwsb = Lo.gemm_bytes;

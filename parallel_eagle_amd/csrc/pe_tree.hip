@@ -91,62 +91,90 @@ __global__ __launch_bounds__(256) void bias_to_bits_kernel(const typename Elem<D
   if (threadIdx.x < words) bits[(int64_t)t * words + threadIdx.x] = w[threadIdx.x];
 }
 
+// Row argmax with torch.argmax's semantics: the largest value, a NaN beats
+// every number, and among equal maxima (or NaNs) the lowest index wins.
+struct ArgBest {
+  float v;
+  int idx;  // -1: none yet
+  int nan;
+};
+
+__device__ __forceinline__ bool arg_better(const ArgBest& b, const ArgBest& a) {  // b beats a
+  if (b.idx < 0) return false;
+  if (a.idx < 0) return true;
+  if (a.nan && b.nan) return b.idx < a.idx;
+  if (a.nan) return false;
+  if (b.nan) return true;
+  return (b.v > a.v) || (b.v == a.v && b.idx < a.idx);
+}
+
+__device__ __forceinline__ void arg_take(ArgBest& a, float v, int i) {
+  ArgBest b = {v, i, v != v};
+  if (arg_better(b, a)) a = b;
+}
+
+constexpr int kArgThreads = 1024;
+
+// One block of kArgThreads per row. Thread t scans 8-element vectors
+// t, t + kArgThreads, ... in increasing index order (all loads issued first),
+// then the block reduces with the same rule.
 template <int DT>
 __device__ void row_argmax(const typename Elem<DT>::T* __restrict__ x, int64_t V, int32_t* out) {
-  // (value, index): larger value wins, NaN beats numbers, ties -> smaller index
-  float best = 0.f;
-  int64_t bi = -1;
-  bool bnan = false;
-  for (int64_t i = threadIdx.x; i < V; i += blockDim.x) {
-    const float v = Elem<DT>::load(x, i);
-    const bool vnan = v != v;
-    bool take;
-    if (bi < 0) take = true;
-    else if (bnan) take = false;  // earlier NaN already holds (indices ascend per thread)
-    else if (vnan) take = true;
-    else take = v > best;
-    if (take) { best = v; bi = i; bnan = vnan; }
-  }
-  __shared__ float sv[256];
-  __shared__ int64_t si[256];
-  __shared__ int sn[256];
-  sv[threadIdx.x] = best;
-  si[threadIdx.x] = bi;
-  sn[threadIdx.x] = bnan;
-  __syncthreads();
-  for (int o = blockDim.x >> 1; o > 0; o >>= 1) {
-    if (threadIdx.x < o) {
-      const float v2 = sv[threadIdx.x + o];
-      const int64_t i2 = si[threadIdx.x + o];
-      const int n2 = sn[threadIdx.x + o];
-      const float v1 = sv[threadIdx.x];
-      const int64_t i1 = si[threadIdx.x];
-      const int n1 = sn[threadIdx.x];
-      bool take2;
-      if (i2 < 0) take2 = false;
-      else if (i1 < 0) take2 = true;
-      else if (n1 && n2) take2 = i2 < i1;
-      else if (n1) take2 = false;
-      else if (n2) take2 = true;
-      else take2 = (v2 > v1) || (v2 == v1 && i2 < i1);
-      if (take2) { sv[threadIdx.x] = v2; si[threadIdx.x] = i2; sn[threadIdx.x] = n2; }
+  typedef typename Elem<DT>::T T;
+  constexpr int kPer = 16 / sizeof(T);  // elements per 16-byte vector
+  constexpr int kVec = 8;               // vectors per thread held in flight
+  ArgBest best = {0.f, -1, 0};
+  const bool aligned = (((uintptr_t)x) & 15) == 0;
+  const int64_t nvec = aligned ? V / kPer : 0;
+  for (int64_t v0 = 0; v0 < nvec; v0 += (int64_t)kVec * kArgThreads) {
+    u32x4_t buf[kVec];
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) {
+      const int64_t vi = v0 + (int64_t)k * kArgThreads + threadIdx.x;
+      if (vi < nvec) buf[k] = *(const u32x4_t*)(x + vi * kPer);
     }
-    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) {
+      const int64_t vi = v0 + (int64_t)k * kArgThreads + threadIdx.x;
+      if (vi < nvec) {
+        const T* e = (const T*)&buf[k];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) arg_take(best, Elem<DT>::load(e, j), (int)(vi * kPer + j));
+      }
+    }
   }
-  if (threadIdx.x == 0) *out = (int32_t)si[0];
+  for (int64_t i = nvec * kPer + threadIdx.x; i < V; i += kArgThreads) arg_take(best, Elem<DT>::load(x, i), (int)i);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    ArgBest b;
+    b.v = __shfl_xor(best.v, o, 64);
+    b.idx = __shfl_xor(best.idx, o, 64);
+    b.nan = __shfl_xor(best.nan, o, 64);
+    if (arg_better(b, best)) best = b;
+  }
+  __shared__ ArgBest wbest[kArgThreads / 64];
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    ArgBest a = wbest[0];
+    for (int w = 1; w < kArgThreads / 64; ++w)
+      if (arg_better(wbest[w], a)) a = wbest[w];
+    *out = a.idx;
+  }
 }
 
 template <int DT>
-__global__ __launch_bounds__(256) void argmax_rows_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t ld,
-                                                          int64_t V, int32_t* __restrict__ out) {
+__global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const typename Elem<DT>::T* __restrict__ x,
+                                                                  int64_t ld, int64_t V, int32_t* __restrict__ out) {
   row_argmax<DT>(x + (int64_t)blockIdx.x * ld, V, out + blockIdx.x);
 }
 
 // row 0 = root logit, rows 1..T = node logits
 template <int DT>
-__global__ __launch_bounds__(256) void accept_argmax_kernel(const typename Elem<DT>::T* __restrict__ root,
-                                                            const typename Elem<DT>::T* __restrict__ nodes, int64_t ld,
-                                                            int64_t V, int32_t* __restrict__ amax) {
+__global__ __launch_bounds__(kArgThreads) void accept_argmax_kernel(const typename Elem<DT>::T* __restrict__ root,
+                                                                    const typename Elem<DT>::T* __restrict__ nodes,
+                                                                    int64_t ld, int64_t V,
+                                                                    int32_t* __restrict__ amax) {
   const int r = blockIdx.x;
   const typename Elem<DT>::T* x = (r == 0) ? root : nodes + (int64_t)(r - 1) * ld;
   row_argmax<DT>(x, V, amax + r);
@@ -274,9 +302,9 @@ extern "C" int pe_argmax_rows(const void* x, int64_t ld, int rows, int64_t V, in
   if (!x || !out_idx || rows <= 0 || V <= 0) return PE_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
-    case PE_DTYPE_F32: argmax_rows_kernel<PE_DTYPE_F32><<<rows, 256, 0, st>>>((const float*)x, ld, V, out_idx); break;
-    case PE_DTYPE_BF16: argmax_rows_kernel<PE_DTYPE_BF16><<<rows, 256, 0, st>>>((const uint16_t*)x, ld, V, out_idx); break;
-    case PE_DTYPE_F16: argmax_rows_kernel<PE_DTYPE_F16><<<rows, 256, 0, st>>>((const uint16_t*)x, ld, V, out_idx); break;
+    case PE_DTYPE_F32: argmax_rows_kernel<PE_DTYPE_F32><<<rows, kArgThreads, 0, st>>>((const float*)x, ld, V, out_idx); break;
+    case PE_DTYPE_BF16: argmax_rows_kernel<PE_DTYPE_BF16><<<rows, kArgThreads, 0, st>>>((const uint16_t*)x, ld, V, out_idx); break;
+    case PE_DTYPE_F16: argmax_rows_kernel<PE_DTYPE_F16><<<rows, kArgThreads, 0, st>>>((const uint16_t*)x, ld, V, out_idx); break;
     default: return PE_ERR_ARG;
   }
   PE_CHECK_LAUNCH();
@@ -291,15 +319,15 @@ extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, i
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
     case PE_DTYPE_F32:
-      accept_argmax_kernel<PE_DTYPE_F32><<<T + 1, 256, 0, st>>>((const float*)root_logit, (const float*)node_logits,
+      accept_argmax_kernel<PE_DTYPE_F32><<<T + 1, kArgThreads, 0, st>>>((const float*)root_logit, (const float*)node_logits,
                                                                 ld, V, scratch);
       break;
     case PE_DTYPE_BF16:
-      accept_argmax_kernel<PE_DTYPE_BF16><<<T + 1, 256, 0, st>>>((const uint16_t*)root_logit,
+      accept_argmax_kernel<PE_DTYPE_BF16><<<T + 1, kArgThreads, 0, st>>>((const uint16_t*)root_logit,
                                                                  (const uint16_t*)node_logits, ld, V, scratch);
       break;
     case PE_DTYPE_F16:
-      accept_argmax_kernel<PE_DTYPE_F16><<<T + 1, 256, 0, st>>>((const uint16_t*)root_logit,
+      accept_argmax_kernel<PE_DTYPE_F16><<<T + 1, kArgThreads, 0, st>>>((const uint16_t*)root_logit,
                                                                 (const uint16_t*)node_logits, ld, V, scratch);
       break;
     default:

@@ -66,6 +66,9 @@ class DeviceModel:
         if self.nf4 and self.dtype != torch.bfloat16:
             raise ValueError("NF4 linears compute in bfloat16")
         self.ipad = padded_intermediate(shape)
+        # 16-bit models with 128-dim heads run the fused pass, whose q/k/v GEMM
+        # applies RoPE in its epilogue: rows of w_qkv in RoPE-paired tile order.
+        self.qkv_paired = self.dtype != torch.float32 and shape.head_dim == 128
         self.layers: list[dict] = []
         self.logical: list[dict] | None = None  # per-layer host-exportable logical weights
         self.embed = None
@@ -142,12 +145,28 @@ class DeviceModel:
         self.lm_head_logical = lm
         self.lm_head = ops.dense_repack(lm) if self.dtype != torch.float32 else lm.contiguous()
 
+    def _qkv_row_order(self, device) -> torch.Tensor | None:
+        """Row gather for PE_QKV_ROPE_PAIRED: within each head, 32-row tiles in the
+        order [0,32) [hd/2, hd/2+32) [32,64) [hd/2+32, hd/2+64) ...; None if plain."""
+        if not self.qkv_paired:
+            return None
+        s = self.shape
+        hd, units = s.head_dim, s.num_heads + 2 * s.num_kv_heads
+        within = torch.cat([torch.cat([torch.arange(32 * j, 32 * j + 32),
+                                       torch.arange(hd // 2 + 32 * j, hd // 2 + 32 * j + 32)])
+                            for j in range(hd // 64)])
+        order = (torch.arange(units)[:, None] * hd + within[None, :]).reshape(-1)
+        return order.to(device)
+
     def _add_layer(self, lin: dict, keep_logical: bool):
         s = self.shape
         out = {"attn_norm": lin["attn_norm"], "mlp_norm": lin["mlp_norm"]}
         if self.nf4:
             qkv_p = torch.cat([lin["q"][0], lin["k"][0], lin["v"][0]], 0).contiguous()
             qkv_a = torch.cat([lin["q"][1], lin["k"][1], lin["v"][1]], 0).contiguous()
+            order = self._qkv_row_order(qkv_p.device)
+            if order is not None:
+                qkv_p, qkv_a = qkv_p[order].contiguous(), qkv_a[order].contiguous()
             out["w_qkv"], out["a_qkv"] = ops.nf4_repack(qkv_p, qkv_a)
             out["w_o"], out["a_o"] = ops.nf4_repack(lin["o"][0], lin["o"][1])
             gp, ga = self._interleave_nf4(lin["gate"], lin["up"])
@@ -156,6 +175,9 @@ class DeviceModel:
             out["w_down"], out["a_down"] = ops.nf4_repack(dp, da)
         else:
             qkv = torch.cat([lin["q"], lin["k"], lin["v"]], 0).contiguous()
+            order = self._qkv_row_order(qkv.device)
+            if order is not None:
+                qkv = qkv[order].contiguous()
             out["w_qkv"] = self._tile(qkv)
             out["w_o"] = self._tile(lin["o"])
             out["w_gu"] = self._tile(self._interleave_dense(lin["gate"], lin["up"]))
@@ -232,6 +254,7 @@ class DeviceModel:
         d.head_dim, d.intermediate, d.vocab, d.intermediate_padded = s.head_dim, s.intermediate, s.vocab, self.ipad
         d.dtype = ops.dcode(self.dtype)
         d.weight_format = _lib.PE_WFMT_NF4 if self.nf4 else _lib.PE_WFMT_DENSE
+        d.qkv_layout = _lib.PE_QKV_ROPE_PAIRED if self.qkv_paired else _lib.PE_QKV_PLAIN
         d.rms_eps = s.rms_eps
         d.max_positions = s.max_positions
         d.embed, d.final_norm = self.embed.data_ptr(), self.final_norm.data_ptr()

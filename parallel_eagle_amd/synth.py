@@ -69,6 +69,7 @@ STREAM_LM_HEAD = 2
 STREAM_PROMPT = 3
 STREAM_DRAFT = 4
 STREAM_KV = 5
+STREAM_KV_V = 6
 STREAM_LAYER0 = 1000  # layer l, tensor j -> 1000 + 16 * l + j
 LINEAR_ORDER = ("q", "k", "v", "o", "gate", "up", "down", "q_bias", "k_bias", "v_bias")
 

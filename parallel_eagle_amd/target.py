@@ -245,6 +245,10 @@ class TargetModel:
                 raise
         return logits.view(1, m, -1), fused.view(1, m, -1), cache
 
+    def verify_step(self, cache: TreeKVCache, tree_nodes: int) -> "VerifyStep":
+        """A device-resident verification step over ``cache`` at its current length."""
+        return VerifyStep(self, cache, tree_nodes)
+
     @torch.no_grad()
     def forward(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None,
                 position_ids: torch.Tensor | None = None) -> TargetOutput:
@@ -275,3 +279,111 @@ class TargetModel:
             parts_l.append(lg)
             parts_f.append(fu)
         return TargetOutput(torch.cat(parts_l, 1), torch.cat(parts_f, 1))
+
+
+class VerifyStep:
+    """One tree-verification step with every buffer preallocated, so it can be
+    enqueued without a host synchronisation and captured in a HIP graph.
+
+    It performs, on the device and in order, what one iteration of the
+    reference's cached tree loop does between proposing the tree and emitting
+    tokens (src/pe/serve.py:292-314):
+
+    1. ``pe_tree_masks``: ancestor bitmasks and positions P + depth from the
+       parent list (masks.py:118-156 without the dense (P+T)^2 matrix),
+    2. ``pe_forward``: the masked verification forward over the cache with the
+       in-place K/V append (target.py:203-224),
+    3. ``pe_accept_tree``: the greedy walk against the root logit
+       (decode/verify.py:104-125),
+    4. ``pe_kv_compact``: the accepted rows move to P, P+1, ... in place
+       (target.py:194-201 with the keep index of serve.py:308-309).
+
+    Inputs live in static device buffers (``load_tree`` fills them); ``result``
+    reads back (path, bonus) and ``commit`` sets the cache length. The prefix
+    length P is fixed at construction: a step replayed at the same P rewrites
+    rows [P, P + T) and leaves [0, P) untouched.
+    """
+
+    def __init__(self, target: TargetModel, cache: TreeKVCache, tree_nodes: int):
+        self.tm, self.cache, self.T = target, cache, int(tree_nodes)
+        dev, s = target.device, target.shape
+        self.P = cache.seq_len
+        cache.ensure_capacity(self.P + self.T)
+        self.words = max(1, math.ceil(self.T / 64))
+        if self.words > _lib.PE_TREE_MAX_WORDS:
+            raise ValueError(f"tree of {self.T} nodes exceeds {64 * _lib.PE_TREE_MAX_WORDS}")
+        self.ids = torch.zeros(self.T, dtype=torch.int64, device=dev)
+        self.parents = torch.full((self.T,), -1, dtype=torch.int32, device=dev)
+        self.bits = torch.zeros((self.T, self.words), dtype=torch.int64, device=dev)
+        self.pos = torch.zeros(self.T, dtype=torch.int64, device=dev)
+        self.depth = torch.zeros(self.T, dtype=torch.int32, device=dev)
+        self.root_logit = torch.zeros(s.vocab, dtype=target.dtype, device=dev)
+        self.logits = torch.empty((self.T, s.vocab), dtype=target.dtype, device=dev)
+        self.fused = torch.empty((self.T, target.feature_dim), dtype=target.dtype, device=dev)
+        self.accept_out = torch.zeros(2 + self.T, dtype=torch.int32, device=dev)
+        self.accept_scratch = torch.zeros(self.T + 1, dtype=torch.int32, device=dev)
+        self.ws = torch.zeros(target.model.workspace_bytes(self.T, self.P + self.T), dtype=torch.uint8,
+                              device=dev)
+        self.graph = None
+        a = _lib.PassArgs()
+        a.input_ids, a.positions, a.M, a.mask_mode, a.prefix_len = (self.ids.data_ptr(), self.pos.data_ptr(),
+                                                                     self.T, _lib.PE_MASK_TREE, self.P)
+        a.tree_bits, a.bits_words = self.bits.data_ptr(), self.words
+        fl = target.feature_layers
+        a.num_features = len(fl)
+        for i, f in enumerate(fl[:4]):
+            a.feature_layers[i] = f
+        a.k_cache, a.v_cache, a.cache_capacity = cache.k.data_ptr(), cache.v.data_ptr(), cache.capacity
+        a.logits, a.fused = self.logits.data_ptr(), self.fused.data_ptr()
+        a.workspace, a.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
+        a.status = target.status.data_ptr()
+        self._args = a
+
+    def load_tree(self, node_tokens, parents, root_logit: torch.Tensor) -> None:
+        """Copy a tree and the root logit into the static buffers (stream-ordered)."""
+        if len(node_tokens) != self.T or len(parents) != self.T:
+            raise ValueError(f"tree must have {self.T} nodes")
+        self.ids.copy_(torch.as_tensor(list(node_tokens), dtype=torch.int64))
+        self.parents.copy_(torch.as_tensor(list(parents), dtype=torch.int32))
+        self.root_logit.copy_(root_logit.reshape(-1))
+
+    def launch(self) -> None:
+        """Enqueue masks -> forward -> acceptance -> compaction on the current stream."""
+        L, st = _lib.load(), ops.stream_ptr()
+        c, s = self.cache, self.tm.shape
+        _lib.check(L.pe_tree_masks(self.parents.data_ptr(), self.T, self.P, self.bits.data_ptr(), self.words,
+                                   self.pos.data_ptr(), self.depth.data_ptr(), self.tm.status.data_ptr(), st),
+                   "pe_tree_masks")
+        _lib.check(L.pe_forward(C.byref(self.tm.model.desc()), C.byref(self._args), st), "pe_forward")
+        _lib.check(L.pe_accept_tree(self.root_logit.data_ptr(), self.logits.data_ptr(), s.vocab, self.T, s.vocab,
+                                    ops.dcode(self.tm.dtype), self.ids.data_ptr(), self.parents.data_ptr(),
+                                    self.accept_out.data_ptr(), self.accept_scratch.data_ptr(), st),
+                   "pe_accept_tree")
+        _lib.check(L.pe_kv_compact(c.k.data_ptr(), c.v.data_ptr(), s.num_layers, s.num_kv_heads, c.capacity,
+                                   s.head_dim, ops.dcode(self.tm.dtype), self.P, self.accept_out.data_ptr(), st),
+                   "pe_kv_compact")
+
+    def capture(self) -> None:
+        """Record ``launch`` into a HIP graph (run it eagerly once first)."""
+        self.launch()
+        torch.cuda.synchronize(self.tm.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.launch()
+        self.graph = g
+
+    def run(self) -> None:
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.launch()
+
+    def result(self) -> tuple[list[int], int]:
+        """(accepted node indices, bonus token); synchronises with the stream."""
+        out = self.accept_out.cpu().tolist()
+        ops.read_status(self.tm.status, "verify step")
+        n = out[0]
+        return out[2: 2 + n], out[1]
+
+    def commit(self, path_len: int) -> None:
+        self.cache.seq_len = self.P + path_len

@@ -231,3 +231,57 @@ def test_qwen14b_width_one_layer(shape):
     wl = WORKLOADS["qwen2.5-14b-fp16-T26-P4096"]
     v, n, err = _run_case(shape, 1, 40, wl.depth, wl.widths, wl.top_k, plant=lambda s: 2, tol=2e-2)
     print(f"{shape.name}: {v}, accepted {n}, max |dlogit| {err:.3g}")
+
+
+@pytest.mark.parametrize("shape,P", [(WORKLOADS["tiny-fp32-T8-P64"].model, 64),
+                                     (LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2)), 300)],
+                         ids=["tiny-fp32", "llama7b-nf4-2layers"])
+def test_verify_step_graph_replays_match_eager_api(shape, P):
+    """The device-resident step (masks -> forward -> acceptance -> compaction),
+    eager and replayed from a HIP graph, equals forward_cached + accept_tree_cached
+    + gather_cache on the same inputs, bit for bit, on every replay with eager
+    work in between."""
+    wl = WORKLOADS["llama2-7b-nf4-T26-P2048"] if shape.weight_format == "nf4" else WORKLOADS["tiny-fp32-T8-P64"]
+    tm = TargetModel.synthetic(shape, seed=3, device=DEV, cache_capacity=P + 64)
+    V = shape.vocab
+    prompt = synth.uniform_int(3, synth.STREAM_PROMPT, P, V).tolist()
+    cache = tm.make_cache()
+    pl, _, cache = tm.forward_cached(torch.tensor([prompt]), cache, torch.arange(P).unsqueeze(0))
+    root = pl[0, -1].clone()
+    tokens, parents = synth.tree_for_seed(3, V, wl.depth, wl.widths, wl.top_k)
+    # plant the device's greedy chain two deep so the walk and the compaction move rows
+    chain = synth.chain_nodes(parents, synth.deepest_first_leaf(parents))[:2]
+    pos = [P + d for d in om.tree_depths(parents)]
+    row = root
+    for node in chain:
+        synth.set_token(tokens, parents, node, int(row.float().argmax()), V)
+        lg, _, cache = tm.forward_cached(torch.tensor([tokens]), cache, torch.tensor([pos]), parents=parents)
+        cache.crop(P)
+        row = lg[0, node]
+    k0 = cache.k.clone()
+    v0 = cache.v.clone()
+    # eager reference through the reference-shaped API
+    lg_e, fu_e, cache = tm.forward_cached(torch.tensor([tokens]), cache, torch.tensor([pos]), parents=parents)
+    path_e, bonus_e = accept_tree_cached(root, lg_e[0], tokens, parents)
+    tm.gather_cache(cache, torch.tensor(list(range(P)) + [P + t for t in path_e], device=DEV))
+    k_e = cache.k[:, :, : cache.seq_len].clone()
+    v_e = cache.v[:, :, : cache.seq_len].clone()
+    assert len(path_e) >= 2
+    # device-resident step over the same starting cache
+    cache.k.copy_(k0)
+    cache.v.copy_(v0)
+    cache.seq_len = P
+    step = tm.verify_step(cache, len(tokens))
+    step.load_tree(tokens, parents, root)
+    step.capture()
+    for rep in range(3):
+        step.run()
+        got = step.result()
+        assert got == (path_e, bonus_e), f"replay {rep}: {got} vs {(path_e, bonus_e)}"
+        assert torch.equal(step.logits, lg_e[0]) and torch.equal(step.fused, fu_e[0])
+        n = P + len(path_e)
+        assert torch.equal(cache.k[:, :, :n], k_e) and torch.equal(cache.v[:, :, :n], v_e)
+        # eager work between replays: scribble over the node rows and the outputs
+        cache.k[:, :, P:P + len(tokens)].normal_()
+        step.logits.zero_()
+        torch.cuda.synchronize()

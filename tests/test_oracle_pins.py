@@ -177,6 +177,21 @@ def test_nf4_dequant_extremes_and_idempotence():
     assert np.array_equal(onf4.unpack(p2), codes)
 
 
+def test_nf4_dequant_torch_is_bit_identical_to_numpy():
+    """The threaded torch dequant (used for the timed CPU path) equals the
+    numpy definition on every code and a spread of absmax values, including
+    subnormal-range fp16 scales and values that round at the bf16 tie."""
+    rng = np.random.default_rng(7)
+    p = rng.integers(0, 256, size=(48, 512), dtype=np.uint8)
+    a = rng.uniform(0, 0.1, size=(48, 16)).astype(np.float16)
+    a[0, 0] = np.float16(6e-8)
+    a[1, :] = np.float16(1.0)
+    a[2, 3] = np.float16(0.0)
+    ref = onf4.dequantize(p, a)
+    got = onf4.dequantize_torch(p, a).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
 def test_nf4_quantize_nearest_code_brute_force():
     rng = np.random.default_rng(3)
     w = rng.normal(0, 0.02, size=(2, 128)).astype(np.float32)
