@@ -23,6 +23,7 @@
 // fp32 path: one block per (row, query head), scores in LDS, VALU arithmetic.
 
 #include "pe_common.h"
+#include "pe_internal.h"
 
 namespace {
 
@@ -268,7 +269,8 @@ template <int DT>
 __global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ opart,
                                                            const float* __restrict__ mlpart, int nh, int nkv, int T,
                                                            int hd, int splits, int rows_pad,
-                                                           typename Elem<DT>::T* __restrict__ out, int64_t ld_out) {
+                                                           typename Elem<DT>::T* __restrict__ out, int64_t ld_out,
+                                                           int out_units) {
   const int r = blockIdx.x, kvh = blockIdx.y;
   const int G = nh / nkv;
   const int t = r / G, hq = kvh * G + r % G;
@@ -282,7 +284,8 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restri
       den += w * mlpart[pidx * 2 + 1];
       num += w * opart[pidx * hd + d];
     }
-    Elem<DT>::store(out, (int64_t)t * ld_out + (int64_t)hq * hd + d, num / den);
+    const int col = hq * hd + d;
+    Elem<DT>::store(out, out_units ? xtile_index(t, col, out_units) : (int64_t)t * ld_out + col, num / den);
   }
 }
 
@@ -375,11 +378,12 @@ extern "C" int64_t pe_attention_workspace_bytes(int T, int nh, int nkv, int hd, 
   return (int64_t)T * nh * kv_len * 4;
 }
 
-extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap, int nh,
-                                 int nkv, int hd, int T, int64_t P, int mask_mode, const uint64_t* bits, int words,
-                                 float scale, int dtype, void* out, int64_t ld_out, void* workspace,
-                                 int64_t workspace_bytes, void* stream) {
+int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap, int nh,
+                               int nkv, int hd, int T, int64_t P, int mask_mode, const uint64_t* bits, int words,
+                               float scale, int dtype, void* out, int64_t ld_out, int out_units, void* workspace,
+                               int64_t workspace_bytes, hipStream_t st) {
   if (!q || !k_cache || !v_cache || !out || !workspace) return PE_ERR_ARG;
+  if (out_units && (dtype == PE_DTYPE_F32 || hd != 128 || T > 64 || out_units * 128 != nh * hd)) return PE_ERR_ARG;
   if (T <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || hd <= 0 || hd > 256 || P < 0) return PE_ERR_ARG;
   if (P + T > cache_cap) return PE_ERR_CAPACITY;
   if (mask_mode != PE_MASK_TREE && mask_mode != PE_MASK_CAUSAL) return PE_ERR_ARG;
@@ -387,7 +391,6 @@ extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void*
     return PE_ERR_TREE;
   const int64_t S = P + T;
   if (workspace_bytes < pe_attention_workspace_bytes(T, nh, nkv, hd, S, dtype)) return PE_ERR_WORKSPACE;
-  hipStream_t st = (hipStream_t)stream;
   if (dtype != PE_DTYPE_F32 && hd == 128) {
     AttnPlan p = attn_plan(T, nh, nkv, S);
     float* opart = (float*)workspace;
@@ -401,7 +404,7 @@ extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void*
                                                            p.splits, p.rows_pad, opart, ml);
       PE_CHECK_LAUNCH();
       attn_combine_kernel<PE_DTYPE_BF16><<<cgrid, 128, 0, st>>>(opart, ml, nh, nkv, T, hd, p.splits, p.rows_pad,
-                                                                (uint16_t*)out, ld_out);
+                                                                (uint16_t*)out, ld_out, out_units);
     } else if (dtype == PE_DTYPE_F16) {
       attn_wg_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
                                                           (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
@@ -409,7 +412,7 @@ extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void*
                                                           p.rows_pad, opart, ml);
       PE_CHECK_LAUNCH();
       attn_combine_kernel<PE_DTYPE_F16><<<cgrid, 128, 0, st>>>(opart, ml, nh, nkv, T, hd, p.splits, p.rows_pad,
-                                                               (uint16_t*)out, ld_out);
+                                                               (uint16_t*)out, ld_out, out_units);
     } else {
       return PE_ERR_ARG;
     }
@@ -442,4 +445,12 @@ extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void*
   }
   PE_CHECK_LAUNCH();
   return PE_OK;
+}
+
+extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap, int nh,
+                                 int nkv, int hd, int T, int64_t P, int mask_mode, const uint64_t* bits, int words,
+                                 float scale, int dtype, void* out, int64_t ld_out, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  return pe_internal_tree_attention(q, k_cache, v_cache, cache_cap, nh, nkv, hd, T, P, mask_mode, bits, words, scale,
+                                    dtype, out, ld_out, 0, workspace, workspace_bytes, (hipStream_t)stream);
 }

@@ -73,6 +73,21 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// A-tiled activations: the order in which the NF4 GEMM reads X as its MFMA A
+// operand, so that every X load instruction of a wave reads 1 KiB contiguous.
+// Element (row, col) of an [M][K] activation (K % 128 == 0, `units` = K / 128)
+// sits in 128-column unit p = col / 128, k-step s = (col % 64) / 8 and lane
+// row % 32 + 32 * ((col % 128) / 64) of M tile row / 32; a lane holds 8
+// consecutive columns. Rows past M inside the last M tile are never written:
+// they only feed MFMA rows whose results are discarded.
+__host__ __device__ __forceinline__ int64_t xtile_index(int row, int col, int units) {
+  const int mt = row >> 5, ln = row & 31;
+  const int p = col >> 7, c = col & 127;
+  return ((((int64_t)mt * units + p) * 8 + ((c & 63) >> 3)) * 64 + ln + 32 * (c >> 6)) * 8 + (c & 7);
+}
+// Bytes of an A-tiled [M][K] 16-bit activation.
+__host__ __device__ __forceinline__ int64_t xtile_bytes(int M, int K) { return (int64_t)((M + 31) / 32) * K * 64; }
+
 #define PE_CHECK_LAUNCH()                                   \
   do {                                                      \
     hipError_t _e = hipGetLastError();                      \

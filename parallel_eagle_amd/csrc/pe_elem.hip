@@ -115,8 +115,8 @@ template <int DT>
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
     const float* __restrict__ partial, int S, int M, typename Elem<DT>::T* __restrict__ h, int H,
     const typename Elem<DT>::T* __restrict__ w, float eps, typename Elem<DT>::T* __restrict__ xn,
-    typename Elem<DT>::T* __restrict__ cap_h, int64_t ld_cap_h, typename Elem<DT>::T* __restrict__ cap_xn,
-    int64_t ld_cap_xn) {
+    typename Elem<DT>::T* __restrict__ xt, typename Elem<DT>::T* __restrict__ cap_h, int64_t ld_cap_h,
+    typename Elem<DT>::T* __restrict__ cap_xn, int64_t ld_cap_xn) {
   typedef Elem<DT> E;
   typedef typename E::T T;
   const int m = blockIdx.x;
@@ -175,6 +175,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
       const float y = E::round(__fmul_rn(v[k][e], inv));
       const float o = __fmul_rn(E::load(w, 4 * c + e), y);
       E::store(orow, 4 * c + e, o);
+      if (xt) E::store(xt, xtile_index(m, 4 * c + e, H >> 7), o);
       if (cap_xn) E::store(cap_xn + (int64_t)m * ld_cap_xn, 4 * c + e, o);
     }
   }
@@ -256,14 +257,15 @@ extern "C" int pe_copy_rows(const void* src, int64_t ld_src, int M, int64_t row_
 }
 
 int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, int H, const void* w, float eps,
-                                 int dtype, void* xn, void* cap_h, int64_t ld_cap_h, void* cap_xn, int64_t ld_cap_xn,
-                                 hipStream_t st) {
+                                 int dtype, void* xn, void* xn_tiled, void* cap_h, int64_t ld_cap_h, void* cap_xn,
+                                 int64_t ld_cap_xn, hipStream_t st) {
   if (!h || !w || !xn || M <= 0 || H <= 0 || S < 0 || (S > 0 && !partial)) return PE_ERR_ARG;
   if (H % 4 || H > 4 * kNormThreads * kNormChunks || S > kNormMaxSplits) return PE_ERR_ARG;
+  if (xn_tiled && (H % 128 || M > 64 || dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
   PE_DISPATCH_DT(dtype, {
     typedef typename Elem<DT>::T T;
     residual_rmsnorm_kernel<DT><<<M, kNormThreads, 0, st>>>(partial, S, M, (T*)h, H, (const T*)w, eps, (T*)xn,
-                                                            (T*)cap_h, ld_cap_h, (T*)cap_xn, ld_cap_xn);
+                                                            (T*)xn_tiled, (T*)cap_h, ld_cap_h, (T*)cap_xn, ld_cap_xn);
   });
   PE_CHECK_LAUNCH();
   return PE_OK;

@@ -8,17 +8,20 @@
 //   * use v_mfma_f32_32x32x16_{bf16,f16} with X as the A operand (32 rows per
 //     M tile) and the weights as the B operand (32 columns per tile); a wave
 //     owns NT = 2 column tiles, so every X fragment feeds two MFMAs;
-//   * prefetch the next iteration's weights and X fragments into registers
-//     before computing the current one;
-//   * split K across the waves of a workgroup (reduced in LDS, fixed order)
-//     and, when there are too few column tiles to fill 256 CUs, across S
-//     workgroups. Split-K workgroups never synchronise with each other (a
-//     device-scope fence costs more than a kernel boundary on a multi-XCD
-//     part): each writes an fp32 partial [split][M][N], and the consumer sums
-//     the S partials in split order. The consumer is either the reduction
-//     kernel here (pe_nf4_gemm / pe_dense_gemm) or, inside pe_forward, the next
-//     kernel of the layer (attention prologue, residual + RMSNorm). Results are
-//     deterministic and independent of M.
+//   * keep the next iteration's weights in flight in a second register set
+//     while computing the current one, and fetch each X fragment of the next
+//     iteration right after the MFMA that used the current one; the loop body
+//     is straight-line (loads past the wave's range are clamped and their
+//     contribution zeroed) so the compiler's wait counts never fall back to
+//     waiting for the prefetch;
+//   * split K across the 4 waves of a workgroup (summed in LDS in wave order)
+//     and across S workgroups, with S chosen so that every launch has about
+//     three 4-wave workgroups per CU. The S workgroups of a column group write
+//     fp32 partials with agent-coherent stores, count themselves on a
+//     per-group counter, and the last one to arrive sums the partials in split
+//     order and applies the epilogue. Nobody waits for anybody: no spin loop,
+//     no grid barrier, no device-scope cache write-back. Results are
+//     deterministic (split order, then wave order) whatever the arrival order.
 //
 // NF4 dequantisation (bitsandbytes' dequantize_4bit, src/pe/target.py:55-62):
 // in the tiled layout each lane owns one 64-element absmax block of one column
@@ -44,10 +47,7 @@
 
 namespace {
 
-constexpr int64_t kGemmWsAlign = 256;
-// Internal epilogues: write the fp32 accumulators to partial[split] even when
-// S == 1; and the q/k/v projection with bias, RoPE and the in-place KV append.
-constexpr int kEpiPartial = 3;
+// Internal epilogue: the q/k/v projection with bias, RoPE and the in-place KV append.
 constexpr int kEpiRopeKV = 4;
 
 struct EpiArgs {
@@ -59,6 +59,7 @@ struct EpiArgs {
   int64_t ld_resid;
   void* out;
   int64_t ld_out;
+  int out_units;  // > 0: out is A-tiled with K = 128 * out_units (SwiGLU / store epilogues)
   // kEpiRopeKV: the q/k/v projection whose weight rows are in head-paired tile
   // order (see write_rope_kv); RoPE at positions[row], q to q_out [M][nh][hd],
   // k and v appended to the caches at rows row0 + row.
@@ -86,7 +87,7 @@ __device__ __forceinline__ void epi_value(const EpiArgs& e, int row, int col, fl
     E::store(out, (int64_t)row * e.ld_out + col, __fadd_rn(E::load(r, (int64_t)row * e.ld_resid + col), h));
   } else {
     if (e.bias) v = __fadd_rn(v, E::load((const typename E::T*)e.bias, col));
-    E::store(out, (int64_t)row * e.ld_out + col, v);
+    E::store(out, e.out_units ? xtile_index(row, col, e.out_units) : (int64_t)row * e.ld_out + col, v);
   }
 }
 
@@ -95,7 +96,8 @@ __device__ __forceinline__ void epi_swiglu(const EpiArgs& e, int row, int col, f
   typedef Elem<DT> E;
   float gr = E::round(gv), ur = E::round(uv);
   float s = E::round(silu_f(gr));
-  E::store((typename E::T*)e.out, (int64_t)row * e.ld_out + col, __fmul_rn(s, ur));
+  E::store((typename E::T*)e.out, e.out_units ? xtile_index(row, col, e.out_units) : (int64_t)row * e.ld_out + col,
+           __fmul_rn(s, ur));
 }
 
 template <int FMT>
@@ -151,75 +153,16 @@ __device__ __forceinline__ void write_rope_kv(const EpiArgs& e, int group, int r
   E::store(dst, d2, o2);
 }
 
-// Output of a GEMM workgroup, after its waves' K slices are summed.
-//   S == 1: the epilogue writes the final values.
-//   S > 1: rows < M of the tile go to partial[split][M][N] (fp32).
-template <int ADT, int NT, int MT>
-__device__ __forceinline__ void write_tile(f32x16_t (&acc)[NT][MT], int group, int split, int S,
-                                           float* __restrict__ partial, const EpiArgs& e) {
-  const int lane = threadIdx.x & 63;
-  const int g = lane >> 5, ln = lane & 31;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = mt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-      if (row >= e.M) continue;
-      if (S > 1 || e.op == kEpiPartial) {
-        float* prow = partial + ((int64_t)split * e.M + row) * e.N;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) prow[(group * NT + nt) * 32 + ln] = acc[nt][mt][r];
-      } else if (e.op == PE_EPI_SWIGLU) {
-        if constexpr (NT == 2) epi_swiglu<ADT>(e, row, group * 32 + ln, acc[0][mt][r], acc[1][mt][r]);
-      } else if (e.op == kEpiRopeKV) {
-        if constexpr (NT == 2) write_rope_kv<ADT>(e, group, row, acc[0][mt][r], acc[1][mt][r]);
-      } else {
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) epi_value<ADT>(e, row, (group * NT + nt) * 32 + ln, acc[nt][mt][r]);
-      }
-    }
-  }
-}
-
-// Sum the waves' K slices in LDS in wave order, then wave 0 writes the tile.
-// `red` needs (WAVES - 1) * 16 * 64 floats; the caller has synchronised the
-// workgroup if that memory had another use.
-template <int ADT, int NT, int MT, int WAVES>
-__device__ __forceinline__ void reduce_waves_and_write(f32x16_t (&acc)[NT][MT], float* red, int group, int split,
-                                                       int S, float* __restrict__ partial, const EpiArgs& e) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if (wave > 0) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) red[((wave - 1) * 16 + r) * 64 + lane] = acc[nt][mt][r];
-      }
-      __syncthreads();
-      if (wave == 0) {
-#pragma unroll
-        for (int w = 0; w < WAVES - 1; ++w)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[nt][mt][r] += red[(w * 16 + r) * 64 + lane];
-      }
-      __syncthreads();
-    }
-  }
-  if (wave == 0) write_tile<ADT, NT, MT>(acc, group, split, S, partial, e);
-}
 
 // ---------------------------------------------------------------------------
-// NF4 lookup primitive (gfx950 assembly)
+// NF4 lookup primitives
 // ---------------------------------------------------------------------------
-// One MFMA k-step of NT tiles: the 8 codes of q[nt] become 8 bf16 table
-// entries, packed in pairs into the MFMA operand. Address updates, loads and
-// the wait are one asm block, so the compiler never touches a register whose
-// load is still in flight; every load is issued at least 8 instructions after
-// the SDWA that wrote its address. The loads are plain zero-extending
-// ds_read_u16: with SRAM ECC enabled (the MI355X default) d16 loads clear the
-// other half of the register instead of preserving it, so the two halves are
-// joined with one v_lshl_or after the wait.
+// Addresses (gfx950 assembly): the 8 codes of dword q go to bits 8..11 of 8
+// address registers whose low byte holds the lane's table base (lane * 4).
+// The table reads themselves are ordinary LDS loads the compiler schedules
+// and counts: plain zero-extending ds_read_u16 (with SRAM ECC enabled, the
+// MI355X default, d16 loads clear the other half of the register instead of
+// preserving it), joined in pairs with one v_lshl_or.
 #define PE_SDWA_LO(a, q, byte) \
   "v_and_b32_sdwa " a ", 15, " q " dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:BYTE_" byte "\n\t"
 #define PE_SDWA_HI(a, q, byte) \
@@ -229,83 +172,216 @@ __device__ __forceinline__ void reduce_waves_and_write(f32x16_t (&acc)[NT][MT], 
   PE_SDWA_LO("%[" A "2]", "%[" Q "]", "1") PE_SDWA_HI("%[" A "3]", "%[" Q "]", "1")                     \
   PE_SDWA_LO("%[" A "4]", "%[" Q "]", "2") PE_SDWA_HI("%[" A "5]", "%[" Q "]", "2")                     \
   PE_SDWA_LO("%[" A "6]", "%[" Q "]", "3") PE_SDWA_HI("%[" A "7]", "%[" Q "]", "3")
-#define PE_READ1(D, A, O) "ds_read_u16 %[" D "], %[" A "] offset:%[" O "]\n\t"
-#define PE_READ8(D, A, O)                                                                                    \
-  PE_READ1(D "0", A "0", O) PE_READ1(D "1", A "1", O) PE_READ1(D "2", A "2", O) PE_READ1(D "3", A "3", O)     \
-  PE_READ1(D "4", A "4", O) PE_READ1(D "5", A "5", O) PE_READ1(D "6", A "6", O) PE_READ1(D "7", A "7", O)
 
-__device__ __forceinline__ uint32_t pack16(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
-
-template <int NT, int OFF0, int OFF1>
-__device__ __forceinline__ void nf4_lookup_step(const uint32_t (&q)[NT], uint32_t (&a)[NT][8], u32x4_t (&bv)[NT]) {
-  uint32_t x[8];
-  if constexpr (NT == 2) {
-    uint32_t y[8];
-    asm volatile(PE_ADDR8("a", "q0") PE_ADDR8("c", "q1") PE_READ8("x", "a", "o0") PE_READ8("y", "c", "o1")
-                 "s_waitcnt lgkmcnt(0)"
-                 : [x0] "=&v"(x[0]), [x1] "=&v"(x[1]), [x2] "=&v"(x[2]), [x3] "=&v"(x[3]), [x4] "=&v"(x[4]),
-                   [x5] "=&v"(x[5]), [x6] "=&v"(x[6]), [x7] "=&v"(x[7]), [y0] "=&v"(y[0]), [y1] "=&v"(y[1]),
-                   [y2] "=&v"(y[2]), [y3] "=&v"(y[3]), [y4] "=&v"(y[4]), [y5] "=&v"(y[5]), [y6] "=&v"(y[6]),
-                   [y7] "=&v"(y[7]), [a0] "+v"(a[0][0]), [a1] "+v"(a[0][1]), [a2] "+v"(a[0][2]),
-                   [a3] "+v"(a[0][3]), [a4] "+v"(a[0][4]), [a5] "+v"(a[0][5]), [a6] "+v"(a[0][6]),
-                   [a7] "+v"(a[0][7]), [c0] "+v"(a[1][0]), [c1] "+v"(a[1][1]), [c2] "+v"(a[1][2]),
-                   [c3] "+v"(a[1][3]), [c4] "+v"(a[1][4]), [c5] "+v"(a[1][5]), [c6] "+v"(a[1][6]),
-                   [c7] "+v"(a[1][7])
-                 : [q0] "v"(q[0]), [q1] "v"(q[1]), [o0] "i"(OFF0), [o1] "i"(OFF1)
-                 : "memory");
-    bv[1] = u32x4_t{pack16(y[0], y[1]), pack16(y[2], y[3]), pack16(y[4], y[5]), pack16(y[6], y[7])};
-  } else {
-    asm volatile(PE_ADDR8("a", "q0") PE_READ8("x", "a", "o0") "s_waitcnt lgkmcnt(0)"
-                 : [x0] "=&v"(x[0]), [x1] "=&v"(x[1]), [x2] "=&v"(x[2]), [x3] "=&v"(x[3]), [x4] "=&v"(x[4]),
-                   [x5] "=&v"(x[5]), [x6] "=&v"(x[6]), [x7] "=&v"(x[7]), [a0] "+v"(a[0][0]), [a1] "+v"(a[0][1]),
-                   [a2] "+v"(a[0][2]), [a3] "+v"(a[0][3]), [a4] "+v"(a[0][4]), [a5] "+v"(a[0][5]),
-                   [a6] "+v"(a[0][6]), [a7] "+v"(a[0][7])
-                 : [q0] "v"(q[0]), [o0] "i"(OFF0)
-                 : "memory");
-  }
-  bv[0] = u32x4_t{pack16(x[0], x[1]), pack16(x[2], x[3]), pack16(x[4], x[5]), pack16(x[6], x[7])};
+__device__ __forceinline__ void nf4_addr8(uint32_t q, uint32_t (&a)[8]) {
+  asm(PE_ADDR8("a", "q")
+      : [a0] "+v"(a[0]), [a1] "+v"(a[1]), [a2] "+v"(a[2]), [a3] "+v"(a[3]), [a4] "+v"(a[4]), [a5] "+v"(a[5]),
+        [a6] "+v"(a[6]), [a7] "+v"(a[7])
+      : [q] "v"(q));
 }
-#undef PE_READ8
-#undef PE_READ1
 #undef PE_ADDR8
 #undef PE_SDWA_HI
 #undef PE_SDWA_LO
 
+typedef __attribute__((address_space(3))) const uint16_t lds_u16_t;
+
+template <int OFF>
+__device__ __forceinline__ void nf4_read8(const uint32_t (&a)[8], uint32_t (&r)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = *(lds_u16_t*)(size_t)(a[i] + OFF);
+}
+
+__device__ __forceinline__ uint32_t pack16(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
-// The lane's 16 table entries bf16_rne(NF4[c] * scale), entry c at lane base + 256 c + OFF.
+// The lane's 16 table entries for two block pairs at once: entry c (at lane
+// base + 256 c + OFF) holds bf16_rne(NF4[c] * scale0) in its low half and
+// bf16_rne(NF4[c] * scale1) in its high half.
 template <int OFF>
-__device__ __forceinline__ void nf4_build_table(uint8_t* lanetab, uint16_t absmax) {
-  const float sc = f16_bits_to_f32(absmax);
+__device__ __forceinline__ void nf4_build_table2(uint8_t* lanetab, uint16_t absmax0, uint16_t absmax1) {
+  const float s0 = f16_bits_to_f32(absmax0), s1 = f16_bits_to_f32(absmax1);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const f32x2_t v = {kNF4[2 * i] * sc, kNF4[2 * i + 1] * sc};
-    const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-    *(uint16_t*)(lanetab + (2 * i) * 256 + OFF) = (uint16_t)w;
-    *(uint16_t*)(lanetab + (2 * i + 1) * 256 + OFF) = (uint16_t)(w >> 16);
+  for (int c = 0; c < 16; ++c) {
+    const f32x2_t v = {kNF4[c] * s0, kNF4[c] * s1};
+    *(uint32_t*)(lanetab + c * 256 + OFF) = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
   }
 }
 
 constexpr int kTabTile = 16 * 64 * 4;  // one tile's table: 16 codes x 64 lanes x dword (2 slots)
 
-template <int MT, int NT>
-struct NF4Regs {
-  u32x4_t q[NT][2];  // codes of the lane's block in each tile (dword s = MFMA k-step s)
-  u32x4_t x[MT][8];  // X fragments of the 8 MFMA k-steps
-  uint16_t a[NT];    // absmax of the lane's block in each tile
-};
 
-// One wave's share of a workgroup's block-pair range; WV = this wave's index
-// (compile time, so table offsets are immediates). Codes, absmax and X
-// fragments of the next block pair are loaded into a second register set
-// while the current pair is computed; tables alternate between the two
-// 16-bit slots of each entry.
-template <int MT, int NT, int WAVES, int WV>
+// ---------------------------------------------------------------------------
+// Workgroup output
+// ---------------------------------------------------------------------------
+constexpr int kWaves = 4;             // waves per GEMM workgroup (K slices)
+constexpr int kCounterBytes = 32768;  // per-column-group arrival counters at the head of the workspace
+constexpr int kMaxGroups = kCounterBytes / 4;
+constexpr int kMaxSplits = 16;
+
+// Epilogue of one output row of a column group: v[nt] is the lane's column of
+// tile nt (SwiGLU and RoPE pair tile 0 with tile 1 in the same lane).
+template <int ADT, int NT>
+__device__ __forceinline__ void epilogue_row(const EpiArgs& e, int group, int row, int ln, const float (&v)[NT]) {
+  if (e.op == PE_EPI_SWIGLU) {
+    if constexpr (NT == 2) epi_swiglu<ADT>(e, row, group * 32 + ln, v[0], v[1]);
+  } else if (e.op == kEpiRopeKV) {
+    if constexpr (NT == 2) write_rope_kv<ADT>(e, group, row, v[0], v[1]);
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) epi_value<ADT>(e, row, (group * NT + nt) * 32 + ln, v[nt]);
+  }
+}
+
+// Bytes of split-K partials of one launch: per split and column group, every
+// wave stores its row quad of each (M tile, column tile) as 64 lanes x 4 floats.
+__host__ __device__ constexpr int64_t partial_bytes_of(int S, int groups, int MT, int NT) {
+  return S > 1 ? (int64_t)S * groups * MT * NT * kWaves * 64 * 16 : 0;
+}
+
+// The waves' K slices summed in LDS (wave order); wave w then owns rows
+// 8 w + 4 g + j (j < 4) of every M tile. With S > 1 the workgroup publishes
+// its sums as split `split` of the group's partials and the last workgroup of
+// the group to arrive sums all S of them in split order. The caller has
+// synchronised the workgroup if `red` had another use.
+template <int ADT, int NT, int MT>
+__device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red, int group, int split, int S,
+                                            float* __restrict__ partial, int* __restrict__ counters,
+                                            const EpiArgs& e) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 5, ln = lane & 31;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[(((wave * NT + nt) * MT + mt) * 16 + r) * 64 + lane] = acc[nt][mt][r];
+  __syncthreads();
+  float v[MT][4][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) s += red[(((w * NT + nt) * MT + mt) * 16 + 4 * wave + j) * 64 + lane];
+        v[mt][j][nt] = s;
+      }
+
+  if (S > 1) {
+    const int groups = e.N / (32 * NT);
+    // partial[split][group][mt][nt][wave][lane][4]
+    auto slot = [&](int sp, int mt, int nt) -> uint64_t* {
+      return (uint64_t*)(partial + ((((((int64_t)sp * groups + group) * MT + mt) * NT + nt) * kWaves + wave) * 64 +
+                                    lane) * 4);
+    };
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        uint64_t* p = slot(split, mt, nt);
+        const uint64_t lo = __builtin_bit_cast(uint64_t, f32x2_t{v[mt][0][nt], v[mt][1][nt]});
+        const uint64_t hi = __builtin_bit_cast(uint64_t, f32x2_t{v[mt][2][nt], v[mt][3][nt]});
+        __hip_atomic_store(p, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    // the stores are acknowledged at agent scope before this workgroup counts itself
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int* flag = (int*)red;
+    if (threadIdx.x == 0)
+      flag[0] = __hip_atomic_fetch_add(counters + group, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (flag[0] != S - 1) return;
+    if (threadIdx.x == 0) __hip_atomic_store(counters + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float sum[MT][4][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) sum[mt][j][nt] = 0.f;
+    // up to 8 splits' loads in flight at a time, summed in split order
+    for (int c0 = 0; c0 < S; c0 += 8) {
+      uint64_t got[8][MT][NT][2];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int sp = c0 + c;
+        if (sp < S && sp != split) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+              uint64_t* p = slot(sp, mt, nt);
+              got[c][mt][nt][0] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              got[c][mt][nt][1] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int sp = c0 + c;
+        if (sp >= S) break;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            float q[4];
+            if (sp == split) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) q[j] = v[mt][j][nt];
+            } else {
+              const f32x2_t a = __builtin_bit_cast(f32x2_t, got[c][mt][nt][0]);
+              const f32x2_t b = __builtin_bit_cast(f32x2_t, got[c][mt][nt][1]);
+              q[0] = a[0]; q[1] = a[1]; q[2] = b[0]; q[3] = b[1];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sum[mt][j][nt] += q[j];
+          }
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) v[mt][j][nt] = sum[mt][j][nt];
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = mt * 32 + 8 * wave + 4 * g + j;
+      if (row < e.M) epilogue_row<ADT, NT>(e, group, row, ln, v[mt][j]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// NF4 GEMM
+// ---------------------------------------------------------------------------
+// One wave's block pairs [w0, w1) of column group `group`; WV = this wave's
+// index (compile time, so table offsets are immediates). The loop runs in
+// rounds of two block pairs p, p + 1:
+//   * one table build per round writes both pairs' entries (low / high halves
+//     of each dword), from absmax loaded a round ahead;
+//   * codes of pair p + 2 are in flight while pair p + 1 is computed;
+//   * X fragment s of the next pair is requested right after the MFMAs of
+//     step s of the current one;
+//   * the table reads of k-step s + 1 are issued before the MFMAs of step s
+//     wait for theirs.
+// A padded block pair (past w1) reloads the last one and gets a zero scale,
+// so its table and its contribution are zero.
+template <int MT, int NT, int WV, bool XT>
 __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* smem,
                                               const uint16_t* __restrict__ X, int64_t ldx,
                                               const uint8_t* __restrict__ W, const uint16_t* __restrict__ Wabs,
                                               int NP, int group, int w0, int w1, int M) {
+  const int n = w1 - w0;
+  if (n <= 0) return;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 5, ln = lane & 31;
   constexpr int TB = WV * NT * kTabTile;  // this wave's table area
@@ -319,61 +395,108 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
     for (int i = 0; i < 8; ++i) addr[nt][i] = (uint32_t)(lane * 4);
 
   // Rows at or beyond M read row M - 1: MFMA rows are independent and those
-  // output rows are never stored, so no masking is needed.
+  // output rows are never stored.
   const uint16_t* xrow[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (int64_t)min(mt * 32 + ln, M - 1) * ldx + 64 * g;
 
-  auto load = [&](NF4Regs<MT, NT>& R, int p) {
+  u32x4_t qa[NT][2], qb[NT][2];  // codes of the lane's block in each tile (dword s = MFMA k-step s)
+  uint16_t ac[2][NT], an[2][NT];  // absmax of the first round's / the next round's two block pairs
+  u32x4_t x[MT][8];               // X fragments of the 8 MFMA k-steps
+
+  auto tile_of = [&](int nt, int p) -> int64_t { return (int64_t)(group * NT + nt) * NP + min(p, w1 - 1); };
+  auto load_codes = [&](u32x4_t (&q)[NT][2], int p) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const int64_t ts = (int64_t)(group * NT + nt) * NP + p;
-      const uint8_t* wp = W + ts * 2048 + lane * 16;
-      R.q[nt][0] = *(const u32x4_t*)(wp);
-      R.q[nt][1] = *(const u32x4_t*)(wp + 1024);
-      R.a[nt] = Wabs[ts * 64 + lane];
+      const uint8_t* wp = W + tile_of(nt, p) * 2048 + lane * 16;
+      q[nt][0] = *(const u32x4_t*)(wp);
+      q[nt][1] = *(const u32x4_t*)(wp + 1024);
     }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int s = 0; s < 8; ++s) R.x[mt][s] = *(const u32x4_t*)(xrow[mt] + 128 * p + 8 * s);
   };
-  auto compute = [&](const NF4Regs<MT, NT>& R, auto slot_c) {
+  auto load_abs = [&](uint16_t (&a)[2][NT], int p) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) a[h][nt] = Wabs[tile_of(nt, p + h) * 64 + lane];
+  };
+  auto load_x = [&](int s, int p) {
+    const int pc = min(p, w1 - 1);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if constexpr (XT) x[mt][s] = *(const u32x4_t*)(X + ((((int64_t)mt * NP + pc) * 8 + s) * 64 + lane) * 8);
+      else x[mt][s] = *(const u32x4_t*)(xrow[mt] + 128 * pc + 8 * s);
+    }
+  };
+  auto pair = [&](const u32x4_t (&q)[NT][2], int p, auto slot_c) {
     constexpr int SL = decltype(slot_c)::value;
-    nf4_build_table<TB + SL>(lanetab, R.a[0]);
-    if constexpr (NT == 2) nf4_build_table<TB + kTabTile + SL>(lanetab, R.a[1]);
+    uint32_t r[2][NT][8];
+    auto lookup = [&](int s, uint32_t (&rr)[NT][8]) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) nf4_addr8(q[nt][s >> 2][s & 3], addr[nt]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        if (nt == 0) nf4_read8<TB + SL>(addr[0], rr[0]);
+        else nf4_read8<TB + kTabTile + SL>(addr[nt], rr[nt]);
+      }
+    };
+    lookup(0, r[0]);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      uint32_t qs[NT];
+      if (s < 7) lookup(s + 1, r[(s + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t (&cur)[NT][8] = r[s & 1];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) qs[nt] = R.q[nt][s >> 2][s & 3];
-      u32x4_t bv[NT];
-      nf4_lookup_step<NT, TB + SL, TB + kTabTile + SL>(qs, addr, bv);
+      for (int nt = 0; nt < NT; ++nt) {
+        const u32x4_t bv = {pack16(cur[nt][0], cur[nt][1]), pack16(cur[nt][2], cur[nt][3]),
+                            pack16(cur[nt][4], cur[nt][5]), pack16(cur[nt][6], cur[nt][7])};
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(R.x[mt][s], bv[nt], acc[nt][mt]);
+        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(x[mt][s], bv, acc[nt][mt]);
+      }
+      load_x(s, p + 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  NF4Regs<MT, NT> A, B;
-  if (w0 < w1) load(A, w0);
-  for (int p = w0; p < w1; p += 2) {
-    if (p + 1 < w1) load(B, p + 1);
-    compute(A, std::integral_constant<int, 0>());
-    if (p + 1 >= w1) break;
-    if (p + 2 < w1) load(A, p + 2);
-    compute(B, std::integral_constant<int, 2>());
+  auto build = [&](const uint16_t (&a)[2][NT], int p) {
+    nf4_build_table2<TB>(lanetab, p < w1 ? a[0][0] : (uint16_t)0, p + 1 < w1 ? a[1][0] : (uint16_t)0);
+    if constexpr (NT == 2)
+      nf4_build_table2<TB + kTabTile>(lanetab, p < w1 ? a[0][1] : (uint16_t)0, p + 1 < w1 ? a[1][1] : (uint16_t)0);
+  };
+
+  // The loads in flight at the top of every round are, in issue order, the
+  // codes of p, the 8 X fragments of p and the codes of p + 1, whether the
+  // round is entered from here or from the previous round, so the compiler's
+  // wait counts inside the loop stay exact.
+  load_abs(ac, w0);
+  build(ac, w0);
+  load_codes(qa, w0);
+#pragma unroll
+  for (int s = 0; s < 8; ++s) load_x(s, w0);
+  load_codes(qb, w0 + 1);
+  const int rounds = (n + 1) >> 1;
+  for (int r = 0; r < rounds; ++r) {
+    const int p = w0 + 2 * r;
+    __builtin_amdgcn_sched_barrier(0);
+    load_abs(an, p + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    pair(qa, p, std::integral_constant<int, 0>());
+    load_codes(qa, p + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    pair(qb, p + 1, std::integral_constant<int, 2>());
+    load_codes(qb, p + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    build(an, p + 2);  // the next round's tables; this round's reads are all issued
   }
 }
 
-template <int MT, int NT, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void nf4_gemm_kernel(const uint16_t* __restrict__ X, int64_t ldx,
-                                                              const uint8_t* __restrict__ W,
-                                                              const uint16_t* __restrict__ Wabs, int NP, int S,
-                                                              int pps, float* __restrict__ partial, EpiArgs e) {
-  constexpr int kTabBytes = WAVES * NT * kTabTile;
-  constexpr int kRedBytes = (WAVES - 1) * 16 * 64 * 4;
+template <int MT, int NT, bool XT>
+__global__ __launch_bounds__(kWaves * 64, 3) void nf4_gemm_kernel(const uint16_t* __restrict__ X, int64_t ldx,
+                                                                  const uint8_t* __restrict__ W,
+                                                                  const uint16_t* __restrict__ Wabs, int NP, int S,
+                                                                  int pps, float* __restrict__ partial,
+                                                                  int* __restrict__ counters, EpiArgs e) {
+  constexpr int kTabBytes = kWaves * NT * kTabTile;
+  constexpr int kRedBytes = kWaves * NT * MT * 16 * 64 * 4;
   static_assert(kTabBytes <= 65536, "table offsets must fit the 16-bit LDS immediate");
   __shared__ __align__(256) uint8_t smem[kTabBytes > kRedBytes ? kTabBytes : kRedBytes];
   const int group = blockIdx.x, split = blockIdx.y;
@@ -381,8 +504,8 @@ __global__ __launch_bounds__(WAVES * 64) void nf4_gemm_kernel(const uint16_t* __
   const int p0 = split * pps;
   const int p1 = min(NP, p0 + pps);
   const int np = max(0, p1 - p0);
-  const int w0 = p0 + (np * wave) / WAVES;
-  const int w1 = p0 + (np * (wave + 1)) / WAVES;
+  const int w0 = p0 + (np * wave) / kWaves;
+  const int w1 = p0 + (np * (wave + 1)) / kWaves;
 
   f32x16_t acc[NT][MT];
 #pragma unroll
@@ -393,35 +516,25 @@ __global__ __launch_bounds__(WAVES * 64) void nf4_gemm_kernel(const uint16_t* __
       for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.f;
 
   switch (wave) {
-#define PE_WAVE_CASE(i)                                                                              \
-  case i:                                                                                            \
-    if constexpr (i < WAVES) nf4_wave_body<MT, NT, WAVES, i>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); \
-    break;
-    PE_WAVE_CASE(0)
-    PE_WAVE_CASE(1)
-    PE_WAVE_CASE(2)
-    PE_WAVE_CASE(3)
-    PE_WAVE_CASE(4)
-    PE_WAVE_CASE(5)
-    PE_WAVE_CASE(6)
-    PE_WAVE_CASE(7)
-#undef PE_WAVE_CASE
-    default:
-      break;
+    case 0: nf4_wave_body<MT, NT, 0, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); break;
+    case 1: nf4_wave_body<MT, NT, 1, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); break;
+    case 2: nf4_wave_body<MT, NT, 2, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); break;
+    default: nf4_wave_body<MT, NT, 3, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); break;
   }
   __syncthreads();  // every wave is done with its tables; smem becomes the reduction buffer
-  reduce_waves_and_write<PE_DTYPE_BF16, NT, MT, WAVES>(acc, (float*)smem, group, split, S, partial, e);
+  finish_tile<PE_DTYPE_BF16, NT, MT>(acc, (float*)smem, group, split, S, partial, counters, e);
 }
 
 // ---------------------------------------------------------------------------
-// Dense 16-bit: one iteration = 4 MFMA k-steps (64 along K) of NT column tiles.
+// Dense 16-bit GEMM: one iteration = 4 MFMA k-steps (64 along K) of NT tiles.
+// Same pipeline as the NF4 kernel; a padded iteration multiplies a zero X.
 // ---------------------------------------------------------------------------
 template <int FMT, int MT, int NT>
-__global__ __launch_bounds__(256) void dense_gemm_kernel(const uint16_t* __restrict__ X, int64_t ldx, int K,
-                                                         const uint16_t* __restrict__ W, int S, int ups,
-                                                         float* __restrict__ partial, EpiArgs e) {
-  constexpr int WAVES = 4;
-  __shared__ __align__(16) float red[(WAVES - 1) * 16 * 64];
+__global__ __launch_bounds__(kWaves * 64, 3) void dense_gemm_kernel(const uint16_t* __restrict__ X, int64_t ldx,
+                                                                    int K, const uint16_t* __restrict__ W, int S,
+                                                                    int ups, float* __restrict__ partial,
+                                                                    int* __restrict__ counters, EpiArgs e) {
+  __shared__ __align__(16) float red[kWaves * NT * MT * 16 * 64];
   const int group = blockIdx.x, split = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 5, ln = lane & 31;
@@ -429,8 +542,8 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(const uint16_t* __restr
   const int u0 = split * ups;
   const int u1 = min(NU, u0 + ups);
   const int nu = max(0, u1 - u0);
-  const int w0 = u0 + (nu * wave) / WAVES;
-  const int w1 = u0 + (nu * (wave + 1)) / WAVES;
+  const int w0 = u0 + (nu * wave) / kWaves;
+  const int w1 = u0 + (nu * (wave + 1)) / kWaves;
 
   f32x16_t acc[NT][MT];
 #pragma unroll
@@ -440,68 +553,55 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(const uint16_t* __restr
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.f;
 
-  const uint16_t* xrow[MT];
+  const int n = w1 - w0;
+  if (n > 0) {
+    const uint16_t* xrow[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (int64_t)min(mt * 32 + ln, e.M - 1) * ldx + 8 * g;
-
-  u32x4_t bn[NT][4], xn[MT][4];
-  auto load = [&](int u) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bn[nt][j] = *(const u32x4_t*)(W + (((int64_t)(group * NT + nt) * KS + 4 * u + j) * 64 + lane) * 8);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xn[mt][j] = *(const u32x4_t*)(xrow[mt] + 64 * u + 16 * j);
-  };
-
-  if (w0 < w1) load(w0);
-  for (int u = w0; u < w1; ++u) {
-    u32x4_t bc[NT][4], xc[MT][4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) bc[nt][j] = bn[nt][j];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xc[mt][j] = xn[mt][j];
-    }
-    if (u + 1 < w1) load(u + 1);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (int64_t)min(mt * 32 + ln, e.M - 1) * ldx + 8 * g;
+    u32x4_t ba[NT][4], bb[NT][4], x[MT][4];
+    auto load_w = [&](u32x4_t (&b)[NT][4], int u) {
+      const int uc = min(u, w1 - 1);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16<FMT>(xc[mt][j], bc[nt][j], acc[nt][mt]);
-  }
-  reduce_waves_and_write<FMT, NT, MT, WAVES>(acc, red, group, split, S, partial, e);
-}
-
-// Sum S fp32 partials [S][M][N] in split order, then the epilogue. One thread
-// per output (swiglu: per gate/up pair).
-template <int DT>
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial, int S, EpiArgs e) {
-  const int n_out = e.op == PE_EPI_SWIGLU ? e.N / 2 : e.N;
-  const int64_t total = (int64_t)e.M * n_out;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int row = (int)(i / n_out), col = (int)(i % n_out);
-    if (e.op == PE_EPI_SWIGLU) {
-      const int gcol = (col >> 5) * 64 + (col & 31);
-      float gv = 0.f, uv = 0.f;
-      for (int s = 0; s < S; ++s) {
-        const float* p = partial + ((int64_t)s * e.M + row) * e.N;
-        gv += p[gcol];
-        uv += p[gcol + 32];
+        for (int j = 0; j < 4; ++j)
+          b[nt][j] = *(const u32x4_t*)(W + (((int64_t)(group * NT + nt) * KS + 4 * uc + j) * 64 + lane) * 8);
+    };
+    auto load_x = [&](int j, int u) {
+      const int uc = min(u, w1 - 1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) x[mt][j] = *(const u32x4_t*)(xrow[mt] + 64 * uc + 16 * j);
+    };
+    auto iter = [&](const u32x4_t (&b)[NT][4], int u) {
+      const uint32_t keep = u < w1 ? 0xffffffffu : 0u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const u32x4_t xa = x[mt][j] & keep;
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) acc[nt][mt] = mfma16<FMT>(xa, b[nt][j], acc[nt][mt]);
+        }
+        load_x(j, u + 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      epi_swiglu<DT>(e, row, col, gv, uv);
-    } else {
-      float v = 0.f;
-      for (int s = 0; s < S; ++s) v += partial[((int64_t)s * e.M + row) * e.N + col];
-      epi_value<DT>(e, row, col, v);
+    };
+    load_w(ba, w0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) load_x(j, w0);
+    load_w(bb, w0 + 1);
+    const int rounds = (n + 1) >> 1;
+    for (int r = 0; r < rounds; ++r) {
+      const int u = w0 + 2 * r;
+      __builtin_amdgcn_sched_barrier(0);
+      iter(ba, u);
+      load_w(ba, u + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      iter(bb, u + 1);
+      load_w(bb, u + 3);
     }
   }
+  finish_tile<FMT, NT, MT>(acc, red, group, split, S, partial, counters, e);
 }
 
 // fp32 linear on VALU: thread = output column, 8 rows per block row.
@@ -536,11 +636,11 @@ __global__ __launch_bounds__(64) void f32_gemm_kernel(const float* __restrict__ 
   }
 }
 
+
 // ---------------------------------------------------------------------------
 // Launch planning
 // ---------------------------------------------------------------------------
 constexpr int kMaxChunkRows = 64;  // M rows per launch (MT <= 2)
-constexpr int kMaxSplits = 16;     // split-K partials a consumer sums (residual RMSNorm's limit)
 
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
@@ -548,57 +648,61 @@ int env_int(const char* name, int dflt) {
 }
 
 struct Plan {
-  int NT, MT, S, per_split, groups, units, waves;
-  int64_t partial_bytes;  // [S][M][N] fp32 when S > 1
+  int NT, MT, S, per_split, groups, units;
+  int64_t partial_bytes;
 };
 
-// units: block pairs (NF4) or 64-wide K steps (dense). With allow_split false
-// the GEMM covers all of K in one workgroup per column group (S == 1);
-// otherwise S gives about `target_wg` workgroups (one per CU).
-Plan make_plan(int M, int N, int K, bool nf4, int epi, bool allow_split) {
-  static const int target_wg = env_int("PE_GEMM_TARGET_WG", 256);
+// units: block pairs (NF4) or 64-wide K steps (dense). A wave gets at least 2
+// units (one double-buffered round); S spreads the work over about
+// `wave_slots` waves (256 CUs x 3 four-wave workgroups by default) and is
+// balanced so that the splits differ by at most one unit per wave.
+Plan make_plan(int M, int N, int K, bool nf4, int epi) {
+  static const int wave_slots = env_int("PE_GEMM_WAVE_SLOTS", 3072);
+  static const int min_units = env_int("PE_GEMM_MIN_UNITS", 2);
   Plan p;
-  p.NT = (epi == PE_EPI_SWIGLU || N % 64 == 0) ? 2 : 1;
+  p.NT = (epi == PE_EPI_SWIGLU || epi == kEpiRopeKV || N % 64 == 0) ? 2 : 1;
   p.MT = M > 32 ? 2 : 1;
   p.groups = N / (32 * p.NT);
   p.units = nf4 ? K / 128 : K / 64;
-  int S = allow_split ? (target_wg + p.groups - 1) / p.groups : 1;
-  // An unsplit NF4 GEMM with few column groups splits K over 8 waves instead of 4.
-  // (only when the workgroups fit in one round at one 8-wave workgroup per CU)
-  static const int wide_groups = env_int("PE_GEMM_WIDE_GROUPS", 257);
-  p.waves = (nf4 && S <= 1 && p.groups < wide_groups && p.units >= 16) ? 8 : 4;
-  const int waves = p.waves;
-  int smax = p.units / waves;
-  if (smax < 1) smax = 1;
-  if (S > smax) S = smax;
+  const int64_t total = (int64_t)p.groups * p.units;
+  int per_wave = (int)((total + wave_slots - 1) / wave_slots);
+  if (per_wave < min_units) per_wave = min_units;
+  int S = (p.units + per_wave * kWaves - 1) / (per_wave * kWaves);
   if (S > kMaxSplits) S = kMaxSplits;
   if (S < 1) S = 1;
   p.per_split = (p.units + S - 1) / S;
   p.S = (p.units + p.per_split - 1) / p.per_split;
-  p.partial_bytes = (p.S > 1) ? (int64_t)p.S * M * N * 4 : 0;
+  p.partial_bytes = partial_bytes_of(p.S, p.groups, p.MT, p.NT);
   return p;
 }
 
+int64_t workspace_of(const Plan& p) { return kCounterBytes + p.partial_bytes; }
+
 // fmt: -1 = NF4 (bf16 compute), else PE_DTYPE_BF16 / PE_DTYPE_F16 dense.
-int launch_gemm(int fmt, const Plan& p, hipStream_t st, const uint16_t* x, int64_t ldx, int K, const void* w,
-                const uint16_t* wabs, float* partial, const EpiArgs& e) {
+// ws: [counters | partials]; the counters are zero on entry and left zero.
+int launch_gemm(int fmt, const Plan& p, hipStream_t st, const uint16_t* x, int64_t ldx, bool x_tiled, int K,
+                const void* w, const uint16_t* wabs, void* ws, const EpiArgs& e) {
+  if (p.groups > kMaxGroups) return PE_ERR_ARG;
   dim3 grid(p.groups, p.S);
+  int* counters = (int*)ws;
+  float* partial = (float*)((char*)ws + kCounterBytes);
   if (fmt < 0) {
-#define PE_NF4(MT_, NT_, WV_)                                                                              \
-  nf4_gemm_kernel<MT_, NT_, WV_><<<grid, WV_ * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, p.S, \
-                                                           p.per_split, partial, e)
-    if (p.waves == 8) {
-      if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, 8); else PE_NF4(2, 2, 8); }
-      else { if (p.MT == 1) PE_NF4(1, 1, 8); else PE_NF4(2, 1, 8); }
+#define PE_NF4(MT_, NT_, XT_)                                                                                  \
+  nf4_gemm_kernel<MT_, NT_, XT_><<<grid, kWaves * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, p.S, \
+                                                                p.per_split, partial, counters, e)
+    if (x_tiled) {
+      if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, true); else PE_NF4(2, 2, true); }
+      else { if (p.MT == 1) PE_NF4(1, 1, true); else PE_NF4(2, 1, true); }
     } else {
-      if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, 4); else PE_NF4(2, 2, 4); }
-      else { if (p.MT == 1) PE_NF4(1, 1, 4); else PE_NF4(2, 1, 4); }
+      if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, false); else PE_NF4(2, 2, false); }
+      else { if (p.MT == 1) PE_NF4(1, 1, false); else PE_NF4(2, 1, false); }
     }
 #undef PE_NF4
   } else {
-#define PE_DENSE(F, MT_, NT_)                                                                                 \
-  dense_gemm_kernel<F, MT_, NT_><<<grid, 256, 0, st>>>(x, ldx, K, (const uint16_t*)w, p.S, p.per_split, partial, \
-                                                       e)
+    if (x_tiled) return PE_ERR_ARG;
+#define PE_DENSE(F, MT_, NT_)                                                                                      \
+  dense_gemm_kernel<F, MT_, NT_><<<grid, kWaves * 64, 0, st>>>(x, ldx, K, (const uint16_t*)w, p.S, p.per_split, \
+                                                               partial, counters, e)
     if (fmt == PE_DTYPE_F16) {
       if (p.NT == 2) { if (p.MT == 1) PE_DENSE(PE_DTYPE_F16, 1, 2); else PE_DENSE(PE_DTYPE_F16, 2, 2); }
       else { if (p.MT == 1) PE_DENSE(PE_DTYPE_F16, 1, 1); else PE_DENSE(PE_DTYPE_F16, 2, 1); }
@@ -631,6 +735,7 @@ EpiArgs make_epi(int epi, int mc, int N, const void* bias, const void* resid, in
   e.ld_resid = ld_resid;
   e.out = out;
   e.ld_out = ld_out;
+  e.out_units = 0;
   e.positions = nullptr;
   e.cos_sin = nullptr;
   e.max_pos = 0;
@@ -641,33 +746,28 @@ EpiArgs make_epi(int epi, int mc, int N, const void* bias, const void* resid, in
   return e;
 }
 
-// The standalone GEMM: split-K partials (if any) are summed by splitk_reduce_kernel.
+// M is processed in chunks of up to 64 rows, one launch each.
+// x_tiled: X is A-tiled (M <= 64, one launch); out_units > 0: out is A-tiled.
 int mfma_gemm(int fmt, const void* x, int64_t ldx, int M, int K, const void* w, const uint16_t* wabs, int N,
               int epi, const void* bias, const void* resid, int64_t ld_resid, void* out, int64_t ld_out,
-              void* ws, int64_t ws_bytes, hipStream_t st) {
+              void* ws, int64_t ws_bytes, hipStream_t st, bool x_tiled = false, int out_units = 0) {
   int rc = check_gemm_args(x, M, K, w, N, epi, resid, out);
   if (rc != PE_OK) return rc;
   const bool nf4 = fmt < 0;
-  const int adt = nf4 ? PE_DTYPE_BF16 : fmt;
+  if ((x_tiled || out_units) && M > kMaxChunkRows) return PE_ERR_ARG;
+  if (out_units && epi == PE_EPI_RESIDUAL) return PE_ERR_ARG;
   int done = 0;
   while (done < M) {
     const int mc = (M - done > kMaxChunkRows) ? kMaxChunkRows : (M - done);
-    Plan p = make_plan(mc, N, K, nf4, epi, true);
-    if (p.S > 1 && (!ws || ws_bytes < p.partial_bytes)) return PE_ERR_WORKSPACE;
+    Plan p = make_plan(mc, N, K, nf4, epi);
+    if (!ws || ws_bytes < workspace_of(p)) return PE_ERR_WORKSPACE;
     const size_t esz = 2;
     EpiArgs e = make_epi(epi, mc, N, bias, resid ? (const char*)resid + (size_t)done * ld_resid * esz : nullptr,
                          ld_resid, (char*)out + (size_t)done * ld_out * esz, ld_out);
-    const uint16_t* xc = (const uint16_t*)x + (size_t)done * ldx;
-    rc = launch_gemm(fmt, p, st, xc, ldx, K, w, wabs, (float*)ws, e);
+    e.out_units = out_units;
+    const uint16_t* xc = x_tiled ? (const uint16_t*)x : (const uint16_t*)x + (size_t)done * ldx;
+    rc = launch_gemm(fmt, p, st, xc, ldx, x_tiled, K, w, wabs, ws, e);
     if (rc != PE_OK) return rc;
-    if (p.S > 1) {
-      const int n_out = epi == PE_EPI_SWIGLU ? N / 2 : N;
-      int blocks = (int)(((int64_t)mc * n_out + 255) / 256);
-      if (blocks > 4096) blocks = 4096;
-      if (adt == PE_DTYPE_F16) splitk_reduce_kernel<PE_DTYPE_F16><<<blocks, 256, 0, st>>>((const float*)ws, p.S, e);
-      else splitk_reduce_kernel<PE_DTYPE_BF16><<<blocks, 256, 0, st>>>((const float*)ws, p.S, e);
-      PE_CHECK_LAUNCH();
-    }
     done += mc;
   }
   return PE_OK;
@@ -677,51 +777,21 @@ constexpr int kFmtNF4 = -1;
 
 }  // namespace
 
-// Internal entries used by pe_forward (one launch over M <= 64 rows of a
-// 16-bit dtype). pe_internal_gemm_partials always writes fp32 partials
-// [S][M][N] to `partial` (S >= 1, reported in S_out) for a consumer kernel to
-// sum; pe_internal_gemm_epilogue covers all of K in each workgroup and applies
-// the epilogue itself.
-int pe_internal_gemm_partials(int wfmt, int dtype, const void* x, int64_t ldx, int M, int K, const void* w,
-                              const uint16_t* wabs, int N, float* partial, int64_t partial_bytes, int* S_out,
-                              hipStream_t st) {
-  if (M > kMaxChunkRows || !partial) return PE_ERR_ARG;
-  int rc = check_gemm_args(x, M, K, w, N, PE_EPI_STORE, nullptr, partial);
-  if (rc != PE_OK) return rc;
-  const bool nf4 = wfmt == PE_WFMT_NF4;
-  Plan p = make_plan(M, N, K, nf4, PE_EPI_STORE, true);
-  if (partial_bytes < (int64_t)p.S * M * N * 4) return PE_ERR_WORKSPACE;
-  EpiArgs e = make_epi(kEpiPartial, M, N, nullptr, nullptr, 0, partial, N);
-  *S_out = p.S;
-  return launch_gemm(nf4 ? kFmtNF4 : dtype, p, st, (const uint16_t*)x, ldx, K, w, wabs, partial, e);
-}
-
-int pe_internal_gemm_epilogue(int wfmt, int dtype, const void* x, int64_t ldx, int M, int K, const void* w,
-                              const uint16_t* wabs, int N, int epi, const void* bias, const void* resid,
-                              int64_t ld_resid, void* out, int64_t ld_out, hipStream_t st) {
-  if (M > kMaxChunkRows) return PE_ERR_ARG;
-  int rc = check_gemm_args(x, M, K, w, N, epi, resid, out);
-  if (rc != PE_OK) return rc;
-  const bool nf4 = wfmt == PE_WFMT_NF4;
-  Plan p = make_plan(M, N, K, nf4, epi, false);
-  EpiArgs e = make_epi(epi, M, N, bias, resid, ld_resid, out, ld_out);
-  return launch_gemm(nf4 ? kFmtNF4 : dtype, p, st, (const uint16_t*)x, ldx, K, w, wabs, nullptr, e);
-}
-
 // The q/k/v projection with its RoPE + KV-append epilogue (weight rows in
-// head-paired tile order; hd % 64 == 0). Covers all of K per workgroup.
+// head-paired tile order; hd % 64 == 0), one launch over M <= 64 rows.
 int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int64_t ldx, int M, int K, const void* w,
                              const uint16_t* wabs, int nh, int nkv, int hd, const void* bias,
                              const int64_t* positions, const void* cos_sin, int64_t max_pos, void* q_out,
-                             void* k_cache, void* v_cache, int64_t cap, int64_t row0, int32_t* status,
-                             hipStream_t st) {
+                             void* k_cache, void* v_cache, int64_t cap, int64_t row0, int32_t* status, void* ws,
+                             int64_t ws_bytes, bool x_tiled, hipStream_t st) {
   const int N = (nh + 2 * nkv) * hd;
   if (M > kMaxChunkRows || hd % 64 || !positions || !cos_sin || !q_out || !k_cache || !v_cache) return PE_ERR_ARG;
   if (row0 < 0 || row0 + M > cap) return PE_ERR_CAPACITY;
   int rc = check_gemm_args(x, M, K, w, N, PE_EPI_SWIGLU, nullptr, q_out);
   if (rc != PE_OK) return rc;
   const bool nf4 = wfmt == PE_WFMT_NF4;
-  Plan p = make_plan(M, N, K, nf4, PE_EPI_SWIGLU, false);  // NT = 2, S = 1
+  Plan p = make_plan(M, N, K, nf4, kEpiRopeKV);
+  if (!ws || ws_bytes < workspace_of(p)) return PE_ERR_WORKSPACE;
   EpiArgs e = make_epi(kEpiRopeKV, M, N, bias, nullptr, 0, nullptr, 0);
   e.positions = positions;
   e.cos_sin = cos_sin;
@@ -735,21 +805,32 @@ int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int64_t ldx, in
   e.nkv = nkv;
   e.hd = hd;
   e.status = status;
-  return launch_gemm(nf4 ? kFmtNF4 : dtype, p, st, (const uint16_t*)x, ldx, K, w, wabs, nullptr, e);
+  return launch_gemm(nf4 ? kFmtNF4 : dtype, p, st, (const uint16_t*)x, ldx, x_tiled, K, w, wabs, ws, e);
 }
 
-int64_t pe_internal_gemm_partial_bytes(int M, int N, int K, int wfmt) {
+int pe_internal_linear(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M, int K, const void* w,
+                       const uint16_t* wabs, int N, int epi, const void* bias, const void* resid, int64_t ld_resid,
+                       void* out, int64_t ld_out, int out_units, void* ws, int64_t ws_bytes, hipStream_t st) {
+  if (wfmt == PE_WFMT_NF4) {
+    if (!wabs) return PE_ERR_ARG;
+    return mfma_gemm(kFmtNF4, x, ldx, M, K, w, wabs, N, epi, bias, resid, ld_resid, out, ld_out, ws, ws_bytes, st,
+                     x_tiled, out_units);
+  }
+  if (dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16) return PE_ERR_ARG;
+  return mfma_gemm(dtype, x, ldx, M, K, w, nullptr, N, epi, bias, resid, ld_resid, out, ld_out, ws, ws_bytes, st,
+                   x_tiled, out_units);
+}
+
+int64_t pe_internal_gemm_rope_kv_bytes(int M, int N, int K, int wfmt) {
   if (M > kMaxChunkRows) M = kMaxChunkRows;
-  const Plan p = make_plan(M, N, K, wfmt == PE_WFMT_NF4, PE_EPI_STORE, true);
-  return (int64_t)p.S * M * N * 4;
+  return workspace_of(make_plan(M, N, K, wfmt == PE_WFMT_NF4, kEpiRopeKV));
 }
 
 extern "C" int64_t pe_gemm_workspace_bytes(int M, int N, int K, int wfmt, int dtype, int epilogue) {
   if (dtype == PE_DTYPE_F32 && wfmt == PE_WFMT_DENSE) return 0;
-  if (M <= 0 || N <= 0 || K < 128) return kGemmWsAlign;
+  if (M <= 0 || N <= 0 || K < 128) return kCounterBytes;
   const int mc = M > kMaxChunkRows ? kMaxChunkRows : M;
-  const int64_t b = make_plan(mc, N, K, wfmt == PE_WFMT_NF4, epilogue, true).partial_bytes;
-  return b > kGemmWsAlign ? b : kGemmWsAlign;
+  return workspace_of(make_plan(mc, N, K, wfmt == PE_WFMT_NF4, epilogue));
 }
 
 extern "C" int pe_nf4_gemm(const void* x, int64_t ldx, int M, int K, const uint8_t* w_tiled,

@@ -7,24 +7,36 @@
 
 #define PE_INTERNAL __attribute__((visibility("hidden")))
 
-// pe_gemm.hip
-PE_INTERNAL int pe_internal_gemm_partials(int wfmt, int dtype, const void* x, int64_t ldx, int M, int K,
-                                          const void* w, const uint16_t* wabs, int N, float* partial,
-                                          int64_t partial_bytes, int* S_out, hipStream_t st);
-PE_INTERNAL int pe_internal_gemm_epilogue(int wfmt, int dtype, const void* x, int64_t ldx, int M, int K,
-                                          const void* w, const uint16_t* wabs, int N, int epi, const void* bias,
-                                          const void* resid, int64_t ld_resid, void* out, int64_t ld_out,
-                                          hipStream_t st);
+// pe_gemm.hip: the q/k/v projection with bias, RoPE and the in-place K/V
+// append in its epilogue (one launch over M <= 64 rows); ws as for
+// pe_nf4_gemm (zeroed counters, then partials), of pe_internal_gemm_rope_kv_bytes.
 PE_INTERNAL int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int64_t ldx, int M, int K,
                                          const void* w, const uint16_t* wabs, int nh, int nkv, int hd,
                                          const void* bias, const int64_t* positions, const void* cos_sin,
                                          int64_t max_pos, void* q_out, void* k_cache, void* v_cache, int64_t cap,
-                                         int64_t row0, int32_t* status, hipStream_t st);
-PE_INTERNAL int64_t pe_internal_gemm_partial_bytes(int M, int N, int K, int wfmt);
+                                         int64_t row0, int32_t* status, void* ws, int64_t ws_bytes, bool x_tiled,
+                                         hipStream_t st);
+PE_INTERNAL int64_t pe_internal_gemm_rope_kv_bytes(int M, int N, int K, int wfmt);
+// pe_nf4_gemm / pe_dense_gemm with A-tiled X (x_tiled, NF4 only, M <= 64)
+// and/or an A-tiled output (out_units = N_out / 128, not with the residual
+// epilogue).
+PE_INTERNAL int pe_internal_linear(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M, int K,
+                                   const void* w, const uint16_t* wabs, int N, int epi, const void* bias,
+                                   const void* resid, int64_t ld_resid, void* out, int64_t ld_out, int out_units,
+                                   void* ws, int64_t ws_bytes, hipStream_t st);
 
 // pe_elem.hip: h = round(h + round(sum_s partial[s])) (S == 0: h unchanged),
-// xn = w * round(h * rsqrt(mean(h^2) + eps)); optional copies of the new h
-// (cap_h) and of xn (cap_xn) into the fused-feature rows.
+// xn = w * round(h * rsqrt(mean(h^2) + eps)), also A-tiled into xn_tiled when
+// given; optional copies of the new h (cap_h) and of xn (cap_xn) into the
+// fused-feature rows.
 PE_INTERNAL int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, int H, const void* w,
-                                             float eps, int dtype, void* xn, void* cap_h, int64_t ld_cap_h,
-                                             void* cap_xn, int64_t ld_cap_xn, hipStream_t st);
+                                             float eps, int dtype, void* xn, void* xn_tiled, void* cap_h,
+                                             int64_t ld_cap_h, void* cap_xn, int64_t ld_cap_xn, hipStream_t st);
+
+// pe_attn.hip: pe_tree_attention whose output is A-tiled when out_units > 0
+// (hd == 128 16-bit path only).
+PE_INTERNAL int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
+                                           int nh, int nkv, int hd, int T, int64_t P, int mask_mode,
+                                           const uint64_t* bits, int words, float scale, int dtype, void* out,
+                                           int64_t ld_out, int out_units, void* workspace, int64_t workspace_bytes,
+                                           hipStream_t st);

@@ -30,9 +30,11 @@ int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 int esize(int dtype) { return dtype == PE_DTYPE_F32 ? 4 : 2; }
 
 struct Layout {
-  int64_t gemm;  // split-K partials of the standalone GEMMs / fp32 partials of the layer GEMMs
+  int64_t gemm;  // GEMM arrival counters, then split-K partials
   int64_t gemm_bytes;
-  int64_t h, xn, qkv, q, attn, act, attn_ws, attn_ws_bytes, total;
+  int64_t h, xn, qkv, q, attn, act, attn_ws, attn_ws_bytes;
+  int64_t xn_t, attn_t, act_t;  // A-tiled GEMM inputs of the fused NF4 pass
+  int64_t total;
 };
 
 // The 16-bit pass with fused epilogues (see pe_forward) needs the q/k/v rows
@@ -40,6 +42,14 @@ struct Layout {
 bool fused_path(const pe_model_desc* m, int M) {
   return m->dtype != PE_DTYPE_F32 && m->qkv_layout == PE_QKV_ROPE_PAIRED && m->head_dim == 128 && M <= 64;
 }
+
+// The fused NF4 pass hands the GEMMs their X A-tiled (see xtile_index).
+bool tiled_path(const pe_model_desc* m, int M) {
+  return fused_path(m, M) && m->weight_format == PE_WFMT_NF4 && m->hidden % 128 == 0 &&
+         (m->num_heads * m->head_dim) % 128 == 0 && m->intermediate_padded % 128 == 0;
+}
+
+int64_t xtile_bytes(int M, int K) { return (int64_t)((M + 31) / 32) * K * 64; }
 
 int64_t gemm_ws(const pe_model_desc* m, int M, int N, int K, int epi) {
   const int wf = m->weight_format;
@@ -52,14 +62,11 @@ Layout make_layout(const pe_model_desc* m, int M, int64_t kv_len) {
   const int H = m->hidden, qd = m->num_heads * m->head_dim, kvd = m->num_kv_heads * m->head_dim;
   const int nqkv = qd + 2 * kvd, ip = m->intermediate_padded;
   int64_t g = kCounterBytes;
-  int64_t cand[7] = {gemm_ws(m, M, nqkv, H, PE_EPI_STORE), gemm_ws(m, M, H, qd, PE_EPI_RESIDUAL),
+  int64_t cand[6] = {gemm_ws(m, M, nqkv, H, PE_EPI_STORE), gemm_ws(m, M, H, qd, PE_EPI_RESIDUAL),
                      gemm_ws(m, M, 2 * ip, H, PE_EPI_SWIGLU), gemm_ws(m, M, H, ip, PE_EPI_RESIDUAL),
-                     pe_gemm_workspace_bytes(M, m->vocab, H, PE_WFMT_DENSE, m->dtype, PE_EPI_STORE), 0, 0};
-  if (fused_path(m, M)) {
-    cand[5] = pe_internal_gemm_partial_bytes(M, H, qd, m->weight_format);
-    cand[6] = pe_internal_gemm_partial_bytes(M, H, ip, m->weight_format);
-  }
-  for (int i = 0; i < 7; ++i)
+                     pe_gemm_workspace_bytes(M, m->vocab, H, PE_WFMT_DENSE, m->dtype, PE_EPI_STORE), 0};
+  if (fused_path(m, M)) cand[5] = pe_internal_gemm_rope_kv_bytes(M, nqkv, H, m->weight_format);
+  for (int i = 0; i < 6; ++i)
     if (cand[i] > g) g = cand[i];
   int64_t off = 0;
   L.gemm = off;
@@ -72,6 +79,12 @@ Layout make_layout(const pe_model_desc* m, int M, int64_t kv_len) {
   L.q = off; off += align_up((int64_t)M * qd * es);
   L.attn = off; off += align_up((int64_t)M * qd * es);
   L.act = off; off += align_up((int64_t)M * ip * es);
+  L.xn_t = L.attn_t = L.act_t = 0;
+  if (tiled_path(m, M)) {
+    L.xn_t = off; off += align_up(xtile_bytes(M, H));
+    L.attn_t = off; off += align_up(xtile_bytes(M, qd));
+    L.act_t = off; off += align_up(xtile_bytes(M, ip));
+  }
   L.attn_ws = off;
   L.attn_ws_bytes = align_up(pe_attention_workspace_bytes(M, m->num_heads, m->num_kv_heads, m->head_dim, kv_len,
                                                           m->dtype));
@@ -117,16 +130,16 @@ extern "C" int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int
 // The 16-bit pass: per layer
 //   q/k/v GEMM with bias + RoPE + in-place K/V append in its epilogue
 //   -> tree attention (split-KV) -> combine
-//   -> o GEMM (fp32 split partials) -> residual add + post-attention RMSNorm
+//   -> o GEMM with the residual add in its epilogue -> post-attention RMSNorm
 //   -> gate/up GEMM with SwiGLU epilogue
-//   -> down GEMM (fp32 split partials) -> residual add + next RMSNorm
+//   -> down GEMM with the residual add in its epilogue -> next RMSNorm
 // The RMSNorm after the down projection is the next layer's input norm, or the
 // final norm after the last layer; hidden-state captures ride on it.
 int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& Lo, hipStream_t st) {
   const int M = a->M;
   char* ws = (char*)a->workspace;
-  float* part = (float*)(ws + Lo.gemm);
-  const int64_t part_bytes = Lo.gemm_bytes;
+  void* gws = ws + Lo.gemm;
+  const int64_t gwsb = Lo.gemm_bytes;
   const int es = esize(m->dtype);
   const int H = m->hidden, nh = m->num_heads, nkv = m->num_kv_heads, hd = m->head_dim;
   const int qd = nh * hd, ip = m->intermediate_padded, L = m->num_layers, wf = m->weight_format;
@@ -136,6 +149,13 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   void* attn = ws + Lo.attn;
   void* act = ws + Lo.act;
   void* aws = ws + Lo.attn_ws;
+  // A-tiled GEMM inputs (NF4): x_* is what the GEMMs read, *_units the tiled output widths
+  const bool tiled = tiled_path(m, M);
+  void* xn_t = tiled ? ws + Lo.xn_t : nullptr;
+  void* x_norm = tiled ? xn_t : xn;
+  void* x_attn = tiled ? ws + Lo.attn_t : attn;
+  void* x_act = tiled ? ws + Lo.act_t : act;
+  const int attn_units = tiled ? qd / 128 : 0, act_units = tiled ? ip / 128 : 0;
   const float scale = (float)(1.0 / std::sqrt((double)hd));
   const int64_t layer_stride = (int64_t)nkv * a->cache_capacity * hd * es;
   const int64_t fused_ld = (int64_t)a->num_features * H;  // elements
@@ -166,37 +186,42 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   PE_TRY(pe_embed(a->input_ids, M, m->embed, m->vocab, H, m->dtype, h, H, a->status, st));
   {
     const int f0 = slot_of(0);
-    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->attn_norm[0], m->rms_eps, m->dtype, xn, slot_ptr(f0),
-                                        fused_ld, nullptr, 0, st));
+    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->attn_norm[0], m->rms_eps, m->dtype, xn, xn_t,
+                                        slot_ptr(f0), fused_ld, nullptr, 0, st));
     PE_TRY(copy_repeats(0, f0));
   }
   for (int l = 0; l < L; ++l) {
     void* kc = (char*)a->k_cache + l * layer_stride;
     void* vc = (char*)a->v_cache + l * layer_stride;
-    int S = 1;
-    PE_TRY(pe_internal_gemm_rope_kv(wf, m->dtype, xn, H, M, H, m->w_qkv[l], (const uint16_t*)(m->a_qkv ? m->a_qkv[l] : nullptr),
-                                    nh, nkv, hd, m->b_qkv ? m->b_qkv[l] : nullptr, a->positions, m->rope_cos_sin,
-                                    m->max_positions, q, kc, vc, a->cache_capacity, a->prefix_len, a->status, st));
-    PE_TRY(pe_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode, a->tree_bits,
-                             a->bits_words, scale, m->dtype, attn, qd, aws, Lo.attn_ws_bytes, st));
-    PE_TRY(pe_internal_gemm_partials(wf, m->dtype, attn, qd, M, qd, m->w_o[l], (const uint16_t*)(m->a_o ? m->a_o[l] : nullptr),
-                                     H, part, part_bytes, &S, st));
-    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, nullptr, 0,
-                                        nullptr, 0, st));
-    PE_TRY(pe_internal_gemm_epilogue(wf, m->dtype, xn, H, M, H, m->w_gu[l], (const uint16_t*)(m->a_gu ? m->a_gu[l] : nullptr),
-                                     2 * ip, PE_EPI_SWIGLU, nullptr, nullptr, 0, act, ip, st));
-    PE_TRY(pe_internal_gemm_partials(wf, m->dtype, act, ip, M, ip, m->w_down[l],
-                                     (const uint16_t*)(m->a_down ? m->a_down[l] : nullptr), H, part, part_bytes, &S, st));
+    PE_TRY(pe_internal_gemm_rope_kv(wf, m->dtype, x_norm, H, M, H, m->w_qkv[l],
+                                    (const uint16_t*)(m->a_qkv ? m->a_qkv[l] : nullptr), nh, nkv, hd,
+                                    m->b_qkv ? m->b_qkv[l] : nullptr, a->positions, m->rope_cos_sin, m->max_positions,
+                                    q, kc, vc, a->cache_capacity, a->prefix_len, a->status, gws, gwsb, tiled, st));
+    PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
+                                      a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
+                                      Lo.attn_ws_bytes, st));
+    PE_TRY(pe_internal_linear(wf, m->dtype, x_attn, qd, tiled, M, qd, m->w_o[l],
+                              (const uint16_t*)(m->a_o ? m->a_o[l] : nullptr), H, PE_EPI_RESIDUAL, nullptr, h, H, h, H,
+                              0, gws, gwsb, st));
+    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, xn_t, nullptr,
+                                        0, nullptr, 0, st));
+    PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, tiled, M, H, m->w_gu[l],
+                              (const uint16_t*)(m->a_gu ? m->a_gu[l] : nullptr), 2 * ip, PE_EPI_SWIGLU, nullptr,
+                              nullptr, 0, x_act, ip, act_units, gws, gwsb, st));
+    PE_TRY(pe_internal_linear(wf, m->dtype, x_act, ip, tiled, M, ip, m->w_down[l],
+                              (const uint16_t*)(m->a_down ? m->a_down[l] : nullptr), H, PE_EPI_RESIDUAL, nullptr, h, H,
+                              h, H, 0, gws, gwsb, st));
     const bool last = l + 1 == L;
     const int fh = last ? -1 : slot_of(l + 1);
     const int fx = last ? slot_of(L) : -1;
-    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, last ? m->final_norm : m->attn_norm[l + 1], m->rms_eps,
-                                        m->dtype, xn, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
+    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, last ? m->final_norm : m->attn_norm[l + 1], m->rms_eps,
+                                        m->dtype, xn, last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx),
+                                        fused_ld, st));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
   if (a->logits)
     PE_TRY(pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
-                         m->vocab, part, part_bytes, st));
+                         m->vocab, gws, gwsb, st));
 #undef PE_TRY
   return PE_OK;
 }
