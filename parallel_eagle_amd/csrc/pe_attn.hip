@@ -15,7 +15,7 @@
 //   O^T += V^T P^T (A = V^T from a wave-private LDS transpose of the 32-key V
 //   block, B = P^T taken directly from the S^T accumulator registers rounded to
 //   the compute dtype), so the per-row rescale is a per-lane scalar.
-//   Partial (O, max, sum) per split are merged by attn_combine_kernel.
+//   Partial (O, max, sum) per split are combined by attn_combine_kernel.
 // Softmax is fp32; exp(s - m) is summed in fp32 and rounded to the compute
 // dtype for the PV product, as torch's CPU flash attention does for reduced
 // precision inputs.
@@ -24,6 +24,8 @@
 
 #include "pe_common.h"
 #include "pe_internal.h"
+
+#include <type_traits>
 
 namespace {
 
@@ -37,25 +39,37 @@ __device__ __forceinline__ bool key_allowed(int64_t key, int64_t P, int t, int m
   return (nb[u >> 6] >> (u & 63)) & 1ull;
 }
 
-// One workgroup = 4 waves = one (KV head, key split, 32-row tile). Each wave
-// takes a contiguous run of the split's 32-key blocks; the next block's K and
-// V fragments are loaded as soon as the current ones are consumed (K after the
-// S MFMAs, V after its LDS transpose), so the loads overlap softmax and PV.
-// Loads are clamped to the wave's last valid key (those scores are masked and
-// their probabilities are exactly zero), so no uninitialised cache row is read.
-// At the end the 4 waves' (m, l, O) are merged in LDS in wave order and one
-// partial per workgroup is written for attn_combine_kernel.
-constexpr int kAttnWaves = 4;
+// One workgroup = 4 waves = one (KV head, key split, 32-row tile); each wave
+// takes a contiguous run of the split's 32-key blocks and processes them two
+// at a time as one 64-key block (a run of odd length ends with a half-masked
+// pair). The K and V loads of a pair are the first instructions of its round,
+// so at the 7B shape the whole KV stream is in flight at once. V of the pair
+// goes to a wave-private LDS transpose before S = K Q^T is formed, the row
+// tile's Q is staged once per workgroup in LDS (the B operand of S^T is read
+// from there per k-step), and a wave stays within 256 VGPRs: two workgroups
+// per CU. Loads are clamped to the wave's last valid key (those scores are
+// masked and their probabilities are exactly zero), so no uninitialised cache
+// row is read. At the end the 4 waves' (m, l, O) are merged in LDS in wave
+// order by all 256 threads, and one partial per workgroup is written for
+// attn_combine_kernel with coalesced stores.
+constexpr int kAttnWaves = 8;
+constexpr int kQStride = 128 + 8;  // LDS row stride of the staged Q tile (elements)
+constexpr int kVRow = 128 + 32;    // LDS row stride of a wave's V tile (elements): 320 B, rows 16 banks apart
+constexpr int kCmbRow = 128 + 1;   // LDS row stride of the wave merge (floats; odd: no bank conflicts)
+constexpr int kAttnMaxSplits = 16;
 
 template <int DT>
-__global__ __launch_bounds__(64 * kAttnWaves) void attn_wg_kernel(
+__global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
     int nh, int nkv, int T, int64_t P, int mask_mode, const uint64_t* __restrict__ bits, int words, float scale,
-    int keys_per_split, int splits, int rows_pad, float* __restrict__ opart, float* __restrict__ mlpart) {
+    int keys_per_split, int splits, int rows_pad, float* __restrict__ opart, float* __restrict__ mlpart,
+    void* __restrict__ out, int64_t ld_out, int out_units) {
   constexpr int HD = 128;
-  constexpr int kVtBytes = HD * (32 + 8) * 2;
-  constexpr int kCmbBytes = (kAttnWaves - 1) * 32 * (HD + 2) * 4;
-  constexpr int kSmem = (kAttnWaves * kVtBytes > kCmbBytes) ? kAttnWaves * kVtBytes : kCmbBytes;
+  constexpr int kQBytes = 32 * kQStride * 2;
+  constexpr int kVtBytes = 32 * kVRow * 2;  // one 32-key V block, row-major
+  constexpr int kCmbBytes = kAttnWaves * 32 * (kCmbRow + 2) * 4;
+  constexpr int kMain = kQBytes + kAttnWaves * kVtBytes;
+  constexpr int kSmem = (kMain > kCmbBytes) ? kMain : kCmbBytes;
   __shared__ __align__(16) uint8_t smem[kSmem];
   const int kvh = blockIdx.x, split = blockIdx.y, rt = blockIdx.z;
   const int G = nh / nkv, rows = T * G;
@@ -66,228 +80,313 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_wg_kernel(
   const int nb = (int)((ks1 - ks0 + 31) / 32);
   const int b0 = (nb * wave) / kAttnWaves, b1 = (nb * (wave + 1)) / kAttnWaves;
   const int64_t j1 = min(ks1, ks0 + 32 * (int64_t)b1);  // end of this wave's keys
-  uint16_t(*vt)[32 + 8] = (uint16_t(*)[32 + 8])(smem + wave * kVtBytes);
+  const int64_t jlast = j1 - 1;
+  uint16_t(*qs)[kQStride] = (uint16_t(*)[kQStride])smem;
+  uint16_t(*vs)[kVRow] = (uint16_t(*)[kVRow])(smem + kQBytes + wave * kVtBytes);
+
+  // wave-uniform bases and 32-bit byte offsets (a head's cache rows span
+  // cap * 256 bytes < 4 GiB), so each load is base + one offset register
+  const char* kbase = (const char*)(kc + (int64_t)kvh * cap * HD);
+  const char* vbase = (const char*)(vc + (int64_t)kvh * cap * HD);
+  u32x4_t kf[2][8], vf[2][8];
+  auto load_pair = [&](int64_t jb) {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      const uint32_t ko = (uint32_t)min(jb + 32 * sb + ln, jlast) * (HD * 2) + 16 * g;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kf[sb][j] = *(const u32x4_t*)(kbase + ko + 32 * j);
+    }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        // 32 keys x 16 chunks of 8 dims: lane covers key 4c + lane / 16, chunk lane % 16
+        const uint32_t vo = (uint32_t)min(jb + 32 * sb + 4 * c + (lane >> 4), jlast) * (HD * 2) + (lane & 15) * 16;
+        vf[sb][c] = *(const u32x4_t*)(vbase + vo);
+      }
+  };
+  // the row tile's Q (rows past `rows` are zero) is requested first, so
+  // staging it waits for Q alone and not for the KV stream behind it
+  constexpr int kQChunks = 512 / (64 * kAttnWaves);  // 32 rows x 16 chunks of 8 dims
+  const u32x4_t zero4 = {0u, 0u, 0u, 0u};
+  u32x4_t qv[kQChunks];
+#pragma unroll
+  for (int c = 0; c < kQChunks; ++c) {
+    const int chunk = c * 64 * kAttnWaves + threadIdx.x;
+    const int qr = chunk >> 4, dc = chunk & 15;
+    const int rr = rt * 32 + qr;
+    qv[c] = zero4;
+    if (rr < rows) qv[c] = *(const u32x4_t*)(q + ((int64_t)(rr / G) * nh + kvh * G + rr % G) * HD + dc * 8);
+  }
+  if (b0 < b1) load_pair(ks0 + 32 * (int64_t)b0);
+#pragma unroll
+  for (int c = 0; c < kQChunks; ++c) {
+    const int chunk = c * 64 * kAttnWaves + threadIdx.x;
+    *(u32x4_t*)&qs[chunk >> 4][(chunk & 15) * 8] = qv[c];
+  }
 
   const int r = rt * 32 + ln;
   const bool rvalid = r < rows;
   const int t = rvalid ? r / G : 0;
-  const int hq = kvh * G + (rvalid ? r % G : 0);
-
   uint64_t nbits[PE_TREE_MAX_WORDS];
 #pragma unroll
   for (int w = 0; w < PE_TREE_MAX_WORDS; ++w)
     nbits[w] = (mask_mode == PE_MASK_TREE && w < words && rvalid) ? bits[(int64_t)t * words + w] : 0ull;
 
-  const u32x4_t zero4 = {0u, 0u, 0u, 0u};
-  u32x4_t qf[8];
-  const uint16_t* qp = q + ((int64_t)t * nh + hq) * HD;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) qf[j] = rvalid ? *(const u32x4_t*)(qp + 16 * j + 8 * g) : zero4;
-
+  // O^T accumulators; the first pair's PV MFMAs start from zero, so O holds
+  // no registers while the first pair's K and V are in flight
   f32x16_t o[4];
-#pragma unroll
-  for (int h = 0; h < 4; ++h)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
   float m = kInitMax, l = 0.f;
+  __syncthreads();  // Q staged
 
-  const uint16_t* kbase = kc + (int64_t)kvh * cap * HD;
-  const uint16_t* vbase = vc + (int64_t)kvh * cap * HD;
-  const int64_t jlast = j1 - 1;
-  u32x4_t kf[8], vf[8];
-  auto load_k = [&](int64_t jb) {
-    const uint16_t* kp = kbase + min(jb + ln, jlast) * HD + 8 * g;
+  auto process = [&](int64_t jb, auto first_c) {
+    constexpr bool kFirst = decltype(first_c)::value;
+    // ---- S^T = K Q^T over hd, two 32-key halves
+    f32x16_t sc[2];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) kf[j] = *(const u32x4_t*)(kp + 16 * j);
-  };
-  auto load_v = [&](int64_t jb) {
+    for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int chunk = c * 64 + lane;  // 32 keys x 16 chunks of 8 dims
-      const int koff = chunk >> 4, dc = chunk & 15;
-      vf[c] = *(const u32x4_t*)(vbase + min(jb + koff, jlast) * HD + dc * 8);
-    }
-  };
-  if (b0 < b1) {
-    load_k(ks0 + 32 * (int64_t)b0);
-    load_v(ks0 + 32 * (int64_t)b0);
-  }
-  for (int b = b0; b < b1; ++b) {
-    const int64_t jb = ks0 + 32 * (int64_t)b;
-    const int64_t jnext = ks0 + 32 * (int64_t)min(b + 1, b1 - 1);
-    // ---- S^T = K Q^T over hd
-    f32x16_t sc;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sc[i] = 0.f;
+      for (int i = 0; i < 16; ++i) sc[sb][i] = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      if constexpr (DT == PE_DTYPE_F16)
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[j]),
-                                                    __builtin_bit_cast(f16x8_t, qf[j]), sc, 0, 0, 0);
-      else
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[j]),
-                                                     __builtin_bit_cast(bf16x8_t, qf[j]), sc, 0, 0, 0);
-    }
-    load_k(jnext);
-    // ---- scale + mask, block max (sc[i] holds key jb + 8*(i/4) + 4*g + (i%4) of row ln)
-    float bmax = kInitMax;
-    if (jb + 32 <= min(P, j1) && (mask_mode == PE_MASK_TREE || jb + 32 <= P + 1)) {
-      // a whole block of prefix keys: every key is visible to every node
+      const u32x4_t qf = *(const u32x4_t*)&qs[ln][16 * j + 8 * g];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        sc[i] = rvalid ? sc[i] * scale : kMaskedScore;
-        bmax = fmaxf(bmax, sc[i]);
+      for (int sb = 0; sb < 2; ++sb) {
+        if constexpr (DT == PE_DTYPE_F16)
+          sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[sb][j]),
+                                                          __builtin_bit_cast(f16x8_t, qf), sc[sb], 0, 0, 0);
+        else
+          sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[sb][j]),
+                                                           __builtin_bit_cast(bf16x8_t, qf), sc[sb], 0, 0, 0);
       }
-    } else {
+    }
+    // ---- scale + mask, pair max (sc[sb][i] holds key jb + 32 sb + 8*(i/4) + 4*g + (i%4) of row ln)
+    float bmax = kInitMax;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int64_t kj = jb + 8 * (i >> 2) + 4 * g + (i & 3);
-        const bool ok = rvalid && kj < j1 && key_allowed(kj, P, t, mask_mode, nbits);
-        sc[i] = ok ? sc[i] * scale : kMaskedScore;
-        bmax = fmaxf(bmax, sc[i]);
+    for (int sb = 0; sb < 2; ++sb) {
+      const int64_t kb = jb + 32 * sb;
+      if (kb + 32 <= min(P, j1) && (mask_mode == PE_MASK_TREE || kb + 32 <= P + 1)) {
+        // a whole 32-key half of prefix keys: every key is visible to every node
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          sc[sb][i] = rvalid ? sc[sb][i] * scale : kMaskedScore;
+          bmax = fmaxf(bmax, sc[sb][i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int64_t kj = kb + 8 * (i >> 2) + 4 * g + (i & 3);
+          const bool ok = rvalid && kj < j1 && key_allowed(kj, P, t, mask_mode, nbits);
+          sc[sb][i] = ok ? sc[sb][i] * scale : kMaskedScore;
+          bmax = fmaxf(bmax, sc[sb][i]);
+        }
       }
     }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
     const float mnew = fmaxf(m, bmax);
     const float alpha = expf(m - mnew);
     float psum = 0.f;
-    uint32_t pb[8];
+    uint32_t pb[2][8];
 #pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-      const float p0 = expf(sc[i] - mnew), p1 = expf(sc[i + 1] - mnew);
-      psum += p0 + p1;
-      pb[i >> 1] = (DT == PE_DTYPE_F16) ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
-                                        : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
-    }
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const float p0 = expf(sc[sb][i] - mnew), p1 = expf(sc[sb][i + 1] - mnew);
+        psum += p0 + p1;
+        pb[sb][i >> 1] = (DT == PE_DTYPE_F16)
+                             ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
+                             : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
+      }
     psum += __shfl_xor(psum, 32, 64);
     l = l * alpha + psum;
     // rescale O only if some row's running max moved (alpha == 1 leaves O as is)
     const bool rescale = __builtin_amdgcn_ballot_w64(mnew != m) != 0ull;
     m = mnew;
-    if (rescale) {
+    if (!kFirst && rescale) {
 #pragma unroll
       for (int h = 0; h < 4; ++h)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[h][i] *= alpha;
     }
-
-    // ---- V^T into LDS, then the next block's V
+    // ---- O^T += V^T P^T, one 32-key half at a time: V rows to LDS with 16-byte
+    // stores, then ds_read_b64_tr_b16 hands each lane 4 consecutive keys of one
+    // dim (within a 16-lane group, out lane i gets element i % 4 of the 8 bytes
+    // at source lanes i / 4 + 4k, k < 4: source lane j points at key kb + j / 4,
+    // dims db + 4 (j % 4), so out lane i holds dim db + i of keys kb .. kb + 3).
+    const int qg = lane >> 4, jl = lane & 15;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int chunk = c * 64 + lane;
-      const int koff = chunk >> 4, dc = chunk & 15;
-      const uint16_t* ve = (const uint16_t*)&vf[c];
+    for (int sb = 0; sb < 2; ++sb) {
+      if (sb == 1) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vt[dc * 8 + e][koff] = ve[e];
-    }
-    load_v(jnext);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ---- O^T += V^T P^T: two 16-key halves c; lane group g holds keys 16c+4g+{0..3}, 16c+8+4g+{0..3}
+      for (int c = 0; c < 8; ++c) *(u32x4_t*)&vs[4 * c + (lane >> 4)][(lane & 15) * 8] = vf[sb][c];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      u32x4_t bp;
-      bp[0] = pb[4 * c + 0];
-      bp[1] = pb[4 * c + 1];
-      bp[2] = pb[4 * c + 2];
-      bp[3] = pb[4 * c + 3];
+      for (int cq = 0; cq < 2; ++cq) {
+        const int c = 2 * sb + cq;  // 16-key quarter of the pair
+        u32x4_t bp;
+        bp[0] = pb[sb][4 * cq + 0];
+        bp[1] = pb[sb][4 * cq + 1];
+        bp[2] = pb[sb][4 * cq + 2];
+        bp[3] = pb[sb][4 * cq + 3];
+        // the P^T operand (from the S^T accumulator) holds keys 4g + {0..3} and
+        // 8 + 4g + {0..3} of the quarter in lane group g; V^T follows the same order
+        const int kb = 16 * cq + 4 * (qg >> 1) + (jl >> 2);
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const int d = h * 32 + ln;
-        const uint2 lo = *(const uint2*)&vt[d][16 * c + 4 * g];
-        const uint2 hi = *(const uint2*)&vt[d][16 * c + 8 + 4 * g];
-        u32x4_t a;
-        a[0] = lo.x;
-        a[1] = lo.y;
-        a[2] = hi.x;
-        a[3] = hi.y;
-        if constexpr (DT == PE_DTYPE_F16)
-          o[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
-                                                        __builtin_bit_cast(f16x8_t, bp), o[h], 0, 0, 0);
-        else
-          o[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                         __builtin_bit_cast(bf16x8_t, bp), o[h], 0, 0, 0);
+        for (int h = 0; h < 4; ++h) {
+          const int db = 32 * h + 16 * (qg & 1) + 4 * (jl & 3);
+          typedef short s4v_t __attribute__((__vector_size__(4 * sizeof(short))));
+          typedef __attribute__((address_space(3))) s4v_t lds_s4v_t;
+          const s4v_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb][db]);
+          const s4v_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb + 8][db]);
+          const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+          u32x4_t a;
+          a[0] = l2.x;
+          a[1] = l2.y;
+          a[2] = h2.x;
+          a[3] = h2.y;
+          f32x16_t cin = o[h];
+          if (kFirst && c == 0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) cin[i] = 0.f;
+          }
+          if constexpr (DT == PE_DTYPE_F16)
+            o[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                          __builtin_bit_cast(f16x8_t, bp), cin, 0, 0, 0);
+          else
+            o[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                           __builtin_bit_cast(bf16x8_t, bp), cin, 0, 0, 0);
+        }
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
+  };
 
-  // ---- merge the waves: (m, l, O) of waves 1..3 through LDS, wave 0 sums in wave order
-  __syncthreads();
-  float* cmb = (float*)smem;
-  if (wave > 0) {
-    float* cw = cmb + (int64_t)(wave - 1) * 32 * (HD + 2);
-    if (g == 0) {
-      cw[ln * (HD + 2) + HD] = m;
-      cw[ln * (HD + 2) + HD + 1] = l;
-    }
+  if (b0 < b1) {
+    process(ks0 + 32 * (int64_t)b0, std::true_type());
+  } else {
 #pragma unroll
     for (int h = 0; h < 4; ++h)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) cw[ln * (HD + 2) + h * 32 + 8 * (i >> 2) + 4 * g + (i & 3)] = o[h][i];
+      for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
   }
-  __syncthreads();
-  if (wave != 0 || !rvalid) return;
-  float mw[kAttnWaves], wt[kAttnWaves];
-  mw[0] = m;
-  float M = m;
-#pragma unroll
-  for (int w = 1; w < kAttnWaves; ++w) {
-    mw[w] = cmb[(int64_t)(w - 1) * 32 * (HD + 2) + ln * (HD + 2) + HD];
-    M = fmaxf(M, mw[w]);
+  for (int b = b0 + 2; b < b1; b += 2) {  // caches longer than one round of pairs
+    load_pair(ks0 + 32 * (int64_t)b);
+    process(ks0 + 32 * (int64_t)b, std::false_type());
   }
-  float L = 0.f;
-#pragma unroll
-  for (int w = 0; w < kAttnWaves; ++w) {
-    wt[w] = expf(mw[w] - M);
-    const float lw = (w == 0) ? l : cmb[(int64_t)(w - 1) * 32 * (HD + 2) + ln * (HD + 2) + HD + 1];
-    L += wt[w] * lw;
-  }
-  const int64_t pidx = ((int64_t)kvh * splits + split) * rows_pad + r;
-  float* op = opart + pidx * HD;
+
+  // ---- merge the waves (wave order) with all threads: thread (row, kDimsT-dim
+  // chunk) sums its outputs over the waves; the merged (O, m, l) is this
+  // workgroup's split partial (a single split writes the output).
+  __syncthreads();  // every wave is done with Q and its V^T tile
+  float* cmb = (float*)smem;                     // [wave][row][kCmbRow]: O of the wave's keys
+  float* mlw = cmb + kAttnWaves * 32 * kCmbRow;  // [wave][row][2]: m, l
 #pragma unroll
   for (int h = 0; h < 4; ++h)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int d = h * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-      float v = wt[0] * o[h][i];
-#pragma unroll
-      for (int w = 1; w < kAttnWaves; ++w) v += wt[w] * cmb[(int64_t)(w - 1) * 32 * (HD + 2) + ln * (HD + 2) + d];
-      op[d] = v;
-    }
+    for (int i = 0; i < 16; ++i) cmb[(wave * 32 + ln) * kCmbRow + h * 32 + 8 * (i >> 2) + 4 * g + (i & 3)] = o[h][i];
   if (g == 0) {
-    mlpart[pidx * 2 + 0] = M;
-    mlpart[pidx * 2 + 1] = L;
+    mlw[(wave * 32 + ln) * 2] = m;
+    mlw[(wave * 32 + ln) * 2 + 1] = l;
   }
+  __syncthreads();
+  constexpr int kDimsT = HD * 32 / (64 * kAttnWaves);  // output dims per thread
+  const int row = threadIdx.x / (HD / kDimsT), dc = (threadIdx.x % (HD / kDimsT)) * kDimsT;
+  float M = kInitMax;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, mlw[(w * 32 + row) * 2]);
+  float L = 0.f, acc[kDimsT];
+#pragma unroll
+  for (int k = 0; k < kDimsT; ++k) acc[k] = 0.f;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) {
+    const float wt = expf(mlw[(w * 32 + row) * 2] - M);
+    L += wt * mlw[(w * 32 + row) * 2 + 1];
+#pragma unroll
+    for (int k = 0; k < kDimsT; ++k) acc[k] += wt * cmb[(w * 32 + row) * kCmbRow + dc + k];
+  }
+  const int rr = rt * 32 + row;
+  auto write_out = [&](const float (&num)[kDimsT], float den) {
+    if (rr >= rows) return;
+    const int tt = rr / G, col0 = (kvh * G + rr % G) * HD + dc;
+#pragma unroll
+    for (int k = 0; k < kDimsT; ++k)
+      Elem<DT>::store((typename Elem<DT>::T*)out,
+                      out_units ? xtile_index(tt, col0 + k, out_units) : (int64_t)tt * ld_out + col0 + k,
+                      num[k] / den);
+  };
+  if (splits == 1) {
+    write_out(acc, L);
+    return;
+  }
+  // partial[pair][split][row][128] and ml[pair][split][row][4] (m, l, -, -),
+  // pair = kvh * row_tiles + rt: plain coalesced stores; attn_combine_kernel
+  // reads them after the kernel boundary
+  const int row_tiles = rows_pad >> 5;
+  const int64_t pr = (((int64_t)(kvh * row_tiles + rt) * splits) + split) * 32 + row;
+  f32x4_t* op = (f32x4_t*)(opart + pr * HD + dc);
+#pragma unroll
+  for (int k = 0; k < kDimsT / 4; ++k) op[k] = f32x4_t{acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]};
+  if (dc == 0) *(f32x4_t*)(mlpart + pr * 4) = f32x4_t{M, L, 0.f, 0.f};
 }
 
-// out[t][hq*hd + d] = sum_s e^{m_s - M} O_s[d] / sum_s e^{m_s - M} l_s
+// out rows of one (KV head, row tile) pair from its split partials, in split
+// order (online: running max, rescaled sums):
+// out = sum_s e^{m_s - M} O_s / sum_s e^{m_s - M} l_s. One wave = 8 rows; a
+// lane owns 16 dims of one row and has every split's loads in flight at once.
 template <int DT>
-__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ opart,
-                                                           const float* __restrict__ mlpart, int nh, int nkv, int T,
-                                                           int hd, int splits, int rows_pad,
-                                                           typename Elem<DT>::T* __restrict__ out, int64_t ld_out,
-                                                           int out_units) {
-  const int r = blockIdx.x, kvh = blockIdx.y;
-  const int G = nh / nkv;
-  const int t = r / G, hq = kvh * G + r % G;
-  float M = kInitMax;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, mlpart[(((int64_t)kvh * splits + s) * rows_pad + r) * 2]);
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < splits; ++s) {
-      const int64_t pidx = ((int64_t)kvh * splits + s) * rows_pad + r;
-      const float w = expf(mlpart[pidx * 2] - M);
-      den += w * mlpart[pidx * 2 + 1];
-      num += w * opart[pidx * hd + d];
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ opart,
+                                                          const float* __restrict__ mlpart, int nh, int nkv, int T,
+                                                          int splits, int rows_pad, void* __restrict__ out,
+                                                          int64_t ld_out, int out_units) {
+  constexpr int HD = 128;
+  const int pair = blockIdx.x, row_tiles = rows_pad >> 5;
+  const int kvh = pair / row_tiles, rt = pair % row_tiles;
+  const int G = nh / nkv, rows = T * G;
+  const int row = blockIdx.y * 8 + (threadIdx.x >> 3), dc = (threadIdx.x & 7) * 16;
+  const int rr = rt * 32 + row;
+  if (rr >= rows) return;
+  const int64_t pb0 = (int64_t)pair * splits * 32 + row;
+  float Mx = kInitMax, den = 0.f, num[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) num[k] = 0.f;
+  for (int c0 = 0; c0 < splits; c0 += 8) {
+    f32x4_t ov[8][4], mv[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int sp = c0 + c;
+      if (sp < splits) {
+        const f32x4_t* op = (const f32x4_t*)(opart + (pb0 + (int64_t)sp * 32) * HD + dc);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ov[c][k] = op[k];
+        mv[c] = *(const f32x4_t*)(mlpart + (pb0 + (int64_t)sp * 32) * 4);
+      }
     }
-    const int col = hq * hd + d;
-    Elem<DT>::store(out, out_units ? xtile_index(t, col, out_units) : (int64_t)t * ld_out + col, num / den);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      if (c0 + c >= splits) break;
+      const float mn = fmaxf(Mx, mv[c][0]);
+      const float a = expf(Mx - mn), wt = expf(mv[c][0] - mn);
+      Mx = mn;
+      den = den * a + wt * mv[c][1];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) num[k] = num[k] * a + wt * ov[c][k >> 2][k & 3];
+    }
   }
+  const int tt = rr / G, col0 = (kvh * G + rr % G) * HD + dc;
+#pragma unroll
+  for (int k = 0; k < 16; ++k)
+    Elem<DT>::store((typename Elem<DT>::T*)out,
+                    out_units ? xtile_index(tt, col0 + k, out_units) : (int64_t)tt * ld_out + col0 + k, num[k] / den);
 }
+
 
 // Generic path (fp32, any hd <= 256): one block per (row t, query head), all keys.
 template <int DT>
@@ -345,7 +444,7 @@ __global__ __launch_bounds__(128) void attn_generic_kernel(
 
 struct AttnPlan {
   int splits, keys_per_split, row_tiles, rows_pad;
-  int64_t opart_bytes, ml_bytes;
+  int64_t opart_bytes, ml_bytes;  // workspace: [O partials | (m, l) partials]
 };
 
 AttnPlan attn_plan(int T, int nh, int nkv, int64_t S) {
@@ -353,17 +452,21 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S) {
   const int rows = T * (nh / nkv);
   p.row_tiles = (rows + 31) / 32;
   p.rows_pad = p.row_tiles * 32;
-  // about one workgroup per CU, each with at least two 32-key blocks per wave
-  int64_t want = (256 + (int64_t)nkv * p.row_tiles - 1) / ((int64_t)nkv * p.row_tiles);
-  int64_t maxsplit = (S + 32 * 2 * kAttnWaves - 1) / (32 * 2 * kAttnWaves);
-  if (want > maxsplit) want = maxsplit;
+  // about one 32-key block per wave (a wave takes up to a pair in one round),
+  // with at most one workgroup per CU; longer caches give each wave more
+  // rounds of pairs
+  const int64_t pairs = (int64_t)nkv * p.row_tiles;
+  int64_t want = ((S + 31) / 32 + kAttnWaves - 1) / kAttnWaves;
+  int64_t cap_splits = 256 / pairs;
+  if (cap_splits > kAttnMaxSplits) cap_splits = kAttnMaxSplits;
+  if (want > cap_splits) want = cap_splits;
   if (want < 1) want = 1;
   int64_t kps = (S + want - 1) / want;
   kps = ((kps + 31) / 32) * 32;
   p.keys_per_split = (int)kps;
   p.splits = (int)((S + kps - 1) / kps);
   p.opart_bytes = (int64_t)nkv * p.splits * p.rows_pad * 128 * 4;
-  p.ml_bytes = (int64_t)nkv * p.splits * p.rows_pad * 2 * 4;
+  p.ml_bytes = (int64_t)nkv * p.splits * p.rows_pad * 4 * 4;
   return p;
 }
 
@@ -396,23 +499,23 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
     float* opart = (float*)workspace;
     float* ml = (float*)((char*)workspace + p.opart_bytes);
     dim3 grid(nkv, p.splits, p.row_tiles);
-    dim3 cgrid(T * (nh / nkv), nkv);
+    dim3 cgrid(nkv * p.row_tiles, 4);
     if (dtype == PE_DTYPE_BF16) {
-      attn_wg_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
-                                                           (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
-                                                           mask_mode, bits, words, scale, p.keys_per_split,
-                                                           p.splits, p.rows_pad, opart, ml);
+      attn_wg_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P, mask_mode,
+          bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, out, ld_out, out_units);
       PE_CHECK_LAUNCH();
-      attn_combine_kernel<PE_DTYPE_BF16><<<cgrid, 128, 0, st>>>(opart, ml, nh, nkv, T, hd, p.splits, p.rows_pad,
-                                                                (uint16_t*)out, ld_out, out_units);
+      if (p.splits > 1)
+        attn_combine_kernel<PE_DTYPE_BF16><<<cgrid, 64, 0, st>>>(opart, ml, nh, nkv, T, p.splits, p.rows_pad, out,
+                                                                 ld_out, out_units);
     } else if (dtype == PE_DTYPE_F16) {
-      attn_wg_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
-                                                          (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
-                                                          mask_mode, bits, words, scale, p.keys_per_split, p.splits,
-                                                          p.rows_pad, opart, ml);
+      attn_wg_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P, mask_mode,
+          bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, out, ld_out, out_units);
       PE_CHECK_LAUNCH();
-      attn_combine_kernel<PE_DTYPE_F16><<<cgrid, 128, 0, st>>>(opart, ml, nh, nkv, T, hd, p.splits, p.rows_pad,
-                                                               (uint16_t*)out, ld_out, out_units);
+      if (p.splits > 1)
+        attn_combine_kernel<PE_DTYPE_F16><<<cgrid, 64, 0, st>>>(opart, ml, nh, nkv, T, p.splits, p.rows_pad, out,
+                                                                ld_out, out_units);
     } else {
       return PE_ERR_ARG;
     }

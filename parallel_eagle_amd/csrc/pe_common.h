@@ -11,6 +11,7 @@ typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 #define PE_WAVE 64
 
@@ -87,6 +88,23 @@ __host__ __device__ __forceinline__ int64_t xtile_index(int row, int col, int un
 }
 // Bytes of an A-tiled [M][K] 16-bit activation.
 __host__ __device__ __forceinline__ int64_t xtile_bytes(int M, int K) { return (int64_t)((M + 31) / 32) * K * 64; }
+
+// Data handed between workgroups of one launch (split partials read by the
+// last workgroup to arrive): 16-byte accesses with cache policy sc1, i.e.
+// agent-coherent, written through to / read from the level all XCDs share,
+// and still coalesced across the wave (unlike one atomic per lane). Through a
+// buffer resource over [base, base + bytes); the compiler tracks the waits.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t agent_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+constexpr int kCpolSC1 = 16;
+typedef unsigned int pe_u4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_agent_x4(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(pe_u4_t, v), r, off, 0, kCpolSC1);
+}
+__device__ __forceinline__ f32x4_t load_agent_x4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSC1));
+}
 
 #define PE_CHECK_LAUNCH()                                   \
   do {                                                      \

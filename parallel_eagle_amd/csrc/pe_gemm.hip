@@ -194,7 +194,6 @@ __device__ __forceinline__ void nf4_read8(const uint32_t (&a)[8], uint32_t (&r)[
 __device__ __forceinline__ uint32_t pack16(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 // The lane's 16 table entries for two block pairs at once: entry c (at lane
 // base + 256 c + OFF) holds bf16_rne(NF4[c] * scale0) in its low half and
@@ -273,21 +272,16 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
 
   if (S > 1) {
     const int groups = e.N / (32 * NT);
-    // partial[split][group][mt][nt][wave][lane][4]
-    auto slot = [&](int sp, int mt, int nt) -> uint64_t* {
-      return (uint64_t*)(partial + ((((((int64_t)sp * groups + group) * MT + mt) * NT + nt) * kWaves + wave) * 64 +
-                                    lane) * 4);
+    // partial[split][group][mt][nt][wave][lane][4], agent-coherent 16-byte accesses
+    const __amdgpu_buffer_rsrc_t rp = agent_rsrc(partial, (uint32_t)partial_bytes_of(S, groups, MT, NT));
+    auto slot = [&](int sp, int mt, int nt) -> uint32_t {
+      return (uint32_t)((((((int64_t)sp * groups + group) * MT + mt) * NT + nt) * kWaves + wave) * 64 + lane) * 16;
     };
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        uint64_t* p = slot(split, mt, nt);
-        const uint64_t lo = __builtin_bit_cast(uint64_t, f32x2_t{v[mt][0][nt], v[mt][1][nt]});
-        const uint64_t hi = __builtin_bit_cast(uint64_t, f32x2_t{v[mt][2][nt], v[mt][3][nt]});
-        __hip_atomic_store(p, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      for (int nt = 0; nt < NT; ++nt)
+        store_agent_x4(rp, slot(split, mt, nt), f32x4_t{v[mt][0][nt], v[mt][1][nt], v[mt][2][nt], v[mt][3][nt]});
     // the stores are acknowledged at agent scope before this workgroup counts itself
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -306,7 +300,7 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
         for (int nt = 0; nt < NT; ++nt) sum[mt][j][nt] = 0.f;
     // up to 8 splits' loads in flight at a time, summed in split order
     for (int c0 = 0; c0 < S; c0 += 8) {
-      uint64_t got[8][MT][NT][2];
+      f32x4_t got[8][MT][NT];
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         const int sp = c0 + c;
@@ -314,11 +308,7 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-              uint64_t* p = slot(sp, mt, nt);
-              got[c][mt][nt][0] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              got[c][mt][nt][1] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            for (int nt = 0; nt < NT; ++nt) got[c][mt][nt] = load_agent_x4(rp, slot(sp, mt, nt));
         }
       }
 #pragma unroll
@@ -328,19 +318,9 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            float q[4];
-            if (sp == split) {
+          for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-              for (int j = 0; j < 4; ++j) q[j] = v[mt][j][nt];
-            } else {
-              const f32x2_t a = __builtin_bit_cast(f32x2_t, got[c][mt][nt][0]);
-              const f32x2_t b = __builtin_bit_cast(f32x2_t, got[c][mt][nt][1]);
-              q[0] = a[0]; q[1] = a[1]; q[2] = b[0]; q[3] = b[1];
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) sum[mt][j][nt] += q[j];
-          }
+            for (int j = 0; j < 4; ++j) sum[mt][j][nt] += (sp == split) ? v[mt][j][nt] : got[c][mt][nt][j];
       }
     }
 #pragma unroll

@@ -29,6 +29,10 @@ constexpr int64_t kCounterBytes = 32768;
 int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 int esize(int dtype) { return dtype == PE_DTYPE_F32 ? 4 : 2; }
 
+// Offsets into the pass workspace. The GEMM arrival counters sit at the head
+// of the GEMM region, at offset 0 whatever M is, so a counter is never memory
+// another pass shape used for data; they are zero on first use and every
+// launch leaves them zero.
 struct Layout {
   int64_t gemm;  // GEMM arrival counters, then split-K partials
   int64_t gemm_bytes;
@@ -305,8 +309,9 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
                   m->b_qkv ? m->b_qkv[l] : nullptr, nullptr, 0, qkv, nqkv, gws, gwsb, st));
     PE_TRY(pe_rope_qkv(qkv, nqkv, M, nh, nkv, hd, a->positions, m->rope_cos_sin, m->max_positions, m->dtype, q, kc, vc,
                        a->cache_capacity, a->prefix_len, a->status, st));
-    PE_TRY(pe_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode, a->tree_bits,
-                             a->bits_words, scale, m->dtype, attn, qd, aws, Lo.attn_ws_bytes, st));
+    PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
+                                      a->tree_bits, a->bits_words, scale, m->dtype, attn, qd, 0, aws,
+                                      Lo.attn_ws_bytes, st));
     PE_TRY(linear(m, attn, qd, M, qd, m->w_o[l], m->a_o ? m->a_o[l] : nullptr, H, PE_EPI_RESIDUAL, nullptr, h, H, h,
                   H, gws, gwsb, st));
     PE_TRY(pe_rmsnorm(h, H, M, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, H, st));
