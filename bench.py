@@ -21,10 +21,15 @@ by the measured pass time (GB/s), ``ms_per_step`` = pass latency, plus
   8 TB/s HBM peak;
 - ``cpu_baseline``: the CPU restatement of the reference path (per-call NF4
   dequantise, bf16 matmuls, masked SDPA, acceptance walk, index_select commit)
-  timed on the host cores on a 2-layer slice of the same shape and scaled to
-  the full layer count.
+  timed on the host cores on a 4-layer slice of the same shape and scaled to
+  the full layer count;
+- ``roofline.traffic``: HBM bytes per NF4 GEMM launch as rocprofv3's
+  FETCH_SIZE + WRITE_SIZE counters read them (calibrated on a plain copy, see
+  ``--calibrate-copy``), taken from the committed profile summary of this
+  workload.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload NAME] [--no-cpu-baseline]
+       python bench.py --calibrate-copy
 """
 
 from __future__ import annotations
@@ -54,9 +59,27 @@ def parse_args(argv=None):
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--gemm-reps", type=int, default=10, help="replays of the per-pass NF4 GEMM sequence")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-layers", type=int, default=2, help="layers of the CPU-path sample")
-    p.add_argument("--cpu-runs", type=int, default=3)
+    p.add_argument("--cpu-layers", type=int, default=4, help="layers of the CPU-path sample")
+    p.add_argument("--cpu-runs", type=int, default=12)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a 256 MiB device copy three times (the known-size kernel the HBM counters "
+                        "FETCH_SIZE / WRITE_SIZE are calibrated on)")
     return p.parse_args(argv)
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "nf4_gemm_traffic_llama2-7b-nf4-T26-P2048.md")
+
+
+def profiled_traffic(workload: str):
+    """HBM bytes per NF4 GEMM launch measured with rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, calibrated on a plain copy) for this workload, from the committed
+    profile summary; None if there is none."""
+    if workload != DEFAULT_WORKLOAD or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    for line in open(TRAFFIC_PROFILE):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
 
 
 def log(msg: str) -> None:
@@ -125,10 +148,10 @@ def time_pass(step, steps: int, warmup: int):
 
 def nf4_gemm_roofline(tm, wl, reps: int):
     """Mean duration and algorithmic bytes per launch of the NF4 dequant-GEMM
-    over one pass's 4 * L launches (same shapes, weights and epilogues as
-    pe_forward issues), replayed from a HIP graph."""
-    import ctypes as C
-
+    kernel as the pass runs it: the 4 * L launches of one pass (q/k/v, o with
+    the residual, gate/up with SwiGLU and an A-tiled output, down with the
+    residual) on A-tiled activations, same weights and shapes, replayed from a
+    HIP graph and timed with HIP events on the stream the launches use."""
     import torch
 
     from parallel_eagle_amd import _lib, ops
@@ -140,12 +163,12 @@ def nf4_gemm_roofline(tm, wl, reps: int):
     nqkv = qd + 2 * kvd
     dev = tm.device
     bf = torch.bfloat16
-    xn = torch.randn((M, H), device=dev).to(bf)
-    attn = torch.randn((M, qd), device=dev).to(bf)
-    act = (0.1 * torch.randn((M, ip), device=dev)).to(bf)
+    xn_t = ops.to_xtile(torch.randn((M, H), device=dev).to(bf))
+    attn_t = ops.to_xtile(torch.randn((M, qd), device=dev).to(bf))
+    act_t = ops.to_xtile((0.1 * torch.randn((M, ip), device=dev)).to(bf))
     qkv = torch.empty((M, nqkv), dtype=bf, device=dev)
     h = torch.randn((M, H), device=dev).to(bf)
-    gu_out = torch.empty((M, ip), dtype=bf, device=dev)
+    gu_t = torch.zeros_like(act_t)
     ws_bytes = max(ops.gemm_workspace_bytes(M, n, k, True, bf, e) for n, k, e in
                    [(nqkv, H, 0), (H, qd, 1), (2 * ip, H, 2), (H, ip, 1)])
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
@@ -153,14 +176,14 @@ def nf4_gemm_roofline(tm, wl, reps: int):
 
     def seq():
         for ly in m.layers:
-            for (x, K, w, a, N, epi, res, out, ldo) in (
-                    (xn, H, ly["w_qkv"], ly["a_qkv"], nqkv, _lib.PE_EPI_STORE, None, qkv, nqkv),
-                    (attn, qd, ly["w_o"], ly["a_o"], H, _lib.PE_EPI_RESIDUAL, h, h, H),
-                    (xn, H, ly["w_gu"], ly["a_gu"], 2 * ip, _lib.PE_EPI_SWIGLU, None, gu_out, ip),
-                    (act, ip, ly["w_down"], ly["a_down"], H, _lib.PE_EPI_RESIDUAL, h, h, H)):
-                _lib.check(L.pe_nf4_gemm(x.data_ptr(), K, M, K, w.data_ptr(), a.data_ptr(), N, epi, None,
-                                         res.data_ptr() if res is not None else None, H, out.data_ptr(), ldo,
-                                         ws.data_ptr(), ws.numel(), st()), "pe_nf4_gemm")
+            for (x, K, w, a, N, epi, res, out, ldo, ou) in (
+                    (xn_t, H, ly["w_qkv"], ly["a_qkv"], nqkv, _lib.PE_EPI_STORE, None, qkv, nqkv, 0),
+                    (attn_t, qd, ly["w_o"], ly["a_o"], H, _lib.PE_EPI_RESIDUAL, h, h, H, 0),
+                    (xn_t, H, ly["w_gu"], ly["a_gu"], 2 * ip, _lib.PE_EPI_SWIGLU, None, gu_t, 0, ip // 128),
+                    (act_t, ip, ly["w_down"], ly["a_down"], H, _lib.PE_EPI_RESIDUAL, h, h, H, 0)):
+                _lib.check(L.pe_nf4_gemm_tiled(x.data_ptr(), M, K, w.data_ptr(), a.data_ptr(), N, epi, None,
+                                               res.data_ptr() if res is not None else None, H, out.data_ptr(), ldo,
+                                               ou, ws.data_ptr(), ws.numel(), st()), "pe_nf4_gemm_tiled")
 
     seq()
     torch.cuda.synchronize()
@@ -169,6 +192,7 @@ def nf4_gemm_roofline(tm, wl, reps: int):
         seq()
     g.replay()
     torch.cuda.synchronize()
+    # events on the current stream, which is the stream the replay runs on
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -188,8 +212,8 @@ def nf4_gemm_roofline(tm, wl, reps: int):
                  + nf4_bytes(H, s.intermediate) + 2 * M * s.intermediate + 2 * 2 * M * H)
     bytes_per_launch = per_layer * s.num_layers / launches
     gbs = bytes_per_launch / (mean_us * 1e-6) / 1e9
-    _ = C
-    return {"kernel": "mfma_gemm_kernel<NF4> (q/k/v, o, gate/up+SwiGLU, down; all launches of one pass)",
+    return {"kernel": "nf4_gemm_kernel (A-tiled X; q/k/v, o+residual, gate/up+SwiGLU, down+residual: "
+                      "the 4 x L launches of one pass)",
             "mean_launch_us": round(mean_us, 3), "bytes_per_launch": int(bytes_per_launch),
             "achieved": round(gbs, 1)}
 
@@ -284,6 +308,14 @@ def main(argv=None) -> int:
 
     from parallel_eagle_amd.config import WORKLOADS, algorithmic_bytes
 
+    if a.calibrate_copy:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied 256 MiB three times")
+        return 0
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
@@ -306,8 +338,9 @@ def main(argv=None) -> int:
         log(f"NF4 GEMM: {r['mean_launch_us']} us per launch, {r['bytes_per_launch'] / 1e6:.2f} MB -> "
             f"{r['achieved']} GB/s")
         roof = {"bound": "hbm", "achieved": r["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": r["kernel"],
-                "mean_launch_us": r["mean_launch_us"], "bytes_per_launch": r["bytes_per_launch"]}
+                "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(wl.name),
+                "kernel": r["kernel"], "mean_launch_us": r["mean_launch_us"],
+                "bytes_per_launch": r["bytes_per_launch"]}
     cpu = None
     if not a.no_cpu_baseline:
         del step

@@ -105,6 +105,16 @@ int pe_nf4_gemm(const void* x, int64_t ldx, int M, int K, const uint8_t* w_tiled
                 const uint16_t* absmax_tiled, int N, int epilogue, const void* bias,
                 const void* resid, int64_t ld_resid, void* out, int64_t ld_out, void* workspace,
                 int64_t workspace_bytes, void* stream);
+/* pe_nf4_gemm on the activation layout the fused pass hands between kernels:
+ * x is A-tiled (element (m, k) at ((((m/32)*(K/128) + k/128)*8 + (k%64)/8)*64
+ * + m%32 + 32*((k%128)/64))*8 + k%8), M <= 64; with out_units > 0 (N/128 for
+ * PE_EPI_STORE, N/256 for PE_EPI_SWIGLU) the output is A-tiled too (not with
+ * PE_EPI_RESIDUAL). Same kernels and results as pe_nf4_gemm; no counterpart in
+ * the reference (a layout variant of its dequantize + F.linear, used by the
+ * pass and timed on its own by the benchmark). */
+int pe_nf4_gemm_tiled(const void* x_tiled, int M, int K, const uint8_t* w_tiled, const uint16_t* absmax_tiled,
+                      int N, int epilogue, const void* bias, const void* resid, int64_t ld_resid, void* out,
+                      int64_t ld_out, int out_units, void* workspace, int64_t workspace_bytes, void* stream);
 /* Dense linear in dtype (bf16/fp16 MFMA on tiled weights, fp32 VALU on row-major).
  * Replaces F.linear in HF modeling_llama.py:175,254-256,280,480. */
 int pe_dense_gemm(const void* x, int64_t ldx, int M, int K, const void* w, int dtype, int N,

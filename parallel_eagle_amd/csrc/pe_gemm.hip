@@ -822,6 +822,15 @@ extern "C" int pe_nf4_gemm(const void* x, int64_t ldx, int M, int K, const uint8
                    ld_out, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
+extern "C" int pe_nf4_gemm_tiled(const void* x_tiled, int M, int K, const uint8_t* w_tiled,
+                                 const uint16_t* absmax_tiled, int N, int epilogue, const void* bias,
+                                 const void* resid, int64_t ld_resid, void* out, int64_t ld_out, int out_units,
+                                 void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!absmax_tiled || M > kMaxChunkRows || out_units < 0) return PE_ERR_ARG;
+  return mfma_gemm(kFmtNF4, x_tiled, K, M, K, w_tiled, absmax_tiled, N, epilogue, bias, resid, ld_resid, out, ld_out,
+                   workspace, workspace_bytes, (hipStream_t)stream, true, out_units);
+}
+
 extern "C" int pe_dense_gemm(const void* x, int64_t ldx, int M, int K, const void* w, int dtype, int N,
                              int epilogue, const void* bias, const void* resid, int64_t ld_resid, void* out,
                              int64_t ld_out, void* workspace, int64_t workspace_bytes, void* stream) {

@@ -136,6 +136,49 @@ def linear(x: torch.Tensor, n: int, *, nf4: tuple | None = None, dense: torch.Te
     return out
 
 
+def xtile_index(m: int, k: int, device=None) -> torch.Tensor:
+    """[m][k] -> flat position of each element in the A-tiled activation layout
+    (the order the NF4 GEMM reads X as its MFMA A operand; k % 128 == 0)."""
+    _req(k % 128 == 0, "A-tiled activations need K % 128 == 0")
+    row = torch.arange(m, device=device).view(m, 1)
+    col = torch.arange(k, device=device).view(1, k)
+    units = k // 128
+    mt, ln = row // 32, row % 32
+    p, c = col // 128, col % 128
+    return ((((mt * units + p) * 8 + (c % 64) // 8) * 64 + ln + 32 * (c // 64)) * 8 + c % 8)
+
+
+def to_xtile(x: torch.Tensor) -> torch.Tensor:
+    """Row-major [M][K] -> A-tiled flat buffer (rows past M of the last 32-row
+    tile are zero)."""
+    m, k = x.shape
+    out = torch.zeros(((m + 31) // 32) * 32 * k, dtype=x.dtype, device=x.device)
+    out[xtile_index(m, k, x.device).flatten()] = x.flatten()
+    return out
+
+
+def from_xtile(t: torch.Tensor, m: int, k: int) -> torch.Tensor:
+    return t[xtile_index(m, k, t.device).flatten()].view(m, k)
+
+
+def linear_tiled(xt: torch.Tensor, m: int, k: int, n: int, nf4: tuple, *, epilogue: int = _lib.PE_EPI_STORE,
+                 resid: torch.Tensor | None = None, out: torch.Tensor | None = None, out_tiled: bool = False,
+                 workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """pe_nf4_gemm_tiled: X given A-tiled (to_xtile); the output row-major, or
+    A-tiled when out_tiled."""
+    n_out = n // 2 if epilogue == _lib.PE_EPI_SWIGLU else n
+    if out is None:
+        out = (torch.zeros(((m + 31) // 32) * 32 * n_out, dtype=xt.dtype, device=xt.device) if out_tiled
+               else torch.empty((m, n_out), dtype=xt.dtype, device=xt.device))
+    if workspace is None:
+        workspace = _workspace(gemm_workspace_bytes(m, n, k, True, xt.dtype, epilogue), xt.device)
+    check(lib().pe_nf4_gemm_tiled(ptr(xt), m, k, ptr(nf4[0]), ptr(nf4[1]), n, epilogue, None, ptr(resid),
+                                  resid.stride(0) if resid is not None else 0, ptr(out),
+                                  0 if out_tiled else out.stride(0), n_out // 128 if out_tiled else 0,
+                                  ptr(workspace), workspace.numel(), stream_ptr()), "linear_tiled")
+    return out
+
+
 # ------------------------------------------------------------------ elementwise
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     _req(x.dim() == 2 and x.stride(1) == 1 and w.dtype == x.dtype, "bad rmsnorm args")

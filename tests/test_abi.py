@@ -7,6 +7,7 @@ import re
 from pathlib import Path
 
 import pytest
+import torch
 
 from parallel_eagle_amd import _lib
 
@@ -63,3 +64,30 @@ def test_host_validation_rejects_bad_arguments(lib):
     # a split-K shape without workspace is refused, not launched
     assert lib.pe_dense_gemm(C.c_void_p(8), 0, 26, 4096, C.c_void_p(8), 1, 4096, 2, None, None, 0,
                              C.c_void_p(8), 0, None, 0, None) == _lib.PE_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("m,k", [(26, 128), (33, 256), (64, 4096), (1, 11008)])
+def test_xtile_index_is_a_permutation_of_the_padded_tile(m, k):
+    """The A-tiled activation order covers each element of the 32-row padded
+    tile exactly once, keeps a lane's 8 columns contiguous, and puts 64
+    consecutive lanes (one wave load) in 1 KiB of consecutive memory."""
+    from parallel_eagle_amd import ops
+    idx = ops.xtile_index(m, k).flatten()
+    assert idx.unique().numel() == m * k
+    assert idx.min().item() >= 0 and idx.max().item() < ((m + 31) // 32) * 32 * k
+    # a lane's 8 consecutive columns are 8 consecutive elements
+    full = ops.xtile_index(32, k)
+    assert torch.equal(full[:, 8:16] - full[:, 8:9], torch.arange(8).expand(32, 8))
+    # k-step s of unit 0: lanes (row r, half g) at ((s * 64) + r + 32 g) * 8
+    for s in (0, 5):
+        for g in (0, 1):
+            col = 64 * g + 8 * s
+            assert torch.equal(full[:, col], (s * 64 + torch.arange(32) + 32 * g) * 8)
+
+
+def test_xtile_round_trip():
+    from parallel_eagle_amd import ops
+    x = torch.randn(40, 256)
+    t = ops.to_xtile(x)
+    assert t.numel() == 64 * 256
+    assert torch.equal(ops.from_xtile(t, 40, 256), x)

@@ -87,6 +87,27 @@ def test_nf4_linear_deterministic_and_batch_invariant():
     assert torch.equal(y1[5:6], y_row)
 
 
+@pytest.mark.parametrize("m", [26, 40])
+@pytest.mark.parametrize("epi", ["store", "residual", "swiglu", "swiglu-tiled-out"])
+def test_nf4_linear_tiled_x_equals_row_major(m, epi):
+    """pe_nf4_gemm_tiled (A-tiled X, optionally A-tiled output) runs the same
+    kernels on the same values as pe_nf4_gemm: results are bit-identical."""
+    n, k = 1024, 2048
+    (tiled, tabs), _ = _nf4_weight(n, k, seed=7 + m)
+    x = torch.from_numpy(synth.normal(m, 34, m * k, 1.0).reshape(m, k)).to(torch.bfloat16).to(DEV)
+    code = {"store": _lib.PE_EPI_STORE, "residual": _lib.PE_EPI_RESIDUAL}.get(epi, _lib.PE_EPI_SWIGLU)
+    n_out = n // 2 if code == _lib.PE_EPI_SWIGLU else n
+    resid = (torch.from_numpy(synth.normal(m, 35, m * n_out, 1.0).reshape(m, n_out)).to(torch.bfloat16).to(DEV)
+             if code == _lib.PE_EPI_RESIDUAL else None)
+    ref = ops.linear(x, n, nf4=(tiled, tabs), epilogue=code, resid=resid)
+    xt = ops.to_xtile(x)
+    if epi == "swiglu-tiled-out":
+        got = ops.from_xtile(ops.linear_tiled(xt, m, k, n, (tiled, tabs), epilogue=code, out_tiled=True), m, n_out)
+    else:
+        got = ops.linear_tiled(xt, m, k, n, (tiled, tabs), epilogue=code, resid=resid)
+    assert torch.equal(got, ref)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("epi", ["store", "bias", "residual", "swiglu"])
 def test_dense_linear_epilogues(dtype, epi):
