@@ -148,10 +148,12 @@ def time_pass(step, steps: int, warmup: int):
 
 def nf4_gemm_roofline(tm, wl, reps: int):
     """Mean duration and algorithmic bytes per launch of the NF4 dequant-GEMM
-    kernel as the pass runs it: the 4 * L launches of one pass (q/k/v, o with
-    the residual, gate/up with SwiGLU and an A-tiled output, down with the
-    residual) on A-tiled activations, same weights and shapes, replayed from a
+    kernel as the pass runs it: the 4 * L launches of one pass (q/k/v, o,
+    gate/up, down; each writing fp32 split partials that the next kernel of the
+    pass sums) on A-tiled activations, same weights and shapes, replayed from a
     HIP graph and timed with HIP events on the stream the launches use."""
+    import ctypes as C
+
     import torch
 
     from parallel_eagle_amd import _lib, ops
@@ -166,24 +168,19 @@ def nf4_gemm_roofline(tm, wl, reps: int):
     xn_t = ops.to_xtile(torch.randn((M, H), device=dev).to(bf))
     attn_t = ops.to_xtile(torch.randn((M, qd), device=dev).to(bf))
     act_t = ops.to_xtile((0.1 * torch.randn((M, ip), device=dev)).to(bf))
-    qkv = torch.empty((M, nqkv), dtype=bf, device=dev)
-    h = torch.randn((M, H), device=dev).to(bf)
-    gu_t = torch.zeros_like(act_t)
-    ws_bytes = max(ops.gemm_workspace_bytes(M, n, k, True, bf, e) for n, k, e in
-                   [(nqkv, H, 0), (H, qd, 1), (2 * ip, H, 2), (H, ip, 1)])
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    part_bytes = max(int(L.pe_nf4_gemm_partials_bytes(M, n, k)) for n, k in
+                     [(nqkv, H), (H, qd), (2 * ip, H), (H, ip)])
+    part = torch.empty(part_bytes // 4, dtype=torch.float32, device=dev)
+    splits = C.c_int(0)
     st = ops.stream_ptr
 
     def seq():
         for ly in m.layers:
-            for (x, K, w, a, N, epi, res, out, ldo, ou) in (
-                    (xn_t, H, ly["w_qkv"], ly["a_qkv"], nqkv, _lib.PE_EPI_STORE, None, qkv, nqkv, 0),
-                    (attn_t, qd, ly["w_o"], ly["a_o"], H, _lib.PE_EPI_RESIDUAL, h, h, H, 0),
-                    (xn_t, H, ly["w_gu"], ly["a_gu"], 2 * ip, _lib.PE_EPI_SWIGLU, None, gu_t, 0, ip // 128),
-                    (act_t, ip, ly["w_down"], ly["a_down"], H, _lib.PE_EPI_RESIDUAL, h, h, H, 0)):
-                _lib.check(L.pe_nf4_gemm_tiled(x.data_ptr(), M, K, w.data_ptr(), a.data_ptr(), N, epi, None,
-                                               res.data_ptr() if res is not None else None, H, out.data_ptr(), ldo,
-                                               ou, ws.data_ptr(), ws.numel(), st()), "pe_nf4_gemm_tiled")
+            for (x, K, w, a, N) in ((xn_t, H, ly["w_qkv"], ly["a_qkv"], nqkv), (attn_t, qd, ly["w_o"], ly["a_o"], H),
+                                    (xn_t, H, ly["w_gu"], ly["a_gu"], 2 * ip), (act_t, ip, ly["w_down"], ly["a_down"], H)):
+                _lib.check(L.pe_nf4_gemm_partials(x.data_ptr(), K, 1, M, K, w.data_ptr(), a.data_ptr(), N,
+                                                  part.data_ptr(), part_bytes, C.byref(splits), st()),
+                           "pe_nf4_gemm_partials")
 
     seq()
     torch.cuda.synchronize()
@@ -201,18 +198,16 @@ def nf4_gemm_roofline(tm, wl, reps: int):
     torch.cuda.synchronize()
     launches = 4 * s.num_layers
     mean_us = e0.elapsed_time(e1) * 1e3 / (reps * launches)
-    # algorithmic bytes: NF4 codes (0.5 B) + fp16 absmax (2 B / 64) + X once + output once
-    # (+ the residual read of the residual epilogues)
+    # algorithmic bytes: NF4 codes (0.5 B) + fp16 absmax (2 B / 64) + bf16 X once + the
+    # linear's bf16 output once
     def nf4_bytes(n, k):
         return n * k // 2 + (n * k // 64) * 2
 
-    per_layer = (nf4_bytes(nqkv, H) + 2 * M * H + 2 * M * nqkv
-                 + nf4_bytes(H, qd) + 2 * M * qd + 2 * 2 * M * H
-                 + nf4_bytes(2 * s.intermediate, H) + 2 * M * H + 2 * M * s.intermediate
-                 + nf4_bytes(H, s.intermediate) + 2 * M * s.intermediate + 2 * 2 * M * H)
+    I = s.intermediate
+    per_layer = sum(nf4_bytes(n, k) + 2 * M * k + 2 * M * n for n, k in ((nqkv, H), (H, qd), (2 * I, H), (H, I)))
     bytes_per_launch = per_layer * s.num_layers / launches
     gbs = bytes_per_launch / (mean_us * 1e-6) / 1e9
-    return {"kernel": "nf4_gemm_kernel (A-tiled X; q/k/v, o+residual, gate/up+SwiGLU, down+residual: "
+    return {"kernel": "nf4_gemm_kernel (A-tiled X, fp32 split partials; q/k/v, o, gate/up, down: "
                       "the 4 x L launches of one pass)",
             "mean_launch_us": round(mean_us, 3), "bytes_per_launch": int(bytes_per_launch),
             "achieved": round(gbs, 1)}

@@ -115,6 +115,16 @@ int pe_nf4_gemm(const void* x, int64_t ldx, int M, int K, const uint8_t* w_tiled
 int pe_nf4_gemm_tiled(const void* x_tiled, int M, int K, const uint8_t* w_tiled, const uint16_t* absmax_tiled,
                       int N, int epilogue, const void* bias, const void* resid, int64_t ld_resid, void* out,
                       int64_t ld_out, int out_units, void* workspace, int64_t workspace_bytes, void* stream);
+/* The NF4 linear as fp32 split partials: partials[S][M][N] with
+ * sum_s partials[s] = X . deq(W)^T (sum in split order s = 0 .. S-1), written
+ * with plain stores and no exchange between workgroups; *splits (host memory)
+ * receives S. X row-major (ldx) or A-tiled (x_tiled != 0). M <= 64, K % 128 == 0,
+ * N % 32 == 0. Layout variant of pe_nf4_gemm with no reference counterpart: the
+ * pass's residual+RMSNorm, RoPE/KV-append and SwiGLU kernels consume it. */
+int64_t pe_nf4_gemm_partials_bytes(int M, int N, int K);
+int pe_nf4_gemm_partials(const void* x, int64_t ldx, int x_tiled, int M, int K, const uint8_t* w_tiled,
+                         const uint16_t* absmax_tiled, int N, float* partials, int64_t partial_bytes, int* splits,
+                         void* stream);
 /* Dense linear in dtype (bf16/fp16 MFMA on tiled weights, fp32 VALU on row-major).
  * Replaces F.linear in HF modeling_llama.py:175,254-256,280,480. */
 int pe_dense_gemm(const void* x, int64_t ldx, int M, int K, const void* w, int dtype, int N,

@@ -97,6 +97,9 @@ SIGNATURES: dict[str, tuple] = {
                               vp, i64, vp]),
     "pe_nf4_gemm_tiled": (C.c_int, [vp, C.c_int, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, i64, vp, i64, C.c_int,
                                     vp, i64, vp]),
+    "pe_nf4_gemm_partials_bytes": (i64, [C.c_int, C.c_int, C.c_int]),
+    "pe_nf4_gemm_partials": (C.c_int, [vp, i64, C.c_int, C.c_int, C.c_int, vp, vp, C.c_int, vp, i64,
+                                       C.POINTER(C.c_int), vp]),
     "pe_dense_gemm": (C.c_int, [vp, i64, C.c_int, C.c_int, vp, C.c_int, C.c_int, C.c_int, vp, vp, i64, vp,
                                 i64, vp, i64, vp]),
     "pe_embed": (C.c_int, [vp, C.c_int, vp, i64, C.c_int, C.c_int, vp, i64, vp, vp]),

@@ -47,8 +47,11 @@
 
 namespace {
 
-// Internal epilogue: the q/k/v projection with bias, RoPE and the in-place KV append.
+// Internal epilogues: the q/k/v projection with bias, RoPE and the in-place KV
+// append; and raw fp32 split partials, out[split][row][col] (ld = N), summed
+// by the kernel that consumes them.
 constexpr int kEpiRopeKV = 4;
+constexpr int kEpiPartial = 5;
 
 struct EpiArgs {
   int op;
@@ -118,10 +121,9 @@ __device__ __forceinline__ f32x16_t mfma16(u32x4_t a, u32x4_t b, f32x16_t c) {
 // j = group % (hd / 64)). The two halves a RoPE pair needs are therefore in
 // the same lane: o1 = r(r(x1 cos1) + r(-x2 sin1)), o2 = r(r(x2 cos2) + r(x1 sin2)).
 template <int DT>
-__device__ __forceinline__ void write_rope_kv(const EpiArgs& e, int group, int row, float a1, float a2) {
+__device__ __forceinline__ void write_rope_kv(const EpiArgs& e, int group, int ln, int row, float a1, float a2) {
   typedef Elem<DT> E;
   typedef typename E::T T;
-  const int lane = threadIdx.x & 63, ln = lane & 31;
   const int gpu = e.hd >> 6;  // column groups per head unit
   const int u = group / gpu, j = group % gpu;
   const int d1 = 32 * j + ln, d2 = d1 + (e.hd >> 1);
@@ -210,6 +212,14 @@ __device__ __forceinline__ void nf4_build_table2(uint8_t* lanetab, uint16_t absm
 
 constexpr int kTabTile = 16 * 64 * 4;  // one tile's table: 16 codes x 64 lanes x dword (2 slots)
 
+// Workgroup barrier that orders LDS accesses only: global loads still in
+// flight (prefetches past the last unit) are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 
 // ---------------------------------------------------------------------------
 // Workgroup output
@@ -226,7 +236,7 @@ __device__ __forceinline__ void epilogue_row(const EpiArgs& e, int group, int ro
   if (e.op == PE_EPI_SWIGLU) {
     if constexpr (NT == 2) epi_swiglu<ADT>(e, row, group * 32 + ln, v[0], v[1]);
   } else if (e.op == kEpiRopeKV) {
-    if constexpr (NT == 2) write_rope_kv<ADT>(e, group, row, v[0], v[1]);
+    if constexpr (NT == 2) write_rope_kv<ADT>(e, group, ln, row, v[0], v[1]);
   } else {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) epi_value<ADT>(e, row, (group * NT + nt) * 32 + ln, v[nt]);
@@ -256,7 +266,7 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) red[(((wave * NT + nt) * MT + mt) * 16 + r) * 64 + lane] = acc[nt][mt][r];
-  __syncthreads();
+  lds_barrier();
   float v[MT][4][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -270,6 +280,19 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
         v[mt][j][nt] = s;
       }
 
+  if (e.op == kEpiPartial) {
+    float* out = (float*)e.out + (int64_t)split * e.M * e.N;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = mt * 32 + 8 * wave + 4 * g + j;
+        if (row < e.M)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) out[(int64_t)row * e.N + (group * NT + nt) * 32 + ln] = v[mt][j][nt];
+      }
+    return;
+  }
   if (S > 1) {
     const int groups = e.N / (32 * NT);
     // partial[split][group][mt][nt][wave][lane][4], agent-coherent 16-byte accesses
@@ -343,36 +366,37 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
 // ---------------------------------------------------------------------------
 // NF4 GEMM
 // ---------------------------------------------------------------------------
-// One wave's block pairs [w0, w1) of column group `group`; WV = this wave's
-// index (compile time, so table offsets are immediates). The loop runs in
-// rounds of two block pairs p, p + 1:
-//   * one table build per round writes both pairs' entries (low / high halves
-//     of each dword), from absmax loaded a round ahead;
-//   * codes of pair p + 2 are in flight while pair p + 1 is computed;
-//   * X fragment s of the next pair is requested right after the MFMAs of
-//     step s of the current one;
-//   * the table reads of k-step s + 1 are issued before the MFMAs of step s
-//     wait for theirs.
-// A padded block pair (past w1) reloads the last one and gets a zero scale,
-// so its table and its contribution are zero.
+// One wave's units [w0, w1) of column group `group` (a unit is 128 along K:
+// the lane's 64-block of each tile, 8 MFMA k-steps); WV = this wave's index
+// (compile time, so table offsets are immediates).
+//   * codes of unit p + 1 are in flight while unit p is computed; X one unit
+//     ahead (four k-steps with two M tiles), each fragment requested before
+//     the codes loaded after the unit, so waiting for X never waits for them;
+//   * table lookups go in batches of 8 reads (one tile, one k-step), the next
+//     batch issued before the current one is waited for, which keeps the LDS
+//     counter (15 outstanding at most) exact;
+//   * one table build writes the entries of two units (low / high halves of
+//     each dword), from absmax loaded a round ahead; a wave's tables are its
+//     own, so no barrier is needed (a wave's LDS accesses run in order).
+// The loop runs whole rounds of two units and is straight-line (prefetches
+// past w1 are clamped to the last unit), so the compiler's wait counts stay
+// exact; an odd last unit follows the loop.
 template <int MT, int NT, int WV, bool XT>
 __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* smem,
                                               const uint16_t* __restrict__ X, int64_t ldx,
                                               const uint8_t* __restrict__ W, const uint16_t* __restrict__ Wabs,
                                               int NP, int group, int w0, int w1, int M) {
-  const int n = w1 - w0;
-  if (n <= 0) return;
+  constexpr int XD = MT == 1 ? 8 : 4;  // X k-steps in flight
+  const int n = max(w1 - w0, 0);
   const int lane = threadIdx.x & 63;
   const int g = lane >> 5, ln = lane & 31;
   constexpr int TB = WV * NT * kTabTile;  // this wave's table area
   uint8_t* lanetab = smem + lane * 4;
   // LDS address registers: the lane's table base in the low byte (the kernel's
   // only LDS object starts at offset 0, so bits 8..15 are free for the code).
-  uint32_t addr[NT][8];
+  uint32_t addr[8];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) addr[nt][i] = (uint32_t)(lane * 4);
+  for (int i = 0; i < 8; ++i) addr[i] = (uint32_t)(lane * 4);
 
   // Rows at or beyond M read row M - 1: MFMA rows are independent and those
   // output rows are never stored.
@@ -381,96 +405,101 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
   for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (int64_t)min(mt * 32 + ln, M - 1) * ldx + 64 * g;
 
   u32x4_t qa[NT][2], qb[NT][2];  // codes of the lane's block in each tile (dword s = MFMA k-step s)
-  uint16_t ac[2][NT], an[2][NT];  // absmax of the first round's / the next round's two block pairs
-  u32x4_t x[MT][8];               // X fragments of the 8 MFMA k-steps
+  uint16_t ac[2][NT];             // absmax of the next two units, for the next table build
+  u32x4_t x[MT][XD];              // X fragments of k-steps s .. s + XD - 1
 
-  auto tile_of = [&](int nt, int p) -> int64_t { return (int64_t)(group * NT + nt) * NP + min(p, w1 - 1); };
+  const int wl = max(w1 - 1, 0);
+  auto tile_of = [&](int nt, int p) -> int64_t { return (int64_t)(group * NT + nt) * NP + min(p, wl); };
   auto load_codes = [&](u32x4_t (&q)[NT][2], int p) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const uint8_t* wp = W + tile_of(nt, p) * 2048 + lane * 16;
-      q[nt][0] = *(const u32x4_t*)(wp);
-      q[nt][1] = *(const u32x4_t*)(wp + 1024);
+      const u32x4_t* wp = (const u32x4_t*)(W + tile_of(nt, p) * 2048 + lane * 16);
+      q[nt][0] = __builtin_nontemporal_load(wp);
+      q[nt][1] = __builtin_nontemporal_load(wp + 64);
     }
   };
-  auto load_abs = [&](uint16_t (&a)[2][NT], int p) {
+  auto load_abs = [&](int p) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) a[h][nt] = Wabs[tile_of(nt, p + h) * 64 + lane];
+      for (int nt = 0; nt < NT; ++nt) ac[h][nt] = Wabs[tile_of(nt, p + h) * 64 + lane];
   };
-  auto load_x = [&](int s, int p) {
-    const int pc = min(p, w1 - 1);
+  auto load_x = [&](int slot, int p, int s) {
+    const int pc = min(p, wl);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      if constexpr (XT) x[mt][s] = *(const u32x4_t*)(X + ((((int64_t)mt * NP + pc) * 8 + s) * 64 + lane) * 8);
-      else x[mt][s] = *(const u32x4_t*)(xrow[mt] + 128 * pc + 8 * s);
+      if constexpr (XT) x[mt][slot] = *(const u32x4_t*)(X + ((((int64_t)mt * NP + pc) * 8 + s) * 64 + lane) * 8);
+      else x[mt][slot] = *(const u32x4_t*)(xrow[mt] + 128 * pc + 8 * s);
     }
   };
-  auto pair = [&](const u32x4_t (&q)[NT][2], int p, auto slot_c) {
+  auto unit = [&](const u32x4_t (&q)[NT][2], int p, auto slot_c) {
     constexpr int SL = decltype(slot_c)::value;
-    uint32_t r[2][NT][8];
-    auto lookup = [&](int s, uint32_t (&rr)[NT][8]) {
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) nf4_addr8(q[nt][s >> 2][s & 3], addr[nt]);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        if (nt == 0) nf4_read8<TB + SL>(addr[0], rr[0]);
-        else nf4_read8<TB + kTabTile + SL>(addr[nt], rr[nt]);
-      }
+    constexpr int NB = 8 * NT;  // batches: k-step b / NT, tile b % NT
+    uint32_t r[2][8];
+    auto issue = [&](int b, uint32_t (&rr)[8]) {
+      const int s = b / NT, nt = b % NT;
+      nf4_addr8(q[nt][s >> 2][s & 3], addr);
+      if (nt == 0) nf4_read8<TB + SL>(addr, rr);
+      else nf4_read8<TB + kTabTile + SL>(addr, rr);
     };
-    lookup(0, r[0]);
+    issue(0, r[0]);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      if (s < 7) lookup(s + 1, r[(s + 1) & 1]);
+    for (int b = 0; b < NB; ++b) {
+      if (b + 1 < NB) issue(b + 1, r[(b + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
-      const uint32_t (&cur)[NT][8] = r[s & 1];
+      const int s = b / NT, nt = b % NT;
+      const uint32_t (&cur)[8] = r[b & 1];
+      const u32x4_t bv = {pack16(cur[0], cur[1]), pack16(cur[2], cur[3]), pack16(cur[4], cur[5]),
+                          pack16(cur[6], cur[7])};
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const u32x4_t bv = {pack16(cur[nt][0], cur[nt][1]), pack16(cur[nt][2], cur[nt][3]),
-                            pack16(cur[nt][4], cur[nt][5]), pack16(cur[nt][6], cur[nt][7])};
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(x[mt][s], bv, acc[nt][mt]);
-      }
-      load_x(s, p + 1);
+      for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(x[mt][s % XD], bv, acc[nt][mt]);
+      if (nt == NT - 1) load_x(s % XD, p + ((s + XD) >> 3), (s + XD) & 7);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-
-  auto build = [&](const uint16_t (&a)[2][NT], int p) {
-    nf4_build_table2<TB>(lanetab, p < w1 ? a[0][0] : (uint16_t)0, p + 1 < w1 ? a[1][0] : (uint16_t)0);
-    if constexpr (NT == 2)
-      nf4_build_table2<TB + kTabTile>(lanetab, p < w1 ? a[0][1] : (uint16_t)0, p + 1 < w1 ? a[1][1] : (uint16_t)0);
+  auto build = [&]() {
+    nf4_build_table2<TB>(lanetab, ac[0][0], ac[1][0]);
+    if constexpr (NT == 2) nf4_build_table2<TB + kTabTile>(lanetab, ac[0][1], ac[1][1]);
   };
+  constexpr std::integral_constant<int, 0> kLo{};
+  constexpr std::integral_constant<int, 2> kHi{};
 
-  // The loads in flight at the top of every round are, in issue order, the
-  // codes of p, the 8 X fragments of p and the codes of p + 1, whether the
-  // round is entered from here or from the previous round, so the compiler's
-  // wait counts inside the loop stay exact.
-  load_abs(ac, w0);
-  build(ac, w0);
+  // At the top of every round p the table holds units p, p + 1, and the loads
+  // in flight are, in issue order, the codes of p, X k-steps 0 .. XD - 1 of p,
+  // the codes of p + 1 and the absmax of p + 2, p + 3 (the codes of p already
+  // arrived when the round is entered from the previous one). Each absmax load
+  // is issued right after a table build has waited for the previous one, so a
+  // build never waits for codes.
+  load_abs(w0);
   load_codes(qa, w0);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int s = 0; s < 8; ++s) load_x(s, w0);
+  for (int s = 0; s < XD; ++s) load_x(s, w0, s);
+  __builtin_amdgcn_sched_barrier(0);
   load_codes(qb, w0 + 1);
-  const int rounds = (n + 1) >> 1;
-  for (int r = 0; r < rounds; ++r) {
-    const int p = w0 + 2 * r;
+  __builtin_amdgcn_sched_barrier(0);
+  build();
+  __builtin_amdgcn_sched_barrier(0);
+  load_abs(w0 + 2);
+  const int rounds = n >> 1;
+  int p = w0;
+  for (int r = 0; r < rounds; ++r, p += 2) {
     __builtin_amdgcn_sched_barrier(0);
-    load_abs(an, p + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    pair(qa, p, std::integral_constant<int, 0>());
+    unit(qa, p, kLo);
     load_codes(qa, p + 2);
     __builtin_amdgcn_sched_barrier(0);
-    pair(qb, p + 1, std::integral_constant<int, 2>());
+    unit(qb, p + 1, kHi);
     load_codes(qb, p + 3);
     __builtin_amdgcn_sched_barrier(0);
-    build(an, p + 2);  // the next round's tables; this round's reads are all issued
+    build();  // units p + 2, p + 3; the reads of p, p + 1 are all issued
+    __builtin_amdgcn_sched_barrier(0);
+    load_abs(p + 4);
   }
+  if (n & 1) unit(qa, p, kLo);
 }
 
 template <int MT, int NT, bool XT>
-__global__ __launch_bounds__(kWaves * 64, 3) void nf4_gemm_kernel(const uint16_t* __restrict__ X, int64_t ldx,
+__global__ __launch_bounds__(kWaves * 64, MT == 1 ? 3 : 2) void nf4_gemm_kernel(const uint16_t* __restrict__ X, int64_t ldx,
                                                                   const uint8_t* __restrict__ W,
                                                                   const uint16_t* __restrict__ Wabs, int NP, int S,
                                                                   int pps, float* __restrict__ partial,
@@ -501,7 +530,7 @@ __global__ __launch_bounds__(kWaves * 64, 3) void nf4_gemm_kernel(const uint16_t
     case 2: nf4_wave_body<MT, NT, 2, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); break;
     default: nf4_wave_body<MT, NT, 3, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); break;
   }
-  __syncthreads();  // every wave is done with its tables; smem becomes the reduction buffer
+  lds_barrier();  // every wave is done with its tables; smem becomes the reduction buffer
   finish_tile<PE_DTYPE_BF16, NT, MT>(acc, (float*)smem, group, split, S, partial, counters, e);
 }
 
@@ -618,6 +647,43 @@ __global__ __launch_bounds__(64) void f32_gemm_kernel(const float* __restrict__ 
 
 
 // ---------------------------------------------------------------------------
+// Consumers of split partials (partial[S][M][N] fp32, summed in split order)
+// ---------------------------------------------------------------------------
+// Thread (row, column group, lane): columns 64 group + ln and 64 group + 32 + ln
+// are the two halves a RoPE pair (q/k/v) or a gate/up pair (SwiGLU) combines.
+template <int DT>
+__global__ __launch_bounds__(256) void rope_kv_partials_kernel(const float* __restrict__ partial, int S, EpiArgs e) {
+  const int pairs = e.N >> 1;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= e.M * pairs) return;
+  const int row = idx / pairs, rem = idx - row * pairs;
+  const int group = rem >> 5, ln = rem & 31;
+  const float* pr = partial + (int64_t)row * e.N + group * 64 + ln;
+  float a1 = 0.f, a2 = 0.f;
+  for (int sp = 0; sp < S; ++sp) {
+    a1 += pr[(int64_t)sp * e.M * e.N];
+    a2 += pr[(int64_t)sp * e.M * e.N + 32];
+  }
+  write_rope_kv<DT>(e, group, ln, row, a1, a2);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void swiglu_partials_kernel(const float* __restrict__ partial, int S, EpiArgs e) {
+  const int pairs = e.N >> 1;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= e.M * pairs) return;
+  const int row = idx / pairs, rem = idx - row * pairs;
+  const int group = rem >> 5, ln = rem & 31;
+  const float* pr = partial + (int64_t)row * e.N + group * 64 + ln;
+  float gv = 0.f, uv = 0.f;
+  for (int sp = 0; sp < S; ++sp) {
+    gv += pr[(int64_t)sp * e.M * e.N];
+    uv += pr[(int64_t)sp * e.M * e.N + 32];
+  }
+  epi_swiglu<DT>(e, row, group * 32 + ln, gv, uv);
+}
+
+// ---------------------------------------------------------------------------
 // Launch planning
 // ---------------------------------------------------------------------------
 constexpr int kMaxChunkRows = 64;  // M rows per launch (MT <= 2)
@@ -632,22 +698,34 @@ struct Plan {
   int64_t partial_bytes;
 };
 
-// units: block pairs (NF4) or 64-wide K steps (dense). A wave gets at least 2
-// units (one double-buffered round); S spreads the work over about
-// `wave_slots` waves (256 CUs x 3 four-wave workgroups by default) and is
-// balanced so that the splits differ by at most one unit per wave.
+// units: 128-wide K units (NF4) or 64-wide K steps (dense).
+// NF4: every workgroup of a launch is resident at once (three per CU with one
+// M tile, two with two), so S is the largest split that keeps groups * S
+// within them and leaves every wave at least `min_units` units.
+// Dense: S spreads the work over about `wave_slots` waves (256 CUs x 3
+// four-wave workgroups), a wave getting at least 2 units.
+// Either way the splits are balanced to differ by at most one unit per wave.
 Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   static const int wave_slots = env_int("PE_GEMM_WAVE_SLOTS", 3072);
+  static const int nf4_wg_slots = env_int("PE_NF4_WG_SLOTS", 768);
+  static const int nf4_min_units = env_int("PE_NF4_MIN_UNITS", 2);
   static const int min_units = env_int("PE_GEMM_MIN_UNITS", 2);
   Plan p;
   p.NT = (epi == PE_EPI_SWIGLU || epi == kEpiRopeKV || N % 64 == 0) ? 2 : 1;
   p.MT = M > 32 ? 2 : 1;
   p.groups = N / (32 * p.NT);
   p.units = nf4 ? K / 128 : K / 64;
-  const int64_t total = (int64_t)p.groups * p.units;
-  int per_wave = (int)((total + wave_slots - 1) / wave_slots);
-  if (per_wave < min_units) per_wave = min_units;
-  int S = (p.units + per_wave * kWaves - 1) / (per_wave * kWaves);
+  int S;
+  if (nf4) {
+    S = (p.MT == 1 ? nf4_wg_slots : nf4_wg_slots * 2 / 3) / p.groups;
+    const int s_units = p.units / (kWaves * nf4_min_units);
+    if (S > s_units) S = s_units;
+  } else {
+    const int64_t total = (int64_t)p.groups * p.units;
+    int per_wave = (int)((total + wave_slots - 1) / wave_slots);
+    if (per_wave < min_units) per_wave = min_units;
+    S = (p.units + per_wave * kWaves - 1) / (per_wave * kWaves);
+  }
   if (S > kMaxSplits) S = kMaxSplits;
   if (S < 1) S = 1;
   p.per_split = (p.units + S - 1) / S;
@@ -806,6 +884,76 @@ int64_t pe_internal_gemm_rope_kv_bytes(int M, int N, int K, int wfmt) {
   return workspace_of(make_plan(M, N, K, wfmt == PE_WFMT_NF4, kEpiRopeKV));
 }
 
+// Y = X . W^T as split partials partial[S][M][N] (fp32, plain stores: no
+// exchange between workgroups, the consumer sums them); one launch, M <= 64.
+int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M, int K,
+                                const void* w, const uint16_t* wabs, int N, float* partial, int64_t partial_bytes,
+                                int* splits, hipStream_t st) {
+  if (M > kMaxChunkRows || !partial || !splits) return PE_ERR_ARG;
+  int rc = check_gemm_args(x, M, K, w, N, PE_EPI_STORE, nullptr, partial);
+  if (rc != PE_OK) return rc;
+  const bool nf4 = wfmt == PE_WFMT_NF4;
+  if (nf4 ? !wabs : (dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16)) return PE_ERR_ARG;
+  if (x_tiled && !nf4) return PE_ERR_ARG;
+  const Plan p = make_plan(M, N, K, nf4, kEpiPartial);
+  if (partial_bytes < (int64_t)p.S * M * N * 4) return PE_ERR_WORKSPACE;
+  EpiArgs e = make_epi(kEpiPartial, M, N, nullptr, nullptr, 0, partial, N);
+  *splits = p.S;
+  return launch_gemm(nf4 ? kFmtNF4 : dtype, p, st, (const uint16_t*)x, ldx, x_tiled, K, w, wabs, nullptr, e);
+}
+
+int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int wfmt) {
+  if (M > kMaxChunkRows) M = kMaxChunkRows;
+  return (int64_t)make_plan(M, N, K, wfmt == PE_WFMT_NF4, kEpiPartial).S * M * N * 4;
+}
+
+// The q/k/v epilogue (bias, RoPE at positions[row], q to q_out, K/V appended
+// at cache rows row0 + row) applied to S split partials of the projection.
+int pe_internal_rope_kv_partials(const float* partial, int S, int M, int nh, int nkv, int hd, const void* bias,
+                                 const int64_t* positions, const void* cos_sin, int64_t max_pos, void* q_out,
+                                 void* k_cache, void* v_cache, int64_t cap, int64_t row0, int32_t* status, int dtype,
+                                 hipStream_t st) {
+  if (!partial || S < 1 || M <= 0 || hd <= 0 || hd % 64 || !positions || !cos_sin || !q_out || !k_cache ||
+      !v_cache)
+    return PE_ERR_ARG;
+  if (row0 < 0 || row0 + M > cap) return PE_ERR_CAPACITY;
+  const int N = (nh + 2 * nkv) * hd;
+  EpiArgs e = make_epi(kEpiRopeKV, M, N, bias, nullptr, 0, nullptr, 0);
+  e.positions = positions;
+  e.cos_sin = cos_sin;
+  e.max_pos = max_pos;
+  e.q_out = q_out;
+  e.k_cache = k_cache;
+  e.v_cache = v_cache;
+  e.cap = cap;
+  e.row0 = row0;
+  e.nh = nh;
+  e.nkv = nkv;
+  e.hd = hd;
+  e.status = status;
+  const int grid = pe_cdiv((int64_t)M * (N / 2), 256);
+  if (dtype == PE_DTYPE_BF16) rope_kv_partials_kernel<PE_DTYPE_BF16><<<grid, 256, 0, st>>>(partial, S, e);
+  else if (dtype == PE_DTYPE_F16) rope_kv_partials_kernel<PE_DTYPE_F16><<<grid, 256, 0, st>>>(partial, S, e);
+  else return PE_ERR_ARG;
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+// SwiGLU of S split partials of the interleaved gate/up projection (N columns,
+// N / 2 outputs), row-major or A-tiled (out_units > 0).
+int pe_internal_swiglu_partials(const float* partial, int S, int M, int N, void* out, int64_t ld_out, int out_units,
+                                int dtype, hipStream_t st) {
+  if (!partial || !out || S < 1 || M <= 0 || N <= 0 || N % 64) return PE_ERR_ARG;
+  EpiArgs e = make_epi(PE_EPI_SWIGLU, M, N, nullptr, nullptr, 0, out, ld_out);
+  e.out_units = out_units;
+  const int grid = pe_cdiv((int64_t)M * (N / 2), 256);
+  if (dtype == PE_DTYPE_BF16) swiglu_partials_kernel<PE_DTYPE_BF16><<<grid, 256, 0, st>>>(partial, S, e);
+  else if (dtype == PE_DTYPE_F16) swiglu_partials_kernel<PE_DTYPE_F16><<<grid, 256, 0, st>>>(partial, S, e);
+  else return PE_ERR_ARG;
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
 extern "C" int64_t pe_gemm_workspace_bytes(int M, int N, int K, int wfmt, int dtype, int epilogue) {
   if (dtype == PE_DTYPE_F32 && wfmt == PE_WFMT_DENSE) return 0;
   if (M <= 0 || N <= 0 || K < 128) return kCounterBytes;
@@ -829,6 +977,18 @@ extern "C" int pe_nf4_gemm_tiled(const void* x_tiled, int M, int K, const uint8_
   if (!absmax_tiled || M > kMaxChunkRows || out_units < 0) return PE_ERR_ARG;
   return mfma_gemm(kFmtNF4, x_tiled, K, M, K, w_tiled, absmax_tiled, N, epilogue, bias, resid, ld_resid, out, ld_out,
                    workspace, workspace_bytes, (hipStream_t)stream, true, out_units);
+}
+
+extern "C" int64_t pe_nf4_gemm_partials_bytes(int M, int N, int K) {
+  if (M <= 0 || M > kMaxChunkRows || N <= 0 || K < 128) return 0;
+  return pe_internal_linear_partials_bytes(M, N, K, PE_WFMT_NF4);
+}
+
+extern "C" int pe_nf4_gemm_partials(const void* x, int64_t ldx, int x_tiled, int M, int K, const uint8_t* w_tiled,
+                                    const uint16_t* absmax_tiled, int N, float* partials, int64_t partial_bytes,
+                                    int* splits, void* stream) {
+  return pe_internal_linear_partials(PE_WFMT_NF4, PE_DTYPE_BF16, x, x_tiled ? K : ldx, x_tiled != 0, M, K, w_tiled,
+                                     absmax_tiled, N, partials, partial_bytes, splits, (hipStream_t)stream);
 }
 
 extern "C" int pe_dense_gemm(const void* x, int64_t ldx, int M, int K, const void* w, int dtype, int N,

@@ -25,6 +25,24 @@ PE_INTERNAL int pe_internal_linear(int wfmt, int dtype, const void* x, int64_t l
                                    const void* resid, int64_t ld_resid, void* out, int64_t ld_out, int out_units,
                                    void* ws, int64_t ws_bytes, hipStream_t st);
 
+// pe_gemm.hip: Y = X . W^T as split partials partial[S][M][N] fp32 (plain
+// stores, summed by the consumer in split order); *splits receives S. M <= 64.
+PE_INTERNAL int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M,
+                                            int K, const void* w, const uint16_t* wabs, int N, float* partial,
+                                            int64_t partial_bytes, int* splits, hipStream_t st);
+PE_INTERNAL int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int wfmt);
+
+// pe_gemm.hip: the q/k/v epilogue (bias, RoPE, q out, K/V appended at cache rows
+// row0 + row) and the SwiGLU epilogue (N / 2 outputs, A-tiled when out_units)
+// applied to the S split partials of their projections (the head-paired /
+// gate-up interleaved column orders of the fused path).
+PE_INTERNAL int pe_internal_rope_kv_partials(const float* partial, int S, int M, int nh, int nkv, int hd,
+                                             const void* bias, const int64_t* positions, const void* cos_sin,
+                                             int64_t max_pos, void* q_out, void* k_cache, void* v_cache, int64_t cap,
+                                             int64_t row0, int32_t* status, int dtype, hipStream_t st);
+PE_INTERNAL int pe_internal_swiglu_partials(const float* partial, int S, int M, int N, void* out, int64_t ld_out,
+                                            int out_units, int dtype, hipStream_t st);
+
 // pe_elem.hip: h = round(h + round(sum_s partial[s])) (S == 0: h unchanged),
 // xn = w * round(h * rsqrt(mean(h^2) + eps)), also A-tiled into xn_tiled when
 // given; optional copies of the new h (cap_h) and of xn (cap_xn) into the

@@ -38,6 +38,7 @@ struct Layout {
   int64_t gemm_bytes;
   int64_t h, xn, qkv, q, attn, act, attn_ws, attn_ws_bytes;
   int64_t xn_t, attn_t, act_t;  // A-tiled GEMM inputs of the fused NF4 pass
+  int64_t part, part_bytes;      // split partials of the fused NF4 pass's GEMMs
   int64_t total;
 };
 
@@ -83,11 +84,20 @@ Layout make_layout(const pe_model_desc* m, int M, int64_t kv_len) {
   L.q = off; off += align_up((int64_t)M * qd * es);
   L.attn = off; off += align_up((int64_t)M * qd * es);
   L.act = off; off += align_up((int64_t)M * ip * es);
-  L.xn_t = L.attn_t = L.act_t = 0;
+  L.xn_t = L.attn_t = L.act_t = L.part = L.part_bytes = 0;
   if (tiled_path(m, M)) {
     L.xn_t = off; off += align_up(xtile_bytes(M, H));
     L.attn_t = off; off += align_up(xtile_bytes(M, qd));
     L.act_t = off; off += align_up(xtile_bytes(M, ip));
+    const int wf = m->weight_format;
+    const int64_t pb[4] = {pe_internal_linear_partials_bytes(M, nqkv, H, wf),
+                           pe_internal_linear_partials_bytes(M, H, qd, wf),
+                           pe_internal_linear_partials_bytes(M, 2 * ip, H, wf),
+                           pe_internal_linear_partials_bytes(M, H, ip, wf)};
+    for (int i = 0; i < 4; ++i)
+      if (pb[i] > L.part_bytes) L.part_bytes = pb[i];
+    L.part_bytes = align_up(L.part_bytes);
+    L.part = off; off += L.part_bytes;
   }
   L.attn_ws = off;
   L.attn_ws_bytes = align_up(pe_attention_workspace_bytes(M, m->num_heads, m->num_kv_heads, m->head_dim, kv_len,
@@ -194,33 +204,66 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
                                         slot_ptr(f0), fused_ld, nullptr, 0, st));
     PE_TRY(copy_repeats(0, f0));
   }
+  // The tiled (NF4) pass: every GEMM writes split partials with plain stores
+  // and the kernel that consumes its output sums them (q/k/v: RoPE + KV append;
+  // o, down: residual + RMSNorm; gate/up: SwiGLU), so no GEMM waits on
+  // another workgroup of its own launch.
+  float* part = tiled ? (float*)(ws + Lo.part) : nullptr;
+  const int nqkv = (nh + 2 * nkv) * hd;
+  int S = 0;
   for (int l = 0; l < L; ++l) {
     void* kc = (char*)a->k_cache + l * layer_stride;
     void* vc = (char*)a->v_cache + l * layer_stride;
-    PE_TRY(pe_internal_gemm_rope_kv(wf, m->dtype, x_norm, H, M, H, m->w_qkv[l],
-                                    (const uint16_t*)(m->a_qkv ? m->a_qkv[l] : nullptr), nh, nkv, hd,
-                                    m->b_qkv ? m->b_qkv[l] : nullptr, a->positions, m->rope_cos_sin, m->max_positions,
-                                    q, kc, vc, a->cache_capacity, a->prefix_len, a->status, gws, gwsb, tiled, st));
+    const uint16_t* a_qkv = (const uint16_t*)(m->a_qkv ? m->a_qkv[l] : nullptr);
+    const void* b_qkv = m->b_qkv ? m->b_qkv[l] : nullptr;
+    if (tiled) {
+      PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_norm, H, true, M, H, m->w_qkv[l], a_qkv, nqkv, part,
+                                         Lo.part_bytes, &S, st));
+      PE_TRY(pe_internal_rope_kv_partials(part, S, M, nh, nkv, hd, b_qkv, a->positions, m->rope_cos_sin,
+                                          m->max_positions, q, kc, vc, a->cache_capacity, a->prefix_len, a->status,
+                                          m->dtype, st));
+    } else {
+      PE_TRY(pe_internal_gemm_rope_kv(wf, m->dtype, x_norm, H, M, H, m->w_qkv[l], a_qkv, nh, nkv, hd, b_qkv,
+                                      a->positions, m->rope_cos_sin, m->max_positions, q, kc, vc, a->cache_capacity,
+                                      a->prefix_len, a->status, gws, gwsb, false, st));
+    }
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
                                       a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
                                       Lo.attn_ws_bytes, st));
-    PE_TRY(pe_internal_linear(wf, m->dtype, x_attn, qd, tiled, M, qd, m->w_o[l],
-                              (const uint16_t*)(m->a_o ? m->a_o[l] : nullptr), H, PE_EPI_RESIDUAL, nullptr, h, H, h, H,
-                              0, gws, gwsb, st));
-    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, xn_t, nullptr,
-                                        0, nullptr, 0, st));
-    PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, tiled, M, H, m->w_gu[l],
-                              (const uint16_t*)(m->a_gu ? m->a_gu[l] : nullptr), 2 * ip, PE_EPI_SWIGLU, nullptr,
-                              nullptr, 0, x_act, ip, act_units, gws, gwsb, st));
-    PE_TRY(pe_internal_linear(wf, m->dtype, x_act, ip, tiled, M, ip, m->w_down[l],
-                              (const uint16_t*)(m->a_down ? m->a_down[l] : nullptr), H, PE_EPI_RESIDUAL, nullptr, h, H,
-                              h, H, 0, gws, gwsb, st));
+    const uint16_t* a_o = (const uint16_t*)(m->a_o ? m->a_o[l] : nullptr);
+    if (tiled) {
+      PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, true, M, qd, m->w_o[l], a_o, H, part,
+                                         Lo.part_bytes, &S, st));
+      PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, xn_t, nullptr,
+                                          0, nullptr, 0, st));
+    } else {
+      PE_TRY(pe_internal_linear(wf, m->dtype, x_attn, qd, false, M, qd, m->w_o[l], a_o, H, PE_EPI_RESIDUAL, nullptr,
+                                h, H, h, H, 0, gws, gwsb, st));
+      PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, nullptr,
+                                          nullptr, 0, nullptr, 0, st));
+    }
+    const uint16_t* a_gu = (const uint16_t*)(m->a_gu ? m->a_gu[l] : nullptr);
+    const uint16_t* a_down = (const uint16_t*)(m->a_down ? m->a_down[l] : nullptr);
     const bool last = l + 1 == L;
     const int fh = last ? -1 : slot_of(l + 1);
     const int fx = last ? slot_of(L) : -1;
-    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, last ? m->final_norm : m->attn_norm[l + 1], m->rms_eps,
-                                        m->dtype, xn, last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx),
-                                        fused_ld, st));
+    const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
+    if (tiled) {
+      PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_norm, H, true, M, H, m->w_gu[l], a_gu, 2 * ip, part,
+                                         Lo.part_bytes, &S, st));
+      PE_TRY(pe_internal_swiglu_partials(part, S, M, 2 * ip, x_act, ip, act_units, m->dtype, st));
+      PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_act, ip, true, M, ip, m->w_down[l], a_down, H, part,
+                                         Lo.part_bytes, &S, st));
+      PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, m->dtype, xn,
+                                          last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
+    } else {
+      PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, false, M, H, m->w_gu[l], a_gu, 2 * ip, PE_EPI_SWIGLU,
+                                nullptr, nullptr, 0, x_act, ip, 0, gws, gwsb, st));
+      PE_TRY(pe_internal_linear(wf, m->dtype, x_act, ip, false, M, ip, m->w_down[l], a_down, H, PE_EPI_RESIDUAL,
+                                nullptr, h, H, h, H, 0, gws, gwsb, st));
+      PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, next_norm, m->rms_eps, m->dtype, xn, nullptr,
+                                          slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
+    }
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
   if (a->logits)

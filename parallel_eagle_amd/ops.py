@@ -180,6 +180,21 @@ def linear_tiled(xt: torch.Tensor, m: int, k: int, n: int, nf4: tuple, *, epilog
 
 
 # ------------------------------------------------------------------ elementwise
+def nf4_linear_partials(x: torch.Tensor, m: int, k: int, n: int, nf4: tuple, *, x_tiled: bool = False,
+                        partials: torch.Tensor | None = None) -> tuple[torch.Tensor, int]:
+    """pe_nf4_gemm_partials: fp32 split partials [S][m][n] of X . deq(W)^T (X
+    row-major [m][k] or A-tiled); returns (partials, S)."""
+    nbytes = int(lib().pe_nf4_gemm_partials_bytes(m, n, k))
+    _req(nbytes > 0, "unsupported shape for split partials")
+    if partials is None:
+        partials = torch.empty(nbytes // 4, dtype=torch.float32, device=x.device)
+    s = C.c_int(0)
+    check(lib().pe_nf4_gemm_partials(ptr(x), k if x_tiled else x.stride(0), int(x_tiled), m, k, ptr(nf4[0]),
+                                     ptr(nf4[1]), n, ptr(partials), partials.numel() * 4, C.byref(s), stream_ptr()),
+          "nf4_linear_partials")
+    return partials[: s.value * m * n].view(s.value, m, n), s.value
+
+
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     _req(x.dim() == 2 and x.stride(1) == 1 and w.dtype == x.dtype, "bad rmsnorm args")
     out = torch.empty_like(x)

@@ -108,6 +108,26 @@ def test_nf4_linear_tiled_x_equals_row_major(m, epi):
     assert torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("m", [1, 26, 33, 64])
+@pytest.mark.parametrize("n,k,tiled", [(4096, 4096, True), (22016, 4096, True), (4096, 11008, True),
+                                       (256, 1024, False)])
+def test_nf4_partials_sum_to_the_product(m, n, k, tiled):
+    """pe_nf4_gemm_partials: the split partials, summed in split order in fp32,
+    equal the fp32 product of the exact dequantised operands up to fp32
+    accumulation order (every split sums the same bf16 products)."""
+    (tiled_w, tabs), wdq = _nf4_weight(n, k, seed=m + n + k)
+    x = torch.from_numpy(synth.normal(m, 36, m * k, 1.0).reshape(m, k)).to(torch.bfloat16)
+    xd = ops.to_xtile(x.to(DEV)) if tiled else x.to(DEV)
+    parts, s = ops.nf4_linear_partials(xd, m, k, n, (tiled_w, tabs), x_tiled=tiled)
+    assert 1 <= s <= 16 and parts.shape == (s, m, n)
+    tot = parts[0].clone()
+    for i in range(1, s):
+        tot += parts[i]
+    ref32 = x.float() @ wdq.float().t()
+    err = (tot.cpu() - ref32).abs()
+    assert torch.all(err <= 1e-4 * (1 + ref32.abs()) * (k / 1024)), err.max()
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("epi", ["store", "bias", "residual", "swiglu"])
 def test_dense_linear_epilogues(dtype, epi):
