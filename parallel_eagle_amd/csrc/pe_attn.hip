@@ -381,10 +381,16 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
     }
   }
   const int tt = rr / G, col0 = (kvh * G + rr % G) * HD + dc;
+  typedef typename Elem<DT>::T Te;
+  // 16 consecutive dims: four 4-element stores (consecutive in either layout)
 #pragma unroll
-  for (int k = 0; k < 16; ++k)
-    Elem<DT>::store((typename Elem<DT>::T*)out,
-                    out_units ? xtile_index(tt, col0 + k, out_units) : (int64_t)tt * ld_out + col0 + k, num[k] / den);
+  for (int k4 = 0; k4 < 4; ++k4) {
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = Elem<DT>::round(num[4 * k4 + i] / den);
+    const int col = col0 + 4 * k4;
+    Vec4<DT>::store((Te*)out + (out_units ? xtile_index(tt, col, out_units) : (int64_t)tt * ld_out + col), o);
+  }
 }
 
 

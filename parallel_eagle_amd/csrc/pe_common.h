@@ -55,6 +55,36 @@ template <> struct Elem<PE_DTYPE_F16> {
   static __device__ __forceinline__ float round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
 };
 
+// Four consecutive elements as floats through one access: 8 bytes for the
+// 16-bit types, 16 bytes for fp32 (the pointer is aligned to that size).
+template <int DT> struct Vec4;
+template <> struct Vec4<PE_DTYPE_F32> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
+    const float4 t = *(const float4*)p;
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&v)[4]) {
+    *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+template <int DT> struct Vec4Half {
+  static __device__ __forceinline__ float cvt(uint32_t b) {
+    return DT == PE_DTYPE_BF16 ? bf16_bits_to_f32((uint16_t)b) : f16_bits_to_f32((uint16_t)b);
+  }
+  static __device__ __forceinline__ uint32_t bits(float f) {
+    return DT == PE_DTYPE_BF16 ? f32_to_bf16_bits(f) : f32_to_f16_bits(f);
+  }
+  static __device__ __forceinline__ void load(const uint16_t* p, float (&v)[4]) {
+    const uint2 t = *(const uint2*)p;
+    v[0] = cvt(t.x & 0xffffu); v[1] = cvt(t.x >> 16); v[2] = cvt(t.y & 0xffffu); v[3] = cvt(t.y >> 16);
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const float (&v)[4]) {
+    *(uint2*)p = make_uint2(bits(v[0]) | (bits(v[1]) << 16), bits(v[2]) | (bits(v[3]) << 16));
+  }
+};
+template <> struct Vec4<PE_DTYPE_BF16> : Vec4Half<PE_DTYPE_BF16> {};
+template <> struct Vec4<PE_DTYPE_F16> : Vec4Half<PE_DTYPE_F16> {};
+
 // The published NF4 code book (QLoRA / bitsandbytes), fp32. Code 7 is 0.
 __device__ __constant__ static const float kNF4[16] = {
     -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,

@@ -12,16 +12,40 @@
 
 namespace {
 
+// One block per row; 16-byte pieces, all of a thread's loads issued before its
+// stores (rows of the table are random HBM reads).
 template <int DT>
 __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ ids, const typename Elem<DT>::T* __restrict__ table,
                                                     int64_t V, int H, typename Elem<DT>::T* __restrict__ out,
                                                     int64_t ld_out, int32_t* status) {
+  typedef typename Elem<DT>::T T;
   const int m = blockIdx.x;
   const int64_t id = ids[m];
   const bool ok = id >= 0 && id < V;
   if (!ok && threadIdx.x == 0 && status) atomicOr(status, PE_ERR_TOKEN);
-  for (int c = threadIdx.x; c < H; c += blockDim.x)
-    out[(int64_t)m * ld_out + c] = ok ? table[id * H + c] : (typename Elem<DT>::T)0;
+  const int64_t row_bytes = (int64_t)H * sizeof(T);
+  const uint8_t* src = (const uint8_t*)(table + (ok ? id : 0) * H);
+  uint8_t* dst = (uint8_t*)(out + (int64_t)m * ld_out);
+  if ((row_bytes & 15) == 0 && (((uintptr_t)src | (uintptr_t)dst) & 15) == 0) {
+    const int nvec = (int)(row_bytes >> 4);
+    constexpr int kU = 4;
+    for (int i0 = threadIdx.x; i0 < nvec; i0 += kU * 256) {
+      uint4 t[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int i = i0 + u * 256;
+        t[u] = i < nvec ? ((const uint4*)src)[i] : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int i = i0 + u * 256;
+        if (i < nvec) ((uint4*)dst)[i] = ok ? t[u] : make_uint4(0, 0, 0, 0);
+      }
+    }
+  } else {
+    for (int c = threadIdx.x; c < H; c += blockDim.x)
+      out[(int64_t)m * ld_out + c] = ok ? table[id * H + c] : (T)0;
+  }
 }
 
 template <int DT>
@@ -119,43 +143,36 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
     typename Elem<DT>::T* __restrict__ cap_xn, int64_t ld_cap_xn) {
   typedef Elem<DT> E;
   typedef typename E::T T;
+  typedef Vec4<DT> V;
   const int m = blockIdx.x;
   T* hr = h + (int64_t)m * H;
   const int nchunk = H >> 2;
+  const int64_t sstride = (int64_t)M * H;
   float v[kNormChunks][4];
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < kNormChunks; ++k) {
     const int c = threadIdx.x + k * kNormThreads;
     if (c >= nchunk) continue;
-    float4 pv[kNormMaxSplits];
-#pragma unroll
-    for (int sp = 0; sp < kNormMaxSplits; ++sp)
-      if (sp < S) pv[sp] = *(const float4*)(partial + ((int64_t)sp * M + m) * H + 4 * c);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[k][e] = E::load(hr, 4 * c + e);
+    V::load(hr + 4 * c, v[k]);
     if (S > 0) {
+      const float* pp = partial + (int64_t)m * H + 4 * c;
       float a[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int sp = 0; sp < kNormMaxSplits; ++sp) {
-        if (sp < S) {
-          a[0] += pv[sp].x;
-          a[1] += pv[sp].y;
-          a[2] += pv[sp].z;
-          a[3] += pv[sp].w;
-        }
+#pragma unroll 4
+      for (int sp = 0; sp < S; ++sp) {
+        const float4 t = *(const float4*)(pp + sp * sstride);
+        a[0] += t.x;
+        a[1] += t.y;
+        a[2] += t.z;
+        a[3] += t.w;
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[k][e] = E::round(__fadd_rn(v[k][e], E::round(a[e])));
-        E::store(hr, 4 * c + e, v[k][e]);
-      }
+      for (int e = 0; e < 4; ++e) v[k][e] = E::round(__fadd_rn(v[k][e], E::round(a[e])));
+      V::store(hr + 4 * c, v[k]);
     }
+    if (cap_h) V::store(cap_h + (int64_t)m * ld_cap_h + 4 * c, v[k]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (cap_h) E::store(cap_h + (int64_t)m * ld_cap_h, 4 * c + e, v[k][e]);
-      ss = __fadd_rn(ss, __fmul_rn(v[k][e], v[k][e]));
-    }
+    for (int e = 0; e < 4; ++e) ss = __fadd_rn(ss, __fmul_rn(v[k][e], v[k][e]));
   }
   __shared__ float part[kNormThreads / 64];
   ss = wave_sum(ss);
@@ -170,14 +187,14 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
   for (int k = 0; k < kNormChunks; ++k) {
     const int c = threadIdx.x + k * kNormThreads;
     if (c >= nchunk) continue;
+    float wv[4], o[4];
+    V::load(w + 4 * c, wv);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float y = E::round(__fmul_rn(v[k][e], inv));
-      const float o = __fmul_rn(E::load(w, 4 * c + e), y);
-      E::store(orow, 4 * c + e, o);
-      if (xt) E::store(xt, xtile_index(m, 4 * c + e, H >> 7), o);
-      if (cap_xn) E::store(cap_xn + (int64_t)m * ld_cap_xn, 4 * c + e, o);
-    }
+    for (int e = 0; e < 4; ++e) o[e] = E::round(__fmul_rn(wv[e], E::round(__fmul_rn(v[k][e], inv))));
+    V::store(orow + 4 * c, o);
+    // four consecutive columns are consecutive in the A-tiled layout too
+    if (xt) V::store(xt + xtile_index(m, 4 * c, H >> 7), o);
+    if (cap_xn) V::store(cap_xn + (int64_t)m * ld_cap_xn + 4 * c, o);
   }
 }
 

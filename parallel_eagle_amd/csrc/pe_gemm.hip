@@ -432,7 +432,7 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
       else x[mt][slot] = *(const u32x4_t*)(xrow[mt] + 128 * pc + 8 * s);
     }
   };
-  auto unit = [&](const u32x4_t (&q)[NT][2], int p, auto slot_c) {
+  auto unit = [&](const u32x4_t (&q)[NT][2], int p, auto slot_c, u32x4_t (&xs)[MT][XD], bool prefetch) {
     constexpr int SL = decltype(slot_c)::value;
     constexpr int NB = 8 * NT;  // batches: k-step b / NT, tile b % NT
     uint32_t r[2][8];
@@ -452,8 +452,8 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
       const u32x4_t bv = {pack16(cur[0], cur[1]), pack16(cur[2], cur[3]), pack16(cur[4], cur[5]),
                           pack16(cur[6], cur[7])};
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(x[mt][s % XD], bv, acc[nt][mt]);
-      if (nt == NT - 1) load_x(s % XD, p + ((s + XD) >> 3), (s + XD) & 7);
+      for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(xs[mt][s % XD], bv, acc[nt][mt]);
+      if (prefetch && nt == NT - 1) load_x(s % XD, p + ((s + XD) >> 3), (s + XD) & 7);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -464,6 +464,33 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
   constexpr std::integral_constant<int, 0> kLo{};
   constexpr std::integral_constant<int, 2> kHi{};
 
+  if constexpr (MT == 1) {
+    if (n <= 2) {
+      // At most two units: every load of the wave is issued at once (absmax,
+      // then codes and X of the first unit, then of the second), one table
+      // build covers both, and each unit waits only for its own loads.
+      u32x4_t xb[MT][XD];
+      load_abs(w0);
+      load_codes(qa, w0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < XD; ++s) load_x(s, w0, s);
+      __builtin_amdgcn_sched_barrier(0);
+      load_codes(qb, w0 + 1);
+#pragma unroll
+      for (int s = 0; s < XD; ++s) {
+        const int pc = min(w0 + 1, wl);
+        if constexpr (XT) xb[0][s] = *(const u32x4_t*)(X + (((int64_t)pc * 8 + s) * 64 + lane) * 8);
+        else xb[0][s] = *(const u32x4_t*)(xrow[0] + 128 * pc + 8 * s);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      build();
+      __builtin_amdgcn_sched_barrier(0);
+      if (n > 0) unit(qa, w0, kLo, x, false);
+      if (n > 1) unit(qb, w0 + 1, kHi, xb, false);
+      return;
+    }
+  }
   // At the top of every round p the table holds units p, p + 1, and the loads
   // in flight are, in issue order, the codes of p, X k-steps 0 .. XD - 1 of p,
   // the codes of p + 1 and the absmax of p + 2, p + 3 (the codes of p already
@@ -485,17 +512,17 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
   int p = w0;
   for (int r = 0; r < rounds; ++r, p += 2) {
     __builtin_amdgcn_sched_barrier(0);
-    unit(qa, p, kLo);
+    unit(qa, p, kLo, x, true);
     load_codes(qa, p + 2);
     __builtin_amdgcn_sched_barrier(0);
-    unit(qb, p + 1, kHi);
+    unit(qb, p + 1, kHi, x, true);
     load_codes(qb, p + 3);
     __builtin_amdgcn_sched_barrier(0);
     build();  // units p + 2, p + 3; the reads of p, p + 1 are all issued
     __builtin_amdgcn_sched_barrier(0);
     load_abs(p + 4);
   }
-  if (n & 1) unit(qa, p, kLo);
+  if (n & 1) unit(qa, p, kLo, x, true);
 }
 
 template <int MT, int NT, bool XT>
@@ -649,38 +676,106 @@ __global__ __launch_bounds__(64) void f32_gemm_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 // Consumers of split partials (partial[S][M][N] fp32, summed in split order)
 // ---------------------------------------------------------------------------
-// Thread (row, column group, lane): columns 64 group + ln and 64 group + 32 + ln
-// are the two halves a RoPE pair (q/k/v) or a gate/up pair (SwiGLU) combines.
+// Thread (row, column group, quad q): columns 64 group + 4q .. + 3 and the same
+// 32 further on are the halves a RoPE pair (q/k/v) or a gate/up pair (SwiGLU)
+// combines; four columns per thread make every access 16 (fp32) or 8 bytes.
+__device__ __forceinline__ void sum_partials4(const float* __restrict__ pr, int S, int64_t sstride, float (&a)[4],
+                                              float (&b)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = b[i] = 0.f;
+#pragma unroll 4
+  for (int sp = 0; sp < S; ++sp) {
+    const float4 t = *(const float4*)(pr + sp * sstride);
+    const float4 u = *(const float4*)(pr + sp * sstride + 32);
+    a[0] += t.x; a[1] += t.y; a[2] += t.z; a[3] += t.w;
+    b[0] += u.x; b[1] += u.y; b[2] += u.z; b[3] += u.w;
+  }
+}
+
+// write_rope_kv for four consecutive dims d1 .. d1 + 3 (and d1 + hd/2 ..).
+template <int DT>
+__device__ __forceinline__ void write_rope_kv4(const EpiArgs& e, int group, int ln0, int row, const float (&a1)[4],
+                                               const float (&a2)[4]) {
+  typedef Elem<DT> E;
+  typedef typename E::T T;
+  typedef Vec4<DT> V;
+  const int gpu = e.hd >> 6;
+  const int u = group / gpu, j = group % gpu;
+  const int d1 = 32 * j + ln0, d2 = d1 + (e.hd >> 1);
+  float x1[4], x2[4];
+  if (e.bias) {
+    float b1[4], b2[4];
+    V::load((const T*)e.bias + u * e.hd + d1, b1);
+    V::load((const T*)e.bias + u * e.hd + d2, b2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x1[i] = E::round(__fadd_rn(a1[i], b1[i]));
+      x2[i] = E::round(__fadd_rn(a2[i], b2[i]));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x1[i] = E::round(a1[i]);
+      x2[i] = E::round(a2[i]);
+    }
+  }
+  if (u >= e.nh + e.nkv) {  // v: appended as is
+    T* dst = (T*)e.v_cache + ((int64_t)(u - e.nh - e.nkv) * e.cap + e.row0 + row) * e.hd;
+    V::store(dst + d1, x1);
+    V::store(dst + d2, x2);
+    return;
+  }
+  const int64_t p = e.positions[row];
+  if (p < 0 || p >= e.max_pos) {
+    if (e.status) atomicOr(e.status, PE_ERR_CAPACITY);
+    return;
+  }
+  const T* cosr = (const T*)e.cos_sin + p * e.hd;
+  const T* sinr = (const T*)e.cos_sin + (e.max_pos + p) * e.hd;
+  float c1[4], c2[4], s1[4], s2[4], o1[4], o2[4];
+  V::load(cosr + d1, c1);
+  V::load(cosr + d2, c2);
+  V::load(sinr + d1, s1);
+  V::load(sinr + d2, s2);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o1[i] = E::round(__fadd_rn(E::round(__fmul_rn(x1[i], c1[i])), E::round(__fmul_rn(-x2[i], s1[i]))));
+    o2[i] = E::round(__fadd_rn(E::round(__fmul_rn(x2[i], c2[i])), E::round(__fmul_rn(x1[i], s2[i]))));
+  }
+  T* dst = (u < e.nh) ? (T*)e.q_out + ((int64_t)row * e.nh + u) * e.hd
+                      : (T*)e.k_cache + ((int64_t)(u - e.nh) * e.cap + e.row0 + row) * e.hd;
+  V::store(dst + d1, o1);
+  V::store(dst + d2, o2);
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void rope_kv_partials_kernel(const float* __restrict__ partial, int S, EpiArgs e) {
-  const int pairs = e.N >> 1;
+  const int quads = e.N >> 3;
   const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= e.M * pairs) return;
-  const int row = idx / pairs, rem = idx - row * pairs;
-  const int group = rem >> 5, ln = rem & 31;
-  const float* pr = partial + (int64_t)row * e.N + group * 64 + ln;
-  float a1 = 0.f, a2 = 0.f;
-  for (int sp = 0; sp < S; ++sp) {
-    a1 += pr[(int64_t)sp * e.M * e.N];
-    a2 += pr[(int64_t)sp * e.M * e.N + 32];
-  }
-  write_rope_kv<DT>(e, group, ln, row, a1, a2);
+  if (idx >= e.M * quads) return;
+  const int row = idx / quads, rem = idx - row * quads;
+  const int group = rem >> 3, ln0 = (rem & 7) * 4;
+  float a1[4], a2[4];
+  sum_partials4(partial + (int64_t)row * e.N + group * 64 + ln0, S, (int64_t)e.M * e.N, a1, a2);
+  write_rope_kv4<DT>(e, group, ln0, row, a1, a2);
 }
 
 template <int DT>
 __global__ __launch_bounds__(256) void swiglu_partials_kernel(const float* __restrict__ partial, int S, EpiArgs e) {
-  const int pairs = e.N >> 1;
+  typedef Elem<DT> E;
+  typedef typename E::T T;
+  const int quads = e.N >> 3;
   const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= e.M * pairs) return;
-  const int row = idx / pairs, rem = idx - row * pairs;
-  const int group = rem >> 5, ln = rem & 31;
-  const float* pr = partial + (int64_t)row * e.N + group * 64 + ln;
-  float gv = 0.f, uv = 0.f;
-  for (int sp = 0; sp < S; ++sp) {
-    gv += pr[(int64_t)sp * e.M * e.N];
-    uv += pr[(int64_t)sp * e.M * e.N + 32];
-  }
-  epi_swiglu<DT>(e, row, group * 32 + ln, gv, uv);
+  if (idx >= e.M * quads) return;
+  const int row = idx / quads, rem = idx - row * quads;
+  const int group = rem >> 3, ln0 = (rem & 7) * 4;
+  float gv[4], uv[4], o[4];
+  sum_partials4(partial + (int64_t)row * e.N + group * 64 + ln0, S, (int64_t)e.M * e.N, gv, uv);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = E::round(__fmul_rn(E::round(silu_f(E::round(gv[i]))), E::round(uv[i])));
+  const int col = group * 32 + ln0;
+  T* out = (T*)e.out;
+  Vec4<DT>::store(out + (e.out_units ? xtile_index(row, col, e.out_units) : (int64_t)row * e.ld_out + col), o);
 }
 
 // ---------------------------------------------------------------------------
@@ -699,15 +794,15 @@ struct Plan {
 };
 
 // units: 128-wide K units (NF4) or 64-wide K steps (dense).
-// NF4: every workgroup of a launch is resident at once (three per CU with one
-// M tile, two with two), so S is the largest split that keeps groups * S
-// within them and leaves every wave at least `min_units` units.
+// NF4: the fewest splits that give at least `min_wgs` workgroups (one CU
+// pulls under 1/128 of the HBM bandwidth), keeping every wave at least
+// `min_units` units.
 // Dense: S spreads the work over about `wave_slots` waves (256 CUs x 3
 // four-wave workgroups), a wave getting at least 2 units.
 // Either way the splits are balanced to differ by at most one unit per wave.
 Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   static const int wave_slots = env_int("PE_GEMM_WAVE_SLOTS", 3072);
-  static const int nf4_wg_slots = env_int("PE_NF4_WG_SLOTS", 768);
+  static const int nf4_min_wgs = env_int("PE_NF4_MIN_WGS", 128);
   static const int nf4_min_units = env_int("PE_NF4_MIN_UNITS", 2);
   static const int min_units = env_int("PE_GEMM_MIN_UNITS", 2);
   Plan p;
@@ -716,8 +811,11 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   p.groups = N / (32 * p.NT);
   p.units = nf4 ? K / 128 : K / 64;
   int S;
-  if (nf4) {
-    S = (p.MT == 1 ? nf4_wg_slots : nf4_wg_slots * 2 / 3) / p.groups;
+  if (nf4 && p.MT == 1 && p.units <= kMaxSplits * kWaves * 2) {
+    // at most two units per wave: the wave issues all of its loads at once
+    S = (p.units + kWaves * 2 - 1) / (kWaves * 2);
+  } else if (nf4) {
+    S = (nf4_min_wgs + p.groups - 1) / p.groups;
     const int s_units = p.units / (kWaves * nf4_min_units);
     if (S > s_units) S = s_units;
   } else {
@@ -931,7 +1029,7 @@ int pe_internal_rope_kv_partials(const float* partial, int S, int M, int nh, int
   e.nkv = nkv;
   e.hd = hd;
   e.status = status;
-  const int grid = pe_cdiv((int64_t)M * (N / 2), 256);
+  const int grid = pe_cdiv((int64_t)M * (N / 8), 256);
   if (dtype == PE_DTYPE_BF16) rope_kv_partials_kernel<PE_DTYPE_BF16><<<grid, 256, 0, st>>>(partial, S, e);
   else if (dtype == PE_DTYPE_F16) rope_kv_partials_kernel<PE_DTYPE_F16><<<grid, 256, 0, st>>>(partial, S, e);
   else return PE_ERR_ARG;
@@ -946,7 +1044,7 @@ int pe_internal_swiglu_partials(const float* partial, int S, int M, int N, void*
   if (!partial || !out || S < 1 || M <= 0 || N <= 0 || N % 64) return PE_ERR_ARG;
   EpiArgs e = make_epi(PE_EPI_SWIGLU, M, N, nullptr, nullptr, 0, out, ld_out);
   e.out_units = out_units;
-  const int grid = pe_cdiv((int64_t)M * (N / 2), 256);
+  const int grid = pe_cdiv((int64_t)M * (N / 8), 256);
   if (dtype == PE_DTYPE_BF16) swiglu_partials_kernel<PE_DTYPE_BF16><<<grid, 256, 0, st>>>(partial, S, e);
   else if (dtype == PE_DTYPE_F16) swiglu_partials_kernel<PE_DTYPE_F16><<<grid, 256, 0, st>>>(partial, S, e);
   else return PE_ERR_ARG;

@@ -93,37 +93,27 @@ __global__ __launch_bounds__(256) void bias_to_bits_kernel(const typename Elem<D
 
 // Row argmax with torch.argmax's semantics: the largest value, a NaN beats
 // every number, and among equal maxima (or NaNs) the lowest index wins.
-struct ArgBest {
-  float v;
-  int idx;  // -1: none yet
-  int nan;
-};
-
-__device__ __forceinline__ bool arg_better(const ArgBest& b, const ArgBest& a) {  // b beats a
-  if (b.idx < 0) return false;
-  if (a.idx < 0) return true;
-  if (a.nan && b.nan) return b.idx < a.idx;
-  if (a.nan) return false;
-  if (b.nan) return true;
-  return (b.v > a.v) || (b.v == a.v && b.idx < a.idx);
-}
-
-__device__ __forceinline__ void arg_take(ArgBest& a, float v, int i) {
-  ArgBest b = {v, i, v != v};
-  if (arg_better(b, a)) a = b;
-}
-
 constexpr int kArgThreads = 1024;
 
-// One block of kArgThreads per row. Thread t scans 8-element vectors
-// t, t + kArgThreads, ... in increasing index order (all loads issued first),
-// then the block reduces with the same rule.
+// Order-preserving key of a value for the argmax: larger value -> larger key,
+// every NaN -> the largest key, -0 and +0 -> the same key (they compare equal).
+__device__ __forceinline__ uint32_t arg_key(float f) {
+  if (f != f) return 0xFFFFFFFFu;
+  const uint32_t u = f == 0.f ? 0u : __float_as_uint(f);
+  return (u >> 31) ? ~u : (u | 0x80000000u);
+}
+
+// One block of kArgThreads per row. Thread t scans 16-byte vectors t,
+// t + kArgThreads, ... in increasing index order (all loads issued first)
+// keeping the first element of the largest key; the block then reduces with
+// (key descending, index ascending).
 template <int DT>
 __device__ void row_argmax(const typename Elem<DT>::T* __restrict__ x, int64_t V, int32_t* out) {
   typedef typename Elem<DT>::T T;
   constexpr int kPer = 16 / sizeof(T);  // elements per 16-byte vector
   constexpr int kVec = 8;               // vectors per thread held in flight
-  ArgBest best = {0.f, -1, 0};
+  uint32_t bk = 0;                      // below every real key
+  int bi = -1;
   const bool aligned = (((uintptr_t)x) & 15) == 0;
   const int64_t nvec = aligned ? V / kPer : 0;
   for (int64_t v0 = 0; v0 < nvec; v0 += (int64_t)kVec * kArgThreads) {
@@ -139,27 +129,53 @@ __device__ void row_argmax(const typename Elem<DT>::T* __restrict__ x, int64_t V
       if (vi < nvec) {
         const T* e = (const T*)&buf[k];
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) arg_take(best, Elem<DT>::load(e, j), (int)(vi * kPer + j));
+        for (int j = 0; j < kPer; ++j) {
+          const uint32_t key = arg_key(Elem<DT>::load(e, j));
+          if (key > bk) {
+            bk = key;
+            bi = (int)(vi * kPer + j);
+          }
+        }
       }
     }
   }
-  for (int64_t i = nvec * kPer + threadIdx.x; i < V; i += kArgThreads) arg_take(best, Elem<DT>::load(x, i), (int)i);
+  for (int64_t i = nvec * kPer + threadIdx.x; i < V; i += kArgThreads) {
+    const uint32_t key = arg_key(Elem<DT>::load(x, i));
+    if (key > bk) {
+      bk = key;
+      bi = (int)i;
+    }
+  }
+  auto better = [](uint32_t k2, int i2, uint32_t k1, int i1) {  // (k2, i2) beats (k1, i1)
+    if (i2 < 0) return false;
+    if (i1 < 0) return true;
+    return k2 > k1 || (k2 == k1 && i2 < i1);
+  };
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    ArgBest b;
-    b.v = __shfl_xor(best.v, o, 64);
-    b.idx = __shfl_xor(best.idx, o, 64);
-    b.nan = __shfl_xor(best.nan, o, 64);
-    if (arg_better(b, best)) best = b;
+    const uint32_t k2 = __shfl_xor(bk, o, 64);
+    const int i2 = __shfl_xor(bi, o, 64);
+    if (better(k2, i2, bk, bi)) {
+      bk = k2;
+      bi = i2;
+    }
   }
-  __shared__ ArgBest wbest[kArgThreads / 64];
-  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+  __shared__ uint32_t wk[kArgThreads / 64];
+  __shared__ int wi[kArgThreads / 64];
+  if ((threadIdx.x & 63) == 0) {
+    wk[threadIdx.x >> 6] = bk;
+    wi[threadIdx.x >> 6] = bi;
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
-    ArgBest a = wbest[0];
+    uint32_t k1 = wk[0];
+    int i1 = wi[0];
     for (int w = 1; w < kArgThreads / 64; ++w)
-      if (arg_better(wbest[w], a)) a = wbest[w];
-    *out = a.idx;
+      if (better(wk[w], wi[w], k1, i1)) {
+        k1 = wk[w];
+        i1 = wi[w];
+      }
+    *out = i1;
   }
 }
 
@@ -180,21 +196,40 @@ __global__ __launch_bounds__(kArgThreads) void accept_argmax_kernel(const typena
   row_argmax<DT>(x, V, amax + r);
 }
 
-__global__ void accept_walk_kernel(const int32_t* __restrict__ amax, int T, const int64_t* __restrict__ tokens,
-                                   const int32_t* __restrict__ parents, int32_t* __restrict__ out) {
+// The walk reads every node's argmax, parent and token once: the block stages
+// them in LDS, then one thread walks (at most kWalkMax nodes).
+constexpr int kWalkThreads = 256;
+constexpr int kWalkMax = 64 * PE_TREE_MAX_WORDS;
+
+__global__ __launch_bounds__(kWalkThreads) void accept_walk_kernel(const int32_t* __restrict__ amax, int T,
+                                                                   const int64_t* __restrict__ tokens,
+                                                                   const int32_t* __restrict__ parents,
+                                                                   int32_t* __restrict__ out) {
+  __shared__ int32_t s_amax[kWalkMax + 1], s_par[kWalkMax];
+  __shared__ int64_t s_tok[kWalkMax];
+  const int n = min(T, kWalkMax);
+  for (int t = threadIdx.x; t <= n; t += kWalkThreads) s_amax[t] = amax[t];
+  for (int t = threadIdx.x; t < n; t += kWalkThreads) {
+    s_par[t] = parents[t];
+    s_tok[t] = tokens[t];
+  }
+  __syncthreads();
   if (threadIdx.x != 0) return;
   int cur = -1, len = 0;
-  int truth = amax[0];
+  int truth = s_amax[0];
   for (;;) {
     int nxt = -1;
-    for (int t = 0; t < T; ++t) {
-      if (parents[t] == cur && tokens[t] == (int64_t)truth) { nxt = t; break; }
+    for (int t = 0; t < n; ++t) {
+      if (s_par[t] == cur && s_tok[t] == (int64_t)truth) {
+        nxt = t;
+        break;
+      }
     }
-    if (nxt < 0 || len >= T) break;
+    if (nxt < 0 || len >= n) break;
     out[2 + len] = nxt;
     ++len;
     cur = nxt;
-    truth = amax[1 + nxt];
+    truth = s_amax[1 + nxt];
   }
   out[0] = len;
   out[1] = truth;
@@ -316,6 +351,7 @@ extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, i
                               void* stream) {
   if (!root_logit || !out || !scratch || T < 0 || V <= 0) return PE_ERR_ARG;
   if (T > 0 && (!node_logits || !node_tokens || !parents)) return PE_ERR_ARG;
+  if (T > kWalkMax) return PE_ERR_TREE;
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
     case PE_DTYPE_F32:
@@ -334,7 +370,7 @@ extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, i
       return PE_ERR_ARG;
   }
   PE_CHECK_LAUNCH();
-  accept_walk_kernel<<<1, 64, 0, st>>>(scratch, T, node_tokens, parents, out);
+  accept_walk_kernel<<<1, kWalkThreads, 0, st>>>(scratch, T, node_tokens, parents, out);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }
