@@ -794,9 +794,11 @@ struct Plan {
 };
 
 // units: 128-wide K units (NF4) or 64-wide K steps (dense).
-// NF4: the fewest splits that give at least `min_wgs` workgroups (one CU
-// pulls under 1/128 of the HBM bandwidth), keeping every wave at least
-// `min_units` units.
+// NF4 split partials (one M tile): K / 1024 splits, two units per wave.
+// NF4 otherwise: the fewest splits that give at least `min_wgs` workgroups
+// (one CU pulls under 1/128 of the HBM bandwidth), keeping every wave at least
+// `min_units` units; at the 7B shapes q/k/v and gate/up get one split (the
+// epilogue runs in the GEMM, no exchange).
 // Dense: S spreads the work over about `wave_slots` waves (256 CUs x 3
 // four-wave workgroups), a wave getting at least 2 units.
 // Either way the splits are balanced to differ by at most one unit per wave.
@@ -805,15 +807,17 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   static const int nf4_min_wgs = env_int("PE_NF4_MIN_WGS", 128);
   static const int nf4_min_units = env_int("PE_NF4_MIN_UNITS", 2);
   static const int min_units = env_int("PE_GEMM_MIN_UNITS", 2);
+  static const int nf4_upw = env_int("PE_NF4_UNITS_PER_WAVE", 2) == 1 ? 1 : 2;
   Plan p;
   p.NT = (epi == PE_EPI_SWIGLU || epi == kEpiRopeKV || N % 64 == 0) ? 2 : 1;
   p.MT = M > 32 ? 2 : 1;
   p.groups = N / (32 * p.NT);
   p.units = nf4 ? K / 128 : K / 64;
   int S;
-  if (nf4 && p.MT == 1 && p.units <= kMaxSplits * kWaves * 2) {
-    // at most two units per wave: the wave issues all of its loads at once
-    S = (p.units + kWaves * 2 - 1) / (kWaves * 2);
+  if (nf4 && p.MT == 1 && epi == kEpiPartial && p.units <= kMaxSplits * kWaves * nf4_upw) {
+    // split partials, at most two units per wave: the wave issues all of its
+    // loads at once
+    S = (p.units + kWaves * nf4_upw - 1) / (kWaves * nf4_upw);
   } else if (nf4) {
     S = (nf4_min_wgs + p.groups - 1) / p.groups;
     const int s_units = p.units / (kWaves * nf4_min_units);

@@ -90,11 +90,9 @@ Layout make_layout(const pe_model_desc* m, int M, int64_t kv_len) {
     L.attn_t = off; off += align_up(xtile_bytes(M, qd));
     L.act_t = off; off += align_up(xtile_bytes(M, ip));
     const int wf = m->weight_format;
-    const int64_t pb[4] = {pe_internal_linear_partials_bytes(M, nqkv, H, wf),
-                           pe_internal_linear_partials_bytes(M, H, qd, wf),
-                           pe_internal_linear_partials_bytes(M, 2 * ip, H, wf),
+    const int64_t pb[2] = {pe_internal_linear_partials_bytes(M, H, qd, wf),
                            pe_internal_linear_partials_bytes(M, H, ip, wf)};
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
       if (pb[i] > L.part_bytes) L.part_bytes = pb[i];
     L.part_bytes = align_up(L.part_bytes);
     L.part = off; off += L.part_bytes;
@@ -204,10 +202,10 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
                                         slot_ptr(f0), fused_ld, nullptr, 0, st));
     PE_TRY(copy_repeats(0, f0));
   }
-  // The tiled (NF4) pass: every GEMM writes split partials with plain stores
-  // and the kernel that consumes its output sums them (q/k/v: RoPE + KV append;
-  // o, down: residual + RMSNorm; gate/up: SwiGLU), so no GEMM waits on
-  // another workgroup of its own launch.
+  // The tiled (NF4) pass: q/k/v and gate/up run unsplit with their RoPE + KV
+  // append / SwiGLU epilogues in the GEMM; o and down write split partials
+  // with plain stores that the residual + RMSNorm kernel sums, so no GEMM
+  // waits on another workgroup of its own launch.
   float* part = tiled ? (float*)(ws + Lo.part) : nullptr;
   const int nqkv = (nh + 2 * nkv) * hd;
   int S = 0;
@@ -216,17 +214,9 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     void* vc = (char*)a->v_cache + l * layer_stride;
     const uint16_t* a_qkv = (const uint16_t*)(m->a_qkv ? m->a_qkv[l] : nullptr);
     const void* b_qkv = m->b_qkv ? m->b_qkv[l] : nullptr;
-    if (tiled) {
-      PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_norm, H, true, M, H, m->w_qkv[l], a_qkv, nqkv, part,
-                                         Lo.part_bytes, &S, st));
-      PE_TRY(pe_internal_rope_kv_partials(part, S, M, nh, nkv, hd, b_qkv, a->positions, m->rope_cos_sin,
-                                          m->max_positions, q, kc, vc, a->cache_capacity, a->prefix_len, a->status,
-                                          m->dtype, st));
-    } else {
-      PE_TRY(pe_internal_gemm_rope_kv(wf, m->dtype, x_norm, H, M, H, m->w_qkv[l], a_qkv, nh, nkv, hd, b_qkv,
-                                      a->positions, m->rope_cos_sin, m->max_positions, q, kc, vc, a->cache_capacity,
-                                      a->prefix_len, a->status, gws, gwsb, false, st));
-    }
+    PE_TRY(pe_internal_gemm_rope_kv(wf, m->dtype, x_norm, H, M, H, m->w_qkv[l], a_qkv, nh, nkv, hd, b_qkv,
+                                    a->positions, m->rope_cos_sin, m->max_positions, q, kc, vc, a->cache_capacity,
+                                    a->prefix_len, a->status, gws, gwsb, tiled, st));
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
                                       a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
                                       Lo.attn_ws_bytes, st));
@@ -249,9 +239,8 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     const int fx = last ? slot_of(L) : -1;
     const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
     if (tiled) {
-      PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_norm, H, true, M, H, m->w_gu[l], a_gu, 2 * ip, part,
-                                         Lo.part_bytes, &S, st));
-      PE_TRY(pe_internal_swiglu_partials(part, S, M, 2 * ip, x_act, ip, act_units, m->dtype, st));
+      PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, true, M, H, m->w_gu[l], a_gu, 2 * ip, PE_EPI_SWIGLU,
+                                nullptr, nullptr, 0, x_act, ip, act_units, gws, gwsb, st));
       PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_act, ip, true, M, ip, m->w_down[l], a_down, H, part,
                                          Lo.part_bytes, &S, st));
       PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, m->dtype, xn,
