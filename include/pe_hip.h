@@ -171,7 +171,8 @@ int64_t pe_attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_
 /* softmax(q k^T * scale + mask) v over cache rows [0, P + T) of one layer,
  * replacing HF sdpa_attention_forward (integrations/sdpa_attention.py:79-154)
  * with the tree bias of masks.py:127-147. q [T][nh][hd], caches [nkv][cap][hd],
- * out [T][ld_out] with head h at columns [h*hd, (h+1)*hd). */
+ * out [T][ld_out] with head h at columns [h*hd, (h+1)*hd). The workspace's
+ * first 4 KiB are arrival counters (zero before the first call, left zero). */
 int pe_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
                       int nh, int nkv, int hd, int T, int64_t P, int mask_mode,
                       const uint64_t* bits, int words, float scale, int dtype, void* out,

@@ -15,7 +15,9 @@
 //   O^T += V^T P^T (A = V^T from a wave-private LDS transpose of the 32-key V
 //   block, B = P^T taken directly from the S^T accumulator registers rounded to
 //   the compute dtype), so the per-row rescale is a per-lane scalar.
-//   Partial (O, max, sum) per split are combined by attn_combine_kernel.
+//   Each workgroup merges its waves and publishes its split's partial
+//   (O, max, sum); the last workgroup of a (KV head, row tile) to arrive
+//   combines the splits in split order and writes the output.
 // Softmax is fp32; exp(s - m) is summed in fp32 and rounded to the compute
 // dtype for the PV product, as torch's CPU flash attention does for reduced
 // precision inputs.
@@ -49,9 +51,14 @@ __device__ __forceinline__ bool key_allowed(int64_t key, int64_t P, int t, int m
 // from there per k-step), and a wave stays within 256 VGPRs: two workgroups
 // per CU. Loads are clamped to the wave's last valid key (those scores are
 // masked and their probabilities are exactly zero), so no uninitialised cache
-// row is read. At the end the 4 waves' (m, l, O) are merged in LDS in wave
-// order by all 256 threads, and one partial per workgroup is written for
-// attn_combine_kernel with coalesced stores.
+// row is read. At the end the waves' (m, l, O) are merged in LDS in wave
+// order by all threads. With several splits the workgroup publishes that
+// partial with agent-coherent 16-byte stores and counts itself on the pair's
+// arrival counter; the last to arrive reads every split's partial (its own
+// from registers) and combines them in split order: out = sum_s e^{m_s - M}
+// O_s / sum_s e^{m_s - M} l_s, accumulated online (running max, rescaled
+// sums). Nobody waits for anybody, and the result does not depend on the
+// arrival order.
 constexpr int kAttnWaves = 8;
 constexpr int kQStride = 128 + 8;  // LDS row stride of the staged Q tile (elements)
 constexpr int kVRow = 128 + 32;    // LDS row stride of a wave's V tile (elements): 320 B, rows 16 banks apart
@@ -63,7 +70,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
     int nh, int nkv, int T, int64_t P, int mask_mode, const uint64_t* __restrict__ bits, int words, float scale,
     int keys_per_split, int splits, int rows_pad, float* __restrict__ opart, float* __restrict__ mlpart,
-    void* __restrict__ out, int64_t ld_out, int out_units) {
+    int* __restrict__ counters, void* __restrict__ out, int64_t ld_out, int out_units) {
   constexpr int HD = 128;
   constexpr int kQBytes = 32 * kQStride * 2;
   constexpr int kVtBytes = 32 * kVRow * 2;  // one 32-key V block, row-major
@@ -327,72 +334,55 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
     return;
   }
   // partial[pair][split][row][128] and ml[pair][split][row][4] (m, l, -, -),
-  // pair = kvh * row_tiles + rt: plain coalesced stores; attn_combine_kernel
-  // reads them after the kernel boundary
+  // pair = kvh * row_tiles + rt
   const int row_tiles = rows_pad >> 5;
-  const int64_t pr = (((int64_t)(kvh * row_tiles + rt) * splits) + split) * 32 + row;
-  f32x4_t* op = (f32x4_t*)(opart + pr * HD + dc);
+  const int pair = kvh * row_tiles + rt;
+  const uint32_t nrows = (uint32_t)(nkv * row_tiles * splits * 32);
+  const __amdgpu_buffer_rsrc_t ro = agent_rsrc(opart, nrows * HD * 4), rm = agent_rsrc(mlpart, nrows * 16);
+  auto prow = [&](int sp) -> uint32_t { return (uint32_t)((pair * splits + sp) * 32 + row); };
 #pragma unroll
-  for (int k = 0; k < kDimsT / 4; ++k) op[k] = f32x4_t{acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]};
-  if (dc == 0) *(f32x4_t*)(mlpart + pr * 4) = f32x4_t{M, L, 0.f, 0.f};
-}
-
-// out rows of one (KV head, row tile) pair from its split partials, in split
-// order (online: running max, rescaled sums):
-// out = sum_s e^{m_s - M} O_s / sum_s e^{m_s - M} l_s. One wave = 8 rows; a
-// lane owns 16 dims of one row and has every split's loads in flight at once.
-template <int DT>
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ opart,
-                                                          const float* __restrict__ mlpart, int nh, int nkv, int T,
-                                                          int splits, int rows_pad, void* __restrict__ out,
-                                                          int64_t ld_out, int out_units) {
-  constexpr int HD = 128;
-  const int pair = blockIdx.x, row_tiles = rows_pad >> 5;
-  const int kvh = pair / row_tiles, rt = pair % row_tiles;
-  const int G = nh / nkv, rows = T * G;
-  const int row = blockIdx.y * 8 + (threadIdx.x >> 3), dc = (threadIdx.x & 7) * 16;
-  const int rr = rt * 32 + row;
-  if (rr >= rows) return;
-  const int64_t pb0 = (int64_t)pair * splits * 32 + row;
-  float Mx = kInitMax, den = 0.f, num[16];
+  for (int k = 0; k < kDimsT / 4; ++k)
+    store_agent_x4(ro, (prow(split) * HD + dc) * 4 + 16 * k,
+                   f32x4_t{acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]});
+  if (dc == 0) store_agent_x4(rm, prow(split) * 16, f32x4_t{M, L, 0.f, 0.f});
+  // the stores are acknowledged at agent scope before this workgroup counts itself
+  __builtin_amdgcn_s_waitcnt(0);
+  __shared__ int s_arrived;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_arrived = __hip_atomic_fetch_add(counters + pair, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_arrived != splits - 1) return;
+  if (threadIdx.x == 0) __hip_atomic_store(counters + pair, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float Mx = kInitMax, den = 0.f, num[kDimsT];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) num[k] = 0.f;
-  for (int c0 = 0; c0 < splits; c0 += 8) {
-    f32x4_t ov[8][4], mv[8];
+  for (int k = 0; k < kDimsT; ++k) num[k] = 0.f;
+  for (int c0 = 0; c0 < splits; c0 += 8) {  // up to 8 splits' loads in flight
+    f32x4_t ov[8][kDimsT / 4], mv[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const int sp = c0 + c;
-      if (sp < splits) {
-        const f32x4_t* op = (const f32x4_t*)(opart + (pb0 + (int64_t)sp * 32) * HD + dc);
+      if (sp < splits && sp != split) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) ov[c][k] = op[k];
-        mv[c] = *(const f32x4_t*)(mlpart + (pb0 + (int64_t)sp * 32) * 4);
+        for (int k = 0; k < kDimsT / 4; ++k) ov[c][k] = load_agent_x4(ro, (prow(sp) * HD + dc) * 4 + 16 * k);
+        mv[c] = load_agent_x4(rm, prow(sp) * 16);
       }
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      if (c0 + c >= splits) break;
-      const float mn = fmaxf(Mx, mv[c][0]);
-      const float a = expf(Mx - mn), wt = expf(mv[c][0] - mn);
+      const int sp = c0 + c;
+      if (sp >= splits) break;
+      const float ms = sp == split ? M : mv[c][0], ls = sp == split ? L : mv[c][1];
+      const float mn = fmaxf(Mx, ms);
+      const float a = expf(Mx - mn), wt = expf(ms - mn);
       Mx = mn;
-      den = den * a + wt * mv[c][1];
+      den = den * a + wt * ls;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) num[k] = num[k] * a + wt * ov[c][k >> 2][k & 3];
+      for (int k = 0; k < kDimsT; ++k) num[k] = num[k] * a + wt * (sp == split ? acc[k] : ov[c][k >> 2][k & 3]);
     }
   }
-  const int tt = rr / G, col0 = (kvh * G + rr % G) * HD + dc;
-  typedef typename Elem<DT>::T Te;
-  // 16 consecutive dims: four 4-element stores (consecutive in either layout)
-#pragma unroll
-  for (int k4 = 0; k4 < 4; ++k4) {
-    float o[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = Elem<DT>::round(num[4 * k4 + i] / den);
-    const int col = col0 + 4 * k4;
-    Vec4<DT>::store((Te*)out + (out_units ? xtile_index(tt, col, out_units) : (int64_t)tt * ld_out + col), o);
-  }
+  write_out(num, den);
 }
-
 
 // Generic path (fp32, any hd <= 256): one block per (row t, query head), all keys.
 template <int DT>
@@ -448,9 +438,11 @@ __global__ __launch_bounds__(128) void attn_generic_kernel(
   }
 }
 
+constexpr int64_t kAttnCounterBytes = 4096;  // per-pair arrival counters (zero between launches)
+
 struct AttnPlan {
   int splits, keys_per_split, row_tiles, rows_pad;
-  int64_t opart_bytes, ml_bytes;  // workspace: [O partials | (m, l) partials]
+  int64_t opart_bytes, ml_bytes;  // workspace: [counters | O partials | (m, l) partials]
 };
 
 AttnPlan attn_plan(int T, int nh, int nkv, int64_t S) {
@@ -482,7 +474,7 @@ extern "C" int64_t pe_attention_workspace_bytes(int T, int nh, int nkv, int hd, 
   if (T <= 0 || nh <= 0 || nkv <= 0 || kv_len <= 0) return 0;
   if (dtype != PE_DTYPE_F32 && hd == 128) {
     AttnPlan p = attn_plan(T, nh, nkv, kv_len);
-    return p.opart_bytes + p.ml_bytes;
+    return kAttnCounterBytes + p.opart_bytes + p.ml_bytes;
   }
   return (int64_t)T * nh * kv_len * 4;
 }
@@ -490,7 +482,7 @@ extern "C" int64_t pe_attention_workspace_bytes(int T, int nh, int nkv, int hd, 
 int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap, int nh,
                                int nkv, int hd, int T, int64_t P, int mask_mode, const uint64_t* bits, int words,
                                float scale, int dtype, void* out, int64_t ld_out, int out_units, void* workspace,
-                               int64_t workspace_bytes, hipStream_t st) {
+                               int64_t workspace_bytes, int* counters, hipStream_t st) {
   if (!q || !k_cache || !v_cache || !out || !workspace) return PE_ERR_ARG;
   if (out_units && (dtype == PE_DTYPE_F32 || hd != 128 || T > 64 || out_units * 128 != nh * hd)) return PE_ERR_ARG;
   if (T <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || hd <= 0 || hd > 256 || P < 0) return PE_ERR_ARG;
@@ -502,26 +494,19 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
   if (workspace_bytes < pe_attention_workspace_bytes(T, nh, nkv, hd, S, dtype)) return PE_ERR_WORKSPACE;
   if (dtype != PE_DTYPE_F32 && hd == 128) {
     AttnPlan p = attn_plan(T, nh, nkv, S);
-    float* opart = (float*)workspace;
-    float* ml = (float*)((char*)workspace + p.opart_bytes);
+    if ((int64_t)nkv * p.row_tiles * 4 > kAttnCounterBytes) return PE_ERR_ARG;
+    if (!counters) counters = (int*)workspace;
+    float* opart = (float*)((char*)workspace + kAttnCounterBytes);
+    float* ml = (float*)((char*)workspace + kAttnCounterBytes + p.opart_bytes);
     dim3 grid(nkv, p.splits, p.row_tiles);
-    dim3 cgrid(nkv * p.row_tiles, 4);
     if (dtype == PE_DTYPE_BF16) {
       attn_wg_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>(
           (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P, mask_mode,
-          bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, out, ld_out, out_units);
-      PE_CHECK_LAUNCH();
-      if (p.splits > 1)
-        attn_combine_kernel<PE_DTYPE_BF16><<<cgrid, 64, 0, st>>>(opart, ml, nh, nkv, T, p.splits, p.rows_pad, out,
-                                                                 ld_out, out_units);
+          bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters, out, ld_out, out_units);
     } else if (dtype == PE_DTYPE_F16) {
       attn_wg_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>(
           (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P, mask_mode,
-          bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, out, ld_out, out_units);
-      PE_CHECK_LAUNCH();
-      if (p.splits > 1)
-        attn_combine_kernel<PE_DTYPE_F16><<<cgrid, 64, 0, st>>>(opart, ml, nh, nkv, T, p.splits, p.rows_pad, out,
-                                                                ld_out, out_units);
+          bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters, out, ld_out, out_units);
     } else {
       return PE_ERR_ARG;
     }
@@ -561,5 +546,5 @@ extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void*
                                  float scale, int dtype, void* out, int64_t ld_out, void* workspace,
                                  int64_t workspace_bytes, void* stream) {
   return pe_internal_tree_attention(q, k_cache, v_cache, cache_cap, nh, nkv, hd, T, P, mask_mode, bits, words, scale,
-                                    dtype, out, ld_out, 0, workspace, workspace_bytes, (hipStream_t)stream);
+                                    dtype, out, ld_out, 0, workspace, workspace_bytes, nullptr, (hipStream_t)stream);
 }

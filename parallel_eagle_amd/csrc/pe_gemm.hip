@@ -249,12 +249,12 @@ __host__ __device__ constexpr int64_t partial_bytes_of(int S, int groups, int MT
   return S > 1 ? (int64_t)S * groups * MT * NT * kWaves * 64 * 16 : 0;
 }
 
-// The waves' K slices summed in LDS (wave order); wave w then owns rows
+// The KW waves' K slices summed in LDS (wave order); wave w < 4 then owns rows
 // 8 w + 4 g + j (j < 4) of every M tile. With S > 1 the workgroup publishes
 // its sums as split `split` of the group's partials and the last workgroup of
 // the group to arrive sums all S of them in split order. The caller has
 // synchronised the workgroup if `red` had another use.
-template <int ADT, int NT, int MT>
+template <int ADT, int NT, int MT, int KW = kWaves>
 __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red, int group, int split, int S,
                                             float* __restrict__ partial, int* __restrict__ counters,
                                             const EpiArgs& e) {
@@ -267,6 +267,7 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
 #pragma unroll
       for (int r = 0; r < 16; ++r) red[(((wave * NT + nt) * MT + mt) * 16 + r) * 64 + lane] = acc[nt][mt][r];
   lds_barrier();
+  if (KW > kWaves && wave >= kWaves) return;
   float v[MT][4][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -276,7 +277,7 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
       for (int nt = 0; nt < NT; ++nt) {
         float s = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) s += red[(((w * NT + nt) * MT + mt) * 16 + 4 * wave + j) * 64 + lane];
+        for (int w = 0; w < KW; ++w) s += red[(((w * NT + nt) * MT + mt) * 16 + 4 * wave + j) * 64 + lane];
         v[mt][j][nt] = s;
       }
 
@@ -385,18 +386,19 @@ template <int MT, int NT, int WV, bool XT>
 __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* smem,
                                               const uint16_t* __restrict__ X, int64_t ldx,
                                               const uint8_t* __restrict__ W, const uint16_t* __restrict__ Wabs,
-                                              int NP, int group, int w0, int w1, int M) {
+                                              int NP, int group, int w0, int w1, int M, uint32_t region) {
   constexpr int XD = MT == 1 ? 8 : 4;  // X k-steps in flight
   const int n = max(w1 - w0, 0);
   const int lane = threadIdx.x & 63;
   const int g = lane >> 5, ln = lane & 31;
   constexpr int TB = WV * NT * kTabTile;  // this wave's table area
-  uint8_t* lanetab = smem + lane * 4;
-  // LDS address registers: the lane's table base in the low byte (the kernel's
-  // only LDS object starts at offset 0, so bits 8..15 are free for the code).
+  uint8_t* lanetab = smem + region + lane * 4;
+  // LDS address registers: the lane's table base in the low byte and the
+  // table region (a multiple of 64 KiB) above bit 16 (the kernel's only LDS
+  // object starts at offset 0, so bits 8..15 are free for the code).
   uint32_t addr[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) addr[i] = (uint32_t)(lane * 4);
+  for (int i = 0; i < 8; ++i) addr[i] = region + (uint32_t)(lane * 4);
 
   // Rows at or beyond M read row M - 1: MFMA rows are independent and those
   // output rows are never stored.
@@ -409,7 +411,16 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
   u32x4_t x[MT][XD];              // X fragments of k-steps s .. s + XD - 1
 
   const int wl = max(w1 - 1, 0);
-  auto tile_of = [&](int nt, int p) -> int64_t { return (int64_t)(group * NT + nt) * NP + min(p, wl); };
+  // The wave visits its units starting at a group-dependent rotation, so the
+  // workgroups streaming at the same time touch different offsets of their
+  // 64 KiB-aligned tiles. Unit p (w0 <= p, clamped to the last) -> stored unit.
+  const int rot = n > 0 ? group % n : 0;
+  auto unit_of = [&](int p) -> int {
+    int r = min(p, wl) - w0 + rot;
+    if (r >= n) r -= n;
+    return n > 0 ? w0 + r : min(p, wl);
+  };
+  auto tile_of = [&](int nt, int p) -> int64_t { return (int64_t)(group * NT + nt) * NP + unit_of(p); };
   auto load_codes = [&](u32x4_t (&q)[NT][2], int p) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -425,7 +436,7 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
       for (int nt = 0; nt < NT; ++nt) ac[h][nt] = Wabs[tile_of(nt, p + h) * 64 + lane];
   };
   auto load_x = [&](int slot, int p, int s) {
-    const int pc = min(p, wl);
+    const int pc = unit_of(p);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       if constexpr (XT) x[mt][slot] = *(const u32x4_t*)(X + ((((int64_t)mt * NP + pc) * 8 + s) * 64 + lane) * 8);
@@ -479,7 +490,7 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
       load_codes(qb, w0 + 1);
 #pragma unroll
       for (int s = 0; s < XD; ++s) {
-        const int pc = min(w0 + 1, wl);
+        const int pc = unit_of(w0 + 1);
         if constexpr (XT) xb[0][s] = *(const u32x4_t*)(X + (((int64_t)pc * 8 + s) * 64 + lane) * 8);
         else xb[0][s] = *(const u32x4_t*)(xrow[0] + 128 * pc + 8 * s);
       }
@@ -525,23 +536,26 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
   if (n & 1) unit(qa, p, kLo, x, true);
 }
 
-template <int MT, int NT, bool XT>
-__global__ __launch_bounds__(kWaves * 64, MT == 1 ? 3 : 2) void nf4_gemm_kernel(const uint16_t* __restrict__ X, int64_t ldx,
-                                                                  const uint8_t* __restrict__ W,
-                                                                  const uint16_t* __restrict__ Wabs, int NP, int S,
-                                                                  int pps, float* __restrict__ partial,
-                                                                  int* __restrict__ counters, EpiArgs e) {
+// KW = 4 or 8 waves. Waves w and w + 4 run the same code (table offsets are
+// immediates of wave index w % 4); the second four keep their tables 64 KiB
+// higher, selected by bit 16 of the LDS address.
+template <int MT, int NT, bool XT, int KW>
+__global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_gemm_kernel(
+    const uint16_t* __restrict__ X, int64_t ldx, const uint8_t* __restrict__ W, const uint16_t* __restrict__ Wabs,
+    int NP, int S, int pps, float* __restrict__ partial, int* __restrict__ counters, EpiArgs e) {
   constexpr int kTabBytes = kWaves * NT * kTabTile;
-  constexpr int kRedBytes = kWaves * NT * MT * 16 * 64 * 4;
   static_assert(kTabBytes <= 65536, "table offsets must fit the 16-bit LDS immediate");
-  __shared__ __align__(256) uint8_t smem[kTabBytes > kRedBytes ? kTabBytes : kRedBytes];
+  constexpr int kTabAll = KW == 8 ? 65536 + kTabBytes : kTabBytes;
+  constexpr int kRedBytes = KW * NT * MT * 16 * 64 * 4;
+  __shared__ __align__(256) uint8_t smem[kTabAll > kRedBytes ? kTabAll : kRedBytes];
   const int group = blockIdx.x, split = blockIdx.y;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int p0 = split * pps;
   const int p1 = min(NP, p0 + pps);
   const int np = max(0, p1 - p0);
-  const int w0 = p0 + (np * wave) / kWaves;
-  const int w1 = p0 + (np * (wave + 1)) / kWaves;
+  const int w0 = p0 + (np * wave) / KW;
+  const int w1 = p0 + (np * (wave + 1)) / KW;
+  const uint32_t region = wave >= 4 ? 65536u : 0u;
 
   f32x16_t acc[NT][MT];
 #pragma unroll
@@ -551,14 +565,14 @@ __global__ __launch_bounds__(kWaves * 64, MT == 1 ? 3 : 2) void nf4_gemm_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.f;
 
-  switch (wave) {
-    case 0: nf4_wave_body<MT, NT, 0, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); break;
-    case 1: nf4_wave_body<MT, NT, 1, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); break;
-    case 2: nf4_wave_body<MT, NT, 2, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); break;
-    default: nf4_wave_body<MT, NT, 3, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M); break;
+  switch (wave & 3) {
+    case 0: nf4_wave_body<MT, NT, 0, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region); break;
+    case 1: nf4_wave_body<MT, NT, 1, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region); break;
+    case 2: nf4_wave_body<MT, NT, 2, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region); break;
+    default: nf4_wave_body<MT, NT, 3, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region); break;
   }
   lds_barrier();  // every wave is done with its tables; smem becomes the reduction buffer
-  finish_tile<PE_DTYPE_BF16, NT, MT>(acc, (float*)smem, group, split, S, partial, counters, e);
+  finish_tile<PE_DTYPE_BF16, NT, MT, KW>(acc, (float*)smem, group, split, S, partial, counters, e);
 }
 
 // ---------------------------------------------------------------------------
@@ -790,6 +804,7 @@ int env_int(const char* name, int dflt) {
 
 struct Plan {
   int NT, MT, S, per_split, groups, units;
+  int KW;  // NF4 waves per workgroup (4, or 8 for an unsplit launch of at most one workgroup per CU)
   int64_t partial_bytes;
 };
 
@@ -808,6 +823,7 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   static const int nf4_min_units = env_int("PE_NF4_MIN_UNITS", 2);
   static const int min_units = env_int("PE_GEMM_MIN_UNITS", 2);
   static const int nf4_upw = env_int("PE_NF4_UNITS_PER_WAVE", 2) == 1 ? 1 : 2;
+  static const int nf4_wide_groups = env_int("PE_NF4_WIDE_GROUPS", 256);
   Plan p;
   p.NT = (epi == PE_EPI_SWIGLU || epi == kEpiRopeKV || N % 64 == 0) ? 2 : 1;
   p.MT = M > 32 ? 2 : 1;
@@ -833,6 +849,9 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   p.per_split = (p.units + S - 1) / S;
   p.S = (p.units + p.per_split - 1) / p.per_split;
   p.partial_bytes = partial_bytes_of(p.S, p.groups, p.MT, p.NT);
+  // Fewer column groups than CUs: eight waves per workgroup, two per SIMD, so
+  // one wave's waits overlap the other's issue.
+  p.KW = (nf4 && p.MT == 1 && p.NT == 2 && p.S == 1 && p.groups <= nf4_wide_groups) ? 8 : 4;
   return p;
 }
 
@@ -848,10 +867,13 @@ int launch_gemm(int fmt, const Plan& p, hipStream_t st, const uint16_t* x, int64
   float* partial = (float*)((char*)ws + kCounterBytes);
   if (fmt < 0) {
 #define PE_NF4(MT_, NT_, XT_)                                                                                  \
-  nf4_gemm_kernel<MT_, NT_, XT_><<<grid, kWaves * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, p.S, \
-                                                                p.per_split, partial, counters, e)
+  nf4_gemm_kernel<MT_, NT_, XT_, kWaves><<<grid, kWaves * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, \
+                                                                        p.S, p.per_split, partial, counters, e)
     if (x_tiled) {
-      if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, true); else PE_NF4(2, 2, true); }
+      if (p.NT == 2 && p.MT == 1 && p.KW == 8)
+        nf4_gemm_kernel<1, 2, true, 8><<<grid, 8 * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, p.S,
+                                                                 p.per_split, partial, counters, e);
+      else if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, true); else PE_NF4(2, 2, true); }
       else { if (p.MT == 1) PE_NF4(1, 1, true); else PE_NF4(2, 1, true); }
     } else {
       if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, false); else PE_NF4(2, 2, false); }

@@ -57,4 +57,4 @@ PE_INTERNAL int pe_internal_tree_attention(const void* q, const void* k_cache, c
                                            int nh, int nkv, int hd, int T, int64_t P, int mask_mode,
                                            const uint64_t* bits, int words, float scale, int dtype, void* out,
                                            int64_t ld_out, int out_units, void* workspace, int64_t workspace_bytes,
-                                           hipStream_t st);
+                                           int* counters, hipStream_t st);

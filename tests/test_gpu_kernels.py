@@ -108,6 +108,21 @@ def test_nf4_linear_tiled_x_equals_row_major(m, epi):
     assert torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("m", [1, 26, 32])
+@pytest.mark.parametrize("n,k", [(12288, 4096), (8192, 1024), (16384, 512)])
+def test_nf4_tiled_unsplit_wide_workgroups(m, n, k):
+    """Unsplit launches with 128..256 column groups run eight waves per
+    workgroup (two table regions): the stored bf16 product equals the fp32
+    product of the exact dequantised operands up to bf16 rounding of the
+    output and fp32 accumulation order."""
+    (tiled, tabs), wdq = _nf4_weight(n, k, seed=m + n + k + 1)
+    x = torch.from_numpy(synth.normal(m, 37, m * k, 1.0).reshape(m, k)).to(torch.bfloat16)
+    got = ops.linear_tiled(ops.to_xtile(x.to(DEV)), m, k, n, (tiled, tabs)).cpu().float()
+    ref32 = x.float() @ wdq.float().t()
+    err = (got - ref32).abs()
+    assert torch.all(err <= 2.0 ** -8 * ref32.abs() + 1e-4 * (1 + ref32.abs()) * (k / 1024)), err.max()
+
+
 @pytest.mark.parametrize("m", [1, 26, 33, 64])
 @pytest.mark.parametrize("n,k,tiled", [(4096, 4096, True), (22016, 4096, True), (4096, 11008, True),
                                        (256, 1024, False)])
