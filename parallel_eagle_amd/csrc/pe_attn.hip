@@ -20,7 +20,9 @@
 //   combines the splits in split order and writes the output.
 // Softmax is fp32; exp(s - m) is summed in fp32 and rounded to the compute
 // dtype for the PV product, as torch's CPU flash attention does for reduced
-// precision inputs.
+// precision inputs. Scores are kept in base 2 (q.k * scale * log2 e), so every
+// exponential is one v_exp_f32 (2^x) and the running maxima and split partials
+// are in base 2 as well.
 //
 // fp32 path: one block per (row, query head), scores in LDS, VALU arithmetic.
 
@@ -62,7 +64,7 @@ __device__ __forceinline__ bool key_allowed(int64_t key, int64_t P, int t, int m
 constexpr int kAttnWaves = 8;
 constexpr int kQStride = 128 + 8;  // LDS row stride of the staged Q tile (elements)
 constexpr int kVRow = 128 + 32;    // LDS row stride of a wave's V tile (elements): 320 B, rows 16 banks apart
-constexpr int kCmbRow = 128 + 1;   // LDS row stride of the wave merge (floats; odd: no bank conflicts)
+constexpr int kCmbRow = 128 + 4;   // LDS row stride of the wave merge (floats; 16-byte aligned rows)
 constexpr int kAttnMaxSplits = 16;
 
 template <int DT>
@@ -97,20 +99,24 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
   const char* vbase = (const char*)(vc + (int64_t)kvh * cap * HD);
   u32x4_t kf[2][8], vf[2][8];
   auto load_pair = [&](int64_t jb) {
+    const int nsb = jb + 32 < j1 ? 2 : 1;  // a wave's last block may be a single one
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
+      if (sb == 1 && nsb == 1) break;
       const uint32_t ko = (uint32_t)min(jb + 32 * sb + ln, jlast) * (HD * 2) + 16 * g;
 #pragma unroll
       for (int j = 0; j < 8; ++j) kf[sb][j] = *(const u32x4_t*)(kbase + ko + 32 * j);
     }
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
+    for (int sb = 0; sb < 2; ++sb) {
+      if (sb == 1 && nsb == 1) break;
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         // 32 keys x 16 chunks of 8 dims: lane covers key 4c + lane / 16, chunk lane % 16
         const uint32_t vo = (uint32_t)min(jb + 32 * sb + 4 * c + (lane >> 4), jlast) * (HD * 2) + (lane & 15) * 16;
         vf[sb][c] = *(const u32x4_t*)(vbase + vo);
       }
+    }
   };
   // the row tile's Q (rows past `rows` are zero) is requested first, so
   // staging it waits for Q alone and not for the KV stream behind it
@@ -146,8 +152,10 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
   float m = kInitMax, l = 0.f;
   __syncthreads();  // Q staged
 
+  const float scale2 = scale * 1.44269504088896341f;  // natural-log scores -> base 2
   auto process = [&](int64_t jb, auto first_c) {
     constexpr bool kFirst = decltype(first_c)::value;
+    const bool two = jb + 32 < j1;  // wave-uniform: the pair's second block has keys
     // ---- S^T = K Q^T over hd, two 32-key halves
     f32x16_t sc[2];
 #pragma unroll
@@ -159,6 +167,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
       const u32x4_t qf = *(const u32x4_t*)&qs[ln][16 * j + 8 * g];
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
+        if (sb == 1 && !two) break;
         if constexpr (DT == PE_DTYPE_F16)
           sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[sb][j]),
                                                           __builtin_bit_cast(f16x8_t, qf), sc[sb], 0, 0, 0);
@@ -171,12 +180,13 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
     float bmax = kInitMax;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
+      if (sb == 1 && !two) break;
       const int64_t kb = jb + 32 * sb;
       if (kb + 32 <= min(P, j1) && (mask_mode == PE_MASK_TREE || kb + 32 <= P + 1)) {
         // a whole 32-key half of prefix keys: every key is visible to every node
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          sc[sb][i] = rvalid ? sc[sb][i] * scale : kMaskedScore;
+          sc[sb][i] = rvalid ? sc[sb][i] * scale2 : kMaskedScore;
           bmax = fmaxf(bmax, sc[sb][i]);
         }
       } else {
@@ -184,21 +194,25 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
         for (int i = 0; i < 16; ++i) {
           const int64_t kj = kb + 8 * (i >> 2) + 4 * g + (i & 3);
           const bool ok = rvalid && kj < j1 && key_allowed(kj, P, t, mask_mode, nbits);
-          sc[sb][i] = ok ? sc[sb][i] * scale : kMaskedScore;
+          sc[sb][i] = ok ? sc[sb][i] * scale2 : kMaskedScore;
           bmax = fmaxf(bmax, sc[sb][i]);
         }
       }
     }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
     const float mnew = fmaxf(m, bmax);
-    const float alpha = expf(m - mnew);
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
     float psum = 0.f;
     uint32_t pb[2][8];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
       for (int i = 0; i < 16; i += 2) {
-        const float p0 = expf(sc[sb][i] - mnew), p1 = expf(sc[sb][i + 1] - mnew);
+        if (sb == 1 && !two) {
+          pb[sb][i >> 1] = 0u;
+          continue;
+        }
+        const float p0 = __builtin_amdgcn_exp2f(sc[sb][i] - mnew), p1 = __builtin_amdgcn_exp2f(sc[sb][i + 1] - mnew);
         psum += p0 + p1;
         pb[sb][i >> 1] = (DT == PE_DTYPE_F16)
                              ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
@@ -223,6 +237,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
     const int qg = lane >> 4, jl = lane & 15;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
+      if (sb == 1 && !two) break;
       if (sb == 1) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -295,10 +310,13 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
   __syncthreads();  // every wave is done with Q and its V^T tile
   float* cmb = (float*)smem;                     // [wave][row][kCmbRow]: O of the wave's keys
   float* mlw = cmb + kAttnWaves * 32 * kCmbRow;  // [wave][row][2]: m, l
+  // o[h][4c .. 4c + 3] are dims 32 h + 8 c + 4 g + 0..3 of row ln: 16-byte stores
 #pragma unroll
   for (int h = 0; h < 4; ++h)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) cmb[(wave * 32 + ln) * kCmbRow + h * 32 + 8 * (i >> 2) + 4 * g + (i & 3)] = o[h][i];
+    for (int c = 0; c < 4; ++c)
+      *(f32x4_t*)&cmb[(wave * 32 + ln) * kCmbRow + h * 32 + 8 * c + 4 * g] =
+          f32x4_t{o[h][4 * c], o[h][4 * c + 1], o[h][4 * c + 2], o[h][4 * c + 3]};
   if (g == 0) {
     mlw[(wave * 32 + ln) * 2] = m;
     mlw[(wave * 32 + ln) * 2 + 1] = l;
@@ -314,10 +332,14 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
   for (int k = 0; k < kDimsT; ++k) acc[k] = 0.f;
 #pragma unroll
   for (int w = 0; w < kAttnWaves; ++w) {
-    const float wt = expf(mlw[(w * 32 + row) * 2] - M);
+    const float wt = __builtin_amdgcn_exp2f(mlw[(w * 32 + row) * 2] - M);
     L += wt * mlw[(w * 32 + row) * 2 + 1];
 #pragma unroll
-    for (int k = 0; k < kDimsT; ++k) acc[k] += wt * cmb[(w * 32 + row) * kCmbRow + dc + k];
+    for (int k4 = 0; k4 < kDimsT / 4; ++k4) {
+      const f32x4_t cv = *(const f32x4_t*)&cmb[(w * 32 + row) * kCmbRow + dc + 4 * k4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[4 * k4 + k] += wt * cv[k];
+    }
   }
   const int rr = rt * 32 + row;
   auto write_out = [&](const float (&num)[kDimsT], float den) {
@@ -374,7 +396,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
       if (sp >= splits) break;
       const float ms = sp == split ? M : mv[c][0], ls = sp == split ? L : mv[c][1];
       const float mn = fmaxf(Mx, ms);
-      const float a = expf(Mx - mn), wt = expf(ms - mn);
+      const float a = __builtin_amdgcn_exp2f(Mx - mn), wt = __builtin_amdgcn_exp2f(ms - mn);
       Mx = mn;
       den = den * a + wt * ls;
 #pragma unroll
