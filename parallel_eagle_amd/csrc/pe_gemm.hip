@@ -254,32 +254,46 @@ __host__ __device__ constexpr int64_t partial_bytes_of(int S, int groups, int MT
 // its sums as split `split` of the group's partials and the last workgroup of
 // the group to arrive sums all S of them in split order. The caller has
 // synchronised the workgroup if `red` had another use.
+// LDS of the reduction: per (wave, tile, M tile) 64 lanes x kRedLane floats,
+// the lane's 16 accumulators at a 20-float (80-byte) stride, so 16-byte
+// accesses of 16 consecutive lanes hit 64 distinct banks.
+constexpr int kRedLane = 20;
+__host__ __device__ constexpr int red_floats(int KW, int NT, int MT) { return KW * NT * MT * 64 * kRedLane; }
+
 template <int ADT, int NT, int MT, int KW = kWaves>
 __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red, int group, int split, int S,
                                             float* __restrict__ partial, int* __restrict__ counters,
                                             const EpiArgs& e) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 5, ln = lane & 31;
+  auto slot = [&](int w, int nt, int mt) -> f32x4_t* {
+    return (f32x4_t*)(red + ((((w * NT + nt) * MT + mt) * 64) + lane) * kRedLane);
+  };
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[(((wave * NT + nt) * MT + mt) * 16 + r) * 64 + lane] = acc[nt][mt][r];
+      for (int q = 0; q < 4; ++q)
+        slot(wave, nt, mt)[q] = f32x4_t{acc[nt][mt][4 * q], acc[nt][mt][4 * q + 1], acc[nt][mt][4 * q + 2],
+                                        acc[nt][mt][4 * q + 3]};
   lds_barrier();
   if (KW > kWaves && wave >= kWaves) return;
   float v[MT][4][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int nt = 0; nt < NT; ++nt) {
+      f32x4_t s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        float s = 0.f;
+      for (int w = 0; w < KW; ++w) {
+        const f32x4_t t = slot(w, nt, mt)[wave];
 #pragma unroll
-        for (int w = 0; w < KW; ++w) s += red[(((w * NT + nt) * MT + mt) * 16 + 4 * wave + j) * 64 + lane];
-        v[mt][j][nt] = s;
+        for (int j = 0; j < 4; ++j) s[j] += t[j];
       }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[mt][j][nt] = s[j];
+    }
 
   if (e.op == kEpiPartial) {
     float* out = (float*)e.out + (int64_t)split * e.M * e.N;
@@ -546,7 +560,7 @@ __global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_
   constexpr int kTabBytes = kWaves * NT * kTabTile;
   static_assert(kTabBytes <= 65536, "table offsets must fit the 16-bit LDS immediate");
   constexpr int kTabAll = KW == 8 ? 65536 + kTabBytes : kTabBytes;
-  constexpr int kRedBytes = KW * NT * MT * 16 * 64 * 4;
+  constexpr int kRedBytes = red_floats(KW, NT, MT) * 4;
   __shared__ __align__(256) uint8_t smem[kTabAll > kRedBytes ? kTabAll : kRedBytes];
   const int group = blockIdx.x, split = blockIdx.y;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -584,7 +598,7 @@ __global__ __launch_bounds__(kWaves * 64, 3) void dense_gemm_kernel(const uint16
                                                                     int K, const uint16_t* __restrict__ W, int S,
                                                                     int ups, float* __restrict__ partial,
                                                                     int* __restrict__ counters, EpiArgs e) {
-  __shared__ __align__(16) float red[kWaves * NT * MT * 16 * 64];
+  __shared__ __align__(16) float red[red_floats(kWaves, NT, MT)];
   const int group = blockIdx.x, split = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 5, ln = lane & 31;
