@@ -148,10 +148,12 @@ def time_pass(step, steps: int, warmup: int):
 
 def nf4_gemm_roofline(tm, wl, reps: int):
     """Mean duration and algorithmic bytes per launch of the NF4 dequant-GEMM
-    kernel as the pass runs it: the 4 * L launches of one pass (q/k/v, o,
-    gate/up, down; each writing fp32 split partials that the next kernel of the
-    pass sums) on A-tiled activations, same weights and shapes, replayed from a
-    HIP graph and timed with HIP events on the stream the launches use."""
+    kernel as the pass runs it: the 4 * L launches of one pass on A-tiled
+    activations, same weights, shapes and launch plans (q/k/v unsplit with
+    eight waves per workgroup, here with the plain store epilogue in place of
+    RoPE + KV append; o and down as fp32 split partials; gate/up unsplit with
+    the SwiGLU epilogue into the A-tiled activation), replayed from a HIP graph
+    and timed with HIP events on the stream the launches use."""
     import ctypes as C
 
     import torch
@@ -173,14 +175,28 @@ def nf4_gemm_roofline(tm, wl, reps: int):
     part = torch.empty(part_bytes // 4, dtype=torch.float32, device=dev)
     splits = C.c_int(0)
     st = ops.stream_ptr
+    qkv_out = torch.empty((M, nqkv), dtype=bf, device=dev)
+    act_out = torch.zeros_like(act_t)
+    ws_bytes = max(int(L.pe_gemm_workspace_bytes(M, n, H, _lib.PE_WFMT_NF4, _lib.PE_DTYPE_BF16, epi))
+                   for n, epi in ((nqkv, _lib.PE_EPI_STORE), (2 * ip, _lib.PE_EPI_SWIGLU)))
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+
+    def unsplit(x, K, w, a, N, epi, out, ld_out, out_units):
+        _lib.check(L.pe_nf4_gemm_tiled(x.data_ptr(), M, K, w.data_ptr(), a.data_ptr(), N, epi, None, None, 0,
+                                       out.data_ptr(), ld_out, out_units, ws.data_ptr(), ws_bytes, st()),
+                   "pe_nf4_gemm_tiled")
+
+    def partials(x, K, w, a, N):
+        _lib.check(L.pe_nf4_gemm_partials(x.data_ptr(), K, 1, M, K, w.data_ptr(), a.data_ptr(), N,
+                                          part.data_ptr(), part_bytes, C.byref(splits), st()),
+                   "pe_nf4_gemm_partials")
 
     def seq():
         for ly in m.layers:
-            for (x, K, w, a, N) in ((xn_t, H, ly["w_qkv"], ly["a_qkv"], nqkv), (attn_t, qd, ly["w_o"], ly["a_o"], H),
-                                    (xn_t, H, ly["w_gu"], ly["a_gu"], 2 * ip), (act_t, ip, ly["w_down"], ly["a_down"], H)):
-                _lib.check(L.pe_nf4_gemm_partials(x.data_ptr(), K, 1, M, K, w.data_ptr(), a.data_ptr(), N,
-                                                  part.data_ptr(), part_bytes, C.byref(splits), st()),
-                           "pe_nf4_gemm_partials")
+            unsplit(xn_t, H, ly["w_qkv"], ly["a_qkv"], nqkv, _lib.PE_EPI_STORE, qkv_out, nqkv, 0)
+            partials(attn_t, qd, ly["w_o"], ly["a_o"], H)
+            unsplit(xn_t, H, ly["w_gu"], ly["a_gu"], 2 * ip, _lib.PE_EPI_SWIGLU, act_out, 0, ip // 128)
+            partials(act_t, ip, ly["w_down"], ly["a_down"], H)
 
     seq()
     torch.cuda.synchronize()
@@ -207,7 +223,7 @@ def nf4_gemm_roofline(tm, wl, reps: int):
     per_layer = sum(nf4_bytes(n, k) + 2 * M * k + 2 * M * n for n, k in ((nqkv, H), (H, qd), (2 * I, H), (H, I)))
     bytes_per_launch = per_layer * s.num_layers / launches
     gbs = bytes_per_launch / (mean_us * 1e-6) / 1e9
-    return {"kernel": "nf4_gemm_kernel (A-tiled X, fp32 split partials; q/k/v, o, gate/up, down: "
+    return {"kernel": "nf4_gemm_kernel (A-tiled X; q/k/v and gate/up unsplit, o and down fp32 split partials: "
                       "the 4 x L launches of one pass)",
             "mean_launch_us": round(mean_us, 3), "bytes_per_launch": int(bytes_per_launch),
             "achieved": round(gbs, 1)}
