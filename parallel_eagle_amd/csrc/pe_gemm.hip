@@ -120,8 +120,11 @@ __device__ __forceinline__ f32x16_t mfma16(u32x4_t a, u32x4_t b, f32x16_t c) {
 // of one head unit u (units: nh q heads, then nkv k heads, then nkv v heads;
 // j = group % (hd / 64)). The two halves a RoPE pair needs are therefore in
 // the same lane: o1 = r(r(x1 cos1) + r(-x2 sin1)), o2 = r(r(x2 cos2) + r(x1 sin2)).
+// c1, s1, c2, s2: cos / sin at dims d1, d2 of position p (read by the caller;
+// unused for v and for an out-of-range p).
 template <int DT>
-__device__ __forceinline__ void write_rope_kv(const EpiArgs& e, int group, int ln, int row, float a1, float a2) {
+__device__ __forceinline__ void write_rope_kv_core(const EpiArgs& e, int group, int ln, int row, float a1, float a2,
+                                                   int64_t p, float c1, float s1, float c2, float s2) {
   typedef Elem<DT> E;
   typedef typename E::T T;
   const int gpu = e.hd >> 6;  // column groups per head unit
@@ -140,20 +143,55 @@ __device__ __forceinline__ void write_rope_kv(const EpiArgs& e, int group, int l
     E::store(dst, d2, x2);
     return;
   }
-  const int64_t p = e.positions[row];
   if (p < 0 || p >= e.max_pos) {
     if (e.status) atomicOr(e.status, PE_ERR_CAPACITY);
     return;
   }
-  const T* cosr = (const T*)e.cos_sin + p * e.hd;
-  const T* sinr = (const T*)e.cos_sin + (e.max_pos + p) * e.hd;
-  const float o1 = __fadd_rn(E::round(__fmul_rn(x1, E::load(cosr, d1))), E::round(__fmul_rn(-x2, E::load(sinr, d1))));
-  const float o2 = __fadd_rn(E::round(__fmul_rn(x2, E::load(cosr, d2))), E::round(__fmul_rn(x1, E::load(sinr, d2))));
+  const float o1 = __fadd_rn(E::round(__fmul_rn(x1, c1)), E::round(__fmul_rn(-x2, s1)));
+  const float o2 = __fadd_rn(E::round(__fmul_rn(x2, c2)), E::round(__fmul_rn(x1, s2)));
   T* dst = (u < e.nh) ? (T*)e.q_out + ((int64_t)row * e.nh + u) * e.hd
                       : (T*)e.k_cache + ((int64_t)(u - e.nh) * e.cap + e.row0 + row) * e.hd;
   E::store(dst, d1, o1);
   E::store(dst, d2, o2);
 }
+
+// cos / sin of position p at dims d1, d2 (zeros for v heads or p out of range).
+template <int DT>
+__device__ __forceinline__ void rope_fetch(const EpiArgs& e, int group, int ln, int64_t p, float& c1, float& s1,
+                                           float& c2, float& s2) {
+  typedef Elem<DT> E;
+  typedef typename E::T T;
+  const int gpu = e.hd >> 6;
+  const int u = group / gpu, j = group % gpu;
+  c1 = s1 = c2 = s2 = 0.f;
+  if (u >= e.nh + e.nkv || p < 0 || p >= e.max_pos) return;
+  const int d1 = 32 * j + ln, d2 = d1 + (e.hd >> 1);
+  const T* cosr = (const T*)e.cos_sin + p * e.hd;
+  const T* sinr = (const T*)e.cos_sin + (e.max_pos + p) * e.hd;
+  c1 = E::load(cosr, d1);
+  s1 = E::load(sinr, d1);
+  c2 = E::load(cosr, d2);
+  s2 = E::load(sinr, d2);
+}
+
+template <int DT>
+__device__ __forceinline__ void write_rope_kv(const EpiArgs& e, int group, int ln, int row, float a1, float a2) {
+  const int gpu = e.hd >> 6;
+  const bool v = group / gpu >= e.nh + e.nkv;
+  const int64_t p = v ? 0 : e.positions[row];
+  float c1, s1, c2, s2;
+  rope_fetch<DT>(e, group, ln, p, c1, s1, c2, s2);
+  write_rope_kv_core<DT>(e, group, ln, row, a1, a2, p, c1, s1, c2, s2);
+}
+
+// RoPE epilogue operands of a wave's output rows (rows 8 w + 4 g + j of each
+// M tile), fetched while the GEMM runs: positions at kernel start, cos / sin
+// once the wave's first loads are issued.
+template <int MT>
+struct RopePre {
+  int64_t pos[MT][4];
+  float c1[MT][4], s1[MT][4], c2[MT][4], s2[MT][4];
+};
 
 
 // ---------------------------------------------------------------------------
@@ -263,7 +301,8 @@ __host__ __device__ constexpr int red_floats(int KW, int NT, int MT) { return KW
 template <int ADT, int NT, int MT, int KW = kWaves>
 __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red, int group, int split, int S,
                                             float* __restrict__ partial, int* __restrict__ counters,
-                                            const EpiArgs& e) {
+                                            const EpiArgs& e, const RopePre<MT>* rp = nullptr,
+                                            bool use_rp = false) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 5, ln = lane & 31;
   auto slot = [&](int w, int nt, int mt) -> f32x4_t* {
@@ -374,7 +413,15 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = mt * 32 + 8 * wave + 4 * g + j;
-      if (row < e.M) epilogue_row<ADT, NT>(e, group, row, ln, v[mt][j]);
+      if (row >= e.M) continue;
+      if constexpr (NT == 2) {
+        if (use_rp && e.op == kEpiRopeKV) {
+          write_rope_kv_core<ADT>(e, group, ln, row, v[mt][j][0], v[mt][j][1], rp->pos[mt][j], rp->c1[mt][j],
+                                  rp->s1[mt][j], rp->c2[mt][j], rp->s2[mt][j]);
+          continue;
+        }
+      }
+      epilogue_row<ADT, NT>(e, group, row, ln, v[mt][j]);
     }
 }
 
@@ -396,11 +443,13 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
 // The loop runs whole rounds of two units and is straight-line (prefetches
 // past w1 are clamped to the last unit), so the compiler's wait counts stay
 // exact; an odd last unit follows the loop.
-template <int MT, int NT, int WV, bool XT>
+// `mid` runs once the wave's first loads are issued (epilogue operands that
+// do not depend on the product are requested there).
+template <int MT, int NT, int WV, bool XT, typename Mid>
 __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* smem,
                                               const uint16_t* __restrict__ X, int64_t ldx,
                                               const uint8_t* __restrict__ W, const uint16_t* __restrict__ Wabs,
-                                              int NP, int group, int w0, int w1, int M, uint32_t region) {
+                                              int NP, int group, int w0, int w1, int M, uint32_t region, Mid&& mid) {
   constexpr int XD = MT == 1 ? 8 : 4;  // X k-steps in flight
   const int n = max(w1 - w0, 0);
   const int lane = threadIdx.x & 63;
@@ -510,6 +559,7 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
       }
       __builtin_amdgcn_sched_barrier(0);
       build();
+      mid();
       __builtin_amdgcn_sched_barrier(0);
       if (n > 0) unit(qa, w0, kLo, x, false);
       if (n > 1) unit(qb, w0 + 1, kHi, xb, false);
@@ -533,6 +583,7 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
   build();
   __builtin_amdgcn_sched_barrier(0);
   load_abs(w0 + 2);
+  mid();
   const int rounds = n >> 1;
   int p = w0;
   for (int r = 0; r < rounds; ++r, p += 2) {
@@ -570,6 +621,29 @@ __global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_
   const int w0 = p0 + (np * wave) / KW;
   const int w1 = p0 + (np * (wave + 1)) / KW;
   const uint32_t region = wave >= 4 ? 65536u : 0u;
+  // eight-wave q/k/v launches fetch their RoPE operands while the GEMM runs
+  const bool rope_pre = KW == 8 && NT == 2 && e.op == kEpiRopeKV && wave < kWaves;
+  RopePre<MT> rp;
+  {
+    const int lane = threadIdx.x & 63, g = lane >> 5;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = mt * 32 + 8 * wave + 4 * g + j;
+        rp.pos[mt][j] = (rope_pre && row < e.M) ? e.positions[row] : -1;
+      }
+  }
+  auto mid = [&]() {
+    if (!rope_pre) return;
+    const int ln = threadIdx.x & 31;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        rope_fetch<PE_DTYPE_BF16>(e, group, ln, rp.pos[mt][j], rp.c1[mt][j], rp.s1[mt][j], rp.c2[mt][j],
+                                  rp.s2[mt][j]);
+  };
 
   f32x16_t acc[NT][MT];
 #pragma unroll
@@ -580,13 +654,13 @@ __global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_
       for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.f;
 
   switch (wave & 3) {
-    case 0: nf4_wave_body<MT, NT, 0, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region); break;
-    case 1: nf4_wave_body<MT, NT, 1, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region); break;
-    case 2: nf4_wave_body<MT, NT, 2, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region); break;
-    default: nf4_wave_body<MT, NT, 3, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region); break;
+    case 0: nf4_wave_body<MT, NT, 0, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
+    case 1: nf4_wave_body<MT, NT, 1, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
+    case 2: nf4_wave_body<MT, NT, 2, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
+    default: nf4_wave_body<MT, NT, 3, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
   }
   lds_barrier();  // every wave is done with its tables; smem becomes the reduction buffer
-  finish_tile<PE_DTYPE_BF16, NT, MT, KW>(acc, (float*)smem, group, split, S, partial, counters, e);
+  finish_tile<PE_DTYPE_BF16, NT, MT, KW>(acc, (float*)smem, group, split, S, partial, counters, e, &rp, rope_pre);
 }
 
 // ---------------------------------------------------------------------------
