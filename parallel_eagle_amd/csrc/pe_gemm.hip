@@ -607,16 +607,32 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
 template <int MT, int NT, bool XT, int KW>
 __global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_gemm_kernel(
     const uint16_t* __restrict__ X, int64_t ldx, const uint8_t* __restrict__ W, const uint16_t* __restrict__ Wabs,
-    int NP, int S, int pps, float* __restrict__ partial, int* __restrict__ counters, EpiArgs e) {
+    int NP, int S, int pps, float* __restrict__ partial, int* __restrict__ counters, EpiArgs e, int nl, int tS,
+    int tpps) {
   constexpr int kTabBytes = kWaves * NT * kTabTile;
   static_assert(kTabBytes <= 65536, "table offsets must fit the 16-bit LDS immediate");
   constexpr int kTabAll = KW == 8 ? 65536 + kTabBytes : kTabBytes;
   constexpr int kRedBytes = red_floats(KW, NT, MT) * 4;
   __shared__ __align__(256) uint8_t smem[kTabAll > kRedBytes ? kTabAll : kRedBytes];
-  const int group = blockIdx.x, split = blockIdx.y;
+  // nl > 0: workgroups [0, nl) take column groups [0, nl) whole; the rest take
+  // the remaining groups in tS splits of tpps units each (split-K exchange)
+  int group = blockIdx.x, split = blockIdx.y, Sg = S, ppsg = pps;
+  if (nl > 0) {
+    if ((int)blockIdx.x < nl) {
+      split = 0;
+      Sg = 1;
+      ppsg = NP;
+    } else {
+      const int t = blockIdx.x - nl;
+      group = nl + t / tS;
+      split = t % tS;
+      Sg = tS;
+      ppsg = tpps;
+    }
+  }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int p0 = split * pps;
-  const int p1 = min(NP, p0 + pps);
+  const int p0 = split * ppsg;
+  const int p1 = min(NP, p0 + ppsg);
   const int np = max(0, p1 - p0);
   const int w0 = p0 + (np * wave) / KW;
   const int w1 = p0 + (np * (wave + 1)) / KW;
@@ -660,7 +676,7 @@ __global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_
     default: nf4_wave_body<MT, NT, 3, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
   }
   lds_barrier();  // every wave is done with its tables; smem becomes the reduction buffer
-  finish_tile<PE_DTYPE_BF16, NT, MT, KW>(acc, (float*)smem, group, split, S, partial, counters, e, &rp, rope_pre);
+  finish_tile<PE_DTYPE_BF16, NT, MT, KW>(acc, (float*)smem, group, split, Sg, partial, counters, e, &rp, rope_pre);
 }
 
 // ---------------------------------------------------------------------------
@@ -892,6 +908,9 @@ int env_int(const char* name, int dflt) {
 
 struct Plan {
   int NT, MT, S, per_split, groups, units;
+  // NF4 hybrid launch (column groups between one and two per CU): nl whole
+  // groups, the other groups in tS splits of tpps units; nl = 0 otherwise
+  int nl, tS, tpps;
   int KW;  // NF4 waves per workgroup (4, or 8 for an unsplit launch of at most one workgroup per CU)
   int64_t partial_bytes;
 };
@@ -905,6 +924,18 @@ struct Plan {
 // Dense: S spreads the work over about `wave_slots` waves (256 CUs x 3
 // four-wave workgroups), a wave getting at least 2 units.
 // Either way the splits are balanced to differ by at most one unit per wave.
+// CUs of the current device (256 on MI355X), queried once.
+int cu_count() {
+  static const int n = [] {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                  hipSuccess || cus <= 0)
+      cus = 256;
+    return cus;
+  }();
+  return n;
+}
+
 Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   static const int wave_slots = env_int("PE_GEMM_WAVE_SLOTS", 3072);
   static const int nf4_min_wgs = env_int("PE_NF4_MIN_WGS", 128);
@@ -912,6 +943,7 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   static const int min_units = env_int("PE_GEMM_MIN_UNITS", 2);
   static const int nf4_upw = env_int("PE_NF4_UNITS_PER_WAVE", 2) == 1 ? 1 : 2;
   static const int nf4_wide_groups = env_int("PE_NF4_WIDE_GROUPS", 256);
+  static const bool nf4_hybrid = env_int("PE_NF4_HYBRID", 1) != 0;
   Plan p;
   p.NT = (epi == PE_EPI_SWIGLU || epi == kEpiRopeKV || N % 64 == 0) ? 2 : 1;
   p.MT = M > 32 ? 2 : 1;
@@ -940,6 +972,19 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   // Fewer column groups than CUs: eight waves per workgroup, two per SIMD, so
   // one wave's waits overlap the other's issue.
   p.KW = (nf4 && p.MT == 1 && p.NT == 2 && p.S == 1 && p.groups <= nf4_wide_groups) ? 8 : 4;
+  // Between one and two column groups per CU (unsplit): one whole group per
+  // CU, the rest split 4 ways, so each CU carries one whole group and one or
+  // two quarter groups instead of one or two whole ones; the quarters finish
+  // early and their exchange is off the critical path.
+  p.nl = p.tS = p.tpps = 0;
+  const int ncu = cu_count();
+  if (nf4 && p.MT == 1 && p.NT == 2 && p.S == 1 && epi != kEpiPartial && nf4_hybrid && p.groups > ncu &&
+      p.groups < 2 * ncu && p.units >= 4 * kWaves) {
+    p.nl = ncu;
+    p.tS = 4;
+    p.tpps = (p.units + p.tS - 1) / p.tS;
+    p.partial_bytes = partial_bytes_of(p.tS, p.groups, p.MT, p.NT);
+  }
   return p;
 }
 
@@ -951,16 +996,19 @@ int launch_gemm(int fmt, const Plan& p, hipStream_t st, const uint16_t* x, int64
                 const void* w, const uint16_t* wabs, void* ws, const EpiArgs& e) {
   if (p.groups > kMaxGroups) return PE_ERR_ARG;
   dim3 grid(p.groups, p.S);
+  if (p.nl > 0) grid = dim3(p.nl + (p.groups - p.nl) * p.tS, 1);
   int* counters = (int*)ws;
   float* partial = (float*)((char*)ws + kCounterBytes);
   if (fmt < 0) {
 #define PE_NF4(MT_, NT_, XT_)                                                                                  \
   nf4_gemm_kernel<MT_, NT_, XT_, kWaves><<<grid, kWaves * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, \
-                                                                        p.S, p.per_split, partial, counters, e)
+                                                                        p.S, p.per_split, partial, counters, e, \
+                                                                        p.nl, p.tS, p.tpps)
     if (x_tiled) {
       if (p.NT == 2 && p.MT == 1 && p.KW == 8)
         nf4_gemm_kernel<1, 2, true, 8><<<grid, 8 * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, p.S,
-                                                                 p.per_split, partial, counters, e);
+                                                                 p.per_split, partial, counters, e, p.nl, p.tS,
+                                                                 p.tpps);
       else if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, true); else PE_NF4(2, 2, true); }
       else { if (p.MT == 1) PE_NF4(1, 1, true); else PE_NF4(2, 1, true); }
     } else {
