@@ -944,6 +944,8 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   static const int nf4_upw = env_int("PE_NF4_UNITS_PER_WAVE", 2) == 1 ? 1 : 2;
   static const int nf4_wide_groups = env_int("PE_NF4_WIDE_GROUPS", 256);
   static const bool nf4_hybrid = env_int("PE_NF4_HYBRID", 1) != 0;
+  static const int nf4_hybrid_ts = env_int("PE_NF4_HYBRID_TS", 4);
+  static const int nf4_hybrid_less = env_int("PE_NF4_HYBRID_LESS", 0);
   Plan p;
   p.NT = (epi == PE_EPI_SWIGLU || epi == kEpiRopeKV || N % 64 == 0) ? 2 : 1;
   p.MT = M > 32 ? 2 : 1;
@@ -980,8 +982,8 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   const int ncu = cu_count();
   if (nf4 && p.MT == 1 && p.NT == 2 && p.S == 1 && epi != kEpiPartial && nf4_hybrid && p.groups > ncu &&
       p.groups < 2 * ncu && p.units >= 4 * kWaves) {
-    p.nl = ncu;
-    p.tS = 4;
+    p.nl = ncu - nf4_hybrid_less;
+    p.tS = nf4_hybrid_ts;
     p.tpps = (p.units + p.tS - 1) / p.tS;
     p.partial_bytes = partial_bytes_of(p.tS, p.groups, p.MT, p.NT);
   }
