@@ -345,11 +345,21 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
   auto write_out = [&](const float (&num)[kDimsT], float den) {
     if (rr >= rows) return;
     const int tt = rr / G, col0 = (kvh * G + rr % G) * HD + dc;
+    typedef typename Elem<DT>::T Te;
+    if (!out_units && ((ld_out & 3) || ((uintptr_t)out & 7))) {  // row-major output not 8-byte aligned
 #pragma unroll
-    for (int k = 0; k < kDimsT; ++k)
-      Elem<DT>::store((typename Elem<DT>::T*)out,
-                      out_units ? xtile_index(tt, col0 + k, out_units) : (int64_t)tt * ld_out + col0 + k,
-                      num[k] / den);
+      for (int k = 0; k < kDimsT; ++k) Elem<DT>::store((Te*)out, (int64_t)tt * ld_out + col0 + k, num[k] / den);
+      return;
+    }
+    // four consecutive dims per store (consecutive in either layout)
+#pragma unroll
+    for (int k4 = 0; k4 < kDimsT / 4; ++k4) {
+      float o4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o4[i] = num[4 * k4 + i] / den;
+      const int col = col0 + 4 * k4;
+      Vec4<DT>::store((Te*)out + (out_units ? xtile_index(tt, col, out_units) : (int64_t)tt * ld_out + col), o4);
+    }
   };
   if (splits == 1) {
     write_out(acc, L);
