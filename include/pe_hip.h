@@ -10,7 +10,8 @@
  * bit; the host reads it after the stream synchronises.
  *
  * Scratch buffers (`workspace`) are caller-owned; their counters region must
- * be zero when first used and is left zero by every call.
+ * be zero when first used. GEMM calls leave their counters zero; attention
+ * calls leave theirs multiples of 16.
  *
  * The reference implements this pass in Python over transformers/torch/
  * bitsandbytes; each entry point below names the reference function it
@@ -120,7 +121,7 @@ int pe_nf4_gemm_tiled(const void* x_tiled, int M, int K, const uint8_t* w_tiled,
  * with plain stores and no exchange between workgroups; *splits (host memory)
  * receives S. X row-major (ldx) or A-tiled (x_tiled != 0). M <= 64, K % 128 == 0,
  * N % 32 == 0. Layout variant of pe_nf4_gemm with no reference counterpart: the
- * pass's residual+RMSNorm, RoPE/KV-append and SwiGLU kernels consume it. */
+ * pass's residual + RMSNorm kernel consumes it (o and down projections). */
 int64_t pe_nf4_gemm_partials_bytes(int M, int N, int K);
 int pe_nf4_gemm_partials(const void* x, int64_t ldx, int x_tiled, int M, int K, const uint8_t* w_tiled,
                          const uint16_t* absmax_tiled, int N, float* partials, int64_t partial_bytes, int* splits,
@@ -172,7 +173,8 @@ int64_t pe_attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_
  * replacing HF sdpa_attention_forward (integrations/sdpa_attention.py:79-154)
  * with the tree bias of masks.py:127-147. q [T][nh][hd], caches [nkv][cap][hd],
  * out [T][ld_out] with head h at columns [h*hd, (h+1)*hd). The workspace's
- * first 4 KiB are arrival counters (zero before the first call, left zero). */
+ * first 4 KiB are arrival counters: zero before the first call; every call
+ * leaves them multiples of 16. */
 int pe_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
                       int nh, int nkv, int hd, int T, int64_t P, int mask_mode,
                       const uint64_t* bits, int words, float scale, int dtype, void* out,

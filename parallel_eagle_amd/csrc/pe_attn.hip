@@ -86,7 +86,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
   const int64_t S = P + T;
   const int64_t ks0 = (int64_t)split * keys_per_split;
   const int64_t ks1 = min(S, ks0 + keys_per_split);
-  const int nb = (int)((ks1 - ks0 + 31) / 32);
+  const int nb = ks1 > ks0 ? (int)((ks1 - ks0 + 31) / 32) : 0;  // trailing splits may be empty
   const int b0 = (nb * wave) / kAttnWaves, b1 = (nb * (wave + 1)) / kAttnWaves;
   const int64_t j1 = min(ks1, ks0 + 32 * (int64_t)b1);  // end of this wave's keys
   const int64_t jlast = j1 - 1;
@@ -379,13 +379,17 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
   if (dc == 0) store_agent_x4(rm, prow(split) * 16, f32x4_t{M, L, 0.f, 0.f});
   // the stores are acknowledged at agent scope before this workgroup counts itself
   __builtin_amdgcn_s_waitcnt(0);
+  // Each workgroup adds kAttnMaxSplits / splits (splits is a power of two), so
+  // a launch adds kAttnMaxSplits to the pair's counter and the workgroup that
+  // brings it to a multiple of kAttnMaxSplits is the last of this launch; the
+  // counter is never reset (wrap-around keeps the multiples).
+  const int inc = kAttnMaxSplits / splits;
   __shared__ int s_arrived;
   __syncthreads();
   if (threadIdx.x == 0)
-    s_arrived = __hip_atomic_fetch_add(counters + pair, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_arrived = __hip_atomic_fetch_add(counters + pair, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  if (s_arrived != splits - 1) return;
-  if (threadIdx.x == 0) __hip_atomic_store(counters + pair, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (((s_arrived + inc) & (kAttnMaxSplits - 1)) != 0) return;
   float Mx = kInitMax, den = 0.f, num[kDimsT];
 #pragma unroll
   for (int k = 0; k < kDimsT; ++k) num[k] = 0.f;
@@ -470,7 +474,9 @@ __global__ __launch_bounds__(128) void attn_generic_kernel(
   }
 }
 
-constexpr int64_t kAttnCounterBytes = 4096;  // per-pair arrival counters (zero between launches)
+// per-pair arrival counters: zero before first use, multiples of
+// kAttnMaxSplits between launches
+constexpr int64_t kAttnCounterBytes = 4096;
 
 struct AttnPlan {
   int splits, keys_per_split, row_tiles, rows_pad;
@@ -490,11 +496,13 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S) {
   int64_t cap_splits = 256 / pairs;
   if (cap_splits > kAttnMaxSplits) cap_splits = kAttnMaxSplits;
   if (want > cap_splits) want = cap_splits;
-  if (want < 1) want = 1;
-  int64_t kps = (S + want - 1) / want;
+  // a power of two (the arrival count is kept modulo kAttnMaxSplits)
+  int64_t pw = 1;
+  while (pw * 2 <= want) pw *= 2;
+  int64_t kps = (S + pw - 1) / pw;
   kps = ((kps + 31) / 32) * 32;
   p.keys_per_split = (int)kps;
-  p.splits = (int)((S + kps - 1) / kps);
+  p.splits = (int)pw;
   p.opart_bytes = (int64_t)nkv * p.splits * p.rows_pad * 128 * 4;
   p.ml_bytes = (int64_t)nkv * p.splits * p.rows_pad * 4 * 4;
   return p;

@@ -264,7 +264,7 @@ __device__ __forceinline__ void lds_barrier() {
 // ---------------------------------------------------------------------------
 constexpr int kWaves = 4;             // waves per GEMM workgroup (K slices)
 constexpr int kCounterBytes = 32768;  // per-column-group arrival counters at the head of the workspace
-constexpr int kMaxGroups = kCounterBytes / 4;
+constexpr int kMaxGroups = kGemmCounterInts;  // the rest of the counter area belongs to attention
 constexpr int kMaxSplits = 16;
 
 // Epilogue of one output row of a column group: v[nt] is the lane's column of

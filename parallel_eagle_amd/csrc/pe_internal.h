@@ -51,8 +51,16 @@ PE_INTERNAL int pe_internal_residual_rmsnorm(const float* partial, int S, int M,
                                              float eps, int dtype, void* xn, void* xn_tiled, void* cap_h,
                                              int64_t ld_cap_h, void* cap_xn, int64_t ld_cap_xn, hipStream_t st);
 
+// The pass workspace's first 32 KiB hold arrival counters: GEMM column
+// groups use ints [0, kGemmCounterInts) and return them to zero; attention
+// (head, row tile) pairs use the 1024 ints from kPassAttnCounterInt on, which
+// stay multiples of 16.
+constexpr int kGemmCounterInts = 7168;
+constexpr int kPassAttnCounterInt = 7168;
+
 // pe_attn.hip: pe_tree_attention whose output is A-tiled when out_units > 0
-// (hd == 128 16-bit path only).
+// (hd == 128 16-bit path only). counters: the launch's arrival counters
+// (nullptr: the head of the workspace).
 PE_INTERNAL int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
                                            int nh, int nkv, int hd, int T, int64_t P, int mask_mode,
                                            const uint64_t* bits, int words, float scale, int dtype, void* out,

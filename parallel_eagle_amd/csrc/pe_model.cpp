@@ -219,7 +219,7 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
                                     a->prefix_len, a->status, gws, gwsb, tiled, st));
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
                                       a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
-                                      Lo.attn_ws_bytes, (int*)gws, st));
+                                      Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st));
     const uint16_t* a_o = (const uint16_t*)(m->a_o ? m->a_o[l] : nullptr);
     if (tiled) {
       PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, true, M, qd, m->w_o[l], a_o, H, part,
@@ -343,7 +343,7 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
                        a->cache_capacity, a->prefix_len, a->status, st));
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
                                       a->tree_bits, a->bits_words, scale, m->dtype, attn, qd, 0, aws,
-                                      Lo.attn_ws_bytes, (int*)gws, st));
+                                      Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st));
     PE_TRY(linear(m, attn, qd, M, qd, m->w_o[l], m->a_o ? m->a_o[l] : nullptr, H, PE_EPI_RESIDUAL, nullptr, h, H, h,
                   H, gws, gwsb, st));
     PE_TRY(pe_rmsnorm(h, H, M, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, H, st));
