@@ -43,24 +43,28 @@ __device__ __forceinline__ bool key_allowed(int64_t key, int64_t P, int t, int m
   return (nb[u >> 6] >> (u & 63)) & 1ull;
 }
 
-// One workgroup = 4 waves = one (KV head, key split, 32-row tile); each wave
-// takes a contiguous run of the split's 32-key blocks and processes them two
-// at a time as one 64-key block (a run of odd length ends with a half-masked
-// pair). The K and V loads of a pair are the first instructions of its round,
-// so at the 7B shape the whole KV stream is in flight at once. V of the pair
+// One workgroup = 8 waves = one (KV head, key split, 32-row tile); each wave
+// takes a contiguous run of the split's 32-key blocks. Its first two blocks
+// are loaded and processed together as one 64-key block (a run of one block
+// processes half of it); a longer run continues one block per round, so the
+// O accumulators never share the register file with a second pair in flight
+// and a wave stays within 240 VGPRs without spilling. The row's ancestor
+// bits, the row tile's Q and the first pair's K and V are the first loads of
+// the wave, so at the 7B shape the whole KV stream is in flight at once. V
 // goes to a wave-private LDS transpose before S = K Q^T is formed, the row
 // tile's Q is staged once per workgroup in LDS (the B operand of S^T is read
-// from there per k-step), and a wave stays within 256 VGPRs: two workgroups
-// per CU. Loads are clamped to the wave's last valid key (those scores are
-// masked and their probabilities are exactly zero), so no uninitialised cache
-// row is read. At the end the waves' (m, l, O) are merged in LDS in wave
-// order by all threads. With several splits the workgroup publishes that
-// partial with agent-coherent 16-byte stores and counts itself on the pair's
-// arrival counter; the last to arrive reads every split's partial (its own
-// from registers) and combines them in split order: out = sum_s e^{m_s - M}
-// O_s / sum_s e^{m_s - M} l_s, accumulated online (running max, rescaled
-// sums). Nobody waits for anybody, and the result does not depend on the
-// arrival order.
+// from there per k-step); the LDS footprint (about 89 KiB) allows one
+// workgroup per CU. Loads are clamped to the wave's last valid key (those
+// scores are masked and their probabilities are exactly zero), so no
+// uninitialised cache row is read. At the end the waves' (m, l, O) are
+// merged in LDS in wave order by all threads. With several splits the
+// workgroup publishes that partial (rows past the tile's real rows are
+// skipped) with agent-coherent 16-byte stores and counts itself on the
+// pair's arrival counter; the last to arrive reads every split's partial
+// (its own from registers) and combines them in split order: out = sum_s
+// e^{m_s - M} O_s / sum_s e^{m_s - M} l_s, accumulated online (running max,
+// rescaled sums). Nobody waits for anybody, and the result does not depend
+// on the arrival order.
 constexpr int kAttnWaves = 8;
 constexpr int kQStride = 128 + 8;  // LDS row stride of the staged Q tile (elements)
 constexpr int kVRow = 128 + 32;    // LDS row stride of a wave's V tile (elements): 320 B, rows 16 banks apart
@@ -68,7 +72,7 @@ constexpr int kCmbRow = 128 + 4;   // LDS row stride of the wave merge (floats; 
 constexpr int kAttnMaxSplits = 16;
 
 template <int DT>
-__global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
+__global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
     int nh, int nkv, int T, int64_t P, int mask_mode, const uint64_t* __restrict__ bits, int words, float scale,
     int keys_per_split, int splits, int rows_pad, float* __restrict__ opart, float* __restrict__ mlpart,
@@ -118,33 +122,53 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
       }
     }
   };
+  // one block into the first slots (later rounds, while O is live)
+  auto load_one = [&](int64_t jb) {
+    const uint32_t ko = (uint32_t)min(jb + ln, jlast) * (HD * 2) + 16 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kf[0][j] = *(const u32x4_t*)(kbase + ko + 32 * j);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t vo = (uint32_t)min(jb + 4 * c + (lane >> 4), jlast) * (HD * 2) + (lane & 15) * 16;
+      vf[0][c] = *(const u32x4_t*)(vbase + vo);
+    }
+  };
   // the row tile's Q (rows past `rows` are zero) is requested first, so
   // staging it waits for Q alone and not for the KV stream behind it
+  // the row's ancestor bits, then Q (rows past `rows` read row rows - 1 and
+  // stage zeros), then K and V: all requested before anything waits
+  const int r = rt * 32 + ln;
+  const bool rvalid = r < rows;
+  const int t = rvalid ? r / G : 0;
+  uint64_t nbits[PE_TREE_MAX_WORDS];
+  if (mask_mode == PE_MASK_TREE) {
+    // a visible tree key u < T <= 64 * words only reads words below `words`
+#pragma unroll
+    for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = bits[(int64_t)t * words + min(w, words - 1)];
+  } else {
+#pragma unroll
+    for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = 0ull;
+  }
   constexpr int kQChunks = 512 / (64 * kAttnWaves);  // 32 rows x 16 chunks of 8 dims
   const u32x4_t zero4 = {0u, 0u, 0u, 0u};
   u32x4_t qv[kQChunks];
+  bool qok[kQChunks];
 #pragma unroll
   for (int c = 0; c < kQChunks; ++c) {
     const int chunk = c * 64 * kAttnWaves + threadIdx.x;
     const int qr = chunk >> 4, dc = chunk & 15;
-    const int rr = rt * 32 + qr;
-    qv[c] = zero4;
-    if (rr < rows) qv[c] = *(const u32x4_t*)(q + ((int64_t)(rr / G) * nh + kvh * G + rr % G) * HD + dc * 8);
+    const int rr0 = rt * 32 + qr;
+    qok[c] = rr0 < rows;
+    const int rr = min(rr0, rows - 1);
+    qv[c] = *(const u32x4_t*)(q + ((int64_t)(rr / G) * nh + kvh * G + rr % G) * HD + dc * 8);
   }
   if (b0 < b1) load_pair(ks0 + 32 * (int64_t)b0);
 #pragma unroll
   for (int c = 0; c < kQChunks; ++c) {
     const int chunk = c * 64 * kAttnWaves + threadIdx.x;
-    *(u32x4_t*)&qs[chunk >> 4][(chunk & 15) * 8] = qv[c];
+    *(u32x4_t*)&qs[chunk >> 4][(chunk & 15) * 8] = qok[c] ? qv[c] : zero4;
   }
 
-  const int r = rt * 32 + ln;
-  const bool rvalid = r < rows;
-  const int t = rvalid ? r / G : 0;
-  uint64_t nbits[PE_TREE_MAX_WORDS];
-#pragma unroll
-  for (int w = 0; w < PE_TREE_MAX_WORDS; ++w)
-    nbits[w] = (mask_mode == PE_MASK_TREE && w < words && rvalid) ? bits[(int64_t)t * words + w] : 0ull;
 
   // O^T accumulators; the first pair's PV MFMAs start from zero, so O holds
   // no registers while the first pair's K and V are in flight
@@ -153,9 +177,10 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
   __syncthreads();  // Q staged
 
   const float scale2 = scale * 1.44269504088896341f;  // natural-log scores -> base 2
-  auto process = [&](int64_t jb, auto first_c) {
+  auto process = [&](int64_t jb, auto first_c, auto pair_c) {
     constexpr bool kFirst = decltype(first_c)::value;
-    const bool two = jb + 32 < j1;  // wave-uniform: the pair's second block has keys
+    constexpr bool kPair = decltype(pair_c)::value;
+    const bool two = kPair && jb + 32 < j1;  // wave-uniform: the pair's second block has keys
     // ---- S^T = K Q^T over hd, two 32-key halves
     f32x16_t sc[2];
 #pragma unroll
@@ -292,16 +317,16 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
   };
 
   if (b0 < b1) {
-    process(ks0 + 32 * (int64_t)b0, std::true_type());
+    process(ks0 + 32 * (int64_t)b0, std::true_type(), std::true_type());
   } else {
 #pragma unroll
     for (int h = 0; h < 4; ++h)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
   }
-  for (int b = b0 + 2; b < b1; b += 2) {  // caches longer than one round of pairs
-    load_pair(ks0 + 32 * (int64_t)b);
-    process(ks0 + 32 * (int64_t)b, std::false_type());
+  for (int b = b0 + 2; b < b1; ++b) {  // caches longer than one pair: one block per round
+    load_one(ks0 + 32 * (int64_t)b);
+    process(ks0 + 32 * (int64_t)b, std::false_type(), std::false_type());
   }
 
   // ---- merge the waves (wave order) with all threads: thread (row, kDimsT-dim
@@ -372,11 +397,13 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
   const uint32_t nrows = (uint32_t)(nkv * row_tiles * splits * 32);
   const __amdgpu_buffer_rsrc_t ro = agent_rsrc(opart, nrows * HD * 4), rm = agent_rsrc(mlpart, nrows * 16);
   auto prow = [&](int sp) -> uint32_t { return (uint32_t)((pair * splits + sp) * 32 + row); };
+  if (rr < rows) {  // padding rows of the tile are neither stored nor combined
 #pragma unroll
-  for (int k = 0; k < kDimsT / 4; ++k)
-    store_agent_x4(ro, (prow(split) * HD + dc) * 4 + 16 * k,
-                   f32x4_t{acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]});
-  if (dc == 0) store_agent_x4(rm, prow(split) * 16, f32x4_t{M, L, 0.f, 0.f});
+    for (int k = 0; k < kDimsT / 4; ++k)
+      store_agent_x4(ro, (prow(split) * HD + dc) * 4 + 16 * k,
+                     f32x4_t{acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]});
+    if (dc == 0) store_agent_x4(rm, prow(split) * 16, f32x4_t{M, L, 0.f, 0.f});
+  }
   // the stores are acknowledged at agent scope before this workgroup counts itself
   __builtin_amdgcn_s_waitcnt(0);
   // Each workgroup adds kAttnMaxSplits / splits (splits is a power of two), so
@@ -398,7 +425,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, 2) void attn_wg_kernel(
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const int sp = c0 + c;
-      if (sp < splits && sp != split) {
+      if (sp < splits && sp != split && rr < rows) {
 #pragma unroll
         for (int k = 0; k < kDimsT / 4; ++k) ov[c][k] = load_agent_x4(ro, (prow(sp) * HD + dc) * 4 + 16 * k);
         mv[c] = load_agent_x4(rm, prow(sp) * 16);
