@@ -944,7 +944,7 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   static const int nf4_upw = env_int("PE_NF4_UNITS_PER_WAVE", 2) == 1 ? 1 : 2;
   static const int nf4_wide_groups = env_int("PE_NF4_WIDE_GROUPS", 256);
   static const bool nf4_hybrid = env_int("PE_NF4_HYBRID", 1) != 0;
-  static const int nf4_hybrid_ts = env_int("PE_NF4_HYBRID_TS", 4);
+  static const int nf4_hybrid_ts = env_int("PE_NF4_HYBRID_TS", 2);
   static const int nf4_hybrid_less = env_int("PE_NF4_HYBRID_LESS", 0);
   Plan p;
   p.NT = (epi == PE_EPI_SWIGLU || epi == kEpiRopeKV || N % 64 == 0) ? 2 : 1;
@@ -975,9 +975,10 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   // one wave's waits overlap the other's issue.
   p.KW = (nf4 && p.MT == 1 && p.NT == 2 && p.S == 1 && p.groups <= nf4_wide_groups) ? 8 : 4;
   // Between one and two column groups per CU (unsplit): one whole group per
-  // CU, the rest split 4 ways, so each CU carries one whole group and one or
-  // two quarter groups instead of one or two whole ones; the quarters finish
-  // early and their exchange is off the critical path.
+  // CU, the rest split in halves, so each CU carries one whole group and at
+  // most one half group instead of one or two whole ones; the halves finish
+  // early and their exchange is off the critical path. (Quarters, thirds and
+  // more or fewer whole groups measured slower in the 7B pass.)
   p.nl = p.tS = p.tpps = 0;
   const int ncu = cu_count();
   if (nf4 && p.MT == 1 && p.NT == 2 && p.S == 1 && epi != kEpiPartial && nf4_hybrid && p.groups > ncu &&

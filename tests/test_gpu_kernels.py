@@ -109,11 +109,13 @@ def test_nf4_linear_tiled_x_equals_row_major(m, epi):
 
 
 @pytest.mark.parametrize("m", [1, 26, 32])
-@pytest.mark.parametrize("n,k", [(12288, 4096), (8192, 1024), (16384, 512), (22016, 4096), (20480, 1024)])
+@pytest.mark.parametrize("n,k", [(12288, 4096), (8192, 1024), (16384, 512), (22016, 4096), (20480, 1024),
+                                 (24576, 2560)])
 def test_nf4_tiled_unsplit_wide_workgroups(m, n, k):
     """Unsplit launches with 128..256 column groups run eight waves per
     workgroup (two table regions); with 256..512 groups one whole group per CU
-    plus the rest in four K splits joined by the last workgroup. Either way the
+    plus the rest in two K splits joined by the last workgroup (K = 2560: ten
+    units per split, uneven over the four waves). Either way the
     stored bf16 product equals the fp32 product of the exact dequantised
     operands up to bf16 rounding of the output and fp32 accumulation order."""
     (tiled, tabs), wdq = _nf4_weight(n, k, seed=m + n + k + 1)
