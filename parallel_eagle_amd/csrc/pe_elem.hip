@@ -129,13 +129,39 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(const typename Elem<DT>::
 // One block per row: the residual add of a split-K projection (partials summed
 // in split order, HF modeling_llama.py:317,323) fused with the RMSNorm that
 // follows it (modeling_llama.py:62-67) and the hidden-state captures. Each
-// thread owns up to kNormChunks chunks of 4 columns and issues all of its
-// partial loads before summing, so the row costs one memory round trip.
+// thread owns CH chunks of 4 columns. Every load of the row (the residual, the
+// norm weight and the S split partials of the thread's chunks) is issued
+// before the first use, so the row costs one memory round trip; the partial
+// loads past S repeat split S - 1 (SMAX is S rounded up to a multiple of 4)
+// and are not summed. With two chunks and more than eight splits the second
+// chunk's partials are requested after the first chunk is summed.
 constexpr int kNormThreads = 1024;
 constexpr int kNormChunks = 2;    // H <= 4 * 1024 * 2
 constexpr int kNormMaxSplits = 16;
 
-template <int DT>
+// four consecutive elements as one raw access (8 bytes for the 16-bit types)
+template <int DT> struct Raw4 {
+  typedef uint2 R;
+  static __device__ __forceinline__ R load(const uint16_t* p) { return *(const uint2*)p; }
+  static __device__ __forceinline__ void cvt(R t, float (&v)[4]) {
+    v[0] = Vec4Half<DT>::cvt(t.x & 0xffffu);
+    v[1] = Vec4Half<DT>::cvt(t.x >> 16);
+    v[2] = Vec4Half<DT>::cvt(t.y & 0xffffu);
+    v[3] = Vec4Half<DT>::cvt(t.y >> 16);
+  }
+};
+template <> struct Raw4<PE_DTYPE_F32> {
+  typedef float4 R;
+  static __device__ __forceinline__ R load(const float* p) { return *(const float4*)p; }
+  static __device__ __forceinline__ void cvt(R t, float (&v)[4]) {
+    v[0] = t.x;
+    v[1] = t.y;
+    v[2] = t.z;
+    v[3] = t.w;
+  }
+};
+
+template <int DT, int CH, int SMAX>
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
     const float* __restrict__ partial, int S, int M, typename Elem<DT>::T* __restrict__ h, int H,
     const typename Elem<DT>::T* __restrict__ w, float eps, typename Elem<DT>::T* __restrict__ xn,
@@ -144,32 +170,53 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
   typedef Elem<DT> E;
   typedef typename E::T T;
   typedef Vec4<DT> V;
+  typedef Raw4<DT> RW;
+  constexpr int PCH = (CH * SMAX <= 16) ? CH : 1;  // chunks whose partials are in flight together
   const int m = blockIdx.x;
   T* hr = h + (int64_t)m * H;
   const int nchunk = H >> 2;
   const int64_t sstride = (int64_t)M * H;
-  float v[kNormChunks][4];
+  // chunk k of this thread (clamped to the last chunk; a clamped chunk is
+  // loaded but neither summed nor stored)
+  auto chunk = [&](int k) { return min((int)threadIdx.x + k * kNormThreads, nchunk - 1); };
+  typename RW::R hraw[CH], wraw[CH];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    hraw[k] = RW::load(hr + 4 * chunk(k));
+    wraw[k] = RW::load(w + 4 * chunk(k));
+  }
+  float v[CH][4];
+#pragma unroll
+  for (int k0 = 0; k0 < CH; k0 += PCH) {
+    f32x4_t pt[PCH][SMAX > 0 ? SMAX : 1];
+#pragma unroll
+    for (int kk = 0; kk < PCH; ++kk)
+#pragma unroll
+      for (int sp = 0; sp < SMAX; ++sp)
+        pt[kk][sp] = *(const f32x4_t*)(partial + (int64_t)m * H + 4 * chunk(k0 + kk) + min(sp, S - 1) * sstride);
+    __builtin_amdgcn_sched_barrier(0);  // all of the batch's loads issue before the sums
+#pragma unroll
+    for (int kk = 0; kk < PCH; ++kk) {
+      const int k = k0 + kk;
+      RW::cvt(hraw[k], v[k]);
+      if (SMAX > 0) {
+        float a[4] = {0.f, 0.f, 0.f, 0.f};
+        // a select, not an early exit: every partial load stays ahead of the sum
+#pragma unroll
+        for (int sp = 0; sp < SMAX; ++sp)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a[e] = sp < S ? a[e] + pt[kk][sp][e] : a[e];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[k][e] = E::round(__fadd_rn(v[k][e], E::round(a[e])));
+      }
+    }
+  }
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < kNormChunks; ++k) {
+  for (int k = 0; k < CH; ++k) {
     const int c = threadIdx.x + k * kNormThreads;
     if (c >= nchunk) continue;
-    V::load(hr + 4 * c, v[k]);
-    if (S > 0) {
-      const float* pp = partial + (int64_t)m * H + 4 * c;
-      float a[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int sp = 0; sp < S; ++sp) {
-        const float4 t = *(const float4*)(pp + sp * sstride);
-        a[0] += t.x;
-        a[1] += t.y;
-        a[2] += t.z;
-        a[3] += t.w;
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[k][e] = E::round(__fadd_rn(v[k][e], E::round(a[e])));
-      V::store(hr + 4 * c, v[k]);
-    }
+    if (SMAX > 0) V::store(hr + 4 * c, v[k]);
     if (cap_h) V::store(cap_h + (int64_t)m * ld_cap_h + 4 * c, v[k]);
 #pragma unroll
     for (int e = 0; e < 4; ++e) ss = __fadd_rn(ss, __fmul_rn(v[k][e], v[k][e]));
@@ -184,11 +231,11 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
   const float inv = 1.0f / sqrtf(tot / (float)H + eps);
   T* orow = xn + (int64_t)m * H;
 #pragma unroll
-  for (int k = 0; k < kNormChunks; ++k) {
+  for (int k = 0; k < CH; ++k) {
     const int c = threadIdx.x + k * kNormThreads;
     if (c >= nchunk) continue;
     float wv[4], o[4];
-    V::load(w + 4 * c, wv);
+    RW::cvt(wraw[k], wv);
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = E::round(__fmul_rn(wv[e], E::round(__fmul_rn(v[k][e], inv))));
     V::store(orow + 4 * c, o);
@@ -273,16 +320,53 @@ extern "C" int pe_copy_rows(const void* src, int64_t ld_src, int M, int64_t row_
   return PE_OK;
 }
 
+template <typename T> struct NormArgs {
+  const float* partial;
+  int S, M;
+  T* h;
+  int H;
+  const T* w;
+  float eps;
+  T *xn, *xt, *cap_h;
+  int64_t ld_cap_h;
+  T* cap_xn;
+  int64_t ld_cap_xn;
+};
+
+template <int DT, int CH, int SM>
+void launch_norm_sm(const NormArgs<typename Elem<DT>::T>& a, hipStream_t st) {
+  residual_rmsnorm_kernel<DT, CH, SM><<<a.M, kNormThreads, 0, st>>>(a.partial, a.S, a.M, a.h, a.H, a.w, a.eps, a.xn,
+                                                                    a.xt, a.cap_h, a.ld_cap_h, a.cap_xn,
+                                                                    a.ld_cap_xn);
+}
+
+template <int DT, int CH>
+void launch_norm(int smax, const NormArgs<typename Elem<DT>::T>& a, hipStream_t st) {
+  switch (smax) {
+    case 0: launch_norm_sm<DT, CH, 0>(a, st); break;
+    case 4: launch_norm_sm<DT, CH, 4>(a, st); break;
+    case 8: launch_norm_sm<DT, CH, 8>(a, st); break;
+    case 12: launch_norm_sm<DT, CH, 12>(a, st); break;
+    default: launch_norm_sm<DT, CH, 16>(a, st); break;
+  }
+}
+
 int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, int H, const void* w, float eps,
                                  int dtype, void* xn, void* xn_tiled, void* cap_h, int64_t ld_cap_h, void* cap_xn,
                                  int64_t ld_cap_xn, hipStream_t st) {
   if (!h || !w || !xn || M <= 0 || H <= 0 || S < 0 || (S > 0 && !partial)) return PE_ERR_ARG;
   if (H % 4 || H > 4 * kNormThreads * kNormChunks || S > kNormMaxSplits) return PE_ERR_ARG;
   if (xn_tiled && (H % 128 || M > 64 || dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
+  const int ch = (H >> 2) > kNormThreads ? 2 : 1;
+  const int smax = S == 0 ? 0 : (S + 3) / 4 * 4;
   PE_DISPATCH_DT(dtype, {
     typedef typename Elem<DT>::T T;
-    residual_rmsnorm_kernel<DT><<<M, kNormThreads, 0, st>>>(partial, S, M, (T*)h, H, (const T*)w, eps, (T*)xn,
-                                                            (T*)xn_tiled, (T*)cap_h, ld_cap_h, (T*)cap_xn, ld_cap_xn);
+    const NormArgs<T> na{partial, S, M, (T*)h, H, (const T*)w, eps, (T*)xn, (T*)xn_tiled, (T*)cap_h, ld_cap_h,
+                         (T*)cap_xn, ld_cap_xn};
+    if (ch == 1)
+      launch_norm<DT, 1>(smax, na, st);
+    else
+      launch_norm<DT, 2>(smax, na, st);
   });
   PE_CHECK_LAUNCH();
   return PE_OK;
