@@ -186,7 +186,10 @@ int pe_argmax_rows(const void* x, int64_t ld, int rows, int64_t V, int dtype, in
                    void* stream);
 /* Greedy tree walk of accept_tree_cached (src/pe/decode/verify.py:104-125):
  * out[0] = |path|, out[1] = bonus token, out[2 + i] = path node i.
- * scratch: T + 1 int32. */
+ * One launch: per-row argmax blocks, the last of which walks.
+ * scratch: T + 2 int32 (row argmaxes, then an arrival counter), zero before
+ * the first call; every call leaves the counter at zero again. Calls that
+ * share a scratch buffer must not overlap. */
 int pe_accept_tree(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V,
                    int dtype, const int64_t* node_tokens, const int32_t* parents, int32_t* out,
                    int32_t* scratch, void* stream);

@@ -108,7 +108,7 @@ __device__ __forceinline__ uint32_t arg_key(float f) {
 // keeping the first element of the largest key; the block then reduces with
 // (key descending, index ascending).
 template <int DT>
-__device__ void row_argmax(const typename Elem<DT>::T* __restrict__ x, int64_t V, int32_t* out) {
+__device__ int row_argmax(const typename Elem<DT>::T* __restrict__ x, int64_t V, int32_t* out) {
   typedef typename Elem<DT>::T T;
   constexpr int kPer = 16 / sizeof(T);  // elements per 16-byte vector
   constexpr int kVec = 8;               // vectors per thread held in flight
@@ -167,16 +167,18 @@ __device__ void row_argmax(const typename Elem<DT>::T* __restrict__ x, int64_t V
     wi[threadIdx.x >> 6] = bi;
   }
   __syncthreads();
+  int i1 = -1;
   if (threadIdx.x == 0) {
     uint32_t k1 = wk[0];
-    int i1 = wi[0];
+    i1 = wi[0];
     for (int w = 1; w < kArgThreads / 64; ++w)
       if (better(wk[w], wi[w], k1, i1)) {
         k1 = wk[w];
         i1 = wi[w];
       }
-    *out = i1;
+    if (out) *out = i1;
   }
+  return i1;
 }
 
 template <int DT>
@@ -185,54 +187,71 @@ __global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const typename
   row_argmax<DT>(x + (int64_t)blockIdx.x * ld, V, out + blockIdx.x);
 }
 
-// row 0 = root logit, rows 1..T = node logits
-template <int DT>
-__global__ __launch_bounds__(kArgThreads) void accept_argmax_kernel(const typename Elem<DT>::T* __restrict__ root,
-                                                                    const typename Elem<DT>::T* __restrict__ nodes,
-                                                                    int64_t ld, int64_t V,
-                                                                    int32_t* __restrict__ amax) {
-  const int r = blockIdx.x;
-  const typename Elem<DT>::T* x = (r == 0) ? root : nodes + (int64_t)(r - 1) * ld;
-  row_argmax<DT>(x, V, amax + r);
-}
-
-// The walk reads every node's argmax, parent and token once: the block stages
-// them in LDS, then one thread walks (at most kWalkMax nodes).
-constexpr int kWalkThreads = 256;
+// One launch does the whole acceptance. Block r finds the argmax of row r
+// (row 0 = root logit, rows 1..T = node logits) and publishes it in amax[r];
+// the last block to count itself on amax[T + 1] (every row's argmax is then
+// visible) resets that counter and walks the tree. The walk stages every
+// node's argmax, parent and token in LDS; one wave then follows the greedy
+// path, each step a ballot over the nodes for the first child of the current
+// node whose token equals the current truth (at most kWalkMax nodes).
 constexpr int kWalkMax = 64 * PE_TREE_MAX_WORDS;
 
-__global__ __launch_bounds__(kWalkThreads) void accept_walk_kernel(const int32_t* __restrict__ amax, int T,
-                                                                   const int64_t* __restrict__ tokens,
-                                                                   const int32_t* __restrict__ parents,
-                                                                   int32_t* __restrict__ out) {
+template <int DT>
+__global__ __launch_bounds__(kArgThreads) void accept_kernel(const typename Elem<DT>::T* __restrict__ root,
+                                                             const typename Elem<DT>::T* __restrict__ nodes,
+                                                             int64_t ld, int64_t V, int32_t* __restrict__ amax,
+                                                             int T, const int64_t* __restrict__ tokens,
+                                                             const int32_t* __restrict__ parents,
+                                                             int32_t* __restrict__ out) {
+  const int r = blockIdx.x;
+  const typename Elem<DT>::T* x = (r == 0) ? root : nodes + (int64_t)(r - 1) * ld;
+  const int best = row_argmax<DT>(x, V, nullptr);
+  __shared__ int s_last;
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(amax + r, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // release: this row's argmax is visible before the count; acquire: the
+    // last block sees every row's
+    const int old = __hip_atomic_fetch_add(amax + T + 1, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == T;
+    if (old == T) __hip_atomic_store(amax + T + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
   __shared__ int32_t s_amax[kWalkMax + 1], s_par[kWalkMax];
   __shared__ int64_t s_tok[kWalkMax];
   const int n = min(T, kWalkMax);
-  for (int t = threadIdx.x; t <= n; t += kWalkThreads) s_amax[t] = amax[t];
-  for (int t = threadIdx.x; t < n; t += kWalkThreads) {
+  for (int t = threadIdx.x; t <= n; t += kArgThreads)
+    s_amax[t] = __hip_atomic_load(amax + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int t = threadIdx.x; t < n; t += kArgThreads) {
     s_par[t] = parents[t];
     s_tok[t] = tokens[t];
   }
   __syncthreads();
-  if (threadIdx.x != 0) return;
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
   int cur = -1, len = 0;
   int truth = s_amax[0];
   for (;;) {
     int nxt = -1;
-    for (int t = 0; t < n; ++t) {
-      if (s_par[t] == cur && s_tok[t] == (int64_t)truth) {
-        nxt = t;
+    for (int base = 0; base < n; base += 64) {
+      const int t = base + lane;
+      const bool hit = t < n && s_par[t] == cur && s_tok[t] == (int64_t)truth;
+      const uint64_t b = __ballot(hit);
+      if (b) {
+        nxt = base + (int)__builtin_ctzll(b);
         break;
       }
     }
     if (nxt < 0 || len >= n) break;
-    out[2 + len] = nxt;
+    if (lane == 0) out[2 + len] = nxt;
     ++len;
     cur = nxt;
     truth = s_amax[1 + nxt];
   }
-  out[0] = len;
-  out[1] = truth;
+  if (lane == 0) {
+    out[0] = len;
+    out[1] = truth;
+  }
 }
 
 // grid: (L * nkv, 2 for K/V); threads over 16-byte chunks of a row
@@ -355,22 +374,22 @@ extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, i
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
     case PE_DTYPE_F32:
-      accept_argmax_kernel<PE_DTYPE_F32><<<T + 1, kArgThreads, 0, st>>>((const float*)root_logit, (const float*)node_logits,
-                                                                ld, V, scratch);
+      accept_kernel<PE_DTYPE_F32><<<T + 1, kArgThreads, 0, st>>>((const float*)root_logit, (const float*)node_logits,
+                                                                 ld, V, scratch, T, node_tokens, parents, out);
       break;
     case PE_DTYPE_BF16:
-      accept_argmax_kernel<PE_DTYPE_BF16><<<T + 1, kArgThreads, 0, st>>>((const uint16_t*)root_logit,
-                                                                 (const uint16_t*)node_logits, ld, V, scratch);
+      accept_kernel<PE_DTYPE_BF16><<<T + 1, kArgThreads, 0, st>>>((const uint16_t*)root_logit,
+                                                                  (const uint16_t*)node_logits, ld, V, scratch, T,
+                                                                  node_tokens, parents, out);
       break;
     case PE_DTYPE_F16:
-      accept_argmax_kernel<PE_DTYPE_F16><<<T + 1, kArgThreads, 0, st>>>((const uint16_t*)root_logit,
-                                                                (const uint16_t*)node_logits, ld, V, scratch);
+      accept_kernel<PE_DTYPE_F16><<<T + 1, kArgThreads, 0, st>>>((const uint16_t*)root_logit,
+                                                                 (const uint16_t*)node_logits, ld, V, scratch, T,
+                                                                 node_tokens, parents, out);
       break;
     default:
       return PE_ERR_ARG;
   }
-  PE_CHECK_LAUNCH();
-  accept_walk_kernel<<<1, kWalkThreads, 0, st>>>(scratch, T, node_tokens, parents, out);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }

@@ -284,7 +284,8 @@ def accept_tree(root_logit: torch.Tensor, node_logits: torch.Tensor, node_tokens
     if out is None:
         out = torch.empty(2 + max(t, 1), dtype=torch.int32, device=root_logit.device)
     if scratch is None:
-        scratch = torch.empty(t + 1, dtype=torch.int32, device=root_logit.device)
+        scratch = torch.zeros(t + 2, dtype=torch.int32, device=root_logit.device)
+    _req(scratch.dtype == torch.int32 and scratch.numel() >= t + 2, "scratch must hold T + 2 int32")
     ld = node_logits.stride(0) if t > 0 else v
     check(lib().pe_accept_tree(ptr(root_logit), ptr(node_logits) if t > 0 else None, ld, t, v,
                                dcode(root_logit.dtype), ptr(node_tokens) if t > 0 else None,

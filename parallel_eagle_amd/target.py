@@ -321,7 +321,7 @@ class VerifyStep:
         self.logits = torch.empty((self.T, s.vocab), dtype=target.dtype, device=dev)
         self.fused = torch.empty((self.T, target.feature_dim), dtype=target.dtype, device=dev)
         self.accept_out = torch.zeros(2 + self.T, dtype=torch.int32, device=dev)
-        self.accept_scratch = torch.zeros(self.T + 1, dtype=torch.int32, device=dev)
+        self.accept_scratch = torch.zeros(self.T + 2, dtype=torch.int32, device=dev)
         self.ws = torch.zeros(target.model.workspace_bytes(self.T, self.P + self.T), dtype=torch.uint8,
                               device=dev)
         self.graph = None

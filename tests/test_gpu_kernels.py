@@ -301,6 +301,35 @@ def test_accept_tree_matches_oracle(dtype, seed):
     assert (out[2: 2 + out[0]], out[1]) == ref
 
 
+@pytest.mark.parametrize("T", [0, 1, 70, 200])
+def test_accept_tree_shared_scratch_and_wide_trees(T):
+    """One scratch buffer across consecutive calls (its arrival counter must
+    return to zero) on trees wider than one wave, so the walk's child search
+    spans several ballots; each call matches the oracle walk."""
+    rng = np.random.default_rng(T + 5)
+    V = 40
+    scratch = torch.zeros(T + 2, dtype=torch.int32, device=DEV)
+    for call in range(3):
+        parents = ([-1] + [int(rng.integers(-1, t)) for t in range(1, T)])[:T]
+        logits = torch.from_numpy(rng.integers(0, 3, size=(T + 1, V)).astype(np.float32)).to(torch.bfloat16)
+        tokens = [int(x) for x in rng.integers(0, V, size=T)]
+        amax = [ov.first_argmax(logits[r]) for r in range(T + 1)]
+        cur, row = -1, 0
+        for _ in range(6):  # plant a chain, preferring late children (found by a later ballot)
+            kids = [t for t in range(T) if parents[t] == cur]
+            if not kids:
+                break
+            c = kids[-1]
+            tokens[c] = amax[row]
+            cur, row = c, 1 + c
+        ref = ov.accept_tree_cached(logits[0], logits[1:], tokens, parents)
+        nl = logits[1:].to(DEV) if T > 0 else logits[:1].to(DEV)
+        out = ops.accept_tree(logits[0].to(DEV), nl, torch.tensor(tokens, dtype=torch.int64, device=DEV),
+                              torch.tensor(parents, dtype=torch.int32, device=DEV), scratch=scratch).cpu().tolist()
+        assert (out[2: 2 + out[0]], out[1]) == ref, (call, out[:8], ref)
+        assert scratch[T + 1].item() == 0
+
+
 def test_argmax_rows_first_index_and_nan():
     x = torch.zeros((3, 1000), dtype=torch.float32)
     x[0, 7] = 5.0
