@@ -46,6 +46,7 @@ extern "C" {
 /* linear-weight storage formats */
 #define PE_WFMT_DENSE 0 /* dtype weights, MFMA-tiled (16-bit) or row-major (fp32) */
 #define PE_WFMT_NF4 1   /* NF4 codes + fp16 absmax per 64 along K, MFMA-tiled */
+#define PE_WFMT_NF4_F32ABS 2 /* NF4 codes + fp32 absmax (bitsandbytes' own), MFMA-tiled */
 
 /* GEMM epilogues */
 #define PE_EPI_STORE 0    /* out = round(acc + bias) */
@@ -92,6 +93,20 @@ int pe_nf4_repack(const uint8_t* packed, const uint16_t* absmax, int64_t N, int6
  * bitsandbytes dequantize_4bit (src/pe/target.py:55-62). */
 int pe_nf4_dequant(const uint8_t* tiled, const uint16_t* tiled_absmax, int64_t N, int64_t K,
                    uint16_t* out, void* stream);
+/* The same two for fp32 absmax, the type bitsandbytes stores (Params4bit
+ * quant_state.absmax; src/pe/target.py:32-38 loads such checkpoints):
+ * bf16_rne(NF4[c] * absmax) with the fp32 absmax as is. */
+int pe_nf4_repack_f32abs(const uint8_t* packed, const float* absmax, int64_t N, int64_t K, uint8_t* tiled,
+                         float* tiled_absmax, void* stream);
+int pe_nf4_dequant_f32abs(const uint8_t* tiled, const float* tiled_absmax, int64_t N, int64_t K, uint16_t* out,
+                          void* stream);
+/* bitsandbytes double quantisation of the absmax (compress_statistics): the
+ * fp32 absmax of block i is code[q[i]] * nested_absmax[i / nested_blocksize]
+ * + offset, one fp32 product and one fp32 sum, as bitsandbytes'
+ * dequantize_blockwise followed by `absmax += offset` in dequantize_4bit.
+ * code: the 256-entry nested quant map. */
+int pe_nf4_absmax_dequant(const uint8_t* q, int64_t n, const float* code, const float* nested_absmax,
+                          int nested_blocksize, float offset, float* absmax, void* stream);
 /* Row-major 16-bit W[N][K] -> MFMA-tiled layout read by pe_dense_gemm (copy for fp32). */
 int pe_dense_repack(const void* w, int64_t N, int64_t K, int dtype, void* tiled, void* stream);
 
@@ -106,6 +121,10 @@ int pe_nf4_gemm(const void* x, int64_t ldx, int M, int K, const uint8_t* w_tiled
                 const uint16_t* absmax_tiled, int N, int epilogue, const void* bias,
                 const void* resid, int64_t ld_resid, void* out, int64_t ld_out, void* workspace,
                 int64_t workspace_bytes, void* stream);
+/* pe_nf4_gemm on fp32-absmax weights (pe_nf4_repack_f32abs). */
+int pe_nf4_gemm_f32abs(const void* x, int64_t ldx, int M, int K, const uint8_t* w_tiled, const float* absmax_tiled,
+                       int N, int epilogue, const void* bias, const void* resid, int64_t ld_resid, void* out,
+                       int64_t ld_out, void* workspace, int64_t workspace_bytes, void* stream);
 /* pe_nf4_gemm on the activation layout the fused pass hands between kernels:
  * x is A-tiled (element (m, k) at ((((m/32)*(K/128) + k/128)*8 + (k%64)/8)*64
  * + m%32 + 32*((k%128)/64))*8 + k%8), M <= 64; with out_units > 0 (N/128 for

@@ -93,3 +93,20 @@ def dequantize_torch(packed: np.ndarray, absmax: np.ndarray) -> torch.Tensor:
     scale = torch.from_numpy(np.ascontiguousarray(absmax)).float().unsqueeze(-1)
     vals = _TABLE_T[codes].view(n, kh * 2 // 64, 64) * scale
     return vals.view(n, kh * 2).to(torch.bfloat16)
+
+
+def absmax_from_double_quant(q: np.ndarray, code: np.ndarray, nested_absmax: np.ndarray, nested_blocksize: int,
+                             offset: float) -> np.ndarray:
+    """bitsandbytes' double-quantised absmax back to fp32: dequantize_blockwise
+    (out = code[q[i]] * nested_absmax[i // nested_blocksize], one fp32 product)
+    followed by ``absmax += offset`` (one fp32 sum), as dequantize_4bit does with
+    a nested quant state (bitsandbytes functional.py; the reference reaches it
+    through Linear4bit / dequantize_4bit, src/pe/target.py:55-62).
+
+    Pinned in tests/test_bnb_import.py: exact on products and sums that fp32
+    represents, within half an ulp of the exact two-step value elsewhere, and
+    different from a fused multiply-add on inputs where the two differ."""
+    q = np.asarray(q, dtype=np.uint8).reshape(-1)
+    idx = np.arange(q.size) // int(nested_blocksize)
+    prod = np.asarray(code, dtype=np.float32)[q] * np.asarray(nested_absmax, dtype=np.float32)[idx]
+    return (prod.astype(np.float32) + np.float32(offset)).astype(np.float32)

@@ -26,7 +26,7 @@ PE_ERR_INDEX = 64
 PE_ERR_WORKSPACE = 128
 
 PE_DTYPE_F32, PE_DTYPE_BF16, PE_DTYPE_F16 = 0, 1, 2
-PE_WFMT_DENSE, PE_WFMT_NF4 = 0, 1
+PE_WFMT_DENSE, PE_WFMT_NF4, PE_WFMT_NF4_F32ABS = 0, 1, 2
 PE_EPI_STORE, PE_EPI_RESIDUAL, PE_EPI_SWIGLU = 0, 1, 2
 PE_MASK_TREE, PE_MASK_CAUSAL = 0, 1
 PE_QKV_PLAIN, PE_QKV_ROPE_PAIRED = 0, 1
@@ -91,10 +91,15 @@ SIGNATURES: dict[str, tuple] = {
     "pe_nf4_quantize": (C.c_int, [vp, i64, i64, vp, vp, vp]),
     "pe_nf4_repack": (C.c_int, [vp, vp, i64, i64, vp, vp, vp]),
     "pe_nf4_dequant": (C.c_int, [vp, vp, i64, i64, vp, vp]),
+    "pe_nf4_repack_f32abs": (C.c_int, [vp, vp, i64, i64, vp, vp, vp]),
+    "pe_nf4_dequant_f32abs": (C.c_int, [vp, vp, i64, i64, vp, vp]),
+    "pe_nf4_absmax_dequant": (C.c_int, [vp, i64, vp, vp, C.c_int, C.c_float, vp, vp]),
     "pe_dense_repack": (C.c_int, [vp, i64, i64, C.c_int, vp, vp]),
     "pe_gemm_workspace_bytes": (i64, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "pe_nf4_gemm": (C.c_int, [vp, i64, C.c_int, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, i64, vp, i64,
                               vp, i64, vp]),
+    "pe_nf4_gemm_f32abs": (C.c_int, [vp, i64, C.c_int, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, i64, vp, i64,
+                                     vp, i64, vp]),
     "pe_nf4_gemm_tiled": (C.c_int, [vp, C.c_int, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, i64, vp, i64, C.c_int,
                                     vp, i64, vp]),
     "pe_nf4_gemm_partials_bytes": (i64, [C.c_int, C.c_int, C.c_int]),

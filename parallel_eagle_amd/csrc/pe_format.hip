@@ -87,10 +87,11 @@ __global__ void nf4_quantize_kernel(const float* __restrict__ w, int64_t nblocks
   }
 }
 
-// One thread per (tile, super-step, lane).
-__global__ void nf4_repack_kernel(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ absmax,
-                                  int64_t N, int64_t K, uint8_t* __restrict__ tiled,
-                                  uint16_t* __restrict__ tabs) {
+// One thread per (tile, super-step, lane). A: the absmax bits (fp16 or fp32),
+// copied as they are.
+template <typename A>
+__global__ void nf4_repack_kernel(const uint8_t* __restrict__ packed, const A* __restrict__ absmax, int64_t N,
+                                  int64_t K, uint8_t* __restrict__ tiled, A* __restrict__ tabs) {
   const int64_t NS = K / 128, total = (N / 32) * NS * 64;
   int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
@@ -118,8 +119,9 @@ __global__ void nf4_repack_kernel(const uint8_t* __restrict__ packed, const uint
   }
 }
 
-__global__ void nf4_dequant_kernel(const uint8_t* __restrict__ tiled, const uint16_t* __restrict__ tabs,
-                                   int64_t N, int64_t K, uint16_t* __restrict__ out) {
+template <typename A>
+__global__ void nf4_dequant_kernel(const uint8_t* __restrict__ tiled, const A* __restrict__ tabs, int64_t N,
+                                   int64_t K, uint16_t* __restrict__ out) {
   const int64_t NS = K / 128, total = (N / 32) * NS * 64;
   int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
@@ -128,7 +130,8 @@ __global__ void nf4_dequant_kernel(const uint8_t* __restrict__ tiled, const uint
     int64_t nt = ts / NS, s = ts % NS;
     int64_t n = nt * 32 + (lane & 31);
     int64_t b = 2 * s + (lane >> 5);
-    float sc = f16_bits_to_f32(tabs[ts * 64 + lane]);
+    const float sc = sizeof(A) == 4 ? __uint_as_float((uint32_t)tabs[ts * 64 + lane])
+                                    : f16_bits_to_f32((uint16_t)tabs[ts * 64 + lane]);
     for (int j = 0; j < 8; ++j) {
       const uint32_t* src = (const uint32_t*)(tiled + (ts * 2 + (j >> 2)) * 1024 + lane * 16);
       uint32_t q = src[j & 3];
@@ -165,6 +168,20 @@ int grid_for(int64_t n, int block) {
   if (g > 65536) g = 65536;
   if (g < 1) g = 1;
   return (int)g;
+}
+
+// bitsandbytes' blockwise 8-bit dequantisation of the absmax plus its offset:
+// one fp32 product, then one fp32 sum (two roundings: contraction into a
+// fused multiply-add is switched off here).
+__global__ void nf4_absmax_dequant_kernel(const uint8_t* __restrict__ q, int64_t n, const float* __restrict__ code,
+                                          const float* __restrict__ nested, int nbs, float offset,
+                                          float* __restrict__ out) {
+#pragma clang fp contract(off)
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float prod = code[q[i]] * nested[i / nbs];  // rounded to fp32
+    out[i] = prod + offset;                            // rounded again
+  }
 }
 
 }  // namespace
@@ -217,8 +234,28 @@ extern "C" int pe_nf4_repack(const uint8_t* packed, const uint16_t* absmax, int6
   if (!packed || !absmax || !tiled || !tiled_absmax || N <= 0 || N % 32 || K <= 0 || K % 128)
     return PE_ERR_ARG;
   int64_t total = (N / 32) * (K / 128) * 64;
-  nf4_repack_kernel<<<grid_for(total, 256), 256, 0, (hipStream_t)stream>>>(packed, absmax, N, K, tiled,
-                                                                          tiled_absmax);
+  nf4_repack_kernel<uint16_t><<<grid_for(total, 256), 256, 0, (hipStream_t)stream>>>(packed, absmax, N, K, tiled,
+                                                                                    tiled_absmax);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+extern "C" int pe_nf4_repack_f32abs(const uint8_t* packed, const float* absmax, int64_t N, int64_t K,
+                                    uint8_t* tiled, float* tiled_absmax, void* stream) {
+  if (!packed || !absmax || !tiled || !tiled_absmax || N <= 0 || N % 32 || K <= 0 || K % 128)
+    return PE_ERR_ARG;
+  int64_t total = (N / 32) * (K / 128) * 64;
+  nf4_repack_kernel<uint32_t><<<grid_for(total, 256), 256, 0, (hipStream_t)stream>>>(
+      packed, (const uint32_t*)absmax, N, K, tiled, (uint32_t*)tiled_absmax);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+extern "C" int pe_nf4_absmax_dequant(const uint8_t* q, int64_t n, const float* code, const float* nested_absmax,
+                                     int nested_blocksize, float offset, float* absmax, void* stream) {
+  if (!q || !code || !nested_absmax || !absmax || n <= 0 || nested_blocksize <= 0) return PE_ERR_ARG;
+  nf4_absmax_dequant_kernel<<<grid_for(n, 256), 256, 0, (hipStream_t)stream>>>(q, n, code, nested_absmax,
+                                                                                nested_blocksize, offset, absmax);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }
@@ -227,7 +264,18 @@ extern "C" int pe_nf4_dequant(const uint8_t* tiled, const uint16_t* tiled_absmax
                               uint16_t* out, void* stream) {
   if (!tiled || !tiled_absmax || !out || N <= 0 || N % 32 || K <= 0 || K % 128) return PE_ERR_ARG;
   int64_t total = (N / 32) * (K / 128) * 64;
-  nf4_dequant_kernel<<<grid_for(total, 256), 256, 0, (hipStream_t)stream>>>(tiled, tiled_absmax, N, K, out);
+  nf4_dequant_kernel<uint16_t><<<grid_for(total, 256), 256, 0, (hipStream_t)stream>>>(tiled, tiled_absmax, N, K,
+                                                                                     out);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+extern "C" int pe_nf4_dequant_f32abs(const uint8_t* tiled, const float* tiled_absmax, int64_t N, int64_t K,
+                                     uint16_t* out, void* stream) {
+  if (!tiled || !tiled_absmax || !out || N <= 0 || N % 32 || K <= 0 || K % 128) return PE_ERR_ARG;
+  int64_t total = (N / 32) * (K / 128) * 64;
+  nf4_dequant_kernel<uint32_t><<<grid_for(total, 256), 256, 0, (hipStream_t)stream>>>(
+      tiled, (const uint32_t*)tiled_absmax, N, K, out);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }

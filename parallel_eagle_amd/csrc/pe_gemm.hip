@@ -238,9 +238,11 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 // The lane's 16 table entries for two block pairs at once: entry c (at lane
 // base + 256 c + OFF) holds bf16_rne(NF4[c] * scale0) in its low half and
 // bf16_rne(NF4[c] * scale1) in its high half.
-template <int OFF>
-__device__ __forceinline__ void nf4_build_table2(uint8_t* lanetab, uint16_t absmax0, uint16_t absmax1) {
-  const float s0 = f16_bits_to_f32(absmax0), s1 = f16_bits_to_f32(absmax1);
+template <int OFF, bool AF>
+__device__ __forceinline__ void nf4_build_table2(uint8_t* lanetab, uint32_t absmax0, uint32_t absmax1) {
+  // AF: fp32 absmax (bitsandbytes' own), else fp16
+  const float s0 = AF ? __uint_as_float(absmax0) : f16_bits_to_f32((uint16_t)absmax0);
+  const float s1 = AF ? __uint_as_float(absmax1) : f16_bits_to_f32((uint16_t)absmax1);
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
     const f32x2_t v = {kNF4[c] * s0, kNF4[c] * s1};
@@ -445,10 +447,10 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
 // exact; an odd last unit follows the loop.
 // `mid` runs once the wave's first loads are issued (epilogue operands that
 // do not depend on the product are requested there).
-template <int MT, int NT, int WV, bool XT, typename Mid>
+template <int MT, int NT, int WV, bool XT, bool AF, typename Mid>
 __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* smem,
                                               const uint16_t* __restrict__ X, int64_t ldx,
-                                              const uint8_t* __restrict__ W, const uint16_t* __restrict__ Wabs,
+                                              const uint8_t* __restrict__ W, const void* __restrict__ Wabs,
                                               int NP, int group, int w0, int w1, int M, uint32_t region, Mid&& mid) {
   constexpr int XD = MT == 1 ? 8 : 4;  // X k-steps in flight
   const int n = max(w1 - w0, 0);
@@ -470,7 +472,7 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
   for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (int64_t)min(mt * 32 + ln, M - 1) * ldx + 64 * g;
 
   u32x4_t qa[NT][2], qb[NT][2];  // codes of the lane's block in each tile (dword s = MFMA k-step s)
-  uint16_t ac[2][NT];             // absmax of the next two units, for the next table build
+  uint32_t ac[2][NT];             // absmax bits of the next two units, for the next table build
   u32x4_t x[MT][XD];              // X fragments of k-steps s .. s + XD - 1
 
   const int wl = max(w1 - 1, 0);
@@ -496,7 +498,10 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) ac[h][nt] = Wabs[tile_of(nt, p + h) * 64 + lane];
+      for (int nt = 0; nt < NT; ++nt) {
+        const int64_t ai = tile_of(nt, p + h) * 64 + lane;
+        ac[h][nt] = AF ? ((const uint32_t*)Wabs)[ai] : (uint32_t)((const uint16_t*)Wabs)[ai];
+      }
   };
   auto load_x = [&](int slot, int p, int s) {
     const int pc = unit_of(p);
@@ -532,8 +537,8 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
     }
   };
   auto build = [&]() {
-    nf4_build_table2<TB>(lanetab, ac[0][0], ac[1][0]);
-    if constexpr (NT == 2) nf4_build_table2<TB + kTabTile>(lanetab, ac[0][1], ac[1][1]);
+    nf4_build_table2<TB, AF>(lanetab, ac[0][0], ac[1][0]);
+    if constexpr (NT == 2) nf4_build_table2<TB + kTabTile, AF>(lanetab, ac[0][1], ac[1][1]);
   };
   constexpr std::integral_constant<int, 0> kLo{};
   constexpr std::integral_constant<int, 2> kHi{};
@@ -604,9 +609,9 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
 // KW = 4 or 8 waves. Waves w and w + 4 run the same code (table offsets are
 // immediates of wave index w % 4); the second four keep their tables 64 KiB
 // higher, selected by bit 16 of the LDS address.
-template <int MT, int NT, bool XT, int KW>
+template <int MT, int NT, bool XT, int KW, bool AF>
 __global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_gemm_kernel(
-    const uint16_t* __restrict__ X, int64_t ldx, const uint8_t* __restrict__ W, const uint16_t* __restrict__ Wabs,
+    const uint16_t* __restrict__ X, int64_t ldx, const uint8_t* __restrict__ W, const void* __restrict__ Wabs,
     int NP, int S, int pps, float* __restrict__ partial, int* __restrict__ counters, EpiArgs e, int nl, int tS,
     int tpps) {
   constexpr int kTabBytes = kWaves * NT * kTabTile;
@@ -670,10 +675,10 @@ __global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_
       for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.f;
 
   switch (wave & 3) {
-    case 0: nf4_wave_body<MT, NT, 0, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
-    case 1: nf4_wave_body<MT, NT, 1, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
-    case 2: nf4_wave_body<MT, NT, 2, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
-    default: nf4_wave_body<MT, NT, 3, XT>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
+    case 0: nf4_wave_body<MT, NT, 0, XT, AF>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
+    case 1: nf4_wave_body<MT, NT, 1, XT, AF>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
+    case 2: nf4_wave_body<MT, NT, 2, XT, AF>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
+    default: nf4_wave_body<MT, NT, 3, XT, AF>(acc, smem, X, ldx, W, Wabs, NP, group, w0, w1, e.M, region, mid); break;
   }
   lds_barrier();  // every wave is done with its tables; smem becomes the reduction buffer
   finish_tile<PE_DTYPE_BF16, NT, MT, KW>(acc, (float*)smem, group, split, Sg, partial, counters, e, &rp, rope_pre);
@@ -995,30 +1000,44 @@ int64_t workspace_of(const Plan& p) { return kCounterBytes + p.partial_bytes; }
 
 // fmt: -1 = NF4 (bf16 compute), else PE_DTYPE_BF16 / PE_DTYPE_F16 dense.
 // ws: [counters | partials]; the counters are zero on entry and left zero.
+// NF4 format codes of launch_gemm / mfma_gemm (dtype codes are >= 0)
+constexpr int kFmtNF4 = -1;     // fp16 absmax
+constexpr int kFmtNF4F32 = -2;  // fp32 absmax
+int nf4_fmt(int wfmt) { return wfmt == PE_WFMT_NF4_F32ABS ? kFmtNF4F32 : kFmtNF4; }
+
+template <bool AF>
+void launch_nf4(const Plan& p, dim3 grid, hipStream_t st, const uint16_t* x, int64_t ldx, bool x_tiled,
+                const void* w, const void* wabs, float* partial, int* counters, const EpiArgs& e) {
+#define PE_NF4(MT_, NT_, XT_)                                                                                       \
+  nf4_gemm_kernel<MT_, NT_, XT_, kWaves, AF><<<grid, kWaves * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, \
+                                                                            p.S, p.per_split, partial, counters, e,  \
+                                                                            p.nl, p.tS, p.tpps)
+  if (x_tiled) {
+    if (p.NT == 2 && p.MT == 1 && p.KW == 8)
+      nf4_gemm_kernel<1, 2, true, 8, AF><<<grid, 8 * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, p.S,
+                                                                   p.per_split, partial, counters, e, p.nl, p.tS,
+                                                                   p.tpps);
+    else if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, true); else PE_NF4(2, 2, true); }
+    else { if (p.MT == 1) PE_NF4(1, 1, true); else PE_NF4(2, 1, true); }
+  } else {
+    if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, false); else PE_NF4(2, 2, false); }
+    else { if (p.MT == 1) PE_NF4(1, 1, false); else PE_NF4(2, 1, false); }
+  }
+#undef PE_NF4
+}
+
 int launch_gemm(int fmt, const Plan& p, hipStream_t st, const uint16_t* x, int64_t ldx, bool x_tiled, int K,
-                const void* w, const uint16_t* wabs, void* ws, const EpiArgs& e) {
+                const void* w, const void* wabs, void* ws, const EpiArgs& e) {
   if (p.groups > kMaxGroups) return PE_ERR_ARG;
   dim3 grid(p.groups, p.S);
   if (p.nl > 0) grid = dim3(p.nl + (p.groups - p.nl) * p.tS, 1);
   int* counters = (int*)ws;
   float* partial = (float*)((char*)ws + kCounterBytes);
   if (fmt < 0) {
-#define PE_NF4(MT_, NT_, XT_)                                                                                  \
-  nf4_gemm_kernel<MT_, NT_, XT_, kWaves><<<grid, kWaves * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, \
-                                                                        p.S, p.per_split, partial, counters, e, \
-                                                                        p.nl, p.tS, p.tpps)
-    if (x_tiled) {
-      if (p.NT == 2 && p.MT == 1 && p.KW == 8)
-        nf4_gemm_kernel<1, 2, true, 8><<<grid, 8 * 64, 0, st>>>(x, ldx, (const uint8_t*)w, wabs, p.units, p.S,
-                                                                 p.per_split, partial, counters, e, p.nl, p.tS,
-                                                                 p.tpps);
-      else if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, true); else PE_NF4(2, 2, true); }
-      else { if (p.MT == 1) PE_NF4(1, 1, true); else PE_NF4(2, 1, true); }
-    } else {
-      if (p.NT == 2) { if (p.MT == 1) PE_NF4(1, 2, false); else PE_NF4(2, 2, false); }
-      else { if (p.MT == 1) PE_NF4(1, 1, false); else PE_NF4(2, 1, false); }
-    }
-#undef PE_NF4
+    if (fmt == kFmtNF4F32)
+      launch_nf4<true>(p, grid, st, x, ldx, x_tiled, w, wabs, partial, counters, e);
+    else
+      launch_nf4<false>(p, grid, st, x, ldx, x_tiled, w, wabs, partial, counters, e);
   } else {
     if (x_tiled) return PE_ERR_ARG;
 #define PE_DENSE(F, MT_, NT_)                                                                                      \
@@ -1069,7 +1088,7 @@ EpiArgs make_epi(int epi, int mc, int N, const void* bias, const void* resid, in
 
 // M is processed in chunks of up to 64 rows, one launch each.
 // x_tiled: X is A-tiled (M <= 64, one launch); out_units > 0: out is A-tiled.
-int mfma_gemm(int fmt, const void* x, int64_t ldx, int M, int K, const void* w, const uint16_t* wabs, int N,
+int mfma_gemm(int fmt, const void* x, int64_t ldx, int M, int K, const void* w, const void* wabs, int N,
               int epi, const void* bias, const void* resid, int64_t ld_resid, void* out, int64_t ld_out,
               void* ws, int64_t ws_bytes, hipStream_t st, bool x_tiled = false, int out_units = 0) {
   int rc = check_gemm_args(x, M, K, w, N, epi, resid, out);
@@ -1094,14 +1113,12 @@ int mfma_gemm(int fmt, const void* x, int64_t ldx, int M, int K, const void* w, 
   return PE_OK;
 }
 
-constexpr int kFmtNF4 = -1;
-
 }  // namespace
 
 // The q/k/v projection with its RoPE + KV-append epilogue (weight rows in
 // head-paired tile order; hd % 64 == 0), one launch over M <= 64 rows.
 int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int64_t ldx, int M, int K, const void* w,
-                             const uint16_t* wabs, int nh, int nkv, int hd, const void* bias,
+                             const void* wabs, int nh, int nkv, int hd, const void* bias,
                              const int64_t* positions, const void* cos_sin, int64_t max_pos, void* q_out,
                              void* k_cache, void* v_cache, int64_t cap, int64_t row0, int32_t* status, void* ws,
                              int64_t ws_bytes, bool x_tiled, hipStream_t st) {
@@ -1110,7 +1127,7 @@ int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int64_t ldx, in
   if (row0 < 0 || row0 + M > cap) return PE_ERR_CAPACITY;
   int rc = check_gemm_args(x, M, K, w, N, PE_EPI_SWIGLU, nullptr, q_out);
   if (rc != PE_OK) return rc;
-  const bool nf4 = wfmt == PE_WFMT_NF4;
+  const bool nf4 = pe_wfmt_nf4(wfmt);
   Plan p = make_plan(M, N, K, nf4, kEpiRopeKV);
   if (!ws || ws_bytes < workspace_of(p)) return PE_ERR_WORKSPACE;
   EpiArgs e = make_epi(kEpiRopeKV, M, N, bias, nullptr, 0, nullptr, 0);
@@ -1126,15 +1143,15 @@ int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int64_t ldx, in
   e.nkv = nkv;
   e.hd = hd;
   e.status = status;
-  return launch_gemm(nf4 ? kFmtNF4 : dtype, p, st, (const uint16_t*)x, ldx, x_tiled, K, w, wabs, ws, e);
+  return launch_gemm(nf4 ? nf4_fmt(wfmt) : dtype, p, st, (const uint16_t*)x, ldx, x_tiled, K, w, wabs, ws, e);
 }
 
 int pe_internal_linear(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M, int K, const void* w,
-                       const uint16_t* wabs, int N, int epi, const void* bias, const void* resid, int64_t ld_resid,
+                       const void* wabs, int N, int epi, const void* bias, const void* resid, int64_t ld_resid,
                        void* out, int64_t ld_out, int out_units, void* ws, int64_t ws_bytes, hipStream_t st) {
-  if (wfmt == PE_WFMT_NF4) {
+  if (pe_wfmt_nf4(wfmt)) {
     if (!wabs) return PE_ERR_ARG;
-    return mfma_gemm(kFmtNF4, x, ldx, M, K, w, wabs, N, epi, bias, resid, ld_resid, out, ld_out, ws, ws_bytes, st,
+    return mfma_gemm(nf4_fmt(wfmt), x, ldx, M, K, w, wabs, N, epi, bias, resid, ld_resid, out, ld_out, ws, ws_bytes, st,
                      x_tiled, out_units);
   }
   if (dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16) return PE_ERR_ARG;
@@ -1144,30 +1161,30 @@ int pe_internal_linear(int wfmt, int dtype, const void* x, int64_t ldx, bool x_t
 
 int64_t pe_internal_gemm_rope_kv_bytes(int M, int N, int K, int wfmt) {
   if (M > kMaxChunkRows) M = kMaxChunkRows;
-  return workspace_of(make_plan(M, N, K, wfmt == PE_WFMT_NF4, kEpiRopeKV));
+  return workspace_of(make_plan(M, N, K, pe_wfmt_nf4(wfmt), kEpiRopeKV));
 }
 
 // Y = X . W^T as split partials partial[S][M][N] (fp32, plain stores: no
 // exchange between workgroups, the consumer sums them); one launch, M <= 64.
 int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M, int K,
-                                const void* w, const uint16_t* wabs, int N, float* partial, int64_t partial_bytes,
+                                const void* w, const void* wabs, int N, float* partial, int64_t partial_bytes,
                                 int* splits, hipStream_t st) {
   if (M > kMaxChunkRows || !partial || !splits) return PE_ERR_ARG;
   int rc = check_gemm_args(x, M, K, w, N, PE_EPI_STORE, nullptr, partial);
   if (rc != PE_OK) return rc;
-  const bool nf4 = wfmt == PE_WFMT_NF4;
+  const bool nf4 = pe_wfmt_nf4(wfmt);
   if (nf4 ? !wabs : (dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16)) return PE_ERR_ARG;
   if (x_tiled && !nf4) return PE_ERR_ARG;
   const Plan p = make_plan(M, N, K, nf4, kEpiPartial);
   if (partial_bytes < (int64_t)p.S * M * N * 4) return PE_ERR_WORKSPACE;
   EpiArgs e = make_epi(kEpiPartial, M, N, nullptr, nullptr, 0, partial, N);
   *splits = p.S;
-  return launch_gemm(nf4 ? kFmtNF4 : dtype, p, st, (const uint16_t*)x, ldx, x_tiled, K, w, wabs, nullptr, e);
+  return launch_gemm(nf4 ? nf4_fmt(wfmt) : dtype, p, st, (const uint16_t*)x, ldx, x_tiled, K, w, wabs, nullptr, e);
 }
 
 int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int wfmt) {
   if (M > kMaxChunkRows) M = kMaxChunkRows;
-  return (int64_t)make_plan(M, N, K, wfmt == PE_WFMT_NF4, kEpiPartial).S * M * N * 4;
+  return (int64_t)make_plan(M, N, K, pe_wfmt_nf4(wfmt), kEpiPartial).S * M * N * 4;
 }
 
 // The q/k/v epilogue (bias, RoPE at positions[row], q to q_out, K/V appended
@@ -1221,7 +1238,7 @@ extern "C" int64_t pe_gemm_workspace_bytes(int M, int N, int K, int wfmt, int dt
   if (dtype == PE_DTYPE_F32 && wfmt == PE_WFMT_DENSE) return 0;
   if (M <= 0 || N <= 0 || K < 128) return kCounterBytes;
   const int mc = M > kMaxChunkRows ? kMaxChunkRows : M;
-  return workspace_of(make_plan(mc, N, K, wfmt == PE_WFMT_NF4, epilogue));
+  return workspace_of(make_plan(mc, N, K, pe_wfmt_nf4(wfmt), epilogue));
 }
 
 extern "C" int pe_nf4_gemm(const void* x, int64_t ldx, int M, int K, const uint8_t* w_tiled,
@@ -1230,6 +1247,15 @@ extern "C" int pe_nf4_gemm(const void* x, int64_t ldx, int M, int K, const uint8
                            int64_t workspace_bytes, void* stream) {
   if (!absmax_tiled) return PE_ERR_ARG;
   return mfma_gemm(kFmtNF4, x, ldx, M, K, w_tiled, absmax_tiled, N, epilogue, bias, resid, ld_resid, out,
+                   ld_out, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int pe_nf4_gemm_f32abs(const void* x, int64_t ldx, int M, int K, const uint8_t* w_tiled,
+                                  const float* absmax_tiled, int N, int epilogue, const void* bias,
+                                  const void* resid, int64_t ld_resid, void* out, int64_t ld_out, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  if (!absmax_tiled) return PE_ERR_ARG;
+  return mfma_gemm(kFmtNF4F32, x, ldx, M, K, w_tiled, absmax_tiled, N, epilogue, bias, resid, ld_resid, out,
                    ld_out, workspace, workspace_bytes, (hipStream_t)stream);
 }
 

@@ -7,11 +7,17 @@
 
 #define PE_INTERNAL __attribute__((visibility("hidden")))
 
+#include "pe_hip.h"
+
+// NF4 weight formats (absmax fp16 or fp32); wabs points at the tiled absmax
+// of that type
+inline bool pe_wfmt_nf4(int wfmt) { return wfmt == PE_WFMT_NF4 || wfmt == PE_WFMT_NF4_F32ABS; }
+
 // pe_gemm.hip: the q/k/v projection with bias, RoPE and the in-place K/V
 // append in its epilogue (one launch over M <= 64 rows); ws as for
 // pe_nf4_gemm (zeroed counters, then partials), of pe_internal_gemm_rope_kv_bytes.
 PE_INTERNAL int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int64_t ldx, int M, int K,
-                                         const void* w, const uint16_t* wabs, int nh, int nkv, int hd,
+                                         const void* w, const void* wabs, int nh, int nkv, int hd,
                                          const void* bias, const int64_t* positions, const void* cos_sin,
                                          int64_t max_pos, void* q_out, void* k_cache, void* v_cache, int64_t cap,
                                          int64_t row0, int32_t* status, void* ws, int64_t ws_bytes, bool x_tiled,
@@ -21,14 +27,14 @@ PE_INTERNAL int64_t pe_internal_gemm_rope_kv_bytes(int M, int N, int K, int wfmt
 // and/or an A-tiled output (out_units = N_out / 128, not with the residual
 // epilogue).
 PE_INTERNAL int pe_internal_linear(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M, int K,
-                                   const void* w, const uint16_t* wabs, int N, int epi, const void* bias,
+                                   const void* w, const void* wabs, int N, int epi, const void* bias,
                                    const void* resid, int64_t ld_resid, void* out, int64_t ld_out, int out_units,
                                    void* ws, int64_t ws_bytes, hipStream_t st);
 
 // pe_gemm.hip: Y = X . W^T as split partials partial[S][M][N] fp32 (plain
 // stores, summed by the consumer in split order); *splits receives S. M <= 64.
 PE_INTERNAL int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M,
-                                            int K, const void* w, const uint16_t* wabs, int N, float* partial,
+                                            int K, const void* w, const void* wabs, int N, float* partial,
                                             int64_t partial_bytes, int* splits, hipStream_t st);
 PE_INTERNAL int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int wfmt);
 

@@ -50,7 +50,7 @@ bool fused_path(const pe_model_desc* m, int M) {
 
 // The fused NF4 pass hands the GEMMs their X A-tiled (see xtile_index).
 bool tiled_path(const pe_model_desc* m, int M) {
-  return fused_path(m, M) && m->weight_format == PE_WFMT_NF4 && m->hidden % 128 == 0 &&
+  return fused_path(m, M) && pe_wfmt_nf4(m->weight_format) && m->hidden % 128 == 0 &&
          (m->num_heads * m->head_dim) % 128 == 0 && m->intermediate_padded % 128 == 0;
 }
 
@@ -111,6 +111,9 @@ int linear(const pe_model_desc* m, const void* x, int64_t ldx, int M, int K, con
   if (m->weight_format == PE_WFMT_NF4)
     return pe_nf4_gemm(x, ldx, M, K, (const uint8_t*)w, (const uint16_t*)a, N, epi, bias, resid, ldr, out, ldo, ws,
                        wsb, st);
+  if (m->weight_format == PE_WFMT_NF4_F32ABS)
+    return pe_nf4_gemm_f32abs(x, ldx, M, K, (const uint8_t*)w, (const float*)a, N, epi, bias, resid, ldr, out, ldo,
+                              ws, wsb, st);
   return pe_dense_gemm(x, ldx, M, K, w, m->dtype, N, epi, bias, resid, ldr, out, ldo, ws, wsb, st);
 }
 
@@ -212,7 +215,7 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   for (int l = 0; l < L; ++l) {
     void* kc = (char*)a->k_cache + l * layer_stride;
     void* vc = (char*)a->v_cache + l * layer_stride;
-    const uint16_t* a_qkv = (const uint16_t*)(m->a_qkv ? m->a_qkv[l] : nullptr);
+    const void* a_qkv = m->a_qkv ? m->a_qkv[l] : nullptr;
     const void* b_qkv = m->b_qkv ? m->b_qkv[l] : nullptr;
     PE_TRY(pe_internal_gemm_rope_kv(wf, m->dtype, x_norm, H, M, H, m->w_qkv[l], a_qkv, nh, nkv, hd, b_qkv,
                                     a->positions, m->rope_cos_sin, m->max_positions, q, kc, vc, a->cache_capacity,
@@ -220,7 +223,7 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
                                       a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
                                       Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st));
-    const uint16_t* a_o = (const uint16_t*)(m->a_o ? m->a_o[l] : nullptr);
+    const void* a_o = m->a_o ? m->a_o[l] : nullptr;
     if (tiled) {
       PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, true, M, qd, m->w_o[l], a_o, H, part,
                                          Lo.part_bytes, &S, st));
@@ -232,8 +235,8 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
       PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, nullptr,
                                           nullptr, 0, nullptr, 0, st));
     }
-    const uint16_t* a_gu = (const uint16_t*)(m->a_gu ? m->a_gu[l] : nullptr);
-    const uint16_t* a_down = (const uint16_t*)(m->a_down ? m->a_down[l] : nullptr);
+    const void* a_gu = m->a_gu ? m->a_gu[l] : nullptr;
+    const void* a_down = m->a_down ? m->a_down[l] : nullptr;
     const bool last = l + 1 == L;
     const int fh = last ? -1 : slot_of(l + 1);
     const int fx = last ? slot_of(L) : -1;

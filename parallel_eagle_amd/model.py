@@ -63,6 +63,7 @@ class DeviceModel:
         self.device = torch.device(device)
         self.dtype = TORCH_DTYPES[shape.dtype]
         self.nf4 = shape.weight_format == "nf4"
+        self.absmax_dtype = None  # fp16 (the quantiser's) or fp32 (bitsandbytes checkpoints); set by the first layer
         if self.nf4 and self.dtype != torch.bfloat16:
             raise ValueError("NF4 linears compute in bfloat16")
         self.ipad = padded_intermediate(shape)
@@ -117,7 +118,7 @@ class DeviceModel:
     @classmethod
     def from_weights(cls, shape: ModelShape, weights: dict, device="cuda", keep_logical: bool = False):
         """weights: the oracle's dict layout (host tensors; NF4 linears as
-        ("nf4", packed uint8 [N][K/2], absmax fp16 [N][K/64]))."""
+        ("nf4", packed uint8 [N][K/2], absmax fp16 or fp32 [N][K/64]))."""
         self = cls(shape, device)
         dev, dt = self.device, self.dtype
 
@@ -162,6 +163,11 @@ class DeviceModel:
         s = self.shape
         out = {"attn_norm": lin["attn_norm"], "mlp_norm": lin["mlp_norm"]}
         if self.nf4:
+            adt = lin["q"][1].dtype
+            if self.absmax_dtype is None:
+                self.absmax_dtype = adt
+            if any(lin[nm][1].dtype != self.absmax_dtype for nm in ("q", "k", "v", "o", "gate", "up", "down")):
+                raise ValueError("every NF4 linear of a model needs the same absmax dtype (fp16 or fp32)")
             qkv_p = torch.cat([lin["q"][0], lin["k"][0], lin["v"][0]], 0).contiguous()
             qkv_a = torch.cat([lin["q"][1], lin["k"][1], lin["v"][1]], 0).contiguous()
             order = self._qkv_row_order(qkv_p.device)
@@ -204,8 +210,8 @@ class DeviceModel:
         kh, ka = g[0].shape[1], g[1].shape[1]
         gp = torch.full((ip, kh), NF4_ZERO_BYTE, dtype=torch.uint8, device=g[0].device)
         upk = torch.full((ip, kh), NF4_ZERO_BYTE, dtype=torch.uint8, device=g[0].device)
-        ga = torch.zeros((ip, ka), dtype=torch.float16, device=g[0].device)
-        ua = torch.zeros((ip, ka), dtype=torch.float16, device=g[0].device)
+        ga = torch.zeros((ip, ka), dtype=g[1].dtype, device=g[0].device)
+        ua = torch.zeros((ip, ka), dtype=u[1].dtype, device=g[0].device)
         gp[: g[0].shape[0]] = g[0]
         upk[: u[0].shape[0]] = u[0]
         ga[: g[1].shape[0]] = g[1]
@@ -225,7 +231,7 @@ class DeviceModel:
         if d[0].shape[1] * 2 == self.ipad:
             return d[0].contiguous(), d[1].contiguous()
         p = torch.full((d[0].shape[0], self.ipad // 2), NF4_ZERO_BYTE, dtype=torch.uint8, device=d[0].device)
-        a = torch.zeros((d[0].shape[0], self.ipad // 64), dtype=torch.float16, device=d[0].device)
+        a = torch.zeros((d[0].shape[0], self.ipad // 64), dtype=d[1].dtype, device=d[0].device)
         p[:, : d[0].shape[1]] = d[0]
         a[:, : d[1].shape[1]] = d[1]
         return p, a
@@ -253,7 +259,12 @@ class DeviceModel:
         d.num_layers, d.hidden, d.num_heads, d.num_kv_heads = L, s.hidden, s.num_heads, s.num_kv_heads
         d.head_dim, d.intermediate, d.vocab, d.intermediate_padded = s.head_dim, s.intermediate, s.vocab, self.ipad
         d.dtype = ops.dcode(self.dtype)
-        d.weight_format = _lib.PE_WFMT_NF4 if self.nf4 else _lib.PE_WFMT_DENSE
+        if not self.nf4:
+            d.weight_format = _lib.PE_WFMT_DENSE
+        elif self.absmax_dtype == torch.float32:
+            d.weight_format = _lib.PE_WFMT_NF4_F32ABS
+        else:
+            d.weight_format = _lib.PE_WFMT_NF4
         d.qkv_layout = _lib.PE_QKV_ROPE_PAIRED if self.qkv_paired else _lib.PE_QKV_PLAIN
         d.rms_eps = s.rms_eps
         d.max_positions = s.max_positions

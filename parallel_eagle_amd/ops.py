@@ -72,21 +72,40 @@ def nf4_quantize(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 
 def nf4_repack(packed: torch.Tensor, absmax: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Logical NF4 (packed uint8 [N][K/2], absmax fp16 or fp32 [N][K/64]) -> tiled;
+    the tiled absmax keeps the absmax dtype."""
     n, kh = packed.shape
     k = kh * 2
     _req(packed.dtype == torch.uint8 and packed.is_contiguous(), "packed must be contiguous uint8 [N][K/2]")
-    _req(absmax.dtype == torch.float16 and absmax.shape == (n, k // 64) and absmax.is_contiguous(),
-         "absmax must be contiguous fp16 [N][K/64]")
+    _req(absmax.dtype in (torch.float16, torch.float32) and absmax.shape == (n, k // 64) and absmax.is_contiguous(),
+         "absmax must be contiguous fp16 or fp32 [N][K/64]")
     _req(n % 32 == 0 and k % 128 == 0, "N % 32 == 0 and K % 128 == 0 required")
     tiled = torch.empty(n * k // 2, dtype=torch.uint8, device=packed.device)
-    tabs = torch.empty(n * k // 64, dtype=torch.float16, device=packed.device)
-    check(lib().pe_nf4_repack(ptr(packed), ptr(absmax), n, k, ptr(tiled), ptr(tabs), stream_ptr()), "pe_nf4_repack")
+    tabs = torch.empty(n * k // 64, dtype=absmax.dtype, device=packed.device)
+    fn = "pe_nf4_repack_f32abs" if absmax.dtype == torch.float32 else "pe_nf4_repack"
+    check(getattr(lib(), fn)(ptr(packed), ptr(absmax), n, k, ptr(tiled), ptr(tabs), stream_ptr()), fn)
     return tiled, tabs
 
 
 def nf4_dequant(tiled: torch.Tensor, tabs: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    _req(tabs.dtype in (torch.float16, torch.float32), "tiled absmax must be fp16 or fp32")
     out = torch.empty((n, k), dtype=torch.bfloat16, device=tiled.device)
-    check(lib().pe_nf4_dequant(ptr(tiled), ptr(tabs), n, k, ptr(out), stream_ptr()), "pe_nf4_dequant")
+    fn = "pe_nf4_dequant_f32abs" if tabs.dtype == torch.float32 else "pe_nf4_dequant"
+    check(getattr(lib(), fn)(ptr(tiled), ptr(tabs), n, k, ptr(out), stream_ptr()), fn)
+    return out
+
+
+def nf4_absmax_dequant(q: torch.Tensor, code: torch.Tensor, nested_absmax: torch.Tensor, nested_blocksize: int,
+                       offset: float) -> torch.Tensor:
+    """bitsandbytes double-quantised absmax -> fp32: code[q[i]] * nested_absmax[i // bs] + offset."""
+    _req(q.dtype == torch.uint8 and q.is_contiguous(), "q must be contiguous uint8")
+    _req(code.dtype == torch.float32 and code.numel() == 256 and code.is_contiguous(), "code must be 256 fp32")
+    n = q.numel()
+    _req(nested_absmax.dtype == torch.float32 and nested_absmax.is_contiguous()
+         and nested_absmax.numel() * nested_blocksize >= n, "nested_absmax must cover every block")
+    out = torch.empty(n, dtype=torch.float32, device=q.device)
+    check(lib().pe_nf4_absmax_dequant(ptr(q), n, ptr(code), ptr(nested_absmax), nested_blocksize, float(offset),
+                                      ptr(out), stream_ptr()), "pe_nf4_absmax_dequant")
     return out
 
 
@@ -125,9 +144,10 @@ def linear(x: torch.Tensor, n: int, *, nf4: tuple | None = None, dense: torch.Te
     L = lib()
     if nf4 is not None:
         _req(x.dtype == torch.bfloat16, "NF4 linears compute in bf16")
-        rc = L.pe_nf4_gemm(ptr(x), x.stride(0), m, k, ptr(nf4[0]), ptr(nf4[1]), n, epilogue, ptr(bias), ptr(resid),
-                           resid.stride(0) if resid is not None else 0, ptr(out), out.stride(0), ptr(workspace),
-                           workspace.numel(), stream_ptr())
+        fn = L.pe_nf4_gemm_f32abs if nf4[1].dtype == torch.float32 else L.pe_nf4_gemm
+        rc = fn(ptr(x), x.stride(0), m, k, ptr(nf4[0]), ptr(nf4[1]), n, epilogue, ptr(bias), ptr(resid),
+                resid.stride(0) if resid is not None else 0, ptr(out), out.stride(0), ptr(workspace),
+                workspace.numel(), stream_ptr())
     else:
         rc = L.pe_dense_gemm(ptr(x), x.stride(0), m, k, ptr(dense), dcode(x.dtype), n, epilogue, ptr(bias),
                              ptr(resid), resid.stride(0) if resid is not None else 0, ptr(out), out.stride(0),
@@ -172,6 +192,7 @@ def linear_tiled(xt: torch.Tensor, m: int, k: int, n: int, nf4: tuple, *, epilog
                else torch.empty((m, n_out), dtype=xt.dtype, device=xt.device))
     if workspace is None:
         workspace = _workspace(gemm_workspace_bytes(m, n, k, True, xt.dtype, epilogue), xt.device)
+    _req(nf4[1].dtype == torch.float16, "the A-tiled and split-partial NF4 entry points take fp16 absmax")
     check(lib().pe_nf4_gemm_tiled(ptr(xt), m, k, ptr(nf4[0]), ptr(nf4[1]), n, epilogue, None, ptr(resid),
                                   resid.stride(0) if resid is not None else 0, ptr(out),
                                   0 if out_tiled else out.stride(0), n_out // 128 if out_tiled else 0,
@@ -189,6 +210,7 @@ def nf4_linear_partials(x: torch.Tensor, m: int, k: int, n: int, nf4: tuple, *, 
     if partials is None:
         partials = torch.empty(nbytes // 4, dtype=torch.float32, device=x.device)
     s = C.c_int(0)
+    _req(nf4[1].dtype == torch.float16, "the A-tiled and split-partial NF4 entry points take fp16 absmax")
     check(lib().pe_nf4_gemm_partials(ptr(x), k if x_tiled else x.stride(0), int(x_tiled), m, k, ptr(nf4[0]),
                                      ptr(nf4[1]), n, ptr(partials), partials.numel() * 4, C.byref(s), stream_ptr()),
           "nf4_linear_partials")

@@ -111,6 +111,16 @@ class TargetModel:
         noise = kw.pop("norm_noise", 0.0)
         return cls(DeviceModel.synthetic(shape, seed, device, keep_logical=keep, norm_noise=noise), **kw)
 
+    @classmethod
+    def from_bnb_state_dict(cls, shape: ModelShape, state_dict: dict, device="cuda", **kw) -> "TargetModel":
+        """A pre-quantized bitsandbytes NF4 checkpoint (the state dict of the model
+        src/pe/target.py:32-38 loads), run with the fp32-absmax kernels."""
+        from . import bnb
+
+        keep = kw.pop("keep_logical", False)
+        weights = bnb.weights_from_state_dict(shape, state_dict, device)
+        return cls(DeviceModel.from_weights(shape, weights, device, keep_logical=keep), **kw)
+
     # ------------------------------------------------------------ attributes of the reference API
     @property
     def config(self):

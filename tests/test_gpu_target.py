@@ -108,10 +108,12 @@ def _fp32_oracle(shape, host_weights):
     return OracleTarget(replace(shape, dtype="float32", weight_format="dense"), hw32)
 
 
-def _run_case(shape, seed, P, depth, widths, top_k, plant, tol, random_kv=False):
+def _run_case(shape, seed, P, depth, widths, top_k, plant, tol, random_kv=False, tm=None):
+    """tm: a model built with keep_logical=True (default: the seeded synthetic one)."""
     torch.manual_seed(0)
-    tm = TargetModel.synthetic(shape, seed=seed, device=DEV, keep_logical=True, norm_noise=0.1,
-                               cache_capacity=P + 128)
+    if tm is None:
+        tm = TargetModel.synthetic(shape, seed=seed, device=DEV, keep_logical=True, norm_noise=0.1,
+                                   cache_capacity=P + 128)
     hw = tm.model.host_weights()
     orc = OracleTarget(shape, hw)
     orc.cache_dequant = True  # dequantise each NF4 matrix once; values are the same every call
