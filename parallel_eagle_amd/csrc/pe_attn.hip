@@ -89,7 +89,9 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 31, g = lane >> 5;
   const int64_t S = P + T;
   const int64_t ks0 = (int64_t)split * keys_per_split;
-  const int64_t ks1 = min(S, ks0 + keys_per_split);
+  // causal rows of this tile see keys up to P + their last query index
+  const int64_t kvis = mask_mode == PE_MASK_CAUSAL ? P + min(T - 1, (rt * 32 + 31) / G) + 1 : S;
+  const int64_t ks1 = min(min(S, kvis), ks0 + keys_per_split);
   const int nb = ks1 > ks0 ? (int)((ks1 - ks0 + 31) / 32) : 0;  // trailing splits may be empty
   const int b0 = (nb * wave) / kAttnWaves, b1 = (nb * (wave + 1)) / kAttnWaves;
   const int64_t j1 = min(ks1, ks0 + 32 * (int64_t)b1);  // end of this wave's keys
@@ -561,7 +563,7 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
   if (workspace_bytes < pe_attention_workspace_bytes(T, nh, nkv, hd, S, dtype)) return PE_ERR_WORKSPACE;
   if (dtype != PE_DTYPE_F32 && hd == 128) {
     AttnPlan p = attn_plan(T, nh, nkv, S);
-    if ((int64_t)nkv * p.row_tiles * 4 > kAttnCounterBytes) return PE_ERR_ARG;
+    if (p.splits > 1 && (int64_t)nkv * p.row_tiles * 4 > kAttnCounterBytes) return PE_ERR_ARG;
     if (!counters) counters = (int*)workspace;
     float* opart = (float*)((char*)workspace + kAttnCounterBytes);
     float* ml = (float*)((char*)workspace + kAttnCounterBytes + p.opart_bytes);

@@ -15,8 +15,13 @@
 
 #include <hip/hip_runtime.h>
 
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/pe_hip.h"
 #include "pe_internal.h"
@@ -136,10 +141,197 @@ extern "C" int pe_version(void) { return 1; }
 
 constexpr int kFusedChunk = 64;  // rows per fused pass (causal passes are chunked)
 
+// ---------------------------------------------------------------------------
+// Prefill (a causal pass of more than kFusedChunk rows on an NF4 model with
+// RoPE-paired q/k/v): every linear is dequantised once to bf16 (in its tiled
+// row order) and multiplied over all M rows by a rocBLAS GEMM with fp32
+// output; the fused pass's epilogue kernels then treat that output as one
+// split: RoPE + K/V append for q/k/v, SwiGLU for gate/up, residual + RMSNorm
+// (with the captures) after o and down. Attention runs once over all rows.
+// The weights are read once per pass instead of once per 64-row chunk; the
+// dequantisation costs about as much as four chunked passes, so shorter causal
+// passes stay chunked.
+// ---------------------------------------------------------------------------
+constexpr int kPrefillMinRows = 4 * kFusedChunk + 1;
+bool prefill_path(const pe_model_desc* m, int M, int mask_mode) {
+  static const bool on = [] {
+    const char* v = getenv("PE_PREFILL_GEMM");
+    return !v || atoi(v) != 0;
+  }();
+  return on && M >= kPrefillMinRows && mask_mode == PE_MASK_CAUSAL && pe_wfmt_nf4(m->weight_format) &&
+         m->qkv_layout == PE_QKV_ROPE_PAIRED && m->dtype == PE_DTYPE_BF16 && m->head_dim == 128 &&
+         m->hidden % 128 == 0 && m->intermediate_padded % 128 == 0;
+}
+
+struct PrefillLayout {
+  int64_t h, xn, q, attn, act, y, wdeq, attn_ws, attn_ws_bytes, gemm, gemm_bytes, blas, blas_bytes, total;
+};
+constexpr int64_t kBlasWorkspace = 64ll << 20;
+
+PrefillLayout make_prefill_layout(const pe_model_desc* m, int M, int64_t kv_len) {
+  PrefillLayout L;
+  const int64_t H = m->hidden, qd = (int64_t)m->num_heads * m->head_dim;
+  const int64_t nqkv = qd + 2ll * m->num_kv_heads * m->head_dim, ip = m->intermediate_padded;
+  // offset 0: the pass's counters and the lm_head GEMM's workspace, as in the
+  // fused layout (the GEMM and attention counter slices rest at zero or at
+  // multiples of 16 between passes, whichever path ran last)
+  L.gemm = 0;
+  L.gemm_bytes = align_up(std::max<int64_t>(
+      kCounterBytes, pe_gemm_workspace_bytes(kFusedChunk, m->vocab, m->hidden, PE_WFMT_DENSE, m->dtype, PE_EPI_STORE)));
+  int64_t off = L.gemm_bytes;
+  auto take = [&](int64_t bytes) {
+    const int64_t o = off;
+    off += align_up(bytes);
+    return o;
+  };
+  L.h = take(M * H * 2);
+  L.xn = take(M * H * 2);
+  L.q = take(M * qd * 2);
+  L.attn = take(M * qd * 2);
+  L.act = take(M * ip * 2);
+  int64_t ny = nqkv;
+  if (2 * ip > ny) ny = 2 * ip;
+  if (H > ny) ny = H;
+  L.y = take(M * ny * 4);
+  int64_t nw = nqkv * H;
+  if (2 * ip * H > nw) nw = 2 * ip * H;
+  if (H * ip > nw) nw = H * ip;
+  if (H * qd > nw) nw = H * qd;
+  L.wdeq = take(nw * 2);
+  L.attn_ws_bytes = align_up(pe_attention_workspace_bytes(M, m->num_heads, m->num_kv_heads, m->head_dim, kv_len,
+                                                          m->dtype));
+  L.attn_ws = take(L.attn_ws_bytes);
+  L.blas_bytes = kBlasWorkspace;
+  L.blas = take(L.blas_bytes);
+  L.total = off;
+  return L;
+}
+
+// One rocBLAS handle per device, made on first use; each call sets the stream
+// and hands rocBLAS its workspace from the pass's workspace.
+rocblas_handle blas_handle() {
+  static std::mutex mu;
+  static rocblas_handle handles[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!handles[dev] && rocblas_create_handle(&handles[dev]) != rocblas_status_success) handles[dev] = nullptr;
+  return handles[dev];
+}
+
+// y[M][N] (fp32) = x[M][K] . w[N][K]^T, bf16 operands, fp32 accumulation.
+int blas_gemm(hipStream_t st, int M, int N, int K, const void* x, const void* w, float* y, void* bws,
+              int64_t bws_bytes) {
+  rocblas_handle hd = blas_handle();
+  if (!hd) return PE_ERR_LAUNCH;
+  if (rocblas_set_stream(hd, st) != rocblas_status_success) return PE_ERR_LAUNCH;
+  if (rocblas_set_workspace(hd, bws, (size_t)bws_bytes) != rocblas_status_success) return PE_ERR_LAUNCH;
+  const float alpha = 1.f, beta = 0.f;
+  // column-major: y^T [N][M] = (w viewed K x N)^T . (x viewed K x M)
+  const rocblas_status s = rocblas_gemm_ex(hd, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha,
+                                           w, rocblas_datatype_bf16_r, K, x, rocblas_datatype_bf16_r, K, &beta, y,
+                                           rocblas_datatype_f32_r, N, y, rocblas_datatype_f32_r, N,
+                                           rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  return s == rocblas_status_success ? PE_OK : PE_ERR_LAUNCH;
+}
+
+int dequant(const pe_model_desc* m, const void* w, const void* a, int64_t N, int64_t K, void* out, hipStream_t st) {
+  if (m->weight_format == PE_WFMT_NF4_F32ABS)
+    return pe_nf4_dequant_f32abs((const uint8_t*)w, (const float*)a, N, K, (uint16_t*)out, st);
+  return pe_nf4_dequant((const uint8_t*)w, (const uint16_t*)a, N, K, (uint16_t*)out, st);
+}
+
+int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const PrefillLayout& Lp, hipStream_t st) {
+  const int M = a->M;
+  char* ws = (char*)a->workspace;
+  const int es = 2;
+  const int H = m->hidden, nh = m->num_heads, nkv = m->num_kv_heads, hd = m->head_dim;
+  const int qd = nh * hd, ip = m->intermediate_padded, L = m->num_layers;
+  const int nqkv = (nh + 2 * nkv) * hd;
+  void* h = ws + Lp.h;
+  void* xn = ws + Lp.xn;
+  void* q = ws + Lp.q;
+  void* attn = ws + Lp.attn;
+  void* act = ws + Lp.act;
+  float* y = (float*)(ws + Lp.y);
+  void* wdeq = ws + Lp.wdeq;
+  void* bws = ws + Lp.blas;
+  const float scale = (float)(1.0 / std::sqrt((double)hd));
+  const int64_t layer_stride = (int64_t)nkv * a->cache_capacity * hd * es;
+  const int64_t fused_ld = (int64_t)a->num_features * H;
+  int rc;
+#define PE_TRY(expr)            \
+  do {                          \
+    rc = (expr);                \
+    if (rc != PE_OK) return rc; \
+  } while (0)
+  auto slot_of = [&](int layer) -> int {
+    if (!a->fused) return -1;
+    for (int f = 0; f < a->num_features; ++f)
+      if (a->feature_layers[f] == layer) return f;
+    return -1;
+  };
+  auto slot_ptr = [&](int f) -> void* { return f < 0 ? nullptr : (char*)a->fused + (int64_t)f * H * es; };
+  auto copy_repeats = [&](int layer, int first) -> int {
+    if (first < 0) return PE_OK;
+    for (int f = first + 1; f < a->num_features; ++f) {
+      if (a->feature_layers[f] != layer) continue;
+      int r = pe_copy_rows(slot_ptr(first), fused_ld * es, M, (int64_t)H * es, slot_ptr(f), fused_ld * es, st);
+      if (r != PE_OK) return r;
+    }
+    return PE_OK;
+  };
+  auto linear = [&](const void* x, int K, const void* w, const void* ab, int N) -> int {
+    int r = dequant(m, w, ab, N, K, wdeq, st);
+    if (r != PE_OK) return r;
+    return blas_gemm(st, M, N, K, x, wdeq, y, bws, Lp.blas_bytes);
+  };
+
+  PE_TRY(pe_embed(a->input_ids, M, m->embed, m->vocab, H, m->dtype, h, H, a->status, st));
+  {
+    const int f0 = slot_of(0);
+    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->attn_norm[0], m->rms_eps, m->dtype, xn, nullptr,
+                                        slot_ptr(f0), fused_ld, nullptr, 0, st));
+    PE_TRY(copy_repeats(0, f0));
+  }
+  for (int l = 0; l < L; ++l) {
+    void* kc = (char*)a->k_cache + l * layer_stride;
+    void* vc = (char*)a->v_cache + l * layer_stride;
+    PE_TRY(linear(xn, H, m->w_qkv[l], m->a_qkv[l], nqkv));
+    PE_TRY(pe_internal_rope_kv_partials(y, 1, M, nh, nkv, hd, m->b_qkv ? m->b_qkv[l] : nullptr, a->positions,
+                                        m->rope_cos_sin, m->max_positions, q, kc, vc, a->cache_capacity,
+                                        a->prefix_len, a->status, m->dtype, st));
+    PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, PE_MASK_CAUSAL,
+                                      nullptr, 0, scale, m->dtype, attn, qd, 0, ws + Lp.attn_ws, Lp.attn_ws_bytes,
+                                      (int*)(ws + Lp.gemm) + kPassAttnCounterInt, st));
+    PE_TRY(linear(attn, qd, m->w_o[l], m->a_o[l], H));
+    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, nullptr, nullptr, 0,
+                                        nullptr, 0, st));
+    PE_TRY(linear(xn, H, m->w_gu[l], m->a_gu[l], 2 * ip));
+    PE_TRY(pe_internal_swiglu_partials(y, 1, M, 2 * ip, act, ip, 0, m->dtype, st));
+    PE_TRY(linear(act, ip, m->w_down[l], m->a_down[l], H));
+    const bool last = l + 1 == L;
+    const int fh = last ? -1 : slot_of(l + 1);
+    const int fx = last ? slot_of(L) : -1;
+    const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
+    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, next_norm, m->rms_eps, m->dtype, xn, nullptr, slot_ptr(fh),
+                                        fused_ld, slot_ptr(fx), fused_ld, st));
+    PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
+  }
+  if (a->logits)
+    PE_TRY(pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
+                         m->vocab, ws + Lp.gemm, Lp.gemm_bytes, st));
+#undef PE_TRY
+  return PE_OK;
+}
+
 extern "C" int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int64_t kv_len) {
   if (!m || M <= 0 || kv_len <= 0) return 0;
+  // a causal pass of more than one chunk may take the prefill path
+  const int64_t pre = prefill_path(m, M, PE_MASK_CAUSAL) ? make_prefill_layout(m, M, kv_len).total : 0;
   if (m->qkv_layout == PE_QKV_ROPE_PAIRED && M > kFusedChunk) M = kFusedChunk;
-  return make_layout(m, M, kv_len).total;
+  const int64_t fused = make_layout(m, M, kv_len).total;
+  return pre > fused ? pre : fused;
 }
 
 // The 16-bit pass: per layer
@@ -275,6 +467,11 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
   if (m->intermediate_padded % 32 || m->intermediate_padded < m->intermediate) return PE_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   const int64_t kv_len = a->prefix_len + M;
+  if (prefill_path(m, M, a->mask_mode)) {
+    const PrefillLayout Lp = make_prefill_layout(m, M, kv_len);
+    if (a->workspace_bytes < Lp.total) return PE_ERR_WORKSPACE;
+    return forward_prefill(m, a, Lp, st);
+  }
   const Layout Lo = make_layout(m, M, kv_len);
   if (m->qkv_layout == PE_QKV_ROPE_PAIRED) {
     // 16-bit hd-128 models only; a tree pass must fit one chunk (its nodes see

@@ -60,14 +60,14 @@ def test_f32abs_gemm_matches_dequant_then_linear(m, n, k):
     assert torch.all(err <= 2.0 ** -8 * ref32.abs() + 1e-4 * (1 + ref32.abs()) * (k / 1024)), err.max()
 
 
-@pytest.mark.parametrize("nested", [False, True])
-def test_llama7b_width_from_bnb_state_dict(nested):
+@pytest.mark.parametrize("nested,P", [(False, 48), (True, 48), (True, 300)])
+def test_llama7b_width_from_bnb_state_dict(nested, P):
     """A 2-layer 7B-width model saved as bitsandbytes Params4bit (fp32 absmax, or
     uint8 absmax with a nested state) runs the fp32-absmax kernels and matches the
     oracle on the weights the importer decodes."""
     wl = WORKLOADS["llama2-7b-nf4-T26-P2048"]
     shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
-    seed, P = 4, 48
+    seed = 4
     src = TargetModel.synthetic(shape, seed=seed, device=DEV, keep_logical=True, norm_noise=0.1)
     sd = bc.model_state_dict(shape, src.model.host_weights(), nested, seed)
     del src

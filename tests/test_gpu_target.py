@@ -208,6 +208,18 @@ def test_llama7b_nf4_width_two_layers(seed):
     print(f"seed {seed}: {v}, accepted {n}, max |dlogit| {err:.3g}")
 
 
+@pytest.mark.parametrize("P", [130, 300])
+def test_llama7b_nf4_width_prefill_longer_than_a_chunk(P):
+    """A causal prefill of more than 64 tokens: 130 runs as 64-row fused chunks,
+    300 (more than 256) takes the prefill path (each weight dequantised once, one
+    bf16 GEMM over all rows, attention over all rows at once). Its logits, the K/V
+    rows it appends and the tree pass on top match the oracle."""
+    wl = WORKLOADS["llama2-7b-nf4-T26-P2048"]
+    shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
+    v, n, err = _run_case(shape, 7, P, wl.depth, wl.widths, wl.top_k, plant=lambda s: 1 + s % wl.depth, tol=2e-2)
+    print(f"P={P}: {v}, accepted {n}, max |dlogit| {err:.3g}")
+
+
 def test_llama7b_nf4_width_long_random_prefix():
     wl = WORKLOADS["llama2-7b-nf4-T26-P2048"]
     shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
