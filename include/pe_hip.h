@@ -276,7 +276,13 @@ int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int64_t kv_len
 /* The masked verification forward TargetModel.forward_cached
  * (src/pe/target.py:203-224 -> HF LlamaForCausalLM / Qwen2ForCausalLM forward,
  * modeling_llama.py:347-490): embeddings, L decoder layers with in-place KV
- * append, final norm, lm_head over all M rows, fused features. */
+ * append, final norm, lm_head over all M rows, fused features.
+ * A causal pass of more than 256 rows on an NF4 model (a prefill) dequantises
+ * each linear once and multiplies it with rocBLAS (bf16, fp32 accumulation);
+ * rocBLAS gets its workspace from the pass workspace, and the library keeps one
+ * rocBLAS handle per device, made on the first such pass (the handle's own
+ * state is rocBLAS's). Set PE_PREFILL_GEMM=0 to run such passes in 64-row
+ * chunks instead. */
 int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* stream);
 
 #ifdef __cplusplus
