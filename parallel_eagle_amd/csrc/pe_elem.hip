@@ -161,12 +161,16 @@ template <> struct Raw4<PE_DTYPE_F32> {
   }
 };
 
-template <int DT, int CH, int SMAX>
+// EMB: the row is the embedding of token ids[m] (HF modeling_llama.py:381;
+// out-of-range ids flag PE_ERR_TOKEN and read row 0) and is stored to h; the
+// first layer's input norm then needs no separate embedding launch.
+template <int DT, int CH, int SMAX, bool EMB>
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
     const float* __restrict__ partial, int S, int M, typename Elem<DT>::T* __restrict__ h, int H,
     const typename Elem<DT>::T* __restrict__ w, float eps, typename Elem<DT>::T* __restrict__ xn,
     typename Elem<DT>::T* __restrict__ xt, typename Elem<DT>::T* __restrict__ cap_h, int64_t ld_cap_h,
-    typename Elem<DT>::T* __restrict__ cap_xn, int64_t ld_cap_xn) {
+    typename Elem<DT>::T* __restrict__ cap_xn, int64_t ld_cap_xn, const int64_t* __restrict__ ids,
+    const typename Elem<DT>::T* __restrict__ table, int64_t vocab, int32_t* __restrict__ status) {
   typedef Elem<DT> E;
   typedef typename E::T T;
   typedef Vec4<DT> V;
@@ -174,6 +178,13 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
   constexpr int PCH = (CH * SMAX <= 16) ? CH : 1;  // chunks whose partials are in flight together
   const int m = blockIdx.x;
   T* hr = h + (int64_t)m * H;
+  const T* src = hr;
+  if constexpr (EMB) {
+    const int64_t id = ids[m];
+    const bool ok = id >= 0 && id < vocab;
+    if (!ok && threadIdx.x == 0 && status) atomicOr(status, PE_ERR_TOKEN);
+    src = table + (ok ? id : 0) * H;
+  }
   const int nchunk = H >> 2;
   const int64_t sstride = (int64_t)M * H;
   // chunk k of this thread (clamped to the last chunk; a clamped chunk is
@@ -182,7 +193,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
   typename RW::R hraw[CH], wraw[CH];
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
-    hraw[k] = RW::load(hr + 4 * chunk(k));
+    hraw[k] = RW::load(src + 4 * chunk(k));
     wraw[k] = RW::load(w + 4 * chunk(k));
   }
   float v[CH][4];
@@ -216,7 +227,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
   for (int k = 0; k < CH; ++k) {
     const int c = threadIdx.x + k * kNormThreads;
     if (c >= nchunk) continue;
-    if (SMAX > 0) V::store(hr + 4 * c, v[k]);
+    if (SMAX > 0 || EMB) V::store(hr + 4 * c, v[k]);
     if (cap_h) V::store(cap_h + (int64_t)m * ld_cap_h + 4 * c, v[k]);
 #pragma unroll
     for (int e = 0; e < 4; ++e) ss = __fadd_rn(ss, __fmul_rn(v[k][e], v[k][e]));
@@ -331,13 +342,25 @@ template <typename T> struct NormArgs {
   int64_t ld_cap_h;
   T* cap_xn;
   int64_t ld_cap_xn;
+  const int64_t* ids;
+  const T* table;
+  int64_t vocab;
+  int32_t* status;
 };
 
 template <int DT, int CH, int SM>
 void launch_norm_sm(const NormArgs<typename Elem<DT>::T>& a, hipStream_t st) {
-  residual_rmsnorm_kernel<DT, CH, SM><<<a.M, kNormThreads, 0, st>>>(a.partial, a.S, a.M, a.h, a.H, a.w, a.eps, a.xn,
-                                                                    a.xt, a.cap_h, a.ld_cap_h, a.cap_xn,
-                                                                    a.ld_cap_xn);
+  if constexpr (SM == 0) {
+    if (a.table) {
+      residual_rmsnorm_kernel<DT, CH, 0, true><<<a.M, kNormThreads, 0, st>>>(
+          a.partial, a.S, a.M, a.h, a.H, a.w, a.eps, a.xn, a.xt, a.cap_h, a.ld_cap_h, a.cap_xn, a.ld_cap_xn, a.ids,
+          a.table, a.vocab, a.status);
+      return;
+    }
+  }
+  residual_rmsnorm_kernel<DT, CH, SM, false><<<a.M, kNormThreads, 0, st>>>(
+      a.partial, a.S, a.M, a.h, a.H, a.w, a.eps, a.xn, a.xt, a.cap_h, a.ld_cap_h, a.cap_xn, a.ld_cap_xn, nullptr,
+      nullptr, 0, nullptr);
 }
 
 template <int DT, int CH>
@@ -362,11 +385,31 @@ int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, in
   PE_DISPATCH_DT(dtype, {
     typedef typename Elem<DT>::T T;
     const NormArgs<T> na{partial, S, M, (T*)h, H, (const T*)w, eps, (T*)xn, (T*)xn_tiled, (T*)cap_h, ld_cap_h,
-                         (T*)cap_xn, ld_cap_xn};
+                         (T*)cap_xn, ld_cap_xn, nullptr, nullptr, 0, nullptr};
     if (ch == 1)
       launch_norm<DT, 1>(smax, na, st);
     else
       launch_norm<DT, 2>(smax, na, st);
+  });
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+int pe_internal_embed_rmsnorm(const int64_t* ids, int M, const void* table, int64_t V, void* h, int H, const void* w,
+                              float eps, int dtype, void* xn, void* xn_tiled, void* cap_h, int64_t ld_cap_h,
+                              void* cap_xn, int64_t ld_cap_xn, int32_t* status, hipStream_t st) {
+  if (!ids || !table || !h || !w || !xn || M <= 0 || H <= 0 || V <= 0) return PE_ERR_ARG;
+  if (H % 4 || H > 4 * kNormThreads * kNormChunks) return PE_ERR_ARG;
+  if (xn_tiled && (H % 128 || M > 64 || dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
+  const int ch = (H >> 2) > kNormThreads ? 2 : 1;
+  PE_DISPATCH_DT(dtype, {
+    typedef typename Elem<DT>::T T;
+    const NormArgs<T> na{nullptr, 0, M, (T*)h, H, (const T*)w, eps, (T*)xn, (T*)xn_tiled, (T*)cap_h, ld_cap_h,
+                         (T*)cap_xn, ld_cap_xn, ids, (const T*)table, V, status};
+    if (ch == 1)
+      launch_norm_sm<DT, 1, 0>(na, st);
+    else
+      launch_norm_sm<DT, 2, 0>(na, st);
   });
   PE_CHECK_LAUNCH();
   return PE_OK;

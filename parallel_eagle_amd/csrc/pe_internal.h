@@ -56,6 +56,13 @@ PE_INTERNAL int pe_internal_swiglu_partials(const float* partial, int S, int M, 
 PE_INTERNAL int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, int H, const void* w,
                                              float eps, int dtype, void* xn, void* xn_tiled, void* cap_h,
                                              int64_t ld_cap_h, void* cap_xn, int64_t ld_cap_xn, hipStream_t st);
+// pe_elem.hip: the first layer's input norm fused with the embedding gather:
+// h[m] = embed[ids[m]] (out-of-range ids flag PE_ERR_TOKEN in *status and read
+// row 0), then xn / xn_tiled / captures as pe_internal_residual_rmsnorm.
+PE_INTERNAL int pe_internal_embed_rmsnorm(const int64_t* ids, int M, const void* table, int64_t V, void* h, int H,
+                                          const void* w, float eps, int dtype, void* xn, void* xn_tiled, void* cap_h,
+                                          int64_t ld_cap_h, void* cap_xn, int64_t ld_cap_xn, int32_t* status,
+                                          hipStream_t st);
 
 // The pass workspace's first 32 KiB hold arrival counters: GEMM column
 // groups use ints [0, kGemmCounterInts) and return them to zero; attention

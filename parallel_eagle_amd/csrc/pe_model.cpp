@@ -287,11 +287,10 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
     return blas_gemm(st, M, N, K, x, wdeq, y, bws, Lp.blas_bytes);
   };
 
-  PE_TRY(pe_embed(a->input_ids, M, m->embed, m->vocab, H, m->dtype, h, H, a->status, st));
   {
     const int f0 = slot_of(0);
-    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->attn_norm[0], m->rms_eps, m->dtype, xn, nullptr,
-                                        slot_ptr(f0), fused_ld, nullptr, 0, st));
+    PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, m->vocab, h, H, m->attn_norm[0], m->rms_eps,
+                                     m->dtype, xn, nullptr, slot_ptr(f0), fused_ld, nullptr, 0, a->status, st));
     PE_TRY(copy_repeats(0, f0));
   }
   for (int l = 0; l < L; ++l) {
@@ -390,11 +389,10 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     return PE_OK;
   };
 
-  PE_TRY(pe_embed(a->input_ids, M, m->embed, m->vocab, H, m->dtype, h, H, a->status, st));
   {
     const int f0 = slot_of(0);
-    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->attn_norm[0], m->rms_eps, m->dtype, xn, xn_t,
-                                        slot_ptr(f0), fused_ld, nullptr, 0, st));
+    PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, m->vocab, h, H, m->attn_norm[0], m->rms_eps,
+                                     m->dtype, xn, xn_t, slot_ptr(f0), fused_ld, nullptr, 0, a->status, st));
     PE_TRY(copy_repeats(0, f0));
   }
   // The tiled (NF4) pass: q/k/v and gate/up run unsplit with their RoPE + KV
