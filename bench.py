@@ -61,6 +61,9 @@ def parse_args(argv=None):
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-layers", type=int, default=4, help="layers of the CPU-path sample")
     p.add_argument("--cpu-runs", type=int, default=12)
+    p.add_argument("--prefill", action="store_true",
+                   help="instead of the verification pass: time a causal prefill of the workload's prefix length "
+                        "from an empty cache and a one-token continuation (eager forward_cached calls)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a 256 MiB device copy three times (the known-size kernel the HBM counters "
                         "FETCH_SIZE / WRITE_SIZE are calibrated on)")
@@ -309,6 +312,43 @@ def cpu_baseline(wl, seed, n_layers: int, runs: int):
 
 
 # ---------------------------------------------------------------- main
+def prefill_line(wl, seed: int, reps: int = 3) -> dict:
+    """Latency of the causal prefill of the workload's prefix (P tokens from an empty
+    cache, the prompt step before the first verification) and of a one-token
+    continuation (the miss path), eager forward_cached calls after a warm-up call
+    each (the first prefill of a process loads the GEMM library's kernels)."""
+    import torch
+
+    from parallel_eagle_amd import synth
+    from parallel_eagle_amd.target import TargetModel
+
+    shape, P = wl.model, wl.prefix_len
+    tm = TargetModel.synthetic(shape, seed=seed, device="cuda:0", cache_capacity=P + 64)
+    ids = torch.tensor([synth.uniform_int(seed, synth.STREAM_PROMPT, P, shape.vocab).tolist()])
+    pos = torch.arange(P).unsqueeze(0)
+    pre, one = [], []
+    for r in range(reps + 1):
+        cache = tm.make_cache(P + 64)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tm.forward_cached(ids, cache, pos)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        tm.forward_cached(torch.tensor([[5]]), cache, torch.tensor([[P]]))
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        if r:
+            pre.append(t1 - t0)
+            one.append(t2 - t1)
+    ms = statistics.median(pre) * 1e3
+    return {"metric": "prefill latency (causal, from an empty cache) and one-token continuation latency",
+            "value": round(P / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": reps,
+            "ms_prefill": round(ms, 3), "ms_one_token": round(statistics.median(one) * 1e3, 3),
+            "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": wl.name, "prefill_tokens": P, "layers": shape.num_layers,
+                       "weights": shape.weight_format, "eager": True}}
+
+
 def main(argv=None) -> int:
     a = parse_args(argv)
     if a.gpus != 1:
@@ -331,6 +371,9 @@ def main(argv=None) -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
     wl = WORKLOADS[a.workload]
+    if a.prefill:
+        print(json.dumps(prefill_line(wl, a.seed)))
+        return 0
     if wl.batch != 1:
         print(f"workload {wl.name} is batched; the bench measures the batch-1 pass", file=sys.stderr)
         return 2
