@@ -37,6 +37,7 @@ extern "C" {
 #define PE_ERR_TOKEN 32    /* token id outside the vocabulary */
 #define PE_ERR_INDEX 64    /* keep index not strictly increasing / out of range */
 #define PE_ERR_WORKSPACE 128 /* workspace too small */
+#define PE_ERR_VALUE 256   /* NaN in a logit row, or a row with no finite value */
 
 /* element types */
 #define PE_DTYPE_F32 0
@@ -222,6 +223,29 @@ int pe_kv_compact(void* k_cache, void* v_cache, int L, int nkv, int64_t cap, int
  * sequence axis, gather_cache with an arbitrary keep index. */
 int pe_kv_gather(void* k_cache, void* v_cache, int L, int nkv, int64_t cap, int hd, int dtype,
                  const int64_t* keep, int64_t n_keep, int32_t* status, void* stream);
+
+/* ------------------------------------------------------------ tree proposal */
+#define PE_PROPOSE_MAX_DEPTH 16
+#define PE_PROPOSE_MAX_WIDTH 64
+/* Beam tree proposal of propose_tree (src/pe/decode/tree.py:34-55) on k rows
+ * of draft logits already on the device (row d predicts depth d; a caller
+ * with `pending` confirmed depths passes the row after them). For depth d:
+ * log_softmax in fp32; the top c_d = min(top_k, widths[d]) tokens (value
+ * descending, the lowest index first among equal values); every surviving
+ * parent extended by them; the candidates stably ordered by cumulative
+ * log-probability (float64 sums, as the reference's Python floats) and the
+ * best widths[d] kept (fewer when the parents times c_d are fewer).
+ * The reference's rule is widths[d] = max(1, min(top_k, max_nodes / k)).
+ * widths: host array of k values in [1, PE_PROPOSE_MAX_WIDTH]; c_d <= V.
+ * node_tokens (int64) and parents (int32, -1 = hangs off the prefix) receive
+ * the nodes in topological order; *n_nodes (host) their count, known on the
+ * host before the kernels run. scratch: k * PE_PROPOSE_SCRATCH_PER_DEPTH
+ * bytes of device memory. status: PE_ERR_VALUE when a row holds a NaN or no
+ * finite value (the reference's order is undefined there). */
+#define PE_PROPOSE_SCRATCH_PER_DEPTH 512
+int pe_propose_tree(const void* logits, int64_t ld, int k, int64_t V, int dtype, const int32_t* widths, int top_k,
+                    int64_t* node_tokens, int32_t* parents, int32_t* n_nodes, void* scratch, int32_t* status,
+                    void* stream);
 
 /* ---------------------------------------------------------------- whole pass */
 typedef struct pe_model_desc {

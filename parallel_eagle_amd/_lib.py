@@ -24,6 +24,7 @@ PE_ERR_MASK = 16
 PE_ERR_TOKEN = 32
 PE_ERR_INDEX = 64
 PE_ERR_WORKSPACE = 128
+PE_ERR_VALUE = 256
 
 PE_DTYPE_F32, PE_DTYPE_BF16, PE_DTYPE_F16 = 0, 1, 2
 PE_WFMT_DENSE, PE_WFMT_NF4, PE_WFMT_NF4_F32ABS = 0, 1, 2
@@ -31,6 +32,7 @@ PE_EPI_STORE, PE_EPI_RESIDUAL, PE_EPI_SWIGLU = 0, 1, 2
 PE_MASK_TREE, PE_MASK_CAUSAL = 0, 1
 PE_QKV_PLAIN, PE_QKV_ROPE_PAIRED = 0, 1
 PE_TREE_MAX_WORDS = 4
+PE_PROPOSE_MAX_DEPTH, PE_PROPOSE_MAX_WIDTH, PE_PROPOSE_SCRATCH_PER_DEPTH = 16, 64, 512
 
 _ERR_NAMES = {
     PE_ERR_ARG: "invalid argument",
@@ -41,6 +43,7 @@ _ERR_NAMES = {
     PE_ERR_TOKEN: "token id outside the vocabulary",
     PE_ERR_INDEX: "keep index not strictly increasing or out of range",
     PE_ERR_WORKSPACE: "workspace too small",
+    PE_ERR_VALUE: "NaN in a logit row, or a row with no finite value",
 }
 
 
@@ -120,6 +123,8 @@ SIGNATURES: dict[str, tuple] = {
                                     C.c_int, f32, C.c_int, vp, i64, vp, i64, vp]),
     "pe_argmax_rows": (C.c_int, [vp, i64, C.c_int, i64, C.c_int, vp, vp]),
     "pe_accept_tree": (C.c_int, [vp, vp, i64, C.c_int, i64, C.c_int, vp, vp, vp, vp, vp]),
+    "pe_propose_tree": (C.c_int, [vp, i64, C.c_int, i64, C.c_int, C.POINTER(C.c_int32), C.c_int, vp, vp,
+                                  C.POINTER(C.c_int32), vp, vp, vp]),
     "pe_kv_compact": (C.c_int, [vp, vp, C.c_int, C.c_int, i64, C.c_int, C.c_int, i64, vp, vp]),
     "pe_kv_gather": (C.c_int, [vp, vp, C.c_int, C.c_int, i64, C.c_int, C.c_int, vp, i64, vp, vp]),
     "pe_forward_workspace_bytes": (i64, [C.POINTER(ModelDesc), C.c_int, i64]),

@@ -302,6 +302,179 @@ __global__ void kv_gather_kernel(uint8_t* __restrict__ kc, uint8_t* __restrict__
   }
 }
 
+// Beam tree proposal (propose_tree, src/pe/decode/tree.py:34-55) in two
+// launches. draft_topk_kernel: one block per depth row computes the row's
+// log-sum-exp in fp32 and selects the row's top c_d tokens one at a time, each
+// round the best element after the previous one in (value descending, index
+// ascending) order; the winners' log-probabilities (x - max) - log(sum) go to
+// scratch. beam_kernel: one block walks the depths; candidate (parent p, rank
+// j in the row) scores cum[p] + lp[j] in float64, and its position in the
+// stable descending order of the candidate list (parent-major, as the
+// reference builds it) is counted directly: j for its own parent, plus, for
+// every other parent, the candidates that score higher (or equal, for parents
+// before it), found by binary search since each parent's scores do not
+// increase with j.
+constexpr int kBeamThreads = 256;
+
+struct BeamShape {
+  int k;
+  int width[PE_PROPOSE_MAX_DEPTH];  // nodes kept at depth d
+  int cand[PE_PROPOSE_MAX_DEPTH];   // candidates per parent: min(top_k, width[d])
+};
+
+// (k2, i2) before (k1, i1) in the order key descending, index ascending; i < 0 is "none"
+__device__ __forceinline__ bool key_before(uint32_t k2, int i2, uint32_t k1, int i1) {
+  if (i2 < 0) return false;
+  if (i1 < 0) return true;
+  return k2 > k1 || (k2 == k1 && i2 < i1);
+}
+
+// block-wide (key, index) reduction over kArgThreads threads; every thread gets the result
+__device__ void block_best(uint32_t& bk, int& bi, uint32_t* wk, int* wi) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t k2 = __shfl_xor(bk, o, 64);
+    const int i2 = __shfl_xor(bi, o, 64);
+    if (key_before(k2, i2, bk, bi)) {
+      bk = k2;
+      bi = i2;
+    }
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    wk[threadIdx.x >> 6] = bk;
+    wi[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  bk = wk[0];
+  bi = wi[0];
+  for (int w = 1; w < kArgThreads / 64; ++w)
+    if (key_before(wk[w], wi[w], bk, bi)) {
+      bk = wk[w];
+      bi = wi[w];
+    }
+}
+
+__device__ float block_sum(float v, float* ws) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int w = 0; w < kArgThreads / 64; ++w) s += ws[w];
+  return s;
+}
+
+template <int DT>
+__global__ __launch_bounds__(kArgThreads) void draft_topk_kernel(const typename Elem<DT>::T* __restrict__ logits,
+                                                                 int64_t ld, int64_t V, BeamShape bs,
+                                                                 float* __restrict__ lp_out,
+                                                                 int32_t* __restrict__ tok_out, int32_t* status) {
+  const int d = blockIdx.x;
+  const typename Elem<DT>::T* x = logits + (int64_t)d * ld;
+  __shared__ uint32_t wk[kArgThreads / 64];
+  __shared__ int wi[kArgThreads / 64];
+  __shared__ float ws[kArgThreads / 64];
+  // the row maximum (the first selection round) and NaN detection
+  uint32_t bk = 0;
+  int bi = -1;
+  int nan = 0;
+  for (int64_t i = threadIdx.x; i < V; i += kArgThreads) {
+    const float v = Elem<DT>::load(x, i);
+    nan |= v != v;
+    const uint32_t key = arg_key(v);
+    if (key_before(key, (int)i, bk, bi)) {
+      bk = key;
+      bi = (int)i;
+    }
+  }
+  nan = __syncthreads_or(nan);
+  block_best(bk, bi, wk, wi);
+  const float mx = Elem<DT>::load(x, bi);
+  if (nan || !(mx > -INFINITY) || mx == INFINITY) {
+    if (threadIdx.x == 0 && status) atomicOr(status, PE_ERR_VALUE);
+    return;
+  }
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < V; i += kArgThreads) s += expf(Elem<DT>::load(x, i) - mx);
+  const float logsum = logf(block_sum(s, ws));
+  const int c = bs.cand[d];
+  for (int j = 0;; ++j) {
+    if (threadIdx.x == 0) {
+      lp_out[d * PE_PROPOSE_MAX_WIDTH + j] = (Elem<DT>::load(x, bi) - mx) - logsum;
+      tok_out[d * PE_PROPOSE_MAX_WIDTH + j] = bi;
+    }
+    if (j + 1 >= c) break;
+    // next round: the best element after (bk, bi) in the order
+    const uint32_t pk = bk;
+    const int pi = bi;
+    bk = 0;
+    bi = -1;
+    for (int64_t i = threadIdx.x; i < V; i += kArgThreads) {
+      const uint32_t key = arg_key(Elem<DT>::load(x, i));
+      if (key_before(pk, pi, key, (int)i) && key_before(key, (int)i, bk, bi)) {
+        bk = key;
+        bi = (int)i;
+      }
+    }
+    block_best(bk, bi, wk, wi);
+  }
+}
+
+__global__ __launch_bounds__(kBeamThreads) void beam_kernel(BeamShape bs, const float* __restrict__ lp,
+                                                            const int32_t* __restrict__ tok,
+                                                            int64_t* __restrict__ node_tokens,
+                                                            int32_t* __restrict__ parents, const int32_t* status) {
+  if (status && *status & PE_ERR_VALUE) return;
+  __shared__ double cum[PE_PROPOSE_MAX_WIDTH], ncum[PE_PROPOSE_MAX_WIDTH], row[PE_PROPOSE_MAX_WIDTH];
+  __shared__ int node[PE_PROPOSE_MAX_WIDTH];
+  int nb = 1, base = 0;
+  if (threadIdx.x == 0) {
+    cum[0] = 0.0;
+    node[0] = -1;
+  }
+  for (int d = 0; d < bs.k; ++d) {
+    const int c = bs.cand[d];
+    const int n = nb * c;
+    const int kept = min(bs.width[d], n);
+    if (threadIdx.x < c) row[threadIdx.x] = (double)lp[d * PE_PROPOSE_MAX_WIDTH + threadIdx.x];
+    __syncthreads();
+    for (int q = threadIdx.x; q < n; q += kBeamThreads) {
+      const int p = q / c, j = q - p * c;
+      const double sc = cum[p] + row[j];
+      int r = j;
+      for (int p2 = 0; p2 < nb && r < kept; ++p2) {
+        if (p2 == p) continue;
+        // count j2 with cum[p2] + row[j2] > sc (>= sc for parents listed before p)
+        int lo = 0, hi = c;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          const double s2 = cum[p2] + row[mid];
+          if (p2 < p ? s2 >= sc : s2 > sc)
+            lo = mid + 1;
+          else
+            hi = mid;
+        }
+        r += lo;
+      }
+      if (r < kept) {
+        ncum[r] = sc;
+        node_tokens[base + r] = tok[d * PE_PROPOSE_MAX_WIDTH + j];
+        parents[base + r] = node[p];
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < kept) {
+      cum[threadIdx.x] = ncum[threadIdx.x];
+      node[threadIdx.x] = base + threadIdx.x;
+    }
+    __syncthreads();
+    base += kept;
+    nb = kept;
+  }
+}
+
 int esize(int dtype) { return dtype == PE_DTYPE_F32 ? 4 : 2; }
 
 }  // namespace
@@ -390,6 +563,47 @@ extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, i
     default:
       return PE_ERR_ARG;
   }
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+extern "C" int pe_propose_tree(const void* logits, int64_t ld, int k, int64_t V, int dtype, const int32_t* widths,
+                               int top_k, int64_t* node_tokens, int32_t* parents, int32_t* n_nodes, void* scratch,
+                               int32_t* status, void* stream) {
+  if (!logits || !widths || !node_tokens || !parents || !n_nodes || !scratch || k < 1 || k > PE_PROPOSE_MAX_DEPTH ||
+      V < 1 || V > INT32_MAX || ld < V || top_k < 1)
+    return PE_ERR_ARG;
+  BeamShape bs{};
+  bs.k = k;
+  int nb = 1, total = 0;
+  for (int d = 0; d < k; ++d) {
+    const int w = widths[d];
+    if (w < 1 || w > PE_PROPOSE_MAX_WIDTH) return PE_ERR_ARG;
+    bs.width[d] = w;
+    bs.cand[d] = min(top_k, w);
+    if (bs.cand[d] > V) return PE_ERR_ARG;
+    nb = min(w, nb * bs.cand[d]);
+    total += nb;
+  }
+  *n_nodes = total;
+  float* lp = (float*)scratch;
+  int32_t* tok = (int32_t*)((char*)scratch + (size_t)k * PE_PROPOSE_MAX_WIDTH * sizeof(float));
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case PE_DTYPE_F32:
+      draft_topk_kernel<PE_DTYPE_F32><<<k, kArgThreads, 0, st>>>((const float*)logits, ld, V, bs, lp, tok, status);
+      break;
+    case PE_DTYPE_BF16:
+      draft_topk_kernel<PE_DTYPE_BF16><<<k, kArgThreads, 0, st>>>((const uint16_t*)logits, ld, V, bs, lp, tok, status);
+      break;
+    case PE_DTYPE_F16:
+      draft_topk_kernel<PE_DTYPE_F16><<<k, kArgThreads, 0, st>>>((const uint16_t*)logits, ld, V, bs, lp, tok, status);
+      break;
+    default:
+      return PE_ERR_ARG;
+  }
+  PE_CHECK_LAUNCH();
+  beam_kernel<<<1, kBeamThreads, 0, st>>>(bs, lp, tok, node_tokens, parents, status);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }

@@ -315,6 +315,36 @@ def accept_tree(root_logit: torch.Tensor, node_logits: torch.Tensor, node_tokens
     return out
 
 
+def propose_tree(logits: torch.Tensor, widths, top_k: int, status: torch.Tensor | None = None,
+                 scratch: torch.Tensor | None = None):
+    """Beam tree proposal over k draft-logit rows [k][V] on the device.
+
+    Returns (node_tokens int64 [n], parents int32 [n], status int32 [1]) as device
+    tensors; n is known on the host, so nothing here waits for the GPU.
+    PE_ERR_VALUE in ``status`` marks a row with a NaN or no finite value.
+    ``scratch`` (k * PE_PROPOSE_SCRATCH_PER_DEPTH bytes) receives, per depth, 64
+    fp32 log-probabilities and then (after all k of those) 64 int32 tokens."""
+    _req(logits.dim() == 2 and logits.stride(1) == 1, "logits must be [k][V] with contiguous rows")
+    k, v = logits.shape
+    widths = [int(w) for w in widths]
+    _req(len(widths) == k, "one width per depth row")
+    dev = logits.device
+    cap = k * _lib.PE_PROPOSE_MAX_WIDTH
+    tokens = torch.empty(cap, dtype=torch.int64, device=dev)
+    parents = torch.empty(cap, dtype=torch.int32, device=dev)
+    if scratch is None:
+        scratch = torch.empty(k * _lib.PE_PROPOSE_SCRATCH_PER_DEPTH, dtype=torch.uint8, device=dev)
+    _req(scratch.numel() * scratch.element_size() >= k * _lib.PE_PROPOSE_SCRATCH_PER_DEPTH and scratch.is_contiguous(),
+         "scratch must hold k * PE_PROPOSE_SCRATCH_PER_DEPTH bytes")
+    if status is None:
+        status = torch.zeros(1, dtype=torch.int32, device=dev)
+    w = (C.c_int32 * k)(*widths)
+    n = C.c_int32(0)
+    check(lib().pe_propose_tree(ptr(logits), logits.stride(0), k, v, dcode(logits.dtype), w, int(top_k), ptr(tokens),
+                                ptr(parents), C.byref(n), ptr(scratch), ptr(status), stream_ptr()), "pe_propose_tree")
+    return tokens[: n.value], parents[: n.value], status
+
+
 def kv_compact(k_cache, v_cache, prefix_len: int, accept_out: torch.Tensor) -> None:
     """Caches [L][nkv][cap][hd]."""
     L, nkv, cap, hd = k_cache.shape

@@ -239,3 +239,38 @@ def test_synth_generator_known_values():
     x = synth.normal(1, 1, 200_000)
     assert abs(float(x.mean())) < 0.01 and abs(float(x.std()) - 1.0) < 0.01
     assert float(np.abs(x).max()) <= 2 * 1.7320508075688772 + 1e-6
+
+
+@pytest.mark.parametrize("v,widths", [(6, (3, 3, 3)), (5, (4, 2, 2, 1)), (9, (1, 1, 1)), (4, (2, 2))])
+def test_beam_is_the_global_best_sequences(v, widths):
+    """Every depth's log-probabilities are the same for every parent, so with
+    non-increasing widths the beam at depth d holds the best widths[d] token
+    sequences of length d + 1 over all v^(d+1), best first (brute force)."""
+    import itertools
+    k = len(widths)
+    lg = torch.from_numpy(synth.normal(v * 31 + k, synth.STREAM_DRAFT, k * v, 2.0).reshape(k, v))
+    lp = torch.log_softmax(lg.float(), dim=-1).numpy().astype(np.float64)
+    tokens, parents = otree.propose_tree_beam(lg, list(widths), max(widths))
+    assert om.is_topological(parents)
+    seqs = []
+    for t in range(len(tokens)):
+        s, a = [], t
+        while a != -1:
+            s.append(tokens[a])
+            a = parents[a]
+        seqs.append(tuple(reversed(s)))
+    base = 0
+    for d, w in enumerate(widths):
+        every = sorted(itertools.product(range(v), repeat=d + 1), key=lambda q: -sum(lp[e, q[e]] for e in range(d + 1)))
+        assert seqs[base: base + w] == every[:w]
+        base += w
+    assert base == len(tokens)
+
+
+def test_beam_ties_take_the_lowest_token_then_the_earlier_parent():
+    # depth 0: tokens 1 and 2 tie, token 1 first; depth 1: both parents extended by
+    # the same row, equal sums keep parent-major order (the reference's stable sort)
+    lg = torch.tensor([[0.0, 2.0, 2.0, -1.0], [5.0, 5.0, 0.0, 0.0]])
+    tokens, parents = otree.propose_tree_beam(lg, [2, 3], 2)
+    assert tokens == [1, 2, 0, 1, 0]
+    assert parents == [-1, -1, 0, 0, 1]
