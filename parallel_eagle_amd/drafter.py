@@ -1,0 +1,118 @@
+"""The drafter's forward on the device, with the API of ParallelDrafter.draft_logits
+(src/pe/drafter.py:195-236).
+
+The drafter's decoder layers are Llama layers (src/pe/nn.py:103-124), so its
+forward is the target's pass (``pe_forward``) over a second layer stack: dense
+layers in the target's dtype, the target's final norm and lm_head shared (the
+same device tensors, as the reference shares the modules).
+
+The reference's draft mask (real rows causal; the k - 1 mask slots see every
+real row and the slots up to their own) and its positions (0..p-1, then
+(p - 1) + d) are those of one causal pass over the p + k - 1 rows from an empty
+cache, which is how it runs here. The rows are the drafter's inputs, not token
+embeddings: the layer stack's embedding table is a buffer of input rows that
+the pass gathers with ids 0..m-1.
+
+Inputs (drafter.py:126-138): ``in_proj([embed(token); feat_proj(feat_norm(feature
+blocks))])`` for real positions, ``in_proj([mask_emb; h_shared])`` for mask
+slots (computed once). Norms here round like the target's RMSNorm (normalised
+row rounded, then the weight multiply); the reference's drafter norm multiplies
+in fp32 and rounds once: a difference within the dtype's rounding.
+"""
+
+from __future__ import annotations
+
+from dataclasses import replace
+
+import torch
+
+from . import _lib, ops
+from .model import DeviceModel
+from .target import TargetModel, TreeKVCache
+
+
+class DeviceDrafter:
+    """``target``: the TargetModel whose embed, final norm and lm_head the drafter
+    shares. ``weights``: {"feat_norm" [H], "feat_proj" [H][F], "in_proj" [H][2H],
+    "mask_emb" [H], "h_shared" [H], "layers": [{"attn_norm", "mlp_norm", "q", "k",
+    "v", "o", "gate", "up", "down"}]} (host or device tensors, logical [N][K]).
+    ``capacity``: the most rows (context + k - 1) one call may run."""
+
+    def __init__(self, target: TargetModel, weights: dict, max_depth: int, capacity: int = 4096):
+        tm = target.model
+        s = tm.shape
+        dev, dt = tm.device, tm.dtype
+        self.target = target
+        self.max_depth = max_depth
+        self.hidden = s.hidden
+        self.eps = s.rms_eps
+        self.dtype = dt
+        self.device = dev
+        n_layers = len(weights["layers"])
+        self.shape = replace(s, name=f"{s.name}-drafter", num_layers=n_layers, weight_format="dense", qkv_bias=False,
+                             feature_layers=(n_layers,))
+        if capacity > s.vocab:
+            raise ValueError("drafter rows are gathered by ids below the vocabulary size: capacity <= vocab")
+        self.capacity = capacity
+
+        def up(x):
+            return torch.as_tensor(x).to(device=dev, dtype=dt).contiguous()
+
+        def tile(x):
+            x = up(x)
+            return ops.dense_repack(x) if dt != torch.float32 else x
+
+        self.feat_norm = up(weights["feat_norm"])
+        self.feat_dim = int(weights["feat_proj"].shape[1])
+        if self.feat_dim % s.hidden:
+            raise ValueError("feat_proj's input width must be a multiple of hidden")
+        self.feat_proj = tile(weights["feat_proj"])
+        self.in_proj = tile(weights["in_proj"])
+        mask_in = torch.cat([up(weights["mask_emb"]), up(weights["h_shared"])]).view(1, -1)
+        self.mask_vec = ops.linear(mask_in, s.hidden, dense=self.in_proj).view(-1)
+
+        core = DeviceModel(self.shape, dev)
+        core.embed = torch.zeros((capacity, s.hidden), dtype=dt, device=dev)  # the call's input rows
+        core.final_norm = tm.final_norm
+        core.lm_head, core.lm_head_logical = tm.lm_head, tm.lm_head_logical
+        core.logical = None
+        for lw in weights["layers"]:
+            core._add_layer({k: up(v) for k, v in lw.items()}, False)
+        core._finish()
+        self.core = core
+        self.runner = TargetModel(core, cache_capacity=capacity)
+        self.cache = TreeKVCache(self.shape, dt, dev, capacity)
+        self.rows = torch.arange(capacity, dtype=torch.int64, device=dev)
+
+    def real_input(self, token_ids: torch.Tensor, features: torch.Tensor) -> torch.Tensor:
+        """in_proj([embed(token); feat_proj(feat_norm(features))]) (drafter.py:126-133)."""
+        H = self.hidden
+        ids = torch.as_tensor(token_ids, device=self.device).reshape(-1).to(torch.int64).contiguous()
+        p = ids.numel()
+        emb = ops.embed(ids, self.target.model.embed, self.runner.status)
+        f = features.to(device=self.device, dtype=self.dtype).reshape(p * (self.feat_dim // H), H).contiguous()
+        f = ops.rmsnorm(f, self.feat_norm, self.eps).view(p, self.feat_dim)
+        feat = ops.linear(f, H, dense=self.feat_proj)
+        return ops.linear(torch.cat([emb, feat], dim=-1).contiguous(), H, dense=self.in_proj)
+
+    @torch.no_grad()
+    def draft_logits(self, context_ids: torch.Tensor, context_feats: torch.Tensor, k: int) -> torch.Tensor:
+        """Logits (k, V) for the k tokens after ``context_ids``: row 0 from the last
+        real slot, row d from mask slot d."""
+        ids = torch.as_tensor(context_ids, device=self.device).reshape(-1)
+        p = ids.numel()
+        m = p + k - 1
+        if p < 1 or k < 1:
+            raise ValueError("draft_logits needs a context and k >= 1")
+        if m > self.capacity:
+            raise ValueError(f"{m} drafter rows exceed the capacity {self.capacity}")
+        x = self.core.embed
+        x[:p].copy_(self.real_input(ids, context_feats))
+        if k > 1:
+            x[p:m].copy_(self.mask_vec.expand(k - 1, -1))
+        rows = self.rows[:m]
+        self.cache.seq_len = 0
+        logits = torch.empty((m, self.shape.vocab), dtype=self.dtype, device=self.device)
+        self.runner.run_pass(rows, rows, self.cache, _lib.PE_MASK_CAUSAL, None, logits, None)
+        ops.read_status(self.runner.status, "draft_logits")
+        return logits[p - 1:]

@@ -1,0 +1,87 @@
+"""The drafter's forward on the device (DeviceDrafter.draft_logits) against the
+oracle's restatement of ParallelDrafter.draft_logits (src/pe/drafter.py:195-236),
+at the 7B target's width, with the target's embed, final norm and lm_head shared."""
+import pytest
+import torch
+
+from oracle import drafter as od
+from parallel_eagle_amd import tree as ptree
+from parallel_eagle_amd.config import LLAMA2_7B_NF4
+from parallel_eagle_amd.drafter import DeviceDrafter
+from parallel_eagle_amd.target import TargetModel
+from tests.test_oracle_pins import _drafter_weights
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def target():
+    shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
+    tm = TargetModel.synthetic(shape, seed=3, device=DEV, keep_logical=True, norm_noise=0.1)
+    hw = tm.model.host_weights()
+    shared = {"embed": hw["embed"], "final_norm": hw["final_norm"], "lm_head": hw["lm_head"]}
+    return tm, shared
+
+
+@pytest.mark.parametrize("n_layers,p,k", [(1, 40, 5), (2, 300, 6), (1, 1, 1)])
+def test_draft_logits_match_oracle(target, n_layers, p, k):
+    tm, shared = target
+    shape = tm.shape
+    # weights at the target's init scale: larger ones make attention so sharp that
+    # bf16 rounding alone (the oracle's too) moves logits by more than the tolerance
+    w, _ = _drafter_weights(shape, n_layers, 3, torch.bfloat16, seed=p + n_layers, std=shape.init_std)
+    w["feat_norm"] = w["feat_norm"].float().clamp(min=0.5).to(torch.bfloat16)
+    gen = torch.Generator().manual_seed(p)
+    ids = torch.randint(0, shape.vocab, (p,), generator=gen)
+    feats = (torch.randn(p, 3 * shape.hidden, generator=gen) * 4).to(torch.bfloat16)
+    dr = DeviceDrafter(tm, w, max_depth=k, capacity=512)
+    got = dr.draft_logits(ids.to(DEV), feats.to(DEV), k).cpu()
+    assert got.shape == (k, shape.vocab)
+    want = od.OracleDrafter(shape, w, shared, torch.bfloat16).draft_logits(ids, feats, k)
+    f32 = lambda d: {kk: (vv.float() if torch.is_tensor(vv) else [{a: b.float() for a, b in x.items()} for x in vv])
+                     for kk, vv in d.items()}
+    ref32 = od.OracleDrafter(shape, f32(w), f32(shared), torch.float32).draft_logits(ids, feats.float(), k)
+    # Tolerance: both bf16 evaluations are measured against the fp32 evaluation
+    # of the same drafter; the device must be at least as close to it as the
+    # reference's own bf16 arithmetic (the oracle): the fraction of logits within
+    # rtol = atol = 2e-2 no lower (0.02 slack) and the relative L2 error no higher
+    # (10% slack). A single-layer drafter on random weights is less well
+    # conditioned than the target, so neither bf16 evaluation keeps 95% of its
+    # logits within 2e-2 of the other.
+    r = ref32.float()
+    inside = lambda a: ((a.float() - r).abs() <= 2e-2 * (1 + r.abs())).float().mean().item()
+    rel = lambda a: ((a.float() - r).norm() / r.norm()).item()
+    i_gpu, i_orc, e_gpu, e_orc = inside(got), inside(want), rel(got), rel(want)
+    print(f"within 2e-2 of fp32: device {i_gpu:.4f}, oracle {i_orc:.4f}; relL2 device {e_gpu:.4g}, oracle {e_orc:.4g}")
+    assert i_gpu >= i_orc - 0.02 and i_gpu >= 0.8
+    assert e_gpu <= 1.1 * e_orc + 1e-6
+    # the greedy draft agrees with the fp32 evaluation wherever the oracle's does
+    agree = (got.float().argmax(-1) == ref32.argmax(-1)) | (want.float().argmax(-1) != ref32.argmax(-1))
+    assert bool(agree.all())
+
+
+def test_propose_tree_with_the_device_drafter(target):
+    tm, _ = target
+    shape = tm.shape
+    w, _ = _drafter_weights(shape, 1, 3, torch.bfloat16, seed=9)
+    dr = DeviceDrafter(tm, w, max_depth=5, capacity=256)
+    gen = torch.Generator().manual_seed(9)
+    ids = torch.randint(0, shape.vocab, (50,), generator=gen).to(DEV)
+    feats = (torch.randn(50, 3 * shape.hidden, generator=gen) * 4).to(torch.bfloat16).to(DEV)
+    tokens, parents = ptree.propose_tree(dr, ids, feats, 5, 3, 24)
+    assert len(tokens) == 15 and parents[:3] == [-1, -1, -1]
+    assert all(-1 <= q < i for i, q in enumerate(parents))
+    # the drafter is deterministic: the same call gives the same tree
+    assert ptree.propose_tree_from_logits(dr.draft_logits(ids, feats, 5), 5, 3, 24) == (tokens, parents)
+
+
+def test_capacity_and_empty_context_rejected(target):
+    tm, _ = target
+    w, _ = _drafter_weights(tm.shape, 1, 3, torch.bfloat16, seed=1)
+    dr = DeviceDrafter(tm, w, max_depth=4, capacity=64)
+    feats = torch.zeros(70, 3 * tm.shape.hidden, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        dr.draft_logits(torch.zeros(62, dtype=torch.int64, device=DEV), feats[:62], 4)
+    with pytest.raises(ValueError):
+        dr.draft_logits(torch.zeros(0, dtype=torch.int64, device=DEV), feats[:0], 2)

@@ -274,3 +274,73 @@ def test_beam_ties_take_the_lowest_token_then_the_earlier_parent():
     tokens, parents = otree.propose_tree_beam(lg, [2, 3], 2)
     assert tokens == [1, 2, 0, 1, 0]
     assert parents == [-1, -1, 0, 0, 1]
+
+
+# ------------------------------------------------------------------ drafter
+def _drafter_weights(shape, n_layers, nfl, dt, seed, std=0.05):
+    from dataclasses import replace
+    H = shape.hidden
+    g = torch.Generator().manual_seed(seed)
+
+    def r(*sz, std=std):
+        return (torch.randn(*sz, generator=g) * std).to(dt)
+
+    layers = []
+    for _ in range(n_layers):
+        lw = {n: r(o, i) for n, o, i in replace(shape, qkv_bias=False).linear_shapes()}
+        lw["attn_norm"] = (1 + r(H, std=0.1).float()).to(dt)
+        lw["mlp_norm"] = (1 + r(H, std=0.1).float()).to(dt)
+        layers.append(lw)
+    w = {"feat_norm": (1 + r(H, std=0.1).float()).to(dt), "feat_proj": r(H, nfl * H), "in_proj": r(H, 2 * H),
+         "mask_emb": r(H, std=0.02), "h_shared": r(H, std=0.02), "layers": layers}
+    shared = {"embed": r(shape.vocab, H, std=0.5), "final_norm": (1 + r(H, std=0.1).float()).to(dt),
+              "lm_head": r(shape.vocab, H)}
+    return w, shared
+
+
+def test_drafter_layers_equal_the_target_forward_in_fp32():
+    """In fp32 the drafter's RMSNorm and the target's agree, so the drafter's
+    layers + the shared final norm and lm_head over rows x, causal, equal the
+    target oracle (pinned against transformers) whose embedding table is x."""
+    from dataclasses import replace
+    from oracle import drafter as od
+    from oracle.model import OracleTarget
+    from parallel_eagle_amd.config import TINY_LLAMA
+    shape = replace(TINY_LLAMA, num_layers=2, feature_layers=(1, 2, 2))
+    w, shared = _drafter_weights(shape, 2, 3, torch.float32, 0)
+    dr = od.OracleDrafter(shape, w, shared, torch.float32)
+    p, k = 9, 4
+    ids = torch.randint(0, shape.vocab, (p,), generator=torch.Generator().manual_seed(1))
+    feats = torch.randn(p, 3 * shape.hidden, generator=torch.Generator().manual_seed(2)) * 3
+    x = torch.cat([dr.real_input(ids, feats), dr.mask_input(k - 1)])
+    m = p + k - 1
+    assert torch.equal(od.draft_allow_mask(p, k), torch.tril(torch.ones(m, m, dtype=torch.bool)))
+    assert torch.equal(od.draft_positions(p, k), torch.arange(m))
+    tw = {"embed": x, "final_norm": shared["final_norm"], "lm_head": shared["lm_head"],
+          "layers": [dict(lw) for lw in w["layers"]]}
+    logits_t, _, _ = OracleTarget(shape, tw).forward(torch.arange(m), torch.arange(m), None, None)
+    got = dr.draft_logits(ids, feats, k)
+    assert got.shape == (k, shape.vocab)
+    assert torch.allclose(got, logits_t[0, p - 1:], rtol=1e-4, atol=1e-4), (got - logits_t[0, p - 1:]).abs().max()
+
+
+def test_drafter_inputs_closed_forms():
+    from dataclasses import replace
+    from oracle import drafter as od
+    from parallel_eagle_amd.config import TINY_LLAMA
+    shape = replace(TINY_LLAMA, num_layers=1)
+    H = shape.hidden
+    w, shared = _drafter_weights(shape, 1, 2, torch.float32, 3)
+    w["feat_norm"] = torch.ones(H)
+    dr = od.OracleDrafter(shape, w, shared, torch.float32)
+    ids = torch.tensor([3, 5, 7])
+    feats = torch.randn(3, 2 * H) * torch.tensor([1.0] * H + [50.0] * H)
+    # every feature block leaves the norm with unit RMS
+    f = od.drafter_rms_norm(feats.unflatten(-1, (2, H)), w["feat_norm"], shape.rms_eps)
+    assert torch.allclose(f.pow(2).mean(-1), torch.ones(3, 2), atol=1e-4)
+    # in_proj of [emb; feat] is the sum of its column blocks applied separately
+    feat = f.flatten(-2) @ w["feat_proj"].t()
+    want = shared["embed"][ids] @ w["in_proj"][:, :H].t() + feat @ w["in_proj"][:, H:].t()
+    assert torch.allclose(dr.real_input(ids, feats), want, atol=1e-5)
+    mv = w["mask_emb"] @ w["in_proj"][:, :H].t() + w["h_shared"] @ w["in_proj"][:, H:].t()
+    assert torch.allclose(dr.mask_input(2), mv.expand(2, -1), atol=1e-6)
