@@ -64,6 +64,9 @@ def parse_args(argv=None):
     p.add_argument("--prefill", action="store_true",
                    help="instead of the verification pass: time a causal prefill of the workload's prefix length "
                         "from an empty cache and a one-token continuation (eager forward_cached calls)")
+    p.add_argument("--draft", action="store_true",
+                   help="instead of the verification pass: time the drafting step before it (a 2-layer drafter's "
+                        "draft_logits over the workload's prefix plus k - 1 mask slots, then the beam tree proposal)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a 256 MiB device copy three times (the known-size kernel the HBM counters "
                         "FETCH_SIZE / WRITE_SIZE are calibrated on)")
@@ -349,6 +352,64 @@ def prefill_line(wl, seed: int, reps: int = 3) -> dict:
                        "weights": shape.weight_format, "eager": True}}
 
 
+def draft_line(wl, seed: int, reps: int = 10) -> dict:
+    """Latency of one drafting step at the workload's shape: DeviceDrafter.draft_logits
+    (2 dense decoder layers, the reference's default depth, over the P context rows
+    plus k - 1 mask slots, sharing the target's embed / final norm / lm_head) and the
+    device beam over its k logit rows with the workload's per-depth widths. Random
+    drafter weights at the target's init scale; eager calls after a warm-up call."""
+    import torch
+
+    from parallel_eagle_amd import synth
+    from parallel_eagle_amd.drafter import DeviceDrafter
+    from parallel_eagle_amd.target import TargetModel
+    from parallel_eagle_amd.tree import propose_tree_device
+
+    shape, P, k = wl.model, wl.prefix_len, wl.depth
+    # the drafter reads only the target's embed, final norm and lm_head
+    tm = TargetModel.synthetic(shape.reduced(1), seed=seed, device="cuda:0", cache_capacity=64)
+    H, nfl = shape.hidden, len(shape.resolved_feature_layers())
+    g = torch.Generator(device="cuda:0").manual_seed(seed)
+
+    def r(*sz, std=shape.init_std):
+        return (torch.randn(*sz, generator=g, device="cuda:0") * std).to(torch.bfloat16)
+
+    from dataclasses import replace
+    layers = []
+    for _ in range(2):
+        lw = {n: r(o, i) for n, o, i in replace(shape, qkv_bias=False).linear_shapes()}
+        lw["attn_norm"] = torch.ones(H, dtype=torch.bfloat16, device="cuda:0")
+        lw["mlp_norm"] = torch.ones(H, dtype=torch.bfloat16, device="cuda:0")
+        layers.append(lw)
+    w = {"feat_norm": torch.ones(H, dtype=torch.bfloat16, device="cuda:0"), "feat_proj": r(H, nfl * H),
+         "in_proj": r(H, 2 * H), "mask_emb": r(H), "h_shared": r(H), "layers": layers}
+    dr = DeviceDrafter(tm, w, max_depth=k, capacity=P + k)
+    ids = torch.tensor(synth.uniform_int(seed, synth.STREAM_PROMPT, P, shape.vocab).tolist(), device="cuda:0")
+    feats = r(P, nfl * H, std=1.0)
+    full, logit_only = [], []
+    for i in range(reps + 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        lg = dr.draft_logits(ids, feats, k)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        tok, par, st = propose_tree_device(lg, wl.widths, wl.top_k)
+        n = int(st.item()) + tok.numel()  # waits for the beam
+        t2 = time.perf_counter()
+        if i:
+            logit_only.append(t1 - t0)
+            full.append(t2 - t0)
+    assert n == sum(wl.widths)
+    ms = statistics.median(full) * 1e3
+    return {"metric": "drafting step latency (draft_logits over the context + beam tree proposal)",
+            "value": round(ms, 3), "unit": "ms", "n_gpus": 1, "steps": reps,
+            "ms_draft_logits": round(statistics.median(logit_only) * 1e3, 3),
+            "ms_tree_proposal": round(ms - statistics.median(logit_only) * 1e3, 3),
+            "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": wl.name, "context_tokens": P, "depths": k, "tree_nodes": sum(wl.widths),
+                       "drafter_layers": 2, "eager": True}}
+
+
 def main(argv=None) -> int:
     a = parse_args(argv)
     if a.gpus != 1:
@@ -373,6 +434,9 @@ def main(argv=None) -> int:
     wl = WORKLOADS[a.workload]
     if a.prefill:
         print(json.dumps(prefill_line(wl, a.seed)))
+        return 0
+    if a.draft:
+        print(json.dumps(draft_line(wl, a.seed)))
         return 0
     if wl.batch != 1:
         print(f"workload {wl.name} is batched; the bench measures the batch-1 pass", file=sys.stderr)

@@ -9,7 +9,8 @@ same device tensors, as the reference shares the modules).
 The reference's draft mask (real rows causal; the k - 1 mask slots see every
 real row and the slots up to their own) and its positions (0..p-1, then
 (p - 1) + d) are those of one causal pass over the p + k - 1 rows from an empty
-cache, which is how it runs here. The rows are the drafter's inputs, not token
+cache, which is how it runs here (the p - 1 context rows without logits, then the k
+rows whose logits are read as a causal continuation). The rows are the drafter's inputs, not token
 embeddings: the layer stack's embedding table is a buffer of input rows that
 the pass gathers with ids 0..m-1.
 
@@ -110,9 +111,14 @@ class DeviceDrafter:
         x[:p].copy_(self.real_input(ids, context_feats))
         if k > 1:
             x[p:m].copy_(self.mask_vec.expand(k - 1, -1))
-        rows = self.rows[:m]
+        # rows [0, p - 1) only fill the cache (no lm_head); the k rows whose logits
+        # are read continue it causally: the same attention as one pass over m rows
+        rows = self.rows
         self.cache.seq_len = 0
-        logits = torch.empty((m, self.shape.vocab), dtype=self.dtype, device=self.device)
-        self.runner.run_pass(rows, rows, self.cache, _lib.PE_MASK_CAUSAL, None, logits, None)
+        if p > 1:
+            self.runner.run_pass(rows[: p - 1], rows[: p - 1], self.cache, _lib.PE_MASK_CAUSAL, None, None, None)
+            self.cache.seq_len = p - 1
+        logits = torch.empty((k, self.shape.vocab), dtype=self.dtype, device=self.device)
+        self.runner.run_pass(rows[p - 1: m], rows[p - 1: m], self.cache, _lib.PE_MASK_CAUSAL, None, logits, None)
         ops.read_status(self.runner.status, "draft_logits")
-        return logits[p - 1:]
+        return logits
