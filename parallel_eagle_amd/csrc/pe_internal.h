@@ -79,3 +79,6 @@ PE_INTERNAL int pe_internal_tree_attention(const void* q, const void* k_cache, c
                                            const uint64_t* bits, int words, float scale, int dtype, void* out,
                                            int64_t ld_out, int out_units, void* workspace, int64_t workspace_bytes,
                                            int* counters, hipStream_t st);
+
+// MFMA-tiled 16-bit weights [N][K] back to row-major (the inverse of pe_dense_repack)
+int pe_internal_dense_untile(const void* tiled, int64_t N, int64_t K, void* out, hipStream_t st);

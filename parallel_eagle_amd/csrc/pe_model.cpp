@@ -142,9 +142,9 @@ extern "C" int pe_version(void) { return 1; }
 constexpr int kFusedChunk = 64;  // rows per fused pass (causal passes are chunked)
 
 // ---------------------------------------------------------------------------
-// Prefill (a causal pass of more than kFusedChunk rows on an NF4 model with
-// RoPE-paired q/k/v): every linear is dequantised once to bf16 (in its tiled
-// row order) and multiplied over all M rows by a rocBLAS GEMM with fp32
+// Prefill (a causal pass of more than kFusedChunk rows on a bf16 model, NF4 or
+// dense, with RoPE-paired q/k/v): every linear is dequantised (NF4) or untiled
+// (dense) once to row-major bf16 (in its tiled row order) and multiplied over all M rows by a rocBLAS GEMM with fp32
 // output; the fused pass's epilogue kernels then treat that output as one
 // split: RoPE + K/V append for q/k/v, SwiGLU for gate/up, residual + RMSNorm
 // (with the captures) after o and down. Attention runs once over all rows.
@@ -158,7 +158,8 @@ bool prefill_path(const pe_model_desc* m, int M, int mask_mode) {
     const char* v = getenv("PE_PREFILL_GEMM");
     return !v || atoi(v) != 0;
   }();
-  return on && M >= kPrefillMinRows && mask_mode == PE_MASK_CAUSAL && pe_wfmt_nf4(m->weight_format) &&
+  return on && M >= kPrefillMinRows && mask_mode == PE_MASK_CAUSAL &&
+         (pe_wfmt_nf4(m->weight_format) || m->weight_format == PE_WFMT_DENSE) &&
          m->qkv_layout == PE_QKV_ROPE_PAIRED && m->dtype == PE_DTYPE_BF16 && m->head_dim == 128 &&
          m->hidden % 128 == 0 && m->intermediate_padded % 128 == 0;
 }
@@ -236,6 +237,7 @@ int blas_gemm(hipStream_t st, int M, int N, int K, const void* x, const void* w,
 }
 
 int dequant(const pe_model_desc* m, const void* w, const void* a, int64_t N, int64_t K, void* out, hipStream_t st) {
+  if (m->weight_format == PE_WFMT_DENSE) return pe_internal_dense_untile(w, N, K, out, st);
   if (m->weight_format == PE_WFMT_NF4_F32ABS)
     return pe_nf4_dequant_f32abs((const uint8_t*)w, (const float*)a, N, K, (uint16_t*)out, st);
   return pe_nf4_dequant((const uint8_t*)w, (const uint16_t*)a, N, K, (uint16_t*)out, st);
