@@ -133,3 +133,35 @@ class DeviceDrafter:
         self.runner.run_pass(rows[p - 1: m], rows[p - 1: m], self.cache, _lib.PE_MASK_CAUSAL, None, logits, None)
         ops.read_status(self.runner.status, "draft_logits")
         return logits
+
+
+_LAYER_KEYS = {"attn_norm": "input_norm.weight", "mlp_norm": "post_norm.weight", "q": "attn.q_proj.weight",
+               "k": "attn.k_proj.weight", "v": "attn.v_proj.weight", "o": "attn.o_proj.weight",
+               "gate": "mlp.gate_proj.weight", "up": "mlp.up_proj.weight", "down": "mlp.down_proj.weight"}
+
+
+def weights_from_state_dict(sd: dict, num_layers: int) -> dict:
+    """The drafter's weights by ParallelDrafter's parameter names (src/pe/drafter.py:62-76,
+    src/pe/nn.py:59-117) in DeviceDrafter's layout."""
+    def get(key):
+        if key not in sd:
+            raise KeyError(f"drafter state dict has no {key!r}")
+        return sd[key]
+
+    w = {"feat_norm": get("feat_norm.weight"), "feat_proj": get("feat_proj.weight"), "in_proj": get("in_proj.weight"),
+         "mask_emb": get("mask_emb"), "h_shared": get("h_shared")}
+    w["layers"] = [{ours: get(f"layers.{i}.{theirs}") for ours, theirs in _LAYER_KEYS.items()}
+                   for i in range(num_layers)]
+    return w
+
+
+def load_drafter(path, target: TargetModel, capacity: int = 4096) -> DeviceDrafter:
+    """load_drafter (src/pe/drafter.py:289-299) onto the device: the checkpoint's
+    {"state_dict", "num_layers", "max_depth", ...} read without executing anything
+    from the file (weights_only), sharing ``target``'s embed / final norm / lm_head."""
+    from pathlib import Path
+    if not Path(path).exists():
+        raise FileNotFoundError(f"No drafter checkpoint at {path}")
+    ckpt = torch.load(path, map_location="cpu", weights_only=True)
+    w = weights_from_state_dict(ckpt["state_dict"], int(ckpt["num_layers"]))
+    return DeviceDrafter(target, w, max_depth=int(ckpt["max_depth"]), capacity=capacity)

@@ -85,3 +85,22 @@ def test_capacity_and_empty_context_rejected(target):
         dr.draft_logits(torch.zeros(62, dtype=torch.int64, device=DEV), feats[:62], 4)
     with pytest.raises(ValueError):
         dr.draft_logits(torch.zeros(0, dtype=torch.int64, device=DEV), feats[:0], 2)
+
+
+def test_load_drafter_from_a_reference_checkpoint(target, tmp_path):
+    from parallel_eagle_amd.drafter import _LAYER_KEYS, load_drafter
+    tm, _ = target
+    w, _ = _drafter_weights(tm.shape, 1, 3, torch.bfloat16, seed=4, std=tm.shape.init_std)
+    sd = {"feat_norm.weight": w["feat_norm"], "feat_proj.weight": w["feat_proj"], "in_proj.weight": w["in_proj"],
+          "mask_emb": w["mask_emb"], "h_shared": w["h_shared"]}
+    for ours, theirs in _LAYER_KEYS.items():
+        sd[f"layers.0.{theirs}"] = w["layers"][0][ours]
+    path = tmp_path / "drafter.pt"
+    torch.save({"state_dict": sd, "num_layers": 1, "max_depth": 4, "target_name": "synthetic"}, path)
+    dr = load_drafter(path, tm, capacity=128)
+    assert dr.max_depth == 4
+    gen = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, tm.shape.vocab, (20,), generator=gen).to(DEV)
+    feats = torch.randn(20, 3 * tm.shape.hidden, generator=gen).to(torch.bfloat16).to(DEV)
+    direct = DeviceDrafter(tm, w, max_depth=4, capacity=128)
+    assert torch.equal(dr.draft_logits(ids, feats, 4), direct.draft_logits(ids, feats, 4))
