@@ -66,6 +66,12 @@ extern "C" {
 #define PE_MASK_TREE 0   /* rows are tree nodes: whole prefix + ancestor bits */
 #define PE_MASK_CAUSAL 1 /* rows are consecutive tokens: key j allowed iff j <= P + row */
 
+/* RMSNorm rounding (fp32 statistics either way) */
+#define PE_NORM_HF 0          /* w * round(x * rsqrt(mean(x^2) + eps)): HF LlamaRMSNorm
+                                 (modeling_llama.py:62-67), the target's norms */
+#define PE_NORM_FP32_WEIGHT 1 /* round(x * rsqrt(mean(x^2) + eps) * float(w)): one rounding,
+                                 the drafter's RMSNorm (src/pe/nn.py:22-26) */
+
 #define PE_TREE_MAX_WORDS 4 /* ancestor bitmask words per node: T <= 256 */
 
 const char* pe_status_string(int status);
@@ -159,6 +165,11 @@ int pe_embed(const int64_t* ids, int M, const void* table, int64_t V, int H, int
 /* HF LlamaRMSNorm (modeling_llama.py:62-67): w * round(x * rsqrt(mean(x^2) + eps)). */
 int pe_rmsnorm(const void* x, int64_t ldx, int M, int H, const void* w, float eps, int dtype,
                void* out, int64_t ld_out, void* stream);
+/* pe_rmsnorm with the rounding chosen by `mode` (PE_NORM_*): PE_NORM_FP32_WEIGHT
+ * is the drafter's RMSNorm.forward (src/pe/nn.py:22-26), used for its
+ * feat_norm (src/pe/drafter.py:130). */
+int pe_rmsnorm_ex(const void* x, int64_t ldx, int M, int H, const void* w, float eps, int dtype, int mode,
+                  void* out, int64_t ld_out, void* stream);
 /* RoPE at the given positions on q and k of a fused qkv row block, HF
  * apply_rotary_pos_emb (modeling_llama.py:130-160); writes roped q to q_out
  * [M][nh][hd] and appends k, v at cache rows [row0, row0 + M) in place of
@@ -207,9 +218,10 @@ int pe_argmax_rows(const void* x, int64_t ld, int rows, int64_t V, int dtype, in
 /* Greedy tree walk of accept_tree_cached (src/pe/decode/verify.py:104-125):
  * out[0] = |path|, out[1] = bonus token, out[2 + i] = path node i.
  * One launch: per-row argmax blocks, the last of which walks.
- * scratch: T + 2 int32 (row argmaxes, then an arrival counter), zero before
- * the first call; every call leaves the counter at zero again. Calls that
- * share a scratch buffer must not overlap. */
+ * scratch: T + 2 int32 (an arrival counter at index 0, then the row
+ * argmaxes), zero before the first call; every call leaves the counter at
+ * zero again, so one buffer serves calls of any T. Calls that share a
+ * scratch buffer must not overlap. T <= 64 * PE_TREE_MAX_WORDS. */
 int pe_accept_tree(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V,
                    int dtype, const int64_t* node_tokens, const int32_t* parents, int32_t* out,
                    int32_t* scratch, void* stream);
@@ -255,8 +267,10 @@ typedef struct pe_model_desc {
   int32_t weight_format;       /* PE_WFMT_* of the per-layer linears */
   int32_t qkv_layout;          /* PE_QKV_* row order of w_qkv */
   float rms_eps;
+  int32_t norm_mode;        /* PE_NORM_* of the per-layer norms; the final norm is PE_NORM_HF */
+  int32_t embed_rows;       /* rows of `embed` (ids must lie below); 0 = vocab */
   int64_t max_positions;
-  const void* embed;        /* [V][H] */
+  const void* embed;        /* [embed_rows or V][H] */
   const void* final_norm;   /* [H] */
   const void* lm_head;      /* dense [V][H], tiled for 16-bit dtypes */
   const void* rope_cos_sin; /* [max_pos][hd] cos, then [max_pos][hd] sin */

@@ -91,6 +91,12 @@ def read_linear4bit(sd: dict, prefix: str) -> Linear4bit:
         raise CheckpointError(f"{prefix}weight: quant_type {qs.get('quant_type')!r}, only 'nf4' is supported")
     if int(qs.get("blocksize", -1)) != 64:
         raise CheckpointError(f"{prefix}weight: blocksize {qs.get('blocksize')}, the kernels take 64")
+    # the compute dtype the checkpoint was quantised for (QuantState.dtype): the
+    # NF4 kernels compute in bfloat16, and an fp16 model run in bf16 would give
+    # other logits than the reference (target.py:89 takes the dtype from the model)
+    cdt = str(qs.get("dtype", "")).replace("torch.", "")
+    if cdt != "bfloat16":
+        raise CheckpointError(f"{prefix}weight: compute dtype {qs.get('dtype')!r}; the NF4 kernels compute in bfloat16")
     shape = qs.get("shape")
     if not isinstance(shape, (list, tuple)) or len(shape) != 2:
         raise CheckpointError(f"{prefix}weight: shape {shape!r} is not 2-D")
@@ -148,6 +154,11 @@ def weights_from_state_dict(shape: ModelShape, sd: dict, device="cuda") -> dict:
         want = (rows,) if cols is None else (rows, cols)
         if tuple(t.shape) != want:
             raise CheckpointError(f"{key}: shape {tuple(t.shape)}, expected {want}")
+        if t.dtype not in (torch.bfloat16, torch.float32):
+            # an fp16 embedding / norm / lm_head means an fp16 model (the reference
+            # runs it in the embedding's dtype, target.py:89); bf16 here would not
+            # reproduce its logits
+            raise CheckpointError(f"{key}: {t.dtype}; the NF4 model computes in bfloat16")
         return t.to(device=device, dtype=torch.bfloat16).contiguous()
 
     s = shape

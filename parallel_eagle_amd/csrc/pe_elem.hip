@@ -48,10 +48,21 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
   }
 }
 
+// The normalised value of x times the weight w, rounded as PE_NORM_HF (the
+// normalised value rounded, then a rounded multiply by w: HF LlamaRMSNorm,
+// modeling_llama.py:62-67) or PE_NORM_FP32_WEIGHT (x * inv * w in fp32, one
+// rounding: src/pe/nn.py:22-26).
+template <typename E>
+__device__ __forceinline__ float norm_out(int mode, float x, float inv, float w) {
+  const float y = __fmul_rn(x, inv);
+  return mode == PE_NORM_FP32_WEIGHT ? E::round(__fmul_rn(y, w)) : E::round(__fmul_rn(w, E::round(y)));
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t ldx, int H,
                                                       const typename Elem<DT>::T* __restrict__ w, float eps,
-                                                      typename Elem<DT>::T* __restrict__ out, int64_t ld_out) {
+                                                      int mode, typename Elem<DT>::T* __restrict__ out,
+                                                      int64_t ld_out) {
   typedef Elem<DT> E;
   const int m = blockIdx.x;
   const typename E::T* xr = x + (int64_t)m * ldx;
@@ -71,8 +82,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const typename Elem<DT>::T
   const float inv = 1.0f / sqrtf(var + eps);
   typename E::T* orow = out + (int64_t)m * ld_out;
   for (int c = threadIdx.x; c < H; c += blockDim.x) {
-    const float y = E::round(__fmul_rn(E::load(xr, c), inv));
-    E::store(orow, c, __fmul_rn(E::load(w, c), y));
+    E::store(orow, c, norm_out<E>(mode, E::load(xr, c), inv, E::load(w, c)));
   }
 }
 
@@ -167,7 +177,7 @@ template <> struct Raw4<PE_DTYPE_F32> {
 template <int DT, int CH, int SMAX, bool EMB>
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
     const float* __restrict__ partial, int S, int M, typename Elem<DT>::T* __restrict__ h, int H,
-    const typename Elem<DT>::T* __restrict__ w, float eps, typename Elem<DT>::T* __restrict__ xn,
+    const typename Elem<DT>::T* __restrict__ w, float eps, int mode, typename Elem<DT>::T* __restrict__ xn,
     typename Elem<DT>::T* __restrict__ xt, typename Elem<DT>::T* __restrict__ cap_h, int64_t ld_cap_h,
     typename Elem<DT>::T* __restrict__ cap_xn, int64_t ld_cap_xn, const int64_t* __restrict__ ids,
     const typename Elem<DT>::T* __restrict__ table, int64_t vocab, int32_t* __restrict__ status) {
@@ -248,7 +258,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
     float wv[4], o[4];
     RW::cvt(wraw[k], wv);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = E::round(__fmul_rn(wv[e], E::round(__fmul_rn(v[k][e], inv))));
+    for (int e = 0; e < 4; ++e) o[e] = norm_out<E>(mode, v[k][e], inv, wv[e]);
     V::store(orow + 4 * c, o);
     // four consecutive columns are consecutive in the A-tiled layout too
     if (xt) V::store(xt + xtile_index(m, 4 * c, H >> 7), o);
@@ -291,16 +301,22 @@ extern "C" int pe_embed(const int64_t* ids, int M, const void* table, int64_t V,
   return PE_OK;
 }
 
-extern "C" int pe_rmsnorm(const void* x, int64_t ldx, int M, int H, const void* w, float eps, int dtype,
-                          void* out, int64_t ld_out, void* stream) {
+extern "C" int pe_rmsnorm_ex(const void* x, int64_t ldx, int M, int H, const void* w, float eps, int dtype, int mode,
+                             void* out, int64_t ld_out, void* stream) {
   if (!x || !w || !out || M <= 0 || H <= 0) return PE_ERR_ARG;
+  if (mode != PE_NORM_HF && mode != PE_NORM_FP32_WEIGHT) return PE_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   PE_DISPATCH_DT(dtype, {
     typedef typename Elem<DT>::T T;
-    rmsnorm_kernel<DT><<<M, 256, 0, st>>>((const T*)x, ldx, H, (const T*)w, eps, (T*)out, ld_out);
+    rmsnorm_kernel<DT><<<M, 256, 0, st>>>((const T*)x, ldx, H, (const T*)w, eps, mode, (T*)out, ld_out);
   });
   PE_CHECK_LAUNCH();
   return PE_OK;
+}
+
+extern "C" int pe_rmsnorm(const void* x, int64_t ldx, int M, int H, const void* w, float eps, int dtype,
+                          void* out, int64_t ld_out, void* stream) {
+  return pe_rmsnorm_ex(x, ldx, M, H, w, eps, dtype, PE_NORM_HF, out, ld_out, stream);
 }
 
 extern "C" int pe_rope_qkv(const void* qkv, int64_t ld_qkv, int M, int nh, int nkv, int hd,
@@ -338,6 +354,7 @@ template <typename T> struct NormArgs {
   int H;
   const T* w;
   float eps;
+  int mode;
   T *xn, *xt, *cap_h;
   int64_t ld_cap_h;
   T* cap_xn;
@@ -353,13 +370,13 @@ void launch_norm_sm(const NormArgs<typename Elem<DT>::T>& a, hipStream_t st) {
   if constexpr (SM == 0) {
     if (a.table) {
       residual_rmsnorm_kernel<DT, CH, 0, true><<<a.M, kNormThreads, 0, st>>>(
-          a.partial, a.S, a.M, a.h, a.H, a.w, a.eps, a.xn, a.xt, a.cap_h, a.ld_cap_h, a.cap_xn, a.ld_cap_xn, a.ids,
+          a.partial, a.S, a.M, a.h, a.H, a.w, a.eps, a.mode, a.xn, a.xt, a.cap_h, a.ld_cap_h, a.cap_xn, a.ld_cap_xn, a.ids,
           a.table, a.vocab, a.status);
       return;
     }
   }
   residual_rmsnorm_kernel<DT, CH, SM, false><<<a.M, kNormThreads, 0, st>>>(
-      a.partial, a.S, a.M, a.h, a.H, a.w, a.eps, a.xn, a.xt, a.cap_h, a.ld_cap_h, a.cap_xn, a.ld_cap_xn, nullptr,
+      a.partial, a.S, a.M, a.h, a.H, a.w, a.eps, a.mode, a.xn, a.xt, a.cap_h, a.ld_cap_h, a.cap_xn, a.ld_cap_xn, nullptr,
       nullptr, 0, nullptr);
 }
 
@@ -375,7 +392,7 @@ void launch_norm(int smax, const NormArgs<typename Elem<DT>::T>& a, hipStream_t 
 }
 
 int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, int H, const void* w, float eps,
-                                 int dtype, void* xn, void* xn_tiled, void* cap_h, int64_t ld_cap_h, void* cap_xn,
+                                 int mode, int dtype, void* xn, void* xn_tiled, void* cap_h, int64_t ld_cap_h, void* cap_xn,
                                  int64_t ld_cap_xn, hipStream_t st) {
   if (!h || !w || !xn || M <= 0 || H <= 0 || S < 0 || (S > 0 && !partial)) return PE_ERR_ARG;
   if (H % 4 || H > 4 * kNormThreads * kNormChunks || S > kNormMaxSplits) return PE_ERR_ARG;
@@ -384,7 +401,7 @@ int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, in
   const int smax = S == 0 ? 0 : (S + 3) / 4 * 4;
   PE_DISPATCH_DT(dtype, {
     typedef typename Elem<DT>::T T;
-    const NormArgs<T> na{partial, S, M, (T*)h, H, (const T*)w, eps, (T*)xn, (T*)xn_tiled, (T*)cap_h, ld_cap_h,
+    const NormArgs<T> na{partial, S, M, (T*)h, H, (const T*)w, eps, mode, (T*)xn, (T*)xn_tiled, (T*)cap_h, ld_cap_h,
                          (T*)cap_xn, ld_cap_xn, nullptr, nullptr, 0, nullptr};
     if (ch == 1)
       launch_norm<DT, 1>(smax, na, st);
@@ -396,7 +413,7 @@ int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, in
 }
 
 int pe_internal_embed_rmsnorm(const int64_t* ids, int M, const void* table, int64_t V, void* h, int H, const void* w,
-                              float eps, int dtype, void* xn, void* xn_tiled, void* cap_h, int64_t ld_cap_h,
+                              float eps, int mode, int dtype, void* xn, void* xn_tiled, void* cap_h, int64_t ld_cap_h,
                               void* cap_xn, int64_t ld_cap_xn, int32_t* status, hipStream_t st) {
   if (!ids || !table || !h || !w || !xn || M <= 0 || H <= 0 || V <= 0) return PE_ERR_ARG;
   if (H % 4 || H > 4 * kNormThreads * kNormChunks) return PE_ERR_ARG;
@@ -404,7 +421,7 @@ int pe_internal_embed_rmsnorm(const int64_t* ids, int M, const void* table, int6
   const int ch = (H >> 2) > kNormThreads ? 2 : 1;
   PE_DISPATCH_DT(dtype, {
     typedef typename Elem<DT>::T T;
-    const NormArgs<T> na{nullptr, 0, M, (T*)h, H, (const T*)w, eps, (T*)xn, (T*)xn_tiled, (T*)cap_h, ld_cap_h,
+    const NormArgs<T> na{nullptr, 0, M, (T*)h, H, (const T*)w, eps, mode, (T*)xn, (T*)xn_tiled, (T*)cap_h, ld_cap_h,
                          (T*)cap_xn, ld_cap_xn, ids, (const T*)table, V, status};
     if (ch == 1)
       launch_norm_sm<DT, 1, 0>(na, st);

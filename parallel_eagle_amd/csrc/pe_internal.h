@@ -50,17 +50,17 @@ PE_INTERNAL int pe_internal_swiglu_partials(const float* partial, int S, int M, 
                                             int out_units, int dtype, hipStream_t st);
 
 // pe_elem.hip: h = round(h + round(sum_s partial[s])) (S == 0: h unchanged),
-// xn = w * round(h * rsqrt(mean(h^2) + eps)), also A-tiled into xn_tiled when
+// xn = the RMSNorm of h rounded as `mode` (PE_NORM_*), also A-tiled into xn_tiled when
 // given; optional copies of the new h (cap_h) and of xn (cap_xn) into the
 // fused-feature rows.
 PE_INTERNAL int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, int H, const void* w,
-                                             float eps, int dtype, void* xn, void* xn_tiled, void* cap_h,
+                                             float eps, int mode, int dtype, void* xn, void* xn_tiled, void* cap_h,
                                              int64_t ld_cap_h, void* cap_xn, int64_t ld_cap_xn, hipStream_t st);
 // pe_elem.hip: the first layer's input norm fused with the embedding gather:
 // h[m] = embed[ids[m]] (out-of-range ids flag PE_ERR_TOKEN in *status and read
 // row 0), then xn / xn_tiled / captures as pe_internal_residual_rmsnorm.
 PE_INTERNAL int pe_internal_embed_rmsnorm(const int64_t* ids, int M, const void* table, int64_t V, void* h, int H,
-                                          const void* w, float eps, int dtype, void* xn, void* xn_tiled, void* cap_h,
+                                          const void* w, float eps, int mode, int dtype, void* xn, void* xn_tiled, void* cap_h,
                                           int64_t ld_cap_h, void* cap_xn, int64_t ld_cap_xn, int32_t* status,
                                           hipStream_t st);
 

@@ -110,6 +110,9 @@ Layout make_layout(const pe_model_desc* m, int M, int64_t kv_len) {
   return L;
 }
 
+// Rows of the embedding table the pass gathers from.
+int64_t embed_rows(const pe_model_desc* m) { return m->embed_rows > 0 ? m->embed_rows : m->vocab; }
+
 int linear(const pe_model_desc* m, const void* x, int64_t ldx, int M, int K, const void* w, const void* a, int N,
            int epi, const void* bias, const void* resid, int64_t ldr, void* out, int64_t ldo, void* ws, int64_t wsb,
            hipStream_t st) {
@@ -291,8 +294,8 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
 
   {
     const int f0 = slot_of(0);
-    PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, m->vocab, h, H, m->attn_norm[0], m->rms_eps,
-                                     m->dtype, xn, nullptr, slot_ptr(f0), fused_ld, nullptr, 0, a->status, st));
+    PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, embed_rows(m), h, H, m->attn_norm[0], m->rms_eps,
+                                     m->norm_mode, m->dtype, xn, nullptr, slot_ptr(f0), fused_ld, nullptr, 0, a->status, st));
     PE_TRY(copy_repeats(0, f0));
   }
   for (int l = 0; l < L; ++l) {
@@ -306,7 +309,7 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
                                       nullptr, 0, scale, m->dtype, attn, qd, 0, ws + Lp.attn_ws, Lp.attn_ws_bytes,
                                       (int*)(ws + Lp.gemm) + kPassAttnCounterInt, st));
     PE_TRY(linear(attn, qd, m->w_o[l], m->a_o[l], H));
-    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, nullptr, nullptr, 0,
+    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, nullptr, nullptr, 0,
                                         nullptr, 0, st));
     PE_TRY(linear(xn, H, m->w_gu[l], m->a_gu[l], 2 * ip));
     PE_TRY(pe_internal_swiglu_partials(y, 1, M, 2 * ip, act, ip, 0, m->dtype, st));
@@ -315,7 +318,8 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
     const int fh = last ? -1 : slot_of(l + 1);
     const int fx = last ? slot_of(L) : -1;
     const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
-    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, next_norm, m->rms_eps, m->dtype, xn, nullptr, slot_ptr(fh),
+    const int next_mode = last ? PE_NORM_HF : m->norm_mode;
+    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn, nullptr, slot_ptr(fh),
                                         fused_ld, slot_ptr(fx), fused_ld, st));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
@@ -393,8 +397,8 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
 
   {
     const int f0 = slot_of(0);
-    PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, m->vocab, h, H, m->attn_norm[0], m->rms_eps,
-                                     m->dtype, xn, xn_t, slot_ptr(f0), fused_ld, nullptr, 0, a->status, st));
+    PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, embed_rows(m), h, H, m->attn_norm[0], m->rms_eps,
+                                     m->norm_mode, m->dtype, xn, xn_t, slot_ptr(f0), fused_ld, nullptr, 0, a->status, st));
     PE_TRY(copy_repeats(0, f0));
   }
   // The tiled (NF4) pass: q/k/v and gate/up run unsplit with their RoPE + KV
@@ -419,12 +423,12 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     if (tiled) {
       PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, true, M, qd, m->w_o[l], a_o, H, part,
                                          Lo.part_bytes, &S, st));
-      PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, xn_t, nullptr,
+      PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, xn_t, nullptr,
                                           0, nullptr, 0, st));
     } else {
       PE_TRY(pe_internal_linear(wf, m->dtype, x_attn, qd, false, M, qd, m->w_o[l], a_o, H, PE_EPI_RESIDUAL, nullptr,
                                 h, H, h, H, 0, gws, gwsb, st));
-      PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, nullptr,
+      PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, nullptr,
                                           nullptr, 0, nullptr, 0, st));
     }
     const void* a_gu = m->a_gu ? m->a_gu[l] : nullptr;
@@ -433,19 +437,20 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     const int fh = last ? -1 : slot_of(l + 1);
     const int fx = last ? slot_of(L) : -1;
     const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
+    const int next_mode = last ? PE_NORM_HF : m->norm_mode;
     if (tiled) {
       PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, true, M, H, m->w_gu[l], a_gu, 2 * ip, PE_EPI_SWIGLU,
                                 nullptr, nullptr, 0, x_act, ip, act_units, gws, gwsb, st));
       PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_act, ip, true, M, ip, m->w_down[l], a_down, H, part,
                                          Lo.part_bytes, &S, st));
-      PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, m->dtype, xn,
+      PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn,
                                           last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
     } else {
       PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, false, M, H, m->w_gu[l], a_gu, 2 * ip, PE_EPI_SWIGLU,
                                 nullptr, nullptr, 0, x_act, ip, 0, gws, gwsb, st));
       PE_TRY(pe_internal_linear(wf, m->dtype, x_act, ip, false, M, ip, m->w_down[l], a_down, H, PE_EPI_RESIDUAL,
                                 nullptr, h, H, h, H, 0, gws, gwsb, st));
-      PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, next_norm, m->rms_eps, m->dtype, xn, nullptr,
+      PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn, nullptr,
                                           slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
     }
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
@@ -465,6 +470,7 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
   if (a->num_features < 0 || a->num_features > 4) return PE_ERR_ARG;
   if (a->mask_mode == PE_MASK_TREE && !a->tree_bits) return PE_ERR_ARG;
   if (m->intermediate_padded % 32 || m->intermediate_padded < m->intermediate) return PE_ERR_ARG;
+  if (m->norm_mode != PE_NORM_HF && m->norm_mode != PE_NORM_FP32_WEIGHT) return PE_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   const int64_t kv_len = a->prefix_len + M;
   if (prefill_path(m, M, a->mask_mode)) {
@@ -531,12 +537,12 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
     return PE_OK;
   };
 
-  PE_TRY(pe_embed(a->input_ids, M, m->embed, m->vocab, H, m->dtype, h, H, a->status, st));
+  PE_TRY(pe_embed(a->input_ids, M, m->embed, embed_rows(m), H, m->dtype, h, H, a->status, st));
   PE_TRY(capture(0, h));
   for (int l = 0; l < m->num_layers; ++l) {
     void* kc = (char*)a->k_cache + l * layer_stride;
     void* vc = (char*)a->v_cache + l * layer_stride;
-    PE_TRY(pe_rmsnorm(h, H, M, H, m->attn_norm[l], m->rms_eps, m->dtype, xn, H, st));
+    PE_TRY(pe_rmsnorm_ex(h, H, M, H, m->attn_norm[l], m->rms_eps, m->dtype, m->norm_mode, xn, H, st));
     PE_TRY(linear(m, xn, H, M, H, m->w_qkv[l], m->a_qkv ? m->a_qkv[l] : nullptr, nqkv, PE_EPI_STORE,
                   m->b_qkv ? m->b_qkv[l] : nullptr, nullptr, 0, qkv, nqkv, gws, gwsb, st));
     PE_TRY(pe_rope_qkv(qkv, nqkv, M, nh, nkv, hd, a->positions, m->rope_cos_sin, m->max_positions, m->dtype, q, kc, vc,
@@ -546,7 +552,7 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
                                       Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st));
     PE_TRY(linear(m, attn, qd, M, qd, m->w_o[l], m->a_o ? m->a_o[l] : nullptr, H, PE_EPI_RESIDUAL, nullptr, h, H, h,
                   H, gws, gwsb, st));
-    PE_TRY(pe_rmsnorm(h, H, M, H, m->mlp_norm[l], m->rms_eps, m->dtype, xn, H, st));
+    PE_TRY(pe_rmsnorm_ex(h, H, M, H, m->mlp_norm[l], m->rms_eps, m->dtype, m->norm_mode, xn, H, st));
     PE_TRY(linear(m, xn, H, M, H, m->w_gu[l], m->a_gu ? m->a_gu[l] : nullptr, 2 * ip, PE_EPI_SWIGLU, nullptr,
                   nullptr, 0, act, ip, gws, gwsb, st));
     PE_TRY(linear(m, act, ip, M, ip, m->w_down[l], m->a_down ? m->a_down[l] : nullptr, H, PE_EPI_RESIDUAL, nullptr,

@@ -188,9 +188,10 @@ __global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const typename
 }
 
 // One launch does the whole acceptance. Block r finds the argmax of row r
-// (row 0 = root logit, rows 1..T = node logits) and publishes it in amax[r];
-// the last block to count itself on amax[T + 1] (every row's argmax is then
-// visible) resets that counter and walks the tree. The walk stages every
+// (row 0 = root logit, rows 1..T = node logits) and publishes it in
+// work[1 + r]; the last block to count itself on work[0] (every row's argmax
+// is then visible) resets that counter and walks the tree. The counter sits
+// at index 0 whatever T is, so one scratch buffer serves calls of any size. The walk stages every
 // node's argmax, parent and token in LDS; one wave then follows the greedy
 // path, each step a ballot over the nodes for the first child of the current
 // node whose token equals the current truth (at most kWalkMax nodes).
@@ -199,10 +200,12 @@ constexpr int kWalkMax = 64 * PE_TREE_MAX_WORDS;
 template <int DT>
 __global__ __launch_bounds__(kArgThreads) void accept_kernel(const typename Elem<DT>::T* __restrict__ root,
                                                              const typename Elem<DT>::T* __restrict__ nodes,
-                                                             int64_t ld, int64_t V, int32_t* __restrict__ amax,
+                                                             int64_t ld, int64_t V, int32_t* __restrict__ work,
                                                              int T, const int64_t* __restrict__ tokens,
                                                              const int32_t* __restrict__ parents,
                                                              int32_t* __restrict__ out) {
+  int32_t* const counter = work;
+  int32_t* const amax = work + 1;
   const int r = blockIdx.x;
   const typename Elem<DT>::T* x = (r == 0) ? root : nodes + (int64_t)(r - 1) * ld;
   const int best = row_argmax<DT>(x, V, nullptr);
@@ -211,9 +214,9 @@ __global__ __launch_bounds__(kArgThreads) void accept_kernel(const typename Elem
     __hip_atomic_store(amax + r, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // release: this row's argmax is visible before the count; acquire: the
     // last block sees every row's
-    const int old = __hip_atomic_fetch_add(amax + T + 1, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     s_last = old == T;
-    if (old == T) __hip_atomic_store(amax + T + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == T) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!s_last) return;
@@ -538,26 +541,23 @@ extern "C" int pe_argmax_rows(const void* x, int64_t ld, int rows, int64_t V, in
   return PE_OK;
 }
 
-extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V, int dtype,
-                              const int64_t* node_tokens, const int32_t* parents, int32_t* out, int32_t* scratch,
-                              void* stream) {
-  if (!root_logit || !out || !scratch || T < 0 || V <= 0) return PE_ERR_ARG;
-  if (T > 0 && (!node_logits || !node_tokens || !parents)) return PE_ERR_ARG;
-  if (T > kWalkMax) return PE_ERR_TREE;
-  hipStream_t st = (hipStream_t)stream;
+namespace {
+
+int launch_accept(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V, int dtype,
+                  const int64_t* node_tokens, const int32_t* parents, int32_t* out, int32_t* work, hipStream_t st) {
   switch (dtype) {
     case PE_DTYPE_F32:
       accept_kernel<PE_DTYPE_F32><<<T + 1, kArgThreads, 0, st>>>((const float*)root_logit, (const float*)node_logits,
-                                                                 ld, V, scratch, T, node_tokens, parents, out);
+                                                                 ld, V, work, T, node_tokens, parents, out);
       break;
     case PE_DTYPE_BF16:
       accept_kernel<PE_DTYPE_BF16><<<T + 1, kArgThreads, 0, st>>>((const uint16_t*)root_logit,
-                                                                  (const uint16_t*)node_logits, ld, V, scratch, T,
+                                                                  (const uint16_t*)node_logits, ld, V, work, T,
                                                                   node_tokens, parents, out);
       break;
     case PE_DTYPE_F16:
       accept_kernel<PE_DTYPE_F16><<<T + 1, kArgThreads, 0, st>>>((const uint16_t*)root_logit,
-                                                                 (const uint16_t*)node_logits, ld, V, scratch, T,
+                                                                 (const uint16_t*)node_logits, ld, V, work, T,
                                                                  node_tokens, parents, out);
       break;
     default:
@@ -565,6 +565,26 @@ extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, i
   }
   PE_CHECK_LAUNCH();
   return PE_OK;
+}
+
+int check_accept_args(const void* root_logit, const void* node_logits, int T, int64_t V, int dtype,
+                      const int64_t* node_tokens, const int32_t* parents, const int32_t* out) {
+  if (!root_logit || !out || T < 0 || V <= 0) return PE_ERR_ARG;
+  if (dtype != PE_DTYPE_F32 && dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16) return PE_ERR_ARG;
+  if (T > 0 && (!node_logits || !node_tokens || !parents)) return PE_ERR_ARG;
+  if (T > kWalkMax) return PE_ERR_TREE;
+  return PE_OK;
+}
+
+}  // namespace
+
+extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V, int dtype,
+                              const int64_t* node_tokens, const int32_t* parents, int32_t* out, int32_t* work,
+                              void* stream) {
+  int rc = check_accept_args(root_logit, node_logits, T, V, dtype, node_tokens, parents, out);
+  if (rc != PE_OK) return rc;
+  if (!work) return PE_ERR_ARG;
+  return launch_accept(root_logit, node_logits, ld, T, V, dtype, node_tokens, parents, out, work, (hipStream_t)stream);
 }
 
 extern "C" int pe_propose_tree(const void* logits, int64_t ld, int k, int64_t V, int dtype, const int32_t* widths,

@@ -16,9 +16,10 @@ the pass gathers with ids 0..m-1.
 
 Inputs (drafter.py:126-138): ``in_proj([embed(token); feat_proj(feat_norm(feature
 blocks))])`` for real positions, ``in_proj([mask_emb; h_shared])`` for mask
-slots (computed once). Norms here round like the target's RMSNorm (normalised
-row rounded, then the weight multiply); the reference's drafter norm multiplies
-in fp32 and rounds once: a difference within the dtype's rounding.
+slots (computed once). The drafter's own norms (feat_norm and each layer's two)
+multiply by the weight in fp32 and round once, as the reference's RMSNorm does
+(src/pe/nn.py:22-26, PE_NORM_FP32_WEIGHT); the shared final norm is the
+target's HF LlamaRMSNorm (the normalised row rounded, then the weight multiply).
 """
 
 from __future__ import annotations
@@ -54,8 +55,6 @@ class DeviceDrafter:
         n_layers = len(weights["layers"])
         self.shape = replace(s, name=f"{s.name}-drafter", num_layers=n_layers, weight_format="dense", qkv_bias=False,
                              feature_layers=(n_layers,))
-        if capacity > s.vocab:
-            raise ValueError("drafter rows are gathered by ids below the vocabulary size: capacity <= vocab")
         self.capacity = capacity
 
         def up(x):
@@ -87,11 +86,34 @@ class DeviceDrafter:
         core.logical = None
         for lw in weights["layers"]:
             core._add_layer({k: up(v) for k, v in lw.items()}, False)
+        core.norm_mode = _lib.PE_NORM_FP32_WEIGHT
         core._finish()
         self.core = core
         self.runner = TargetModel(core, cache_capacity=capacity)
         self.cache = TreeKVCache(self.shape, dt, dev, capacity)
         self.rows = torch.arange(capacity, dtype=torch.int64, device=dev)
+
+    # nn.Module-style calls the reference's callers chain after load_drafter
+    # (bench/run_bench.py:57: ``load_drafter(path, target).to(device, dtype).eval()``):
+    # the weights already live on the target's device in its dtype, so these
+    # check the request and return the drafter itself.
+    def to(self, *args, **kwargs) -> "DeviceDrafter":
+        dev, dt, _, _ = torch._C._nn._parse_to(*args, **kwargs)
+        if dev is not None:
+            want = torch.device(dev)
+            if want.type != self.device.type or (want.index is not None and want.index != self.device.index):
+                raise ValueError(f"the device drafter lives on {self.device}, not {want}")
+        if dt is not None and dt != self.dtype:
+            raise ValueError(f"the device drafter computes in its target's dtype {self.dtype}, not {dt}")
+        return self
+
+    def eval(self) -> "DeviceDrafter":
+        return self
+
+    def train(self, mode: bool = True) -> "DeviceDrafter":
+        if mode:
+            raise ValueError("the device drafter runs inference only")
+        return self
 
     def real_input(self, token_ids: torch.Tensor, features: torch.Tensor) -> torch.Tensor:
         """in_proj([embed(token); feat_proj(feat_norm(features))]) (drafter.py:126-133)."""
@@ -100,7 +122,7 @@ class DeviceDrafter:
         p = ids.numel()
         emb = ops.embed(ids, self.target.model.embed, self.runner.status)
         f = features.to(device=self.device, dtype=self.dtype).reshape(p * (self.feat_dim // H), H).contiguous()
-        f = ops.rmsnorm(f, self.feat_norm, self.eps).view(p, self.feat_dim)
+        f = ops.rmsnorm(f, self.feat_norm, self.eps, mode=_lib.PE_NORM_FP32_WEIGHT).view(p, self.feat_dim)
         if p > self.library_gemm_rows and self.in_proj_rm is not None:
             feat = torch.nn.functional.linear(f, self.feat_proj_rm)
             return torch.nn.functional.linear(torch.cat([emb, feat], dim=-1), self.in_proj_rm)

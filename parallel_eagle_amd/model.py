@@ -77,6 +77,9 @@ class DeviceModel:
         self.lm_head = None  # tiled (16-bit) / row-major (fp32)
         self.lm_head_logical = None
         self.cos_sin = None
+        # rounding of the per-layer RMSNorms (PE_NORM_*): HF's for a target; the
+        # drafter's layer stack rounds once (src/pe/nn.py:22-26)
+        self.norm_mode = _lib.PE_NORM_HF
         self._desc = None
         self._keep = []
 
@@ -267,6 +270,8 @@ class DeviceModel:
             d.weight_format = _lib.PE_WFMT_NF4
         d.qkv_layout = _lib.PE_QKV_ROPE_PAIRED if self.qkv_paired else _lib.PE_QKV_PLAIN
         d.rms_eps = s.rms_eps
+        d.norm_mode = self.norm_mode
+        d.embed_rows = self.embed.shape[0]
         d.max_positions = s.max_positions
         d.embed, d.final_norm = self.embed.data_ptr(), self.final_norm.data_ptr()
         d.lm_head, d.rope_cos_sin = self.lm_head.data_ptr(), self.cos_sin.data_ptr()

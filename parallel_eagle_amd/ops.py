@@ -217,11 +217,13 @@ def nf4_linear_partials(x: torch.Tensor, m: int, k: int, n: int, nf4: tuple, *, 
     return partials[: s.value * m * n].view(s.value, m, n), s.value
 
 
-def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, mode: int = _lib.PE_NORM_HF) -> torch.Tensor:
+    """RMSNorm of the rows of x [M][H]; ``mode`` PE_NORM_HF (HF LlamaRMSNorm) or
+    PE_NORM_FP32_WEIGHT (the drafter's RMSNorm, one rounding)."""
     _req(x.dim() == 2 and x.stride(1) == 1 and w.dtype == x.dtype, "bad rmsnorm args")
     out = torch.empty_like(x)
-    check(lib().pe_rmsnorm(ptr(x), x.stride(0), x.shape[0], x.shape[1], ptr(w), eps, dcode(x.dtype), ptr(out),
-                           out.stride(0), stream_ptr()), "pe_rmsnorm")
+    check(lib().pe_rmsnorm_ex(ptr(x), x.stride(0), x.shape[0], x.shape[1], ptr(w), eps, dcode(x.dtype), int(mode),
+                              ptr(out), out.stride(0), stream_ptr()), "pe_rmsnorm_ex")
     return out
 
 

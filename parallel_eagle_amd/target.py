@@ -73,7 +73,14 @@ class TreeKVCache:
     def layers(self) -> list[_LayerView]:
         return [_LayerView(self, i) for i in range(self.shape.num_layers)]
 
+    def buffers(self) -> tuple[int, int, int]:
+        """(K pointer, V pointer, capacity): what a captured step baked in."""
+        return self.k.data_ptr(), self.v.data_ptr(), self.capacity
+
     def ensure_capacity(self, n: int) -> None:
+        """Grow to at least ``n`` rows. Growing replaces the K/V buffers (a copy of
+        the cached rows); a ``VerifyStep`` built on the old buffers refuses to run
+        afterwards."""
         if n <= self.capacity:
             return
         cap = max(n, 2 * self.capacity)
@@ -85,9 +92,85 @@ class TreeKVCache:
         self.k, self.v, self.capacity = k, v, cap
 
 
-class _Module:
-    def __init__(self, weight):
-        self.weight = weight
+class _SharedModule(torch.nn.Module):
+    """A frozen module over the target's device tensors. The reference's drafter
+    keeps these in tuples and only calls them (src/pe/drafter.py:81-83,120,123,
+    161); ``to`` checks the request instead of copying, because the pass keeps
+    pointers to the same tensors."""
+
+    def __init__(self, weight: torch.Tensor):
+        super().__init__()
+        object.__setattr__(self, "_w", weight)
+
+    @property
+    def weight(self) -> torch.Tensor:
+        return self._w
+
+    def to(self, *args, **kwargs):
+        dev, dt, _, _ = torch._C._nn._parse_to(*args, **kwargs)
+        if dev is not None and torch.device(dev) != self._w.device and not (
+                torch.device(dev).type == self._w.device.type and torch.device(dev).index is None):
+            raise ValueError(f"shared target module lives on {self._w.device}")
+        if dt is not None and dt != self._w.dtype:
+            raise ValueError(f"shared target module computes in {self._w.dtype}")
+        return self
+
+    def requires_grad_(self, requires_grad: bool = True):
+        return self
+
+    def _rows(self, x: torch.Tensor, width: int) -> torch.Tensor:
+        if not x.is_cuda:
+            raise ValueError("parallel_eagle_amd modules take HIP device tensors")
+        if x.dtype != self._w.dtype:
+            raise TypeError(f"expected {self._w.dtype} input, got {x.dtype}")
+        if x.shape[-1] != width:
+            raise ValueError(f"expected last dimension {width}, got {x.shape[-1]}")
+        return x.reshape(-1, width).contiguous()
+
+
+class DeviceEmbedding(_SharedModule):
+    """The target's embed_tokens (HF modeling_llama.py:381): ids of any shape ->
+    rows (*ids.shape, H), gathered by pe_embed; an id outside the vocabulary
+    raises."""
+
+    def __init__(self, weight: torch.Tensor, status: torch.Tensor):
+        super().__init__(weight)
+        object.__setattr__(self, "_status", status)
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        ids = torch.as_tensor(ids, device=self._w.device)
+        flat = ids.reshape(-1).to(torch.int64).contiguous()
+        out = ops.embed(flat, self._w, self._status)
+        ops.read_status(self._status, "embedding")
+        return out.view(*ids.shape, self._w.shape[1])
+
+
+class DeviceRMSNorm(_SharedModule):
+    """The target's final norm (HF LlamaRMSNorm, modeling_llama.py:62-67):
+    ``w * round(x * rsqrt(mean(x^2) + eps))`` with fp32 statistics, by pe_rmsnorm."""
+
+    def __init__(self, weight: torch.Tensor, eps: float):
+        super().__init__(weight)
+        self.variance_epsilon = float(eps)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        rows = self._rows(x, self._w.shape[0])
+        return ops.rmsnorm(rows, self._w, self.variance_epsilon).view(x.shape)
+
+
+class DeviceLMHead(_SharedModule):
+    """The target's lm_head (HF modeling_llama.py:480, ``F.linear`` without bias):
+    hidden (*, H) -> logits (*, V) in the model dtype, by pe_dense_gemm on the
+    tiled weight. ``weight`` is the logical [V][H] matrix."""
+
+    def __init__(self, logical: torch.Tensor, tiled: torch.Tensor):
+        super().__init__(logical)
+        object.__setattr__(self, "_tiled", tiled)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        v, h = self._w.shape
+        rows = self._rows(x, h)
+        return ops.linear(rows, v, dense=self._tiled).view(*x.shape[:-1], v)
 
 
 class TargetModel:
@@ -150,14 +233,17 @@ class TargetModel:
     def device(self) -> torch.device:
         return self.model.device
 
-    def get_input_embeddings(self):
-        return _Module(self.model.embed)
+    def get_input_embeddings(self) -> DeviceEmbedding:
+        """Callable embedding module over the device table (target.py:150-151)."""
+        return DeviceEmbedding(self.model.embed, torch.zeros(4, dtype=torch.int32, device=self.device))
 
-    def get_lm_head(self):
-        return _Module(self.model.lm_head_logical)
+    def get_lm_head(self) -> DeviceLMHead:
+        """Callable lm_head module (target.py:153-154)."""
+        return DeviceLMHead(self.model.lm_head_logical, self.model.lm_head)
 
-    def get_final_norm(self):
-        return _Module(self.model.final_norm)
+    def get_final_norm(self) -> DeviceRMSNorm:
+        """Callable final RMSNorm with HF rounding (target.py:156-159)."""
+        return DeviceRMSNorm(self.model.final_norm, self.shape.rms_eps)
 
     # ------------------------------------------------------------ cache
     def make_cache(self, capacity: int | None = None) -> TreeKVCache:
@@ -348,6 +434,14 @@ class VerifyStep:
         a.workspace, a.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
         a.status = target.status.data_ptr()
         self._args = a
+        self._buffers = cache.buffers()
+
+    def _check_cache(self) -> None:
+        """The pass arguments hold the cache's K/V pointers and capacity from
+        construction; a cache that has grown since (ensure_capacity replaced the
+        buffers) would be written through freed memory."""
+        if self.cache.buffers() != self._buffers:
+            raise RuntimeError("the KV cache was reallocated after this VerifyStep was built; build a new step")
 
     def load_tree(self, node_tokens, parents, root_logit: torch.Tensor) -> None:
         """Copy a tree and the root logit into the static buffers (stream-ordered)."""
@@ -359,6 +453,7 @@ class VerifyStep:
 
     def launch(self) -> None:
         """Enqueue masks -> forward -> acceptance -> compaction on the current stream."""
+        self._check_cache()
         L, st = _lib.load(), ops.stream_ptr()
         c, s = self.cache, self.tm.shape
         _lib.check(L.pe_tree_masks(self.parents.data_ptr(), self.T, self.P, self.bits.data_ptr(), self.words,
@@ -383,6 +478,7 @@ class VerifyStep:
         self.graph = g
 
     def run(self) -> None:
+        self._check_cache()
         if self.graph is not None:
             self.graph.replay()
         else:

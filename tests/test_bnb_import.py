@@ -48,7 +48,7 @@ def _mutate_state(sd, **changes):
 
 
 @pytest.mark.parametrize("case", ["fp4", "block128", "shape", "quant_map", "missing", "absmax_dtype", "garbled",
-                                  "nested_short"])
+                                  "nested_short", "fp16_compute", "no_compute_dtype"])
 def test_read_linear4bit_rejects_what_the_kernels_cannot_run(case):
     sd, *_ = _linear(nested=case == "nested_short")
     if case == "fp4":
@@ -69,8 +69,30 @@ def test_read_linear4bit_rejects_what_the_kernels_cannot_run(case):
         sd["blk.lin.weight.quant_state.bitsandbytes__nf4"] = torch.tensor([0xff, 0xfe, 0x00], dtype=torch.uint8)
     elif case == "nested_short":
         sd["blk.lin.weight.nested_absmax"] = sd["blk.lin.weight.nested_absmax"][:0]
+    elif case == "fp16_compute":
+        # quantised for an fp16 model: running it in bf16 would change its logits
+        sd = _mutate_state(sd, dtype="float16")
+    elif case == "no_compute_dtype":
+        sd = _mutate_state(sd, dtype="")
     with pytest.raises(bnb.CheckpointError):
         bnb.read_linear4bit(sd, "blk.lin.")
+
+
+def test_torch_prefixed_compute_dtype_is_accepted():
+    sd, *_ = _linear()
+    lin = bnb.read_linear4bit(_mutate_state(sd, dtype="torch.bfloat16"), "blk.lin.")
+    assert (lin.n, lin.k) == (64, 256)
+
+
+def test_fp16_dense_tensors_of_an_nf4_checkpoint_are_refused():
+    """The embedding, norms and lm_head of an fp16 checkpoint name an fp16 model
+    (the reference computes in the embedding's dtype, src/pe/target.py:89)."""
+    from parallel_eagle_amd.config import ModelShape
+    shape = ModelShape(name="t", num_layers=1, hidden=256, num_heads=2, num_kv_heads=2, head_dim=128,
+                       intermediate=256, vocab=64, weight_format="nf4")
+    sd = {"model.embed_tokens.weight": torch.zeros(64, 256, dtype=torch.float16)}
+    with pytest.raises(bnb.CheckpointError, match="bfloat16"):
+        bnb.weights_from_state_dict(shape, sd, device="cpu")
 
 
 def test_nf4_code_book_of_the_importer_is_the_oracles():

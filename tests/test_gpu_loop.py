@@ -1,0 +1,212 @@
+"""The reference's decode loop and its drafter interface over the device path.
+
+- Losslessness (tests/test_lossless.py:56-62 of the reference): the tree loop
+  of src/pe/serve.py:221-355, driven through forward_cached / propose_tree /
+  accept_tree_cached / gather_cache / crop, emits exactly the tokens of greedy
+  decoding (src/pe/decode/baselines.py:49-94) through the same API: exactly on
+  the tiny fp32 model, and at the 7B width in bf16 up to a near tie of the
+  greedy decode itself. The device-resident loop (SpeculativeDecoder) emits
+  the same tokens. Drafters: an untrained device drafter (the miss path: one
+  token at a time) and one that is told the greedy continuation at some depths
+  (accepted paths of every length, compaction across steps).
+- The shared modules a reference drafter calls (src/pe/drafter.py:81-83,120,
+  123,161): get_input_embeddings / get_lm_head / get_final_norm are callable
+  and agree with the oracle.
+"""
+
+import random
+
+import pytest
+import torch
+
+from oracle import drafter as od
+from oracle.model import rms_norm
+from parallel_eagle_amd import ops
+from parallel_eagle_amd.config import LLAMA2_7B_NF4, TINY_LLAMA
+from parallel_eagle_amd.drafter import DeviceDrafter
+from parallel_eagle_amd.serve import SpeculativeDecoder, generate_speculative_cached, vanilla_generate_cached
+from parallel_eagle_amd.target import TargetModel
+from tests.test_oracle_pins import _drafter_weights
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+class PeekingDrafter:
+    """A drafter that, per depth and with probability ``p``, replaces its logits
+    by a peak at the token greedy decoding puts there (``greedy`` = prompt +
+    greedy continuation): depth d of a call with n confirmed tokens predicts
+    greedy[n + d]. The loop must stay lossless whatever the drafter proposes."""
+
+    def __init__(self, inner, greedy: list[int], p: float, seed: int):
+        self.inner, self.greedy, self.p = inner, greedy, p
+        self.rng = random.Random(seed)
+
+    def draft_logits(self, ctx, feats, k):
+        lg = self.inner.draft_logits(ctx, feats, k).clone()
+        n = ctx.numel()
+        for d in range(k):
+            if n + d < len(self.greedy) and self.rng.random() < self.p:
+                lg[d] = lg[d].min()
+                lg[d, self.greedy[n + d]] = 30.0
+        return lg
+
+
+def _tiny():
+    tm = TargetModel.synthetic(TINY_LLAMA, seed=1, device=DEV, norm_noise=0.1, cache_capacity=256)
+    w, _ = _drafter_weights(TINY_LLAMA, 2, len(tm.feature_layers), torch.float32, seed=5, std=0.05)
+    return tm, DeviceDrafter(tm, w, max_depth=5, capacity=256)
+
+
+@pytest.mark.parametrize("p", [0.0, 0.6, 0.95])
+def test_tree_loop_is_lossless_on_the_tiny_fp32_model(p):
+    tm, dr = _tiny()
+    prompt = [1, 2, 3, 4, 5, 6]
+    n = 48
+    ref = vanilla_generate_cached(tm, prompt, n)
+    drafter = PeekingDrafter(dr, prompt + ref.output_ids, p, seed=int(p * 100)) if p else dr
+    res = generate_speculative_cached(tm, drafter, prompt, k=5, mode="tree", max_new_tokens=n, tree_top_k=3,
+                                      tree_max_nodes=15)
+    assert res.output_ids == ref.output_ids
+    assert res.num_generated == n
+    if p >= 0.95:
+        assert res.acceptance_length > 2.0  # most steps commit several tokens
+    dev = SpeculativeDecoder(tm, PeekingDrafter(dr, prompt + ref.output_ids, p, seed=int(p * 100)) if p else dr,
+                             k=5, tree_top_k=3, tree_max_nodes=15).generate(prompt, n)
+    assert dev.output_ids == ref.output_ids
+    print(f"p={p}: steps {res.steps}, target calls {res.target_calls}, acceptance length "
+          f"{res.acceptance_length:.2f}; device loop {dev.steps} steps")
+
+
+def test_tree_loop_unknown_mode_is_refused():
+    tm, dr = _tiny()
+    with pytest.raises(ValueError):
+        generate_speculative_cached(tm, dr, [1, 2], k=3, mode="chain", max_new_tokens=4)
+
+
+def test_tree_loop_at_the_7b_width_bf16():
+    """Two 7B-width NF4 layers in bf16. The tree pass and the one-token pass that
+    greedy decoding uses compute the same logits in different row blocks, so a
+    bf16 rounding can flip a near tie; every token must match up to the first
+    such step, and that step's greedy top-1 / top-2 margin must be small."""
+    shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
+    tm = TargetModel.synthetic(shape, seed=4, device=DEV, norm_noise=0.1, cache_capacity=512)
+    w, _ = _drafter_weights(shape, 1, 3, torch.bfloat16, seed=6, std=shape.init_std)
+    dr = DeviceDrafter(tm, w, max_depth=5, capacity=512)
+    prompt = list(range(100, 140))
+    n = 64
+    ref = vanilla_generate_cached(tm, prompt, n)
+    res = generate_speculative_cached(tm, PeekingDrafter(dr, prompt + ref.output_ids, 0.8, seed=3), prompt, k=5,
+                                      max_new_tokens=n, tree_top_k=4, tree_max_nodes=26)
+    dev = SpeculativeDecoder(tm, PeekingDrafter(dr, prompt + ref.output_ids, 0.8, seed=3), k=5, tree_top_k=4,
+                             tree_max_nodes=26).generate(prompt, n)
+    print(f"7B width: acceptance length {res.acceptance_length:.2f}, steps {res.steps}")
+    for got in (res.output_ids, dev.output_ids):
+        if got == ref.output_ids:
+            continue
+        j = next(i for i, (a, b) in enumerate(zip(got, ref.output_ids)) if a != b)
+        lg = tm.forward(torch.tensor([prompt + ref.output_ids[:j]])).logits[0, -1].float()
+        top = lg.topk(2).values
+        margin = float(top[0] - top[1])
+        print(f"first difference at token {j}: greedy margin {margin:.4g}")
+        assert margin <= 0.0625, f"token {j} differs with a greedy margin of {margin:.4g}"
+
+
+# ------------------------------------------------------------------ the shared modules
+def test_shared_modules_are_callable_and_match_the_oracle():
+    shape = LLAMA2_7B_NF4.reduced(1, feature_layers=(1, 1, 1))
+    tm = TargetModel.synthetic(shape, seed=2, device=DEV, keep_logical=True, norm_noise=0.1)
+    hw = tm.model.host_weights()
+    emb, head, norm = tm.get_input_embeddings(), tm.get_lm_head(), tm.get_final_norm()
+    ids = torch.tensor([[5, 31999, 0], [7, 7, 123]])
+    assert torch.equal(emb(ids.to(DEV)).cpu(), hw["embed"][ids])
+    gen = torch.Generator().manual_seed(2)
+    x = (torch.randn(2, 3, shape.hidden, generator=gen) * 2).to(torch.bfloat16)
+    got = norm(x.to(DEV)).cpu()
+    want = rms_norm(x, hw["final_norm"], shape.rms_eps)
+    assert (got == want).float().mean() > 0.999
+    assert torch.all((got.float() - want.float()).abs() <= 2 ** -7 * want.float().abs())
+    h = want.to(DEV)
+    lg = head(h).cpu().float()
+    assert lg.shape == (2, 3, shape.vocab)
+    ref = want.float() @ hw["lm_head"].float().t()
+    assert torch.all((lg - ref).abs() <= 2e-2 + 2e-2 * ref.abs())
+    with pytest.raises(Exception):
+        emb(torch.tensor([shape.vocab]).to(DEV))  # outside the vocabulary
+
+
+class RefShapedDrafter(torch.nn.Module):
+    """A drafter built the way the reference's ParallelDrafter is (src/pe/drafter.py:
+    36-83,120-160,195-236): its own layers in torch, the target's embed, lm_head
+    and final norm kept in tuples and only called. Its layers follow nn.py in
+    fp32 (rms norm, RoPE, softmax attention with an additive bias, SwiGLU)."""
+
+    def __init__(self, target, w):
+        super().__init__()
+        self.w = w
+        s = target.shape
+        self.s = s
+        self._embed = (target.get_input_embeddings(),)
+        self._lm_head = (target.get_lm_head(),)
+        self._final_norm = (target.get_final_norm(),)
+
+    def real_input(self, ids, feats):
+        H = self.s.hidden
+        emb = self._embed[0](ids).float()
+        f = od.drafter_rms_norm(feats.float().unflatten(-1, (-1, H)), self.w["feat_norm"], self.s.rms_eps)
+        feat = f.flatten(-2) @ self.w["feat_proj"].t()
+        return torch.cat([emb, feat], -1) @ self.w["in_proj"].t()
+
+    def draft_logits(self, ids, feats, k):
+        s, w = self.s, self.w
+        p = ids.numel()
+        m = p + k - 1
+        x = torch.empty(m, s.hidden, device=ids.device)
+        x[:p] = self.real_input(ids, feats)
+        mask_vec = torch.cat([w["mask_emb"], w["h_shared"]]) @ w["in_proj"].t()
+        x[p:] = mask_vec
+        pos = od.draft_positions(p, k).to(ids.device).float()
+        bias = torch.zeros(m, m, device=ids.device).masked_fill_(~od.draft_allow_mask(p, k).to(ids.device), -1e30)
+        inv = 1.0 / (s.rope_theta ** (torch.arange(0, s.head_dim, 2, device=ids.device).float() / s.head_dim))
+        ang = pos[:, None] * inv[None, :]
+        cos, sin = torch.cat([ang, ang], -1).cos(), torch.cat([ang, ang], -1).sin()
+
+        def rope(t):  # t: (heads, m, hd)
+            half = t.shape[-1] // 2
+            return t * cos + torch.cat([-t[..., half:], t[..., :half]], -1) * sin
+
+        for lw in w["layers"]:
+            h = od.drafter_rms_norm(x, lw["attn_norm"], s.rms_eps)
+            q = rope((h @ lw["q"].t()).view(m, s.num_heads, s.head_dim).transpose(0, 1))
+            kk = rope((h @ lw["k"].t()).view(m, s.num_kv_heads, s.head_dim).transpose(0, 1))
+            vv = (h @ lw["v"].t()).view(m, s.num_kv_heads, s.head_dim).transpose(0, 1)
+            g = s.num_heads // s.num_kv_heads
+            kk, vv = kk.repeat_interleave(g, 0), vv.repeat_interleave(g, 0)
+            att = torch.softmax(q @ kk.transpose(-1, -2) / s.head_dim ** 0.5 + bias, -1) @ vv
+            x = x + att.transpose(0, 1).reshape(m, -1) @ lw["o"].t()
+            h = od.drafter_rms_norm(x, lw["mlp_norm"], s.rms_eps)
+            x = x + (torch.nn.functional.silu(h @ lw["gate"].t()) * (h @ lw["up"].t())) @ lw["down"].t()
+        hidden = self._final_norm[0](x)
+        idx = [p - 1] + list(range(p, m))
+        return self._lm_head[0](hidden)[idx]
+
+
+def test_a_reference_shaped_drafter_runs_on_the_shared_modules():
+    """On the tiny fp32 target: the reference-shaped drafter (torch layers on the
+    GPU, the target's modules called through the accessors) gives the oracle's
+    draft logits, and so does the device drafter."""
+    tm = TargetModel.synthetic(TINY_LLAMA, seed=3, device=DEV, keep_logical=True, norm_noise=0.1)
+    hw = tm.model.host_weights()
+    w, _ = _drafter_weights(TINY_LLAMA, 2, len(tm.feature_layers), torch.float32, seed=8, std=0.05)
+    shared = {"embed": hw["embed"], "final_norm": hw["final_norm"], "lm_head": hw["lm_head"]}
+    gen = torch.Generator().manual_seed(8)
+    ids = torch.randint(0, TINY_LLAMA.vocab, (30,), generator=gen)
+    feats = torch.randn(30, tm.feature_dim, generator=gen)
+    want = od.OracleDrafter(TINY_LLAMA, w, shared, torch.float32).draft_logits(ids, feats, 5)
+    wd = {k: (v.to(DEV) if torch.is_tensor(v) else [{a: b.to(DEV) for a, b in x.items()} for x in v])
+          for k, v in w.items()}
+    got = RefShapedDrafter(tm, wd).draft_logits(ids.to(DEV), feats.to(DEV), 5).cpu()
+    assert torch.allclose(got, want, rtol=1e-4, atol=1e-4), float((got - want).abs().max())
+    dev = DeviceDrafter(tm, w, max_depth=5, capacity=64).draft_logits(ids.to(DEV), feats.to(DEV), 5).cpu()
+    assert torch.allclose(dev, want, rtol=1e-4, atol=1e-4), float((dev - want).abs().max())
+    _ = ops  # the modules launch the library's kernels (pe_embed, pe_rmsnorm, pe_dense_gemm)

@@ -79,19 +79,27 @@ def _margin(row: torch.Tensor) -> float:
     return float(v[0] - v[1])
 
 
-def _check_acceptance(gpu, ref, o_root, o_nodes, tokens, parents, tol):
+def _check_acceptance(gpu, ref, o_root, o_nodes, g_root, g_nodes):
+    """"exact" when the device's (path, bonus) equals the oracle's. Otherwise the
+    first row where the two walks decide differently must be a near tie of that
+    row: the oracle's top-1 / top-2 margin there at most twice the largest
+    |device - oracle| difference of that same row (two logits moving by that
+    much in opposite directions swap the order); anything else fails."""
     if gpu == ref:
         return "exact"
-    # walk the oracle's decisions: the first row where the GPU path diverges must be a near tie
     path_g, bonus_g = gpu
     path_r, bonus_r = ref
     i = 0
     while i < min(len(path_g), len(path_r)) and path_g[i] == path_r[i]:
         i += 1
-    row = o_root if i == 0 else o_nodes[path_r[i - 1]]
-    m = _margin(row)
-    assert m <= 2 * tol, f"acceptance differs at depth {i} with oracle margin {m:.4g} > {2 * tol:.4g}"
-    return f"near-tie at depth {i} (margin {m:.3g})"
+    node = None if i == 0 else path_r[i - 1]
+    o_row = o_root if node is None else o_nodes[node]
+    g_row = g_root if node is None else g_nodes[node]
+    row_err = float((g_row.float().cpu() - o_row.float()).abs().max())
+    m = _margin(o_row)
+    assert m <= 2 * row_err, (f"acceptance differs at depth {i}: oracle margin {m:.4g} > twice the deciding "
+                              f"row's logit error {row_err:.4g}")
+    return f"near-tie at depth {i} (margin {m:.3g}, row error {row_err:.3g})"
 
 
 def _fp32_oracle(shape, host_weights):
@@ -173,7 +181,7 @@ def _run_case(shape, seed, P, depth, widths, top_k, plant, tol, random_kv=False,
         assert ok_k and ok_v, f"layer {li} K/V rows differ: {kerr:.3g} / {verr:.3g}"
     gpu = accept_tree_cached(root_g[0, -1], lg[0], tokens, parents)
     ref = ov.accept_tree_cached(root_o[0, -1], o_lg[0], tokens, parents)
-    verdict = _check_acceptance(gpu, ref, root_o[0, -1], o_lg[0], tokens, parents, max(lerr, perr))
+    verdict = _check_acceptance(gpu, ref, root_o[0, -1], o_lg[0], root_g[0, -1], lg[0])
     # the acceptance kernel on the oracle's own logits must be bit-exact
     same = accept_tree_cached(root_o[0, -1].to(DEV), o_lg[0].to(DEV), tokens, parents)
     assert same == ref
@@ -199,13 +207,17 @@ def test_tiny_fp32_full_workload():
     assert max(accepted) >= 3  # the planted chains are accepted
 
 
-@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("seed", WORKLOADS["llama2-7b-nf4-T26-P2048"].seeds)
 def test_llama7b_nf4_width_two_layers(seed):
+    """All ten workload seeds; a planted chain of 1..5 accepted nodes each. The
+    committed path must equal the oracle's, except at a near tie of the deciding
+    row (reported, and bounded by that row's own logit error)."""
     wl = WORKLOADS["llama2-7b-nf4-T26-P2048"]
     shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
     v, n, err = _run_case(shape, seed, 48, wl.depth, wl.widths, wl.top_k, plant=lambda s: 1 + s % wl.depth,
                           tol=2e-2)
     print(f"seed {seed}: {v}, accepted {n}, max |dlogit| {err:.3g}")
+    assert v == "exact" or v.startswith("near-tie")
 
 
 @pytest.mark.parametrize("P", [130, 300])
@@ -247,14 +259,18 @@ def test_qwen14b_width_one_layer(shape):
     print(f"{shape.name}: {v}, accepted {n}, max |dlogit| {err:.3g}")
 
 
-@pytest.mark.parametrize("shape,P", [(WORKLOADS["tiny-fp32-T8-P64"].model, 64),
-                                     (LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2)), 300)],
-                         ids=["tiny-fp32", "llama7b-nf4-2layers"])
-def test_verify_step_graph_replays_match_eager_api(shape, P):
+@pytest.mark.parametrize("shape,P,plant", [(WORKLOADS["tiny-fp32-T8-P64"].model, 64, 2),
+                                           (LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2)), 300, 2),
+                                           (LLAMA2_7B_NF4, 2048, 5)],
+                         ids=["tiny-fp32", "llama7b-nf4-2layers", "llama7b-nf4-32layers-P2048"])
+def test_verify_step_graph_replays_match_eager_api(shape, P, plant):
     """The device-resident step (masks -> forward -> acceptance -> compaction),
     eager and replayed from a HIP graph, equals forward_cached + accept_tree_cached
     + gather_cache on the same inputs, bit for bit, on every replay with eager
-    work in between."""
+    work in between. The full 32-layer 7B model (the benchmark's workload, too
+    deep for the CPU oracle) is held to properties: every logit finite, and a
+    chain of the device's own greedy tokens planted to the tree's full depth is
+    accepted to that depth with the greedy bonus."""
     wl = WORKLOADS["llama2-7b-nf4-T26-P2048"] if shape.weight_format == "nf4" else WORKLOADS["tiny-fp32-T8-P64"]
     tm = TargetModel.synthetic(shape, seed=3, device=DEV, cache_capacity=P + 64)
     V = shape.vocab
@@ -263,8 +279,8 @@ def test_verify_step_graph_replays_match_eager_api(shape, P):
     pl, _, cache = tm.forward_cached(torch.tensor([prompt]), cache, torch.arange(P).unsqueeze(0))
     root = pl[0, -1].clone()
     tokens, parents = synth.tree_for_seed(3, V, wl.depth, wl.widths, wl.top_k)
-    # plant the device's greedy chain two deep so the walk and the compaction move rows
-    chain = synth.chain_nodes(parents, synth.deepest_first_leaf(parents))[:2]
+    # plant the device's greedy chain so the walk and the compaction move rows
+    chain = synth.chain_nodes(parents, synth.deepest_first_leaf(parents))[:plant]
     pos = [P + d for d in om.tree_depths(parents)]
     row = root
     for node in chain:
@@ -280,7 +296,9 @@ def test_verify_step_graph_replays_match_eager_api(shape, P):
     tm.gather_cache(cache, torch.tensor(list(range(P)) + [P + t for t in path_e], device=DEV))
     k_e = cache.k[:, :, : cache.seq_len].clone()
     v_e = cache.v[:, :, : cache.seq_len].clone()
-    assert len(path_e) >= 2
+    assert path_e[: len(chain)] == chain
+    assert bonus_e == int(lg_e[0, chain[-1]].float().argmax()) or len(path_e) > len(chain)
+    assert bool(torch.isfinite(lg_e.float()).all()) and bool(torch.isfinite(fu_e.float()).all())
     # device-resident step over the same starting cache
     cache.k.copy_(k0)
     cache.v.copy_(v0)
