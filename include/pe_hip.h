@@ -72,6 +72,14 @@ extern "C" {
 #define PE_NORM_FP32_WEIGHT 1 /* round(x * rsqrt(mean(x^2) + eps) * float(w)): one rounding,
                                  the drafter's RMSNorm (src/pe/nn.py:22-26) */
 
+/* attention softmax arithmetic */
+#define PE_ATTN_SDPA 0  /* fp32 softmax, unnormalised probabilities rounded to the dtype for PV, one
+                           division at the end: torch's scaled_dot_product_attention as HF calls it
+                           (integrations/sdpa_attention.py:79-154), the target's */
+#define PE_ATTN_EAGER 1 /* scores rounded to the dtype (dot product, then / sqrt(hd)), fp32 softmax,
+                           normalised probabilities rounded to the dtype before PV: the drafter's
+                           attention (src/pe/nn.py:84-87) */
+
 #define PE_TREE_MAX_WORDS 4 /* ancestor bitmask words per node: T <= 256 */
 
 const char* pe_status_string(int status);
@@ -269,6 +277,8 @@ typedef struct pe_model_desc {
   float rms_eps;
   int32_t norm_mode;        /* PE_NORM_* of the per-layer norms; the final norm is PE_NORM_HF */
   int32_t embed_rows;       /* rows of `embed` (ids must lie below); 0 = vocab */
+  int32_t attn_mode;        /* PE_ATTN_* of every layer */
+  int32_t _reserved;
   int64_t max_positions;
   const void* embed;        /* [embed_rows or V][H] */
   const void* final_norm;   /* [H] */

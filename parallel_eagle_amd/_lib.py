@@ -32,6 +32,7 @@ PE_EPI_STORE, PE_EPI_RESIDUAL, PE_EPI_SWIGLU = 0, 1, 2
 PE_MASK_TREE, PE_MASK_CAUSAL = 0, 1
 PE_QKV_PLAIN, PE_QKV_ROPE_PAIRED = 0, 1
 PE_NORM_HF, PE_NORM_FP32_WEIGHT = 0, 1
+PE_ATTN_SDPA, PE_ATTN_EAGER = 0, 1
 PE_TREE_MAX_WORDS = 4
 PE_PROPOSE_MAX_DEPTH, PE_PROPOSE_MAX_WIDTH, PE_PROPOSE_SCRATCH_PER_DEPTH = 16, 64, 512
 
@@ -68,7 +69,7 @@ class ModelDesc(C.Structure):
         ("num_layers", i32), ("hidden", i32), ("num_heads", i32), ("num_kv_heads", i32),
         ("head_dim", i32), ("intermediate", i32), ("vocab", i32), ("intermediate_padded", i32),
         ("dtype", i32), ("weight_format", i32), ("qkv_layout", i32), ("rms_eps", f32), ("norm_mode", i32),
-        ("embed_rows", i32), ("max_positions", i64),
+        ("embed_rows", i32), ("attn_mode", i32), ("_reserved", i32), ("max_positions", i64),
         ("embed", vp), ("final_norm", vp), ("lm_head", vp), ("rope_cos_sin", vp),
         ("attn_norm", C.POINTER(vp)), ("mlp_norm", C.POINTER(vp)),
         ("w_qkv", C.POINTER(vp)), ("a_qkv", C.POINTER(vp)), ("b_qkv", C.POINTER(vp)),

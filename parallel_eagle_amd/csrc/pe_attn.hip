@@ -449,13 +449,19 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   write_out(num, den);
 }
 
-// Generic path (fp32, any hd <= 256): one block per (row t, query head), all keys.
+// Generic path (fp32, any hd <= 256; and the eager semantics in any dtype):
+// one block per (row t, query head), all keys.
+// eager (PE_ATTN_EAGER, the drafter's attention, src/pe/nn.py:84-87): the
+// score is the dot product rounded to the dtype, divided by sqrt(hd) and
+// rounded again (the masked keys' -inf bias leaves them out); softmax in fp32;
+// each probability is normalised and rounded to the dtype before the PV
+// product, which accumulates in fp32 and is rounded once.
 template <int DT>
 __global__ __launch_bounds__(128) void attn_generic_kernel(
     const typename Elem<DT>::T* __restrict__ q, const typename Elem<DT>::T* __restrict__ kc,
     const typename Elem<DT>::T* __restrict__ vc, int64_t cap, int nh, int nkv, int hd, int T, int64_t P,
-    int mask_mode, const uint64_t* __restrict__ bits, int words, float scale, typename Elem<DT>::T* __restrict__ out,
-    int64_t ld_out, float* __restrict__ scores /* [T*nh][P+T] */) {
+    int mask_mode, const uint64_t* __restrict__ bits, int words, float scale, int eager,
+    typename Elem<DT>::T* __restrict__ out, int64_t ld_out, float* __restrict__ scores /* [T*nh][P+T] */) {
   typedef Elem<DT> E;
   const int t = blockIdx.x, hq = blockIdx.y;
   const int G = nh / nkv, kvh = hq / G;
@@ -473,7 +479,7 @@ __global__ __launch_bounds__(128) void attn_generic_kernel(
       const typename E::T* kr = kc + ((int64_t)kvh * cap + j) * hd;
       float acc = 0.f;
       for (int d = 0; d < hd; ++d) acc = fmaf(E::load(qr, d), E::load(kr, d), acc);
-      v = acc * scale;
+      v = eager ? E::round(__fdiv_rn(E::round(acc), sqrtf((float)hd))) : acc * scale;
     }
     sc[j] = v;
     lmax = fmaxf(lmax, v);
@@ -493,13 +499,17 @@ __global__ __launch_bounds__(128) void attn_generic_kernel(
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = lsum;
   __syncthreads();
   const float L = red[0] + red[1];
+  const float invL = 1.0f / L;
   for (int d = threadIdx.x; d < hd; d += blockDim.x) {
     float acc = 0.f;
     for (int64_t j = 0; j < S; ++j) {
       const float p = sc[j];
-      if (p != 0.f) acc = fmaf(E::round(p), E::load(vc + ((int64_t)kvh * cap + j) * hd, d), acc);
+      if (p != 0.f) {
+        const float pr = eager ? E::round(__fmul_rn(p, invL)) : E::round(p);
+        acc = fmaf(pr, E::load(vc + ((int64_t)kvh * cap + j) * hd, d), acc);
+      }
     }
-    E::store(out, (int64_t)t * ld_out + (int64_t)hq * hd + d, acc / L);
+    E::store(out, (int64_t)t * ld_out + (int64_t)hq * hd + d, eager ? acc : acc / L);
   }
 }
 
@@ -539,19 +549,23 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S) {
 
 }  // namespace
 
-extern "C" int64_t pe_attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_len, int dtype) {
+int64_t attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_len, int dtype, int attn_mode) {
   if (T <= 0 || nh <= 0 || nkv <= 0 || kv_len <= 0) return 0;
-  if (dtype != PE_DTYPE_F32 && hd == 128) {
+  if (dtype != PE_DTYPE_F32 && hd == 128 && attn_mode != PE_ATTN_EAGER) {
     AttnPlan p = attn_plan(T, nh, nkv, kv_len);
     return kAttnCounterBytes + p.opart_bytes + p.ml_bytes;
   }
   return (int64_t)T * nh * kv_len * 4;
 }
 
+extern "C" int64_t pe_attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_len, int dtype) {
+  return attention_workspace_bytes(T, nh, nkv, hd, kv_len, dtype, PE_ATTN_SDPA);
+}
+
 int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap, int nh,
                                int nkv, int hd, int T, int64_t P, int mask_mode, const uint64_t* bits, int words,
                                float scale, int dtype, void* out, int64_t ld_out, int out_units, void* workspace,
-                               int64_t workspace_bytes, int* counters, hipStream_t st) {
+                               int64_t workspace_bytes, int* counters, hipStream_t st, int attn_mode) {
   if (!q || !k_cache || !v_cache || !out || !workspace) return PE_ERR_ARG;
   if (out_units && (dtype == PE_DTYPE_F32 || hd != 128 || T > 64 || out_units * 128 != nh * hd)) return PE_ERR_ARG;
   if (T <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || hd <= 0 || hd > 256 || P < 0) return PE_ERR_ARG;
@@ -560,8 +574,11 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
   if (mask_mode == PE_MASK_TREE && (!bits || words <= 0 || words > PE_TREE_MAX_WORDS || T > 64 * words))
     return PE_ERR_TREE;
   const int64_t S = P + T;
-  if (workspace_bytes < pe_attention_workspace_bytes(T, nh, nkv, hd, S, dtype)) return PE_ERR_WORKSPACE;
-  if (dtype != PE_DTYPE_F32 && hd == 128) {
+  if (attn_mode != PE_ATTN_SDPA && attn_mode != PE_ATTN_EAGER) return PE_ERR_ARG;
+  const int eager = attn_mode == PE_ATTN_EAGER;
+  if (eager && out_units) return PE_ERR_ARG;
+  if (workspace_bytes < attention_workspace_bytes(T, nh, nkv, hd, S, dtype, attn_mode)) return PE_ERR_WORKSPACE;
+  if (dtype != PE_DTYPE_F32 && hd == 128 && !eager) {
     AttnPlan p = attn_plan(T, nh, nkv, S);
     if (p.splits > 1 && (int64_t)nkv * p.row_tiles * 4 > kAttnCounterBytes) return PE_ERR_ARG;
     if (!counters) counters = (int*)workspace;
@@ -588,20 +605,20 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
     case PE_DTYPE_F32:
       attn_generic_kernel<PE_DTYPE_F32><<<grid, 128, 0, st>>>((const float*)q, (const float*)k_cache,
                                                               (const float*)v_cache, cache_cap, nh, nkv, hd, T, P,
-                                                              mask_mode, bits, words, scale, (float*)out, ld_out,
-                                                              scores);
+                                                              mask_mode, bits, words, scale, eager, (float*)out,
+                                                              ld_out, scores);
       break;
     case PE_DTYPE_BF16:
       attn_generic_kernel<PE_DTYPE_BF16><<<grid, 128, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
                                                                (const uint16_t*)v_cache, cache_cap, nh, nkv, hd, T,
-                                                               P, mask_mode, bits, words, scale, (uint16_t*)out,
-                                                               ld_out, scores);
+                                                               P, mask_mode, bits, words, scale, eager,
+                                                               (uint16_t*)out, ld_out, scores);
       break;
     case PE_DTYPE_F16:
       attn_generic_kernel<PE_DTYPE_F16><<<grid, 128, 0, st>>>((const uint16_t*)q, (const uint16_t*)k_cache,
                                                               (const uint16_t*)v_cache, cache_cap, nh, nkv, hd, T, P,
-                                                              mask_mode, bits, words, scale, (uint16_t*)out, ld_out,
-                                                              scores);
+                                                              mask_mode, bits, words, scale, eager,
+                                                              (uint16_t*)out, ld_out, scores);
       break;
     default:
       return PE_ERR_ARG;
@@ -615,5 +632,6 @@ extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void*
                                  float scale, int dtype, void* out, int64_t ld_out, void* workspace,
                                  int64_t workspace_bytes, void* stream) {
   return pe_internal_tree_attention(q, k_cache, v_cache, cache_cap, nh, nkv, hd, T, P, mask_mode, bits, words, scale,
-                                    dtype, out, ld_out, 0, workspace, workspace_bytes, nullptr, (hipStream_t)stream);
+                                    dtype, out, ld_out, 0, workspace, workspace_bytes, nullptr, (hipStream_t)stream,
+                                    PE_ATTN_SDPA);
 }

@@ -72,13 +72,16 @@ constexpr int kGemmCounterInts = 7168;
 constexpr int kPassAttnCounterInt = 7168;
 
 // pe_attn.hip: pe_tree_attention whose output is A-tiled when out_units > 0
-// (hd == 128 16-bit path only). counters: the launch's arrival counters
+// (hd == 128 16-bit path only), in softmax mode attn_mode (PE_ATTN_*). counters: the launch's arrival counters
 // (nullptr: the head of the workspace).
 PE_INTERNAL int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
                                            int nh, int nkv, int hd, int T, int64_t P, int mask_mode,
                                            const uint64_t* bits, int words, float scale, int dtype, void* out,
                                            int64_t ld_out, int out_units, void* workspace, int64_t workspace_bytes,
-                                           int* counters, hipStream_t st);
+                                           int* counters, hipStream_t st, int attn_mode = PE_ATTN_SDPA);
+// Workspace of pe_internal_tree_attention in the given PE_ATTN_* mode.
+PE_INTERNAL int64_t attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_len, int dtype,
+                                              int attn_mode);
 
 // MFMA-tiled 16-bit weights [N][K] back to row-major (the inverse of pe_dense_repack)
 int pe_internal_dense_untile(const void* tiled, int64_t N, int64_t K, void* out, hipStream_t st);

@@ -103,8 +103,8 @@ Layout make_layout(const pe_model_desc* m, int M, int64_t kv_len) {
     L.part = off; off += L.part_bytes;
   }
   L.attn_ws = off;
-  L.attn_ws_bytes = align_up(pe_attention_workspace_bytes(M, m->num_heads, m->num_kv_heads, m->head_dim, kv_len,
-                                                          m->dtype));
+  L.attn_ws_bytes = align_up(attention_workspace_bytes(M, m->num_heads, m->num_kv_heads, m->head_dim, kv_len,
+                                                       m->dtype, m->attn_mode));
   off += L.attn_ws_bytes;
   L.total = off;
   return L;
@@ -202,8 +202,8 @@ PrefillLayout make_prefill_layout(const pe_model_desc* m, int M, int64_t kv_len)
   if (H * ip > nw) nw = H * ip;
   if (H * qd > nw) nw = H * qd;
   L.wdeq = take(nw * 2);
-  L.attn_ws_bytes = align_up(pe_attention_workspace_bytes(M, m->num_heads, m->num_kv_heads, m->head_dim, kv_len,
-                                                          m->dtype));
+  L.attn_ws_bytes = align_up(attention_workspace_bytes(M, m->num_heads, m->num_kv_heads, m->head_dim, kv_len,
+                                                       m->dtype, m->attn_mode));
   L.attn_ws = take(L.attn_ws_bytes);
   L.blas_bytes = kBlasWorkspace;
   L.blas = take(L.blas_bytes);
@@ -307,7 +307,7 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
                                         a->prefix_len, a->status, m->dtype, st));
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, PE_MASK_CAUSAL,
                                       nullptr, 0, scale, m->dtype, attn, qd, 0, ws + Lp.attn_ws, Lp.attn_ws_bytes,
-                                      (int*)(ws + Lp.gemm) + kPassAttnCounterInt, st));
+                                      (int*)(ws + Lp.gemm) + kPassAttnCounterInt, st, m->attn_mode));
     PE_TRY(linear(attn, qd, m->w_o[l], m->a_o[l], H));
     PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, nullptr, nullptr, 0,
                                         nullptr, 0, st));
@@ -418,7 +418,7 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
                                     a->prefix_len, a->status, gws, gwsb, tiled, st));
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
                                       a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
-                                      Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st));
+                                      Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st, m->attn_mode));
     const void* a_o = m->a_o ? m->a_o[l] : nullptr;
     if (tiled) {
       PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, true, M, qd, m->w_o[l], a_o, H, part,
@@ -471,6 +471,9 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
   if (a->mask_mode == PE_MASK_TREE && !a->tree_bits) return PE_ERR_ARG;
   if (m->intermediate_padded % 32 || m->intermediate_padded < m->intermediate) return PE_ERR_ARG;
   if (m->norm_mode != PE_NORM_HF && m->norm_mode != PE_NORM_FP32_WEIGHT) return PE_ERR_ARG;
+  if (m->attn_mode != PE_ATTN_SDPA && m->attn_mode != PE_ATTN_EAGER) return PE_ERR_ARG;
+  // eager attention writes row-major output: not the A-tiled NF4 pass
+  if (m->attn_mode == PE_ATTN_EAGER && pe_wfmt_nf4(m->weight_format)) return PE_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   const int64_t kv_len = a->prefix_len + M;
   if (prefill_path(m, M, a->mask_mode)) {
@@ -549,7 +552,7 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
                        a->cache_capacity, a->prefix_len, a->status, st));
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
                                       a->tree_bits, a->bits_words, scale, m->dtype, attn, qd, 0, aws,
-                                      Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st));
+                                      Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st, m->attn_mode));
     PE_TRY(linear(m, attn, qd, M, qd, m->w_o[l], m->a_o ? m->a_o[l] : nullptr, H, PE_EPI_RESIDUAL, nullptr, h, H, h,
                   H, gws, gwsb, st));
     PE_TRY(pe_rmsnorm_ex(h, H, M, H, m->mlp_norm[l], m->rms_eps, m->dtype, m->norm_mode, xn, H, st));

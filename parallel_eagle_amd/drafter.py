@@ -20,6 +20,9 @@ slots (computed once). The drafter's own norms (feat_norm and each layer's two)
 multiply by the weight in fp32 and round once, as the reference's RMSNorm does
 (src/pe/nn.py:22-26, PE_NORM_FP32_WEIGHT); the shared final norm is the
 target's HF LlamaRMSNorm (the normalised row rounded, then the weight multiply).
+Its attention is the reference drafter's explicit softmax (src/pe/nn.py:84-87,
+PE_ATTN_EAGER): scores rounded to the dtype, probabilities normalised and
+rounded before the PV product.
 """
 
 from __future__ import annotations
@@ -87,6 +90,7 @@ class DeviceDrafter:
         for lw in weights["layers"]:
             core._add_layer({k: up(v) for k, v in lw.items()}, False)
         core.norm_mode = _lib.PE_NORM_FP32_WEIGHT
+        core.attn_mode = _lib.PE_ATTN_EAGER
         core._finish()
         self.core = core
         self.runner = TargetModel(core, cache_capacity=capacity)

@@ -80,6 +80,9 @@ class DeviceModel:
         # rounding of the per-layer RMSNorms (PE_NORM_*): HF's for a target; the
         # drafter's layer stack rounds once (src/pe/nn.py:22-26)
         self.norm_mode = _lib.PE_NORM_HF
+        # attention arithmetic (PE_ATTN_*): torch SDPA's for a target, the
+        # drafter's explicit softmax (src/pe/nn.py:84-87) for its layer stack
+        self.attn_mode = _lib.PE_ATTN_SDPA
         self._desc = None
         self._keep = []
 
@@ -272,6 +275,7 @@ class DeviceModel:
         d.rms_eps = s.rms_eps
         d.norm_mode = self.norm_mode
         d.embed_rows = self.embed.shape[0]
+        d.attn_mode = self.attn_mode
         d.max_positions = s.max_positions
         d.embed, d.final_norm = self.embed.data_ptr(), self.final_norm.data_ptr()
         d.lm_head, d.rope_cos_sin = self.lm_head.data_ptr(), self.cos_sin.data_ptr()

@@ -46,22 +46,30 @@ def test_draft_logits_match_oracle(target, n_layers, p, k):
     # of the same drafter; the device must be at least as close to it as the
     # reference's own bf16 arithmetic (the oracle): the fraction of logits within
     # rtol = atol = 2e-2 no lower (0.02 slack) and the relative L2 error no higher
-    # (10% slack). A single-layer drafter on random weights is less well
-    # conditioned than the target, so neither bf16 evaluation keeps 95% of its
-    # logits within 2e-2 of the other.
+    # (10% slack).
     r = ref32.float()
     inside = lambda a: ((a.float() - r).abs() <= 2e-2 * (1 + r.abs())).float().mean().item()
     rel = lambda a: ((a.float() - r).norm() / r.norm()).item()
     i_gpu, i_orc, e_gpu, e_orc = inside(got), inside(want), rel(got), rel(want)
     print(f"within 2e-2 of fp32: device {i_gpu:.4f}, oracle {i_orc:.4f}; relL2 device {e_gpu:.4g}, oracle {e_orc:.4g}")
-    assert i_gpu >= i_orc - 0.02 and i_gpu >= 0.8
+    assert i_gpu >= i_orc - 0.02
     assert e_gpu <= 1.1 * e_orc + 1e-6
     # element-wise against the oracle's restatement of the reference drafter
-    # (its norms round once, src/pe/nn.py:22-26, as the device's do)
+    # (its norms round once, src/pe/nn.py:22-26, and its attention rounds the
+    # scores and the normalised probabilities, nn.py:84-87, as the device's do)
     d = (got.float() - want.float()).abs()
     inside_o = (d <= 2e-2 + 2e-2 * want.float().abs()).float().mean().item()
     print(f"device vs oracle: max |d| {float(d.max()):.4g}, within 2e-2 {inside_o:.5f}")
-    assert inside_o >= 0.8, inside_o
+    # The reference's arithmetic rounds every attention score to bf16 before
+    # the softmax (about 0.06 at a score of 10): a score whose fp32 value lies
+    # within an fp32 ulp of a bf16 rounding boundary rounds to either side
+    # depending on the order of the dot product's sum, and that key's weight
+    # then moves by several per cent. Both sides follow the same rounding
+    # sequence; such flips leave about 1-2% of the logits outside 2e-2 for
+    # one layer. Two random layers are worse conditioned: each bf16 evaluation
+    # keeps only about 79% of its logits within 2e-2 of the fp32 one, and the
+    # two agree on about 92%.
+    assert inside_o >= (0.98 if n_layers == 1 else 0.9), inside_o
     # the greedy draft agrees with the fp32 evaluation wherever the oracle's does
     agree = (got.float().argmax(-1) == ref32.argmax(-1)) | (want.float().argmax(-1) != ref32.argmax(-1))
     assert bool(agree.all())
