@@ -233,6 +233,18 @@ int pe_argmax_rows(const void* x, int64_t ld, int rows, int64_t V, int dtype, in
 int pe_accept_tree(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V,
                    int dtype, const int64_t* node_tokens, const int32_t* parents, int32_t* out,
                    int32_t* scratch, void* stream);
+/* pe_accept_tree without a scratch argument and without any allocation: the
+ * scratch is a library-owned device array of PE_ACCEPT_NOALLOC_MAX_NODES + 2
+ * int32 per GPU (held until the process ends), its counter cleared by a small
+ * kernel before each walk. No counterpart in the reference: for callers that
+ * cannot allocate (HIP graph capture, serving loops that forbid hipMalloc).
+ * T > PE_ACCEPT_NOALLOC_MAX_NODES returns PE_ERR_TREE. Every call on one GPU
+ * shares that array: calls that overlap on one GPU (other streams, other
+ * threads) race. */
+#define PE_ACCEPT_NOALLOC_MAX_NODES (64 * PE_TREE_MAX_WORDS)
+int pe_accept_tree_noalloc(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V,
+                           int dtype, const int64_t* node_tokens, const int32_t* parents, int32_t* out,
+                           void* stream);
 /* Move accepted rows P + path[i] -> P + i in every layer's K and V, in place;
  * path read from a pe_accept_tree result on the device. Replaces
  * TargetModel.gather_cache (src/pe/target.py:194-201) for the keep index

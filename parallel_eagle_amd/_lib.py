@@ -35,6 +35,7 @@ PE_NORM_HF, PE_NORM_FP32_WEIGHT = 0, 1
 PE_ATTN_SDPA, PE_ATTN_EAGER = 0, 1
 PE_TREE_MAX_WORDS = 4
 PE_PROPOSE_MAX_DEPTH, PE_PROPOSE_MAX_WIDTH, PE_PROPOSE_SCRATCH_PER_DEPTH = 16, 64, 512
+PE_ACCEPT_NOALLOC_MAX_NODES = 64 * PE_TREE_MAX_WORDS
 
 _ERR_NAMES = {
     PE_ERR_ARG: "invalid argument",
@@ -127,6 +128,7 @@ SIGNATURES: dict[str, tuple] = {
                                     C.c_int, f32, C.c_int, vp, i64, vp, i64, vp]),
     "pe_argmax_rows": (C.c_int, [vp, i64, C.c_int, i64, C.c_int, vp, vp]),
     "pe_accept_tree": (C.c_int, [vp, vp, i64, C.c_int, i64, C.c_int, vp, vp, vp, vp, vp]),
+    "pe_accept_tree_noalloc": (C.c_int, [vp, vp, i64, C.c_int, i64, C.c_int, vp, vp, vp, vp]),
     "pe_propose_tree": (C.c_int, [vp, i64, C.c_int, i64, C.c_int, C.POINTER(C.c_int32), C.c_int, vp, vp,
                                   C.POINTER(C.c_int32), vp, vp, vp]),
     "pe_kv_compact": (C.c_int, [vp, vp, C.c_int, C.c_int, i64, C.c_int, C.c_int, i64, vp, vp]),

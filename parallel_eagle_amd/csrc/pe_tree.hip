@@ -18,6 +18,8 @@
 
 #include "pe_common.h"
 
+#include <mutex>
+
 namespace {
 
 __global__ void tree_masks_kernel(const int32_t* __restrict__ parents, int T, int64_t P, uint64_t* __restrict__ bits,
@@ -576,6 +578,29 @@ int check_accept_args(const void* root_logit, const void* node_logits, int T, in
   return PE_OK;
 }
 
+// The acceptance scratch of pe_accept_tree_noalloc: an arrival counter and
+// the row argmaxes of a tree of up to kWalkMax nodes. One copy per GPU, kept
+// for the life of the process; calls on one GPU share it.
+static __device__ __align__(256) int32_t scratch[kWalkMax + 2];
+
+// Device address of `scratch` per device (the array's name is a host-side
+// stand-in in host code), looked up once per device with that device current.
+int32_t* scratch_ptr() {
+  static std::mutex mu;
+  static int32_t* ptrs[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    ptrs[dev] = (int32_t*)p;
+  }
+  return ptrs[dev];
+}
+
+__global__ void zero_counter_kernel(int32_t* counter) { *counter = 0; }
+
 }  // namespace
 
 extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V, int dtype,
@@ -585,6 +610,21 @@ extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, i
   if (rc != PE_OK) return rc;
   if (!work) return PE_ERR_ARG;
   return launch_accept(root_logit, node_logits, ld, T, V, dtype, node_tokens, parents, out, work, (hipStream_t)stream);
+}
+
+extern "C" int pe_accept_tree_noalloc(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V,
+                                      int dtype, const int64_t* node_tokens, const int32_t* parents, int32_t* out,
+                                      void* stream) {
+  int rc = check_accept_args(root_logit, node_logits, T, V, dtype, node_tokens, parents, out);
+  if (rc != PE_OK) return rc;  // T > PE_ACCEPT_NOALLOC_MAX_NODES: PE_ERR_TREE
+  int32_t* work = scratch_ptr();
+  if (!work) return PE_ERR_LAUNCH;
+  hipStream_t st = (hipStream_t)stream;
+  // the counter starts at zero: cleared by a kernel (no memset node if the
+  // caller captures this call in a graph)
+  zero_counter_kernel<<<1, 1, 0, st>>>(work);
+  PE_CHECK_LAUNCH();
+  return launch_accept(root_logit, node_logits, ld, T, V, dtype, node_tokens, parents, out, work, st);
 }
 
 extern "C" int pe_propose_tree(const void* logits, int64_t ld, int k, int64_t V, int dtype, const int32_t* widths,
