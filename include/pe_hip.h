@@ -256,6 +256,32 @@ int pe_kv_compact(void* k_cache, void* v_cache, int L, int nkv, int64_t cap, int
 int pe_kv_gather(void* k_cache, void* v_cache, int L, int nkv, int64_t cap, int hd, int dtype,
                  const int64_t* keep, int64_t n_keep, int32_t* status, void* stream);
 
+/* ------------------------------------------------------------ batched trees */
+/* The batched workload's per-sequence steps (no single reference function: the
+ * reference verifies one sequence at a time, src/pe/serve.py:289-314, and this
+ * is that step for each of `batch` sequences in one launch). Rows of sequence
+ * b are [seq_row0[b], seq_row0[b+1]) (device int32 [batch + 1]); parents are in
+ * each sequence's own node numbering. */
+/* tree_depths / tree_allow_mask / tree_position_ids (src/pe/masks.py:118-156)
+ * per sequence: positions = seq_prefix[b] + depth. */
+int pe_tree_masks_batch(const int32_t* parents, const int32_t* seq_row0, const int64_t* seq_prefix, int batch,
+                        int max_seq_rows, uint64_t* bits, int words, int64_t* positions, int32_t* depths,
+                        int32_t* status, void* stream);
+/* accept_tree_cached (src/pe/decode/verify.py:104-125) per sequence: root row
+ * root_logits + b * ld_root; out[b * (2 + max_seq_rows) + ...] as
+ * pe_accept_tree's out; scratch batch * (max_seq_rows + 2) int32, zero before
+ * the first call and left zero. */
+int pe_accept_tree_batch(const void* root_logits, int64_t ld_root, const void* node_logits, int64_t ld, int64_t V,
+                         int dtype, const int32_t* seq_row0, int batch, int max_seq_rows, const int64_t* node_tokens,
+                         const int32_t* parents, int32_t* out, int32_t* scratch, void* stream);
+/* gather_cache with the accepted-path keep index (src/pe/target.py:194-201,
+ * src/pe/serve.py:308-309) per sequence: in sequence b's cache (k_cache /
+ * v_cache + b * cache_seq_stride elements) rows seq_prefix[b] + path[i] move
+ * to seq_prefix[b] + i, the path read from pe_accept_tree_batch's out. */
+int pe_kv_compact_batch(void* k_cache, void* v_cache, int batch, int64_t cache_seq_stride, int L, int nkv,
+                        int64_t cap, int hd, int dtype, const int64_t* seq_prefix, const int32_t* accept_out,
+                        int max_seq_rows, void* stream);
+
 /* ------------------------------------------------------------ tree proposal */
 #define PE_PROPOSE_MAX_DEPTH 16
 #define PE_PROPOSE_MAX_WIDTH 64
@@ -329,10 +355,29 @@ typedef struct pe_pass_args {
   void* workspace;
   int64_t workspace_bytes;
   int32_t* status;
+  /* Batched verification (batch >= 1; 0 = the single sequence above): `batch`
+   * independent sequences, each a tree over its own cached prefix. Sequence b
+   * owns rows [seq_row0[b], seq_row0[b+1]) of the pass (device int32
+   * [batch + 1], seq_row0[0] = 0, seq_row0[batch] = M), its cache is k_cache /
+   * v_cache + b * cache_seq_stride elements (each [L][nkv][cache_capacity][hd])
+   * with seq_prefix[b] rows cached (device int64 [batch]); tree_bits of a row
+   * name nodes of its own sequence (pe_tree_masks_batch). prefix_len is the
+   * largest seq_prefix and max_seq_rows the largest row count: they size the
+   * launches. A row's K/V land at its sequence's rows [prefix, prefix + rows).
+   * 16-bit models with hd 128 and RoPE-paired q/k/v, PE_MASK_TREE. */
+  int32_t batch;
+  int32_t max_seq_rows;
+  const int32_t* seq_row0;
+  const int64_t* seq_prefix;
+  int64_t cache_seq_stride;
 } pe_pass_args;
 
 /* Workspace for pe_forward with up to M rows and kv_len = P + M keys. */
 int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int64_t kv_len);
+/* Workspace for a batched pe_forward: M rows in all, at most max_seq_rows per
+ * sequence, at most max_kv_len = prefix + rows keys per sequence. */
+int64_t pe_forward_batch_workspace_bytes(const pe_model_desc* m, int M, int max_seq_rows, int64_t max_kv_len,
+                                         int batch);
 /* The masked verification forward TargetModel.forward_cached
  * (src/pe/target.py:203-224 -> HF LlamaForCausalLM / Qwen2ForCausalLM forward,
  * modeling_llama.py:347-490): embeddings, L decoder layers with in-place KV

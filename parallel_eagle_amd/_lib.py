@@ -86,6 +86,7 @@ class PassArgs(C.Structure):
         ("tree_bits", vp), ("bits_words", i32), ("num_features", i32), ("feature_layers", i32 * 4),
         ("_pad", i32), ("k_cache", vp), ("v_cache", vp), ("cache_capacity", i64), ("logits", vp),
         ("fused", vp), ("workspace", vp), ("workspace_bytes", i64), ("status", vp),
+        ("batch", i32), ("max_seq_rows", i32), ("seq_row0", vp), ("seq_prefix", vp), ("cache_seq_stride", i64),
     ]
 
 
@@ -135,6 +136,11 @@ SIGNATURES: dict[str, tuple] = {
     "pe_kv_gather": (C.c_int, [vp, vp, C.c_int, C.c_int, i64, C.c_int, C.c_int, vp, i64, vp, vp]),
     "pe_forward_workspace_bytes": (i64, [C.POINTER(ModelDesc), C.c_int, i64]),
     "pe_forward": (C.c_int, [C.POINTER(ModelDesc), C.POINTER(PassArgs), vp]),
+    "pe_forward_batch_workspace_bytes": (i64, [C.POINTER(ModelDesc), C.c_int, C.c_int, i64, C.c_int]),
+    "pe_tree_masks_batch": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, vp, C.c_int, vp, vp, vp, vp]),
+    "pe_accept_tree_batch": (C.c_int, [vp, i64, vp, i64, i64, C.c_int, vp, C.c_int, C.c_int, vp, vp, vp, vp, vp]),
+    "pe_kv_compact_batch": (C.c_int, [vp, vp, C.c_int, i64, C.c_int, C.c_int, i64, C.c_int, C.c_int, vp, vp,
+                                      C.c_int, vp]),
 }
 
 _lib = None

@@ -71,12 +71,24 @@ constexpr int kVRow = 128 + 32;    // LDS row stride of a wave's V tile (element
 constexpr int kCmbRow = 128 + 4;   // LDS row stride of the wave merge (floats; 16-byte aligned rows)
 constexpr int kAttnMaxSplits = 16;
 
+// Batched attention (batch >= 1): grid.z runs over (sequence, row tile);
+// sequence b's query rows are rows [seq_row0[b], seq_row0[b+1]) of q, bits
+// and out, its keys the seq_prefix[b] cached rows plus its own node rows of
+// the cache at kc / vc + b * seq_stride. Row tiles past a sequence's rows
+// leave at once (all splits of such a tile alike, so no arrival is awaited).
+struct AttnBatch {
+  int batch, row_tiles;
+  const int32_t* seq_row0;
+  const int64_t* seq_prefix;
+  int64_t seq_stride;  // elements
+};
+
 template <int DT>
 __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
     int nh, int nkv, int T, int64_t P, int mask_mode, const uint64_t* __restrict__ bits, int words, float scale,
     int keys_per_split, int splits, int rows_pad, float* __restrict__ opart, float* __restrict__ mlpart,
-    int* __restrict__ counters, void* __restrict__ out, int64_t ld_out, int out_units) {
+    int* __restrict__ counters, void* __restrict__ out, int64_t ld_out, int out_units, AttnBatch bt) {
   constexpr int HD = 128;
   constexpr int kQBytes = 32 * kQStride * 2;
   constexpr int kVtBytes = 32 * kVRow * 2;  // one 32-key V block, row-major
@@ -84,7 +96,21 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   constexpr int kMain = kQBytes + kAttnWaves * kVtBytes;
   constexpr int kSmem = (kMain > kCmbBytes) ? kMain : kCmbBytes;
   __shared__ __align__(16) uint8_t smem[kSmem];
-  const int kvh = blockIdx.x, split = blockIdx.y, rt = blockIdx.z;
+  const int kvh = blockIdx.x, split = blockIdx.y;
+  int rt = blockIdx.z, seq = 0;
+  if (bt.batch > 0) {
+    seq = blockIdx.z / bt.row_tiles;
+    rt = blockIdx.z - seq * bt.row_tiles;
+    const int r0 = bt.seq_row0[seq];
+    T = bt.seq_row0[seq + 1] - r0;
+    P = bt.seq_prefix[seq];
+    if (rt * 32 >= T * (nh / nkv) || T <= 0) return;
+    q += (int64_t)r0 * nh * 128;
+    bits += (int64_t)r0 * words;
+    kc += seq * bt.seq_stride;
+    vc += seq * bt.seq_stride;
+    out = (char*)out + (int64_t)r0 * ld_out * 2;
+  }
   const int G = nh / nkv, rows = T * G;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 31, g = lane >> 5;
   const int64_t S = P + T;
@@ -394,9 +420,10 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   }
   // partial[pair][split][row][128] and ml[pair][split][row][4] (m, l, -, -),
   // pair = kvh * row_tiles + rt
-  const int row_tiles = rows_pad >> 5;
-  const int pair = kvh * row_tiles + rt;
-  const uint32_t nrows = (uint32_t)(nkv * row_tiles * splits * 32);
+  const int row_tiles = bt.batch > 0 ? bt.row_tiles : rows_pad >> 5;
+  const int nseq = bt.batch > 0 ? bt.batch : 1;
+  const int pair = (seq * nkv + kvh) * row_tiles + rt;
+  const uint32_t nrows = (uint32_t)(nseq * nkv * row_tiles * splits * 32);
   const __amdgpu_buffer_rsrc_t ro = agent_rsrc(opart, nrows * HD * 4), rm = agent_rsrc(mlpart, nrows * 16);
   auto prow = [&](int sp) -> uint32_t { return (uint32_t)((pair * splits + sp) * 32 + row); };
   if (rr < rows) {  // padding rows of the tile are neither stored nor combined
@@ -522,7 +549,7 @@ struct AttnPlan {
   int64_t opart_bytes, ml_bytes;  // workspace: [counters | O partials | (m, l) partials]
 };
 
-AttnPlan attn_plan(int T, int nh, int nkv, int64_t S) {
+AttnPlan attn_plan(int T, int nh, int nkv, int64_t S, int batch = 1) {
   AttnPlan p;
   const int rows = T * (nh / nkv);
   p.row_tiles = (rows + 31) / 32;
@@ -530,7 +557,7 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S) {
   // about one 32-key block per wave (a wave takes up to a pair in one round),
   // with at most one workgroup per CU; longer caches give each wave more
   // rounds of pairs
-  const int64_t pairs = (int64_t)nkv * p.row_tiles;
+  const int64_t pairs = (int64_t)batch * nkv * p.row_tiles;
   int64_t want = ((S + 31) / 32 + kAttnWaves - 1) / kAttnWaves;
   int64_t cap_splits = 256 / pairs;
   if (cap_splits > kAttnMaxSplits) cap_splits = kAttnMaxSplits;
@@ -542,8 +569,8 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S) {
   kps = ((kps + 31) / 32) * 32;
   p.keys_per_split = (int)kps;
   p.splits = (int)pw;
-  p.opart_bytes = (int64_t)nkv * p.splits * p.rows_pad * 128 * 4;
-  p.ml_bytes = (int64_t)nkv * p.splits * p.rows_pad * 4 * 4;
+  p.opart_bytes = (int64_t)batch * nkv * p.splits * p.rows_pad * 128 * 4;
+  p.ml_bytes = (int64_t)batch * nkv * p.splits * p.rows_pad * 4 * 4;
   return p;
 }
 
@@ -588,11 +615,13 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
     if (dtype == PE_DTYPE_BF16) {
       attn_wg_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>(
           (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P, mask_mode,
-          bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters, out, ld_out, out_units);
+          bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters, out, ld_out, out_units,
+          AttnBatch{0, 0, nullptr, nullptr, 0});
     } else if (dtype == PE_DTYPE_F16) {
       attn_wg_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>(
           (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P, mask_mode,
-          bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters, out, ld_out, out_units);
+          bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters, out, ld_out, out_units,
+          AttnBatch{0, 0, nullptr, nullptr, 0});
     } else {
       return PE_ERR_ARG;
     }
@@ -623,6 +652,44 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
     default:
       return PE_ERR_ARG;
   }
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+int64_t pe_internal_attention_batch_bytes(int max_rows, int nh, int nkv, int64_t max_kv_len, int batch) {
+  const AttnPlan p = attn_plan(max_rows, nh, nkv, max_kv_len, batch);
+  return kAttnCounterBytes + p.opart_bytes + p.ml_bytes;
+}
+
+int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
+                                     int64_t seq_stride, int nh, int nkv, int max_rows, int64_t max_prefix, int batch,
+                                     const int32_t* seq_row0, const int64_t* seq_prefix, const uint64_t* bits,
+                                     int words, float scale, int dtype, void* out, int64_t ld_out, void* workspace,
+                                     int64_t workspace_bytes, int* counters, hipStream_t st) {
+  if (!q || !k_cache || !v_cache || !out || !workspace || !seq_row0 || !seq_prefix || !bits) return PE_ERR_ARG;
+  if (dtype == PE_DTYPE_F32 || batch <= 0 || max_rows <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || max_prefix < 0)
+    return PE_ERR_ARG;
+  if (max_prefix + max_rows > cache_cap) return PE_ERR_CAPACITY;
+  if (words <= 0 || words > PE_TREE_MAX_WORDS || max_rows > 64 * words) return PE_ERR_TREE;
+  const int64_t S = max_prefix + max_rows;
+  if (workspace_bytes < pe_internal_attention_batch_bytes(max_rows, nh, nkv, S, batch)) return PE_ERR_WORKSPACE;
+  const AttnPlan p = attn_plan(max_rows, nh, nkv, S, batch);
+  if (p.splits > 1 && (int64_t)batch * nkv * p.row_tiles * 4 > kAttnCounterBytes) return PE_ERR_ARG;
+  if (!counters) counters = (int*)workspace;
+  float* opart = (float*)((char*)workspace + kAttnCounterBytes);
+  float* ml = (float*)((char*)workspace + kAttnCounterBytes + p.opart_bytes);
+  const dim3 grid(nkv, p.splits, batch * p.row_tiles);
+  const AttnBatch bt{batch, p.row_tiles, seq_row0, seq_prefix, seq_stride};
+  if (dtype == PE_DTYPE_BF16)
+    attn_wg_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>(
+        (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, max_rows,
+        max_prefix, PE_MASK_TREE, bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters,
+        out, ld_out, 0, bt);
+  else
+    attn_wg_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>(
+        (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, max_rows,
+        max_prefix, PE_MASK_TREE, bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters,
+        out, ld_out, 0, bt);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }

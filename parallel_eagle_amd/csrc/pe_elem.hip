@@ -301,6 +301,27 @@ extern "C" int pe_embed(const int64_t* ids, int M, const void* table, int64_t V,
   return PE_OK;
 }
 
+__global__ void kv_offsets_kernel(const int32_t* __restrict__ seq_row0, const int64_t* __restrict__ seq_prefix,
+                                  int batch, int M, int64_t seq_stride, int64_t cap, int hd, int64_t* __restrict__ off,
+                                  int32_t* status) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= M) return;
+  int b = 0;
+  while (b + 1 < batch && seq_row0[b + 1] <= r) ++b;
+  const int64_t slot = seq_prefix[b] + (r - seq_row0[b]);
+  const bool ok = r >= seq_row0[b] && r < seq_row0[b + 1] && seq_prefix[b] >= 0 && slot < cap;
+  if (!ok && status) atomicOr(status, PE_ERR_CAPACITY);
+  off[r] = ok ? b * seq_stride + slot * hd : -1;
+}
+
+int pe_internal_kv_offsets(const int32_t* seq_row0, const int64_t* seq_prefix, int batch, int M, int64_t seq_stride,
+                           int64_t cap, int hd, int64_t* off, int32_t* status, hipStream_t st) {
+  if (!seq_row0 || !seq_prefix || !off || batch <= 0 || M <= 0) return PE_ERR_ARG;
+  kv_offsets_kernel<<<(M + 255) / 256, 256, 0, st>>>(seq_row0, seq_prefix, batch, M, seq_stride, cap, hd, off, status);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
 extern "C" int pe_rmsnorm_ex(const void* x, int64_t ldx, int M, int H, const void* w, float eps, int dtype, int mode,
                              void* out, int64_t ld_out, void* stream) {
   if (!x || !w || !out || M <= 0 || H <= 0) return PE_ERR_ARG;

@@ -74,9 +74,17 @@ struct EpiArgs {
   void* v_cache;
   int64_t cap;
   int64_t row0;
+  // batched passes: element offset of row `row`'s K/V slot in the caches
+  // (sequence base + (prefix + local row) * hd; head h adds h * cap * hd), a
+  // negative entry drops the row's K/V; null: rows row0 + row of one cache
+  const int64_t* kv_off;
   int nh, nkv, hd;
   int32_t* status;
 };
+
+__device__ __forceinline__ int64_t kv_row_elem(const EpiArgs& e, int row) {
+  return e.kv_off ? e.kv_off[row] : (e.row0 + row) * (int64_t)e.hd;
+}
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
@@ -137,8 +145,10 @@ __device__ __forceinline__ void write_rope_kv_core(const EpiArgs& e, int group, 
   }
   x1 = E::round(x1);
   x2 = E::round(x2);
+  const int64_t kvo = u >= e.nh ? kv_row_elem(e, row) : 0;
+  if (kvo < 0) return;
   if (u >= e.nh + e.nkv) {  // v: appended as is
-    T* dst = (T*)e.v_cache + ((int64_t)(u - e.nh - e.nkv) * e.cap + e.row0 + row) * e.hd;
+    T* dst = (T*)e.v_cache + (int64_t)(u - e.nh - e.nkv) * e.cap * e.hd + kvo;
     E::store(dst, d1, x1);
     E::store(dst, d2, x2);
     return;
@@ -150,7 +160,7 @@ __device__ __forceinline__ void write_rope_kv_core(const EpiArgs& e, int group, 
   const float o1 = __fadd_rn(E::round(__fmul_rn(x1, c1)), E::round(__fmul_rn(-x2, s1)));
   const float o2 = __fadd_rn(E::round(__fmul_rn(x2, c2)), E::round(__fmul_rn(x1, s2)));
   T* dst = (u < e.nh) ? (T*)e.q_out + ((int64_t)row * e.nh + u) * e.hd
-                      : (T*)e.k_cache + ((int64_t)(u - e.nh) * e.cap + e.row0 + row) * e.hd;
+                      : (T*)e.k_cache + (int64_t)(u - e.nh) * e.cap * e.hd + kvo;
   E::store(dst, d1, o1);
   E::store(dst, d2, o2);
 }
@@ -842,8 +852,10 @@ __device__ __forceinline__ void write_rope_kv4(const EpiArgs& e, int group, int 
       x2[i] = E::round(a2[i]);
     }
   }
+  const int64_t kvo = u >= e.nh ? kv_row_elem(e, row) : 0;
+  if (kvo < 0) return;
   if (u >= e.nh + e.nkv) {  // v: appended as is
-    T* dst = (T*)e.v_cache + ((int64_t)(u - e.nh - e.nkv) * e.cap + e.row0 + row) * e.hd;
+    T* dst = (T*)e.v_cache + (int64_t)(u - e.nh - e.nkv) * e.cap * e.hd + kvo;
     V::store(dst + d1, x1);
     V::store(dst + d2, x2);
     return;
@@ -866,7 +878,7 @@ __device__ __forceinline__ void write_rope_kv4(const EpiArgs& e, int group, int 
     o2[i] = E::round(__fadd_rn(E::round(__fmul_rn(x2[i], c2[i])), E::round(__fmul_rn(x1[i], s2[i]))));
   }
   T* dst = (u < e.nh) ? (T*)e.q_out + ((int64_t)row * e.nh + u) * e.hd
-                      : (T*)e.k_cache + ((int64_t)(u - e.nh) * e.cap + e.row0 + row) * e.hd;
+                      : (T*)e.k_cache + (int64_t)(u - e.nh) * e.cap * e.hd + kvo;
   V::store(dst + d1, o1);
   V::store(dst + d2, o2);
 }
@@ -1081,6 +1093,7 @@ EpiArgs make_epi(int epi, int mc, int N, const void* bias, const void* resid, in
   e.max_pos = 0;
   e.q_out = e.k_cache = e.v_cache = nullptr;
   e.cap = e.row0 = 0;
+  e.kv_off = nullptr;
   e.nh = e.nkv = e.hd = 0;
   e.status = nullptr;
   return e;
@@ -1121,10 +1134,10 @@ int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int64_t ldx, in
                              const void* wabs, int nh, int nkv, int hd, const void* bias,
                              const int64_t* positions, const void* cos_sin, int64_t max_pos, void* q_out,
                              void* k_cache, void* v_cache, int64_t cap, int64_t row0, int32_t* status, void* ws,
-                             int64_t ws_bytes, bool x_tiled, hipStream_t st) {
+                             int64_t ws_bytes, bool x_tiled, hipStream_t st, const int64_t* kv_off) {
   const int N = (nh + 2 * nkv) * hd;
   if (M > kMaxChunkRows || hd % 64 || !positions || !cos_sin || !q_out || !k_cache || !v_cache) return PE_ERR_ARG;
-  if (row0 < 0 || row0 + M > cap) return PE_ERR_CAPACITY;
+  if (!kv_off && (row0 < 0 || row0 + M > cap)) return PE_ERR_CAPACITY;
   int rc = check_gemm_args(x, M, K, w, N, PE_EPI_SWIGLU, nullptr, q_out);
   if (rc != PE_OK) return rc;
   const bool nf4 = pe_wfmt_nf4(wfmt);
@@ -1139,6 +1152,7 @@ int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int64_t ldx, in
   e.v_cache = v_cache;
   e.cap = cap;
   e.row0 = row0;
+  e.kv_off = kv_off;
   e.nh = nh;
   e.nkv = nkv;
   e.hd = hd;

@@ -21,7 +21,7 @@ PE_INTERNAL int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int
                                          const void* bias, const int64_t* positions, const void* cos_sin,
                                          int64_t max_pos, void* q_out, void* k_cache, void* v_cache, int64_t cap,
                                          int64_t row0, int32_t* status, void* ws, int64_t ws_bytes, bool x_tiled,
-                                         hipStream_t st);
+                                         hipStream_t st, const int64_t* kv_off = nullptr);
 PE_INTERNAL int64_t pe_internal_gemm_rope_kv_bytes(int M, int N, int K, int wfmt);
 // pe_nf4_gemm / pe_dense_gemm with A-tiled X (x_tiled, NF4 only, M <= 64)
 // and/or an A-tiled output (out_units = N_out / 128, not with the residual
@@ -82,6 +82,24 @@ PE_INTERNAL int pe_internal_tree_attention(const void* q, const void* k_cache, c
 // Workspace of pe_internal_tree_attention in the given PE_ATTN_* mode.
 PE_INTERNAL int64_t attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_len, int dtype,
                                               int attn_mode);
+
+// pe_attn.hip: tree attention of `batch` sequences in one launch (16-bit,
+// hd == 128): sequence b's query rows are [seq_row0[b], seq_row0[b+1]) of q,
+// bits and out (row-major), its cache kc / vc + b * seq_stride elements with
+// seq_prefix[b] cached rows; max_prefix and max_rows size the launch.
+PE_INTERNAL int64_t pe_internal_attention_batch_bytes(int max_rows, int nh, int nkv, int64_t max_kv_len, int batch);
+PE_INTERNAL int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const void* v_cache,
+                                                 int64_t cache_cap, int64_t seq_stride, int nh, int nkv, int max_rows,
+                                                 int64_t max_prefix, int batch, const int32_t* seq_row0,
+                                                 const int64_t* seq_prefix, const uint64_t* bits, int words,
+                                                 float scale, int dtype, void* out, int64_t ld_out, void* workspace,
+                                                 int64_t workspace_bytes, int* counters, hipStream_t st);
+// pe_elem.hip: per-row K/V slot offsets of a batched pass (see EpiArgs::kv_off):
+// off[r] = b * seq_stride + (seq_prefix[b] + r - seq_row0[b]) * hd for row r of
+// sequence b, or -1 (and PE_ERR_CAPACITY in *status) past the sequence's cache.
+PE_INTERNAL int pe_internal_kv_offsets(const int32_t* seq_row0, const int64_t* seq_prefix, int batch, int M,
+                                       int64_t seq_stride, int64_t cap, int hd, int64_t* off, int32_t* status,
+                                       hipStream_t st);
 
 // MFMA-tiled 16-bit weights [N][K] back to row-major (the inverse of pe_dense_repack)
 int pe_internal_dense_untile(const void* tiled, int64_t N, int64_t K, void* out, hipStream_t st);

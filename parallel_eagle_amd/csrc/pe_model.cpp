@@ -462,11 +462,157 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   return PE_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Batched verification: `batch` sequences, each a tree over its own cached
+// prefix, all M rows through every linear at once (each weight is streamed
+// once per 64-row chunk launch for the whole batch, not once per sequence);
+// attention runs over every sequence's own keys in one launch, and the q/k/v
+// epilogue appends each row's K/V at its own sequence's rows. Activations are
+// row-major (the A-tiled handoff is for single 64-row passes).
+// ---------------------------------------------------------------------------
+struct BatchLayout {
+  int64_t gemm, gemm_bytes, h, xn, q, attn, act, kvoff, attn_ws, attn_ws_bytes, total;
+};
+
+BatchLayout make_batch_layout(const pe_model_desc* m, int M, int max_rows, int64_t max_kv_len, int batch) {
+  BatchLayout L;
+  const int es = esize(m->dtype);
+  const int H = m->hidden, qd = m->num_heads * m->head_dim, ip = m->intermediate_padded;
+  const int nqkv = qd + 2 * m->num_kv_heads * m->head_dim;
+  const int mc = M < kFusedChunk ? M : kFusedChunk;
+  int64_t g = kCounterBytes;
+  const int64_t cand[5] = {pe_internal_gemm_rope_kv_bytes(mc, nqkv, H, m->weight_format),
+                           gemm_ws(m, M, H, qd, PE_EPI_RESIDUAL), gemm_ws(m, M, 2 * ip, H, PE_EPI_SWIGLU),
+                           gemm_ws(m, M, H, ip, PE_EPI_RESIDUAL),
+                           pe_gemm_workspace_bytes(M, m->vocab, H, PE_WFMT_DENSE, m->dtype, PE_EPI_STORE)};
+  for (int i = 0; i < 5; ++i)
+    if (cand[i] > g) g = cand[i];
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t o = off;
+    off += align_up(bytes);
+    return o;
+  };
+  L.gemm_bytes = align_up(g);
+  L.gemm = take(L.gemm_bytes);
+  L.h = take((int64_t)M * H * es);
+  L.xn = take((int64_t)M * H * es);
+  L.q = take((int64_t)M * qd * es);
+  L.attn = take((int64_t)M * qd * es);
+  L.act = take((int64_t)M * ip * es);
+  L.kvoff = take((int64_t)M * 8);
+  L.attn_ws_bytes =
+      align_up(pe_internal_attention_batch_bytes(max_rows, m->num_heads, m->num_kv_heads, max_kv_len, batch));
+  L.attn_ws = take(L.attn_ws_bytes);
+  L.total = off;
+  return L;
+}
+
+int forward_batched(const pe_model_desc* m, const pe_pass_args* a, const BatchLayout& Lb, hipStream_t st) {
+  const int M = a->M;
+  char* ws = (char*)a->workspace;
+  void* gws = ws + Lb.gemm;
+  const int64_t gwsb = Lb.gemm_bytes;
+  const int es = esize(m->dtype);
+  const int H = m->hidden, nh = m->num_heads, nkv = m->num_kv_heads, hd = m->head_dim;
+  const int qd = nh * hd, ip = m->intermediate_padded, L = m->num_layers, wf = m->weight_format;
+  char* h = ws + Lb.h;
+  char* xn = ws + Lb.xn;
+  char* q = ws + Lb.q;
+  char* attn = ws + Lb.attn;
+  char* act = ws + Lb.act;
+  int64_t* kvoff = (int64_t*)(ws + Lb.kvoff);
+  const float scale = (float)(1.0 / std::sqrt((double)hd));
+  const int64_t layer_stride = (int64_t)nkv * a->cache_capacity * hd * es;
+  const int64_t fused_ld = (int64_t)a->num_features * H;
+  int rc;
+#define PE_TRY(expr)            \
+  do {                          \
+    rc = (expr);                \
+    if (rc != PE_OK) return rc; \
+  } while (0)
+  auto slot_of = [&](int layer) -> int {
+    if (!a->fused) return -1;
+    for (int f = 0; f < a->num_features; ++f)
+      if (a->feature_layers[f] == layer) return f;
+    return -1;
+  };
+  auto slot_ptr = [&](int f) -> void* { return f < 0 ? nullptr : (char*)a->fused + (int64_t)f * H * es; };
+  auto copy_repeats = [&](int layer, int first) -> int {
+    if (first < 0) return PE_OK;
+    for (int f = first + 1; f < a->num_features; ++f) {
+      if (a->feature_layers[f] != layer) continue;
+      int r = pe_copy_rows(slot_ptr(first), fused_ld * es, M, (int64_t)H * es, slot_ptr(f), fused_ld * es, st);
+      if (r != PE_OK) return r;
+    }
+    return PE_OK;
+  };
+  PE_TRY(pe_internal_kv_offsets(a->seq_row0, a->seq_prefix, a->batch, M, a->cache_seq_stride, a->cache_capacity, hd,
+                                kvoff, a->status, st));
+  {
+    const int f0 = slot_of(0);
+    PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, embed_rows(m), h, H, m->attn_norm[0], m->rms_eps,
+                                     m->norm_mode, m->dtype, xn, nullptr, slot_ptr(f0), fused_ld, nullptr, 0,
+                                     a->status, st));
+    PE_TRY(copy_repeats(0, f0));
+  }
+  for (int l = 0; l < L; ++l) {
+    char* kc = (char*)a->k_cache + l * layer_stride;
+    char* vc = (char*)a->v_cache + l * layer_stride;
+    const void* a_qkv = m->a_qkv ? m->a_qkv[l] : nullptr;
+    const void* b_qkv = m->b_qkv ? m->b_qkv[l] : nullptr;
+    for (int c0 = 0; c0 < M; c0 += kFusedChunk) {
+      const int mc = M - c0 < kFusedChunk ? M - c0 : kFusedChunk;
+      PE_TRY(pe_internal_gemm_rope_kv(wf, m->dtype, xn + (int64_t)c0 * H * es, H, mc, H, m->w_qkv[l], a_qkv, nh, nkv,
+                                      hd, b_qkv, a->positions + c0, m->rope_cos_sin, m->max_positions,
+                                      q + (int64_t)c0 * qd * es, kc, vc, a->cache_capacity, 0, a->status, gws, gwsb,
+                                      false, st, kvoff + c0));
+    }
+    PE_TRY(pe_internal_tree_attention_batch(q, kc, vc, a->cache_capacity, a->cache_seq_stride, nh, nkv,
+                                            a->max_seq_rows, a->prefix_len, a->batch, a->seq_row0, a->seq_prefix,
+                                            a->tree_bits, a->bits_words, scale, m->dtype, attn, qd, ws + Lb.attn_ws,
+                                            Lb.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st));
+    const void* a_o = m->a_o ? m->a_o[l] : nullptr;
+    PE_TRY(pe_internal_linear(wf, m->dtype, attn, qd, false, M, qd, m->w_o[l], a_o, H, PE_EPI_RESIDUAL, nullptr, h, H,
+                              h, H, 0, gws, gwsb, st));
+    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn,
+                                        nullptr, nullptr, 0, nullptr, 0, st));
+    const void* a_gu = m->a_gu ? m->a_gu[l] : nullptr;
+    const void* a_down = m->a_down ? m->a_down[l] : nullptr;
+    PE_TRY(pe_internal_linear(wf, m->dtype, xn, H, false, M, H, m->w_gu[l], a_gu, 2 * ip, PE_EPI_SWIGLU, nullptr,
+                              nullptr, 0, act, ip, 0, gws, gwsb, st));
+    PE_TRY(pe_internal_linear(wf, m->dtype, act, ip, false, M, ip, m->w_down[l], a_down, H, PE_EPI_RESIDUAL, nullptr,
+                              h, H, h, H, 0, gws, gwsb, st));
+    const bool last = l + 1 == L;
+    const int fh = last ? -1 : slot_of(l + 1);
+    const int fx = last ? slot_of(L) : -1;
+    const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
+    const int next_mode = last ? PE_NORM_HF : m->norm_mode;
+    PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn, nullptr,
+                                        slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
+    PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
+  }
+  if (a->logits)
+    PE_TRY(pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
+                         m->vocab, gws, gwsb, st));
+#undef PE_TRY
+  return PE_OK;
+}
+
+extern "C" int64_t pe_forward_batch_workspace_bytes(const pe_model_desc* m, int M, int max_seq_rows,
+                                                    int64_t max_kv_len, int batch) {
+  if (!m || M <= 0 || max_seq_rows <= 0 || max_kv_len <= 0 || batch <= 0) return 0;
+  return make_batch_layout(m, M, max_seq_rows, max_kv_len, batch).total;
+}
+
 extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* stream) {
   if (!m || !a) return PE_ERR_ARG;
   const int M = a->M;
   if (M <= 0 || !a->input_ids || !a->positions || !a->k_cache || !a->v_cache || !a->workspace) return PE_ERR_ARG;
-  if (a->prefix_len < 0 || a->prefix_len + M > a->cache_capacity) return PE_ERR_CAPACITY;
+  // a batched pass appends at most max_seq_rows rows to any one cache (each
+  // row's slot is checked again on the device against its own prefix)
+  const int64_t appended = a->batch > 0 ? a->max_seq_rows : M;
+  if (a->prefix_len < 0 || a->prefix_len + appended > a->cache_capacity) return PE_ERR_CAPACITY;
   if (a->num_features < 0 || a->num_features > 4) return PE_ERR_ARG;
   if (a->mask_mode == PE_MASK_TREE && !a->tree_bits) return PE_ERR_ARG;
   if (m->intermediate_padded % 32 || m->intermediate_padded < m->intermediate) return PE_ERR_ARG;
@@ -475,6 +621,21 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
   // eager attention writes row-major output: not the A-tiled NF4 pass
   if (m->attn_mode == PE_ATTN_EAGER && pe_wfmt_nf4(m->weight_format)) return PE_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
+  if (a->batch < 0) return PE_ERR_ARG;
+  if (a->batch > 0) {
+    if (a->mask_mode != PE_MASK_TREE || !a->tree_bits || !a->seq_row0 || !a->seq_prefix) return PE_ERR_ARG;
+    if (m->dtype == PE_DTYPE_F32 || m->head_dim != 128 || m->qkv_layout != PE_QKV_ROPE_PAIRED ||
+        m->attn_mode != PE_ATTN_SDPA)
+      return PE_ERR_ARG;
+    if (a->bits_words <= 0 || a->bits_words > PE_TREE_MAX_WORDS || a->max_seq_rows <= 0 ||
+        a->max_seq_rows > 64 * a->bits_words || a->max_seq_rows > M)
+      return PE_ERR_TREE;
+    const int64_t per_seq = (int64_t)m->num_layers * m->num_kv_heads * a->cache_capacity * m->head_dim;
+    if (a->cache_seq_stride < per_seq) return PE_ERR_ARG;
+    const BatchLayout Lb = make_batch_layout(m, M, a->max_seq_rows, a->prefix_len + a->max_seq_rows, a->batch);
+    if (a->workspace_bytes < Lb.total) return PE_ERR_WORKSPACE;
+    return forward_batched(m, a, Lb, st);
+  }
   const int64_t kv_len = a->prefix_len + M;
   if (prefill_path(m, M, a->mask_mode)) {
     const PrefillLayout Lp = make_prefill_layout(m, M, kv_len);

@@ -22,9 +22,11 @@
 
 namespace {
 
-__global__ void tree_masks_kernel(const int32_t* __restrict__ parents, int T, int64_t P, uint64_t* __restrict__ bits,
-                                  int words, int64_t* __restrict__ positions, int32_t* __restrict__ depths,
-                                  int32_t* status) {
+// Depth, position P + depth and ancestor bits of the T nodes of one tree
+// (parents in the tree's own numbering), by the threads of one block.
+__device__ void tree_masks_rows(const int32_t* __restrict__ parents, int T, int64_t P, uint64_t* __restrict__ bits,
+                                int words, int64_t* __restrict__ positions, int32_t* __restrict__ depths,
+                                int32_t* status) {
   for (int t = threadIdx.x; t < T; t += blockDim.x) {
     uint64_t b[PE_TREE_MAX_WORDS] = {0ull, 0ull, 0ull, 0ull};
     int depth = 0;
@@ -44,6 +46,27 @@ __global__ void tree_masks_kernel(const int32_t* __restrict__ parents, int T, in
     if (positions) positions[t] = P + depth;
     if (depths) depths[t] = depth;
   }
+}
+
+__global__ void tree_masks_kernel(const int32_t* __restrict__ parents, int T, int64_t P, uint64_t* __restrict__ bits,
+                                  int words, int64_t* __restrict__ positions, int32_t* __restrict__ depths,
+                                  int32_t* status) {
+  tree_masks_rows(parents, T, P, bits, words, positions, depths, status);
+}
+
+// Batched trees: block b handles sequence b's rows [seq_row0[b], seq_row0[b+1]).
+__global__ void tree_masks_batch_kernel(const int32_t* __restrict__ parents, const int32_t* __restrict__ seq_row0,
+                                        const int64_t* __restrict__ seq_prefix, int max_rows,
+                                        uint64_t* __restrict__ bits, int words, int64_t* __restrict__ positions,
+                                        int32_t* __restrict__ depths, int32_t* status) {
+  const int b = blockIdx.x;
+  const int r0 = seq_row0[b], T = seq_row0[b + 1] - r0;
+  if (T < 0 || T > max_rows || r0 < 0) {
+    if (threadIdx.x == 0 && status) atomicOr(status, PE_ERR_TREE);
+    return;
+  }
+  tree_masks_rows(parents + r0, T, seq_prefix[b], bits + (int64_t)r0 * words, words,
+                  positions ? positions + r0 : nullptr, depths ? depths + r0 : nullptr, status);
 }
 
 __global__ void allow_dense_kernel(const uint64_t* __restrict__ bits, int T, int words, int64_t P,
@@ -199,13 +222,30 @@ __global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const typename
 // node whose token equals the current truth (at most kWalkMax nodes).
 constexpr int kWalkMax = 64 * PE_TREE_MAX_WORDS;
 
+// Batched trees (seq_row0 non-null): blockIdx.y = sequence b, whose root row
+// is root + b * ld_root, node rows start at row seq_row0[b], scratch at
+// work + b * (T + 2) and result at out + b * (T + 2), T being the largest
+// tree; blocks past the sequence's own node count leave at once.
 template <int DT>
 __global__ __launch_bounds__(kArgThreads) void accept_kernel(const typename Elem<DT>::T* __restrict__ root,
+                                                             int64_t ld_root,
                                                              const typename Elem<DT>::T* __restrict__ nodes,
                                                              int64_t ld, int64_t V, int32_t* __restrict__ work,
-                                                             int T, const int64_t* __restrict__ tokens,
+                                                             int T, const int32_t* __restrict__ seq_row0,
+                                                             const int64_t* __restrict__ tokens,
                                                              const int32_t* __restrict__ parents,
                                                              int32_t* __restrict__ out) {
+  if (seq_row0) {
+    const int b = blockIdx.y, r0 = seq_row0[b];
+    root += b * ld_root;
+    nodes += (int64_t)r0 * ld;
+    work += (int64_t)b * (T + 2);
+    out += (int64_t)b * (T + 2);
+    tokens += r0;
+    parents += r0;
+    T = min(max(seq_row0[b + 1] - r0, 0), T);
+    if ((int)blockIdx.x > T) return;
+  }
   int32_t* const counter = work;
   int32_t* const amax = work + 1;
   const int r = blockIdx.x;
@@ -259,9 +299,19 @@ __global__ __launch_bounds__(kArgThreads) void accept_kernel(const typename Elem
   }
 }
 
-// grid: (L * nkv, 2 for K/V); threads over 16-byte chunks of a row
+// grid: (L * nkv, 2 for K/V, batch); threads over 16-byte chunks of a row.
+// Batched (seq_prefix non-null): sequence b = blockIdx.z has its cache at
+// seq_bytes * b, its prefix seq_prefix[b] and its result at res + b * res_stride.
 __global__ void kv_compact_kernel(uint8_t* __restrict__ kc, uint8_t* __restrict__ vc, int64_t cap, int64_t row_bytes,
-                                  int64_t P, const int32_t* __restrict__ res) {
+                                  int64_t P, const int32_t* __restrict__ res, const int64_t* __restrict__ seq_prefix,
+                                  int64_t seq_bytes, int res_stride) {
+  if (seq_prefix) {
+    const int b = blockIdx.z;
+    P = seq_prefix[b];
+    res += (int64_t)b * res_stride;
+    kc += b * seq_bytes;
+    vc += b * seq_bytes;
+  }
   const int len = res[0];
   uint8_t* base = (blockIdx.y == 0 ? kc : vc) + (int64_t)blockIdx.x * cap * row_bytes;
   const int64_t nchunk = row_bytes / 16;
@@ -493,6 +543,19 @@ extern "C" int pe_tree_masks(const int32_t* parents, int T, int64_t P, uint64_t*
   return PE_OK;
 }
 
+extern "C" int pe_tree_masks_batch(const int32_t* parents, const int32_t* seq_row0, const int64_t* seq_prefix, int batch,
+                                   int max_seq_rows, uint64_t* bits, int words, int64_t* positions, int32_t* depths,
+                                   int32_t* status, void* stream) {
+  if (!parents || !seq_row0 || !seq_prefix || !bits || batch <= 0 || max_seq_rows <= 0 || words <= 0 ||
+      words > PE_TREE_MAX_WORDS)
+    return PE_ERR_ARG;
+  if (max_seq_rows > 64 * words) return PE_ERR_TREE;
+  tree_masks_batch_kernel<<<batch, 256, 0, (hipStream_t)stream>>>(parents, seq_row0, seq_prefix, max_seq_rows, bits,
+                                                                   words, positions, depths, status);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
 extern "C" int pe_tree_allow_dense(const uint64_t* bits, int T, int words, int64_t P, uint8_t* allow, void* stream) {
   if (!bits || !allow || T <= 0 || P < 0 || words <= 0 || words > PE_TREE_MAX_WORDS || T > 64 * words)
     return PE_ERR_ARG;
@@ -545,22 +608,27 @@ extern "C" int pe_argmax_rows(const void* x, int64_t ld, int rows, int64_t V, in
 
 namespace {
 
-int launch_accept(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V, int dtype,
-                  const int64_t* node_tokens, const int32_t* parents, int32_t* out, int32_t* work, hipStream_t st) {
+// batch == 0: one tree of T nodes; batch >= 1: seq_row0 [batch + 1] splits the
+// node rows into trees of at most T nodes each.
+int launch_accept(const void* root_logit, int64_t ld_root, const void* node_logits, int64_t ld, int T, int64_t V,
+                  int dtype, const int32_t* seq_row0, int batch, const int64_t* node_tokens, const int32_t* parents,
+                  int32_t* out, int32_t* work, hipStream_t st) {
+  const dim3 grid(T + 1, batch > 0 ? batch : 1);
   switch (dtype) {
     case PE_DTYPE_F32:
-      accept_kernel<PE_DTYPE_F32><<<T + 1, kArgThreads, 0, st>>>((const float*)root_logit, (const float*)node_logits,
-                                                                 ld, V, work, T, node_tokens, parents, out);
+      accept_kernel<PE_DTYPE_F32><<<grid, kArgThreads, 0, st>>>((const float*)root_logit, ld_root,
+                                                                (const float*)node_logits, ld, V, work, T, seq_row0,
+                                                                node_tokens, parents, out);
       break;
     case PE_DTYPE_BF16:
-      accept_kernel<PE_DTYPE_BF16><<<T + 1, kArgThreads, 0, st>>>((const uint16_t*)root_logit,
-                                                                  (const uint16_t*)node_logits, ld, V, work, T,
-                                                                  node_tokens, parents, out);
+      accept_kernel<PE_DTYPE_BF16><<<grid, kArgThreads, 0, st>>>((const uint16_t*)root_logit, ld_root,
+                                                                 (const uint16_t*)node_logits, ld, V, work, T,
+                                                                 seq_row0, node_tokens, parents, out);
       break;
     case PE_DTYPE_F16:
-      accept_kernel<PE_DTYPE_F16><<<T + 1, kArgThreads, 0, st>>>((const uint16_t*)root_logit,
-                                                                 (const uint16_t*)node_logits, ld, V, work, T,
-                                                                 node_tokens, parents, out);
+      accept_kernel<PE_DTYPE_F16><<<grid, kArgThreads, 0, st>>>((const uint16_t*)root_logit, ld_root,
+                                                                (const uint16_t*)node_logits, ld, V, work, T,
+                                                                seq_row0, node_tokens, parents, out);
       break;
     default:
       return PE_ERR_ARG;
@@ -609,7 +677,21 @@ extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, i
   int rc = check_accept_args(root_logit, node_logits, T, V, dtype, node_tokens, parents, out);
   if (rc != PE_OK) return rc;
   if (!work) return PE_ERR_ARG;
-  return launch_accept(root_logit, node_logits, ld, T, V, dtype, node_tokens, parents, out, work, (hipStream_t)stream);
+  return launch_accept(root_logit, 0, node_logits, ld, T, V, dtype, nullptr, 0, node_tokens, parents, out, work,
+                       (hipStream_t)stream);
+}
+
+extern "C" int pe_accept_tree_batch(const void* root_logits, int64_t ld_root, const void* node_logits, int64_t ld,
+                                    int64_t V, int dtype, const int32_t* seq_row0, int batch, int max_seq_rows,
+                                    const int64_t* node_tokens, const int32_t* parents, int32_t* out, int32_t* scratch,
+                                    void* stream) {
+  if (!root_logits || !node_logits || !seq_row0 || !node_tokens || !parents || !out || !scratch || batch <= 0 ||
+      max_seq_rows <= 0 || V <= 0 || ld_root < V || ld < V)
+    return PE_ERR_ARG;
+  if (dtype != PE_DTYPE_F32 && dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16) return PE_ERR_ARG;
+  if (max_seq_rows > kWalkMax) return PE_ERR_TREE;
+  return launch_accept(root_logits, ld_root, node_logits, ld, max_seq_rows, V, dtype, seq_row0, batch, node_tokens,
+                       parents, out, scratch, (hipStream_t)stream);
 }
 
 extern "C" int pe_accept_tree_noalloc(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V,
@@ -624,7 +706,7 @@ extern "C" int pe_accept_tree_noalloc(const void* root_logit, const void* node_l
   // caller captures this call in a graph)
   zero_counter_kernel<<<1, 1, 0, st>>>(work);
   PE_CHECK_LAUNCH();
-  return launch_accept(root_logit, node_logits, ld, T, V, dtype, node_tokens, parents, out, work, st);
+  return launch_accept(root_logit, 0, node_logits, ld, T, V, dtype, nullptr, 0, node_tokens, parents, out, work, st);
 }
 
 extern "C" int pe_propose_tree(const void* logits, int64_t ld, int k, int64_t V, int dtype, const int32_t* widths,
@@ -675,7 +757,23 @@ extern "C" int pe_kv_compact(void* k_cache, void* v_cache, int L, int nkv, int64
   if (row_bytes % 16) return PE_ERR_ARG;
   dim3 grid(L * nkv, 2);
   kv_compact_kernel<<<grid, 64, 0, (hipStream_t)stream>>>((uint8_t*)k_cache, (uint8_t*)v_cache, cap, row_bytes, P,
-                                                         accept_out);
+                                                         accept_out, nullptr, 0, 0);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+extern "C" int pe_kv_compact_batch(void* k_cache, void* v_cache, int batch, int64_t cache_seq_stride, int L, int nkv,
+                                   int64_t cap, int hd, int dtype, const int64_t* seq_prefix, const int32_t* accept_out,
+                                   int max_seq_rows, void* stream) {
+  if (!k_cache || !v_cache || !accept_out || !seq_prefix || batch <= 0 || L <= 0 || nkv <= 0 || hd <= 0 ||
+      max_seq_rows <= 0)
+    return PE_ERR_ARG;
+  const int64_t row_bytes = (int64_t)hd * esize(dtype);
+  if (row_bytes % 16 || cache_seq_stride < (int64_t)L * nkv * cap * hd) return PE_ERR_ARG;
+  dim3 grid(L * nkv, 2, batch);
+  kv_compact_kernel<<<grid, 64, 0, (hipStream_t)stream>>>((uint8_t*)k_cache, (uint8_t*)v_cache, cap, row_bytes, 0,
+                                                         accept_out, seq_prefix, cache_seq_stride * esize(dtype),
+                                                         2 + max_seq_rows);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }

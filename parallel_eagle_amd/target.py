@@ -56,6 +56,18 @@ class TreeKVCache:
                              device=device)
         self.v = torch.zeros_like(self.k)
         self.seq_len = 0
+        self.fixed = False  # a view into a batch cache: it cannot grow
+
+    @classmethod
+    def view(cls, shape: ModelShape, k: torch.Tensor, v: torch.Tensor) -> "TreeKVCache":
+        """A cache over existing K/V storage [L][nkv][capacity][hd] (one sequence
+        of a BatchKVCache); it cannot be reallocated."""
+        self = cls.__new__(cls)
+        self.shape, self.k, self.v = shape, k, v
+        self.capacity = int(k.shape[2])
+        self.seq_len = 0
+        self.fixed = True
+        return self
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
         return self.seq_len
@@ -83,6 +95,8 @@ class TreeKVCache:
         afterwards."""
         if n <= self.capacity:
             return
+        if self.fixed:
+            raise _lib.PEError(_lib.PE_ERR_CAPACITY, f"cache of {self.capacity} rows (part of a batch) needs {n}")
         cap = max(n, 2 * self.capacity)
         k = torch.zeros((self.k.shape[0], self.k.shape[1], cap, self.k.shape[3]), dtype=self.k.dtype,
                         device=self.k.device)
