@@ -410,6 +410,137 @@ def draft_line(wl, seed: int, reps: int = 10) -> dict:
                        "drafter_layers": 2, "eager": True}}
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def batch_line(wl, seed: int, steps: int, warmup: int, gemm_reps: int) -> dict:
+    """The batched workload: wl.batch sequences, each a wl.tree_nodes-node tree
+    over its own prefix (seeded lengths in [prefix_min, prefix_len]), one
+    BatchVerifyStep (masks -> batched pass -> per-sequence walks -> ragged
+    compaction) replayed from a HIP graph. Roofline: the NF4 GEMM launches of
+    one pass at M = batch * tree_nodes rows (each linear in 64-row launches),
+    replayed from a graph; FLOPs 2 * rows * N * K per launch against the dense
+    bf16 MFMA peak."""
+    import ctypes as C
+
+    import torch
+
+    from parallel_eagle_amd import _lib, ops, synth
+    from parallel_eagle_amd import batch as pb
+    from parallel_eagle_amd.config import algorithmic_bytes
+    from parallel_eagle_amd.target import TargetModel
+
+    shape, T, B = wl.model, wl.tree_nodes, wl.batch
+    prefixes = (synth.uniform_int(seed, 8, B, wl.prefix_len - wl.prefix_min + 1) + wl.prefix_min).tolist()
+    cap = max(prefixes) + T + 32
+    t0 = time.perf_counter()
+    tm = TargetModel.synthetic(shape, seed=seed, device="cuda:0", cache_capacity=cap)
+    torch.cuda.synchronize()
+    log(f"model {shape.name}: {tm.model.weight_bytes() / 1e9:.2f} GB of repacked layer weights "
+        f"in {time.perf_counter() - t0:.1f} s; prefixes {prefixes}")
+    cache = pb.BatchKVCache(tm, B, cap)
+    ops.fill_normal(cache.k, seed, synth.STREAM_KV, 1.0)
+    ops.fill_normal(cache.v, seed, synth.STREAM_KV_V, 1.0)
+    for b, P in enumerate(prefixes):
+        cache.seq(b).seq_len = P
+    trees = [synth.tree_for_seed(16 * seed + b, shape.vocab, wl.depth, wl.widths, wl.top_k) for b in range(B)]
+    tokens = [t for t, _ in trees]
+    parents = [p for _, p in trees]
+    roots = ops.fill_normal(torch.empty((B, shape.vocab), dtype=tm.dtype, device="cuda:0"), seed, 9, 1.0)
+    # plant each sequence's greedy chain (root argmax, then the pass's own node
+    # argmaxes) along its deepest first branch: every timed pass accepts full depth
+    chains = [synth.chain_nodes(p, synth.deepest_first_leaf(p)) for p in parents]
+    rows = [roots[b] for b in range(B)]
+    for d in range(wl.depth):
+        for b in range(B):
+            synth.set_token(tokens[b], parents[b], chains[b][d], int(rows[b].float().argmax()), shape.vocab)
+        step = pb.BatchVerifyStep(tm, cache, tokens, parents)
+        step.root.copy_(roots)
+        step.run()
+        torch.cuda.synchronize()
+        for b in range(B):
+            cache.seq(b).seq_len = prefixes[b]
+        rows = [step.logits[step.trees.row0[b] + chains[b][d]].clone() for b in range(B)]
+    step = pb.BatchVerifyStep(tm, cache, tokens, parents)
+    step.root.copy_(roots)
+    step.run()
+    res = step.results()
+    log(f"accepted per sequence: {[len(p) for p, _ in res]}")
+    ms, med_ms, _ = time_pass(step, steps, warmup)
+    if step.results() != res:
+        log("WARNING: graph replay accepted other paths than the eager pass")
+    pass_bytes = algorithmic_bytes(shape, prefixes, T)
+    M = B * T
+    lin = sum(n * k for _, n, k in shape.linear_shapes()) * shape.num_layers + shape.vocab * shape.hidden
+    kv_flops = sum(4 * shape.num_heads * shape.head_dim * T * (P + T) for P in prefixes) * shape.num_layers
+    pass_flops = 2 * M * lin + kv_flops
+    # the NF4 GEMM launches of one pass, replayed from a graph
+    L = _lib.load()
+    m = tm.model
+    H, ip, qd = shape.hidden, m.ipad, shape.q_dim
+    nqkv = qd + 2 * shape.kv_dim
+    bf = torch.bfloat16
+    xs = {k: (0.5 * torch.randn((M, k), device="cuda:0")).to(bf) for k in (H, qd, ip)}
+    outs = {n: torch.empty((M, n), dtype=bf, device="cuda:0") for n in (nqkv, H, ip)}
+    wsb = max(int(L.pe_gemm_workspace_bytes(M, n, k, _lib.PE_WFMT_NF4, _lib.PE_DTYPE_BF16, e))
+              for n, k, e in ((nqkv, H, 0), (H, qd, 1), (2 * ip, H, 2), (H, ip, 1)))
+    ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda:0")
+
+    def gemm(x, K, w, a, N, epi, out, resid=None):
+        _lib.check(L.pe_nf4_gemm(x.data_ptr(), K, M, K, w.data_ptr(), a.data_ptr(), N, epi, None,
+                                 resid.data_ptr() if resid is not None else None, N if resid is not None else 0,
+                                 out.data_ptr(), out.shape[1], ws.data_ptr(), wsb, ops.stream_ptr()), "pe_nf4_gemm")
+
+    def seq():
+        for ly in m.layers:
+            gemm(xs[H], H, ly["w_qkv"], ly["a_qkv"], nqkv, _lib.PE_EPI_STORE, outs[nqkv])
+            gemm(xs[qd], qd, ly["w_o"], ly["a_o"], H, _lib.PE_EPI_RESIDUAL, outs[H], resid=outs[H])
+            gemm(xs[H], H, ly["w_gu"], ly["a_gu"], 2 * ip, _lib.PE_EPI_SWIGLU, outs[ip])
+            gemm(xs[ip], ip, ly["w_down"], ly["a_down"], H, _lib.PE_EPI_RESIDUAL, outs[H], resid=outs[H])
+
+    seq()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        seq()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(gemm_reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    chunks = (M + 63) // 64
+    launches = 4 * shape.num_layers * chunks
+    gemm_s = e0.elapsed_time(e1) * 1e-3 / gemm_reps
+    gemm_flops = 2 * M * sum(n * k for _, n, k in shape.linear_shapes()) * shape.num_layers
+    tflops = gemm_flops / gemm_s / 1e12
+    log(f"batched pass {ms:.3f} ms; NF4 GEMMs {gemm_s * 1e3:.3f} ms per pass ({launches} launches), "
+        f"{tflops:.1f} TFLOP/s")
+    return {
+        "metric": "batched tree-verify pass latency + MFMA TFLOP/s (% of dense bf16 peak), "
+                  "Qwen2.5-14B-int4 B=8 T=26 KV~U[512,4096]",
+        "value": round(pass_flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": wl.name, "layers": shape.num_layers, "hidden": shape.hidden,
+                   "heads": f"{shape.num_heads}/{shape.num_kv_heads}", "intermediate": shape.intermediate,
+                   "vocab": shape.vocab, "weights": shape.weight_format, "batch": B, "tree_nodes": T,
+                   "rows": M, "prefix_lens": prefixes, "pass_bytes": pass_bytes, "pass_flops": pass_flops,
+                   "hip_graph": True},
+        "latency_ms_median": round(med_ms, 4),
+        "pass_gbs": round(pass_bytes / (ms * 1e-3) / 1e9, 1),
+        "accepted": [len(p) for p, _ in res],
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": f"nf4_gemm_kernel (row-major X, {M} rows in {chunks} launches of <= 64 rows per "
+                               f"linear: the {launches} launches of one pass)",
+                     "mean_launch_us": round(gemm_s * 1e6 / launches, 3)},
+        "cpu_baseline": None,
+    }
+
+
 def main(argv=None) -> int:
     a = parse_args(argv)
     if a.gpus != 1:
@@ -439,8 +570,8 @@ def main(argv=None) -> int:
         print(json.dumps(draft_line(wl, a.seed)))
         return 0
     if wl.batch != 1:
-        print(f"workload {wl.name} is batched; the bench measures the batch-1 pass", file=sys.stderr)
-        return 2
+        print(json.dumps(batch_line(wl, a.seed, a.steps, a.warmup, a.gemm_reps)), flush=True)
+        return 0
     tm, cache, step, (tokens, parents, path, bonus) = build_step(wl, a.seed)
     pass_bytes = algorithmic_bytes(wl.model, [wl.prefix_len], wl.tree_nodes)
     ms, med_ms, wall = time_pass(step, a.steps, a.warmup)

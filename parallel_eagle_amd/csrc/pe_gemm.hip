@@ -1174,8 +1174,14 @@ int pe_internal_linear(int wfmt, int dtype, const void* x, int64_t ldx, bool x_t
 }
 
 int64_t pe_internal_gemm_rope_kv_bytes(int M, int N, int K, int wfmt) {
-  if (M > kMaxChunkRows) M = kMaxChunkRows;
-  return workspace_of(make_plan(M, N, K, pe_wfmt_nf4(wfmt), kEpiRopeKV));
+  // callers with more rows launch 64-row chunks and a shorter last one
+  const bool nf4 = pe_wfmt_nf4(wfmt);
+  int64_t w = workspace_of(make_plan(M > kMaxChunkRows ? kMaxChunkRows : M, N, K, nf4, kEpiRopeKV));
+  if (M > kMaxChunkRows && M % kMaxChunkRows) {
+    const int64_t wr = workspace_of(make_plan(M % kMaxChunkRows, N, K, nf4, kEpiRopeKV));
+    if (wr > w) w = wr;
+  }
+  return w;
 }
 
 // Y = X . W^T as split partials partial[S][M][N] (fp32, plain stores: no
@@ -1251,8 +1257,17 @@ int pe_internal_swiglu_partials(const float* partial, int S, int M, int N, void*
 extern "C" int64_t pe_gemm_workspace_bytes(int M, int N, int K, int wfmt, int dtype, int epilogue) {
   if (dtype == PE_DTYPE_F32 && wfmt == PE_WFMT_DENSE) return 0;
   if (M <= 0 || N <= 0 || K < 128) return kCounterBytes;
+  // M runs as 64-row launches plus a shorter last one, whose plan (one M tile
+  // instead of two) can need more split partials
+  const bool nf4 = pe_wfmt_nf4(wfmt);
   const int mc = M > kMaxChunkRows ? kMaxChunkRows : M;
-  return workspace_of(make_plan(mc, N, K, pe_wfmt_nf4(wfmt), epilogue));
+  int64_t w = workspace_of(make_plan(mc, N, K, nf4, epilogue));
+  const int rem = M % kMaxChunkRows;
+  if (M > kMaxChunkRows && rem) {
+    const int64_t wr = workspace_of(make_plan(rem, N, K, nf4, epilogue));
+    if (wr > w) w = wr;
+  }
+  return w;
 }
 
 extern "C" int pe_nf4_gemm(const void* x, int64_t ldx, int M, int K, const uint8_t* w_tiled,

@@ -334,8 +334,17 @@ extern "C" int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int
   if (!m || M <= 0 || kv_len <= 0) return 0;
   // a causal pass of more than one chunk may take the prefill path
   const int64_t pre = prefill_path(m, M, PE_MASK_CAUSAL) ? make_prefill_layout(m, M, kv_len).total : 0;
-  if (m->qkv_layout == PE_QKV_ROPE_PAIRED && M > kFusedChunk) M = kFusedChunk;
-  const int64_t fused = make_layout(m, M, kv_len).total;
+  int64_t fused;
+  if (m->qkv_layout == PE_QKV_ROPE_PAIRED && M > kFusedChunk) {
+    // 64-row chunks and a shorter last one (its GEMM plans can need more partials)
+    fused = make_layout(m, kFusedChunk, kv_len).total;
+    if (M % kFusedChunk) {
+      const int64_t last = make_layout(m, M % kFusedChunk, kv_len).total;
+      if (last > fused) fused = last;
+    }
+  } else {
+    fused = make_layout(m, M, kv_len).total;
+  }
   return pre > fused ? pre : fused;
 }
 
@@ -479,9 +488,8 @@ BatchLayout make_batch_layout(const pe_model_desc* m, int M, int max_rows, int64
   const int es = esize(m->dtype);
   const int H = m->hidden, qd = m->num_heads * m->head_dim, ip = m->intermediate_padded;
   const int nqkv = qd + 2 * m->num_kv_heads * m->head_dim;
-  const int mc = M < kFusedChunk ? M : kFusedChunk;
   int64_t g = kCounterBytes;
-  const int64_t cand[5] = {pe_internal_gemm_rope_kv_bytes(mc, nqkv, H, m->weight_format),
+  const int64_t cand[5] = {pe_internal_gemm_rope_kv_bytes(M, nqkv, H, m->weight_format),
                            gemm_ws(m, M, H, qd, PE_EPI_RESIDUAL), gemm_ws(m, M, 2 * ip, H, PE_EPI_SWIGLU),
                            gemm_ws(m, M, H, ip, PE_EPI_RESIDUAL),
                            pe_gemm_workspace_bytes(M, m->vocab, H, PE_WFMT_DENSE, m->dtype, PE_EPI_STORE)};
