@@ -418,7 +418,7 @@ def batch_line(wl, seed: int, steps: int, warmup: int, gemm_reps: int) -> dict:
     over its own prefix (seeded lengths in [prefix_min, prefix_len]), one
     BatchVerifyStep (masks -> batched pass -> per-sequence walks -> ragged
     compaction) replayed from a HIP graph. Roofline: the NF4 GEMM launches of
-    one pass at M = batch * tree_nodes rows (each linear in 64-row launches),
+    one pass at M = batch * tree_nodes rows (one many-row launch per linear),
     replayed from a graph; FLOPs 2 * rows * N * K per launch against the dense
     bf16 MFMA peak."""
     import ctypes as C
@@ -474,29 +474,31 @@ def batch_line(wl, seed: int, steps: int, warmup: int, gemm_reps: int) -> dict:
     lin = sum(n * k for _, n, k in shape.linear_shapes()) * shape.num_layers + shape.vocab * shape.hidden
     kv_flops = sum(4 * shape.num_heads * shape.head_dim * T * (P + T) for P in prefixes) * shape.num_layers
     pass_flops = 2 * M * lin + kv_flops
-    # the NF4 GEMM launches of one pass, replayed from a graph
+    # the NF4 GEMM launches of one pass (the many-row kernel on A-tiled
+    # activations, fp32 split partials), replayed from a graph
     L = _lib.load()
     m = tm.model
     H, ip, qd = shape.hidden, m.ipad, shape.q_dim
     nqkv = qd + 2 * shape.kv_dim
     bf = torch.bfloat16
-    xs = {k: (0.5 * torch.randn((M, k), device="cuda:0")).to(bf) for k in (H, qd, ip)}
-    outs = {n: torch.empty((M, n), dtype=bf, device="cuda:0") for n in (nqkv, H, ip)}
-    wsb = max(int(L.pe_gemm_workspace_bytes(M, n, k, _lib.PE_WFMT_NF4, _lib.PE_DTYPE_BF16, e))
-              for n, k, e in ((nqkv, H, 0), (H, qd, 1), (2 * ip, H, 2), (H, ip, 1)))
-    ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda:0")
+    xs = {k: ops.to_xtile((0.5 * torch.randn((M, k), device="cuda:0")).to(bf)) for k in (H, qd, ip)}
+    dims = ((nqkv, H), (H, qd), (2 * ip, H), (H, ip))
+    pb_bytes = max(int(L.pe_nf4_gemm_partials_bytes(M, n, k)) for n, k in dims)
+    if pb_bytes <= 0:
+        raise RuntimeError(f"no many-row NF4 plan for {M} rows")
+    part = torch.empty(pb_bytes // 4, dtype=torch.float32, device="cuda:0")
+    splits = C.c_int(0)
 
-    def gemm(x, K, w, a, N, epi, out, resid=None):
-        _lib.check(L.pe_nf4_gemm(x.data_ptr(), K, M, K, w.data_ptr(), a.data_ptr(), N, epi, None,
-                                 resid.data_ptr() if resid is not None else None, N if resid is not None else 0,
-                                 out.data_ptr(), out.shape[1], ws.data_ptr(), wsb, ops.stream_ptr()), "pe_nf4_gemm")
+    def gemm(x, K, w, a, N):
+        _lib.check(L.pe_nf4_gemm_partials(x.data_ptr(), K, 1, M, K, w.data_ptr(), a.data_ptr(), N, part.data_ptr(),
+                                          pb_bytes, C.byref(splits), ops.stream_ptr()), "pe_nf4_gemm_partials")
 
     def seq():
         for ly in m.layers:
-            gemm(xs[H], H, ly["w_qkv"], ly["a_qkv"], nqkv, _lib.PE_EPI_STORE, outs[nqkv])
-            gemm(xs[qd], qd, ly["w_o"], ly["a_o"], H, _lib.PE_EPI_RESIDUAL, outs[H], resid=outs[H])
-            gemm(xs[H], H, ly["w_gu"], ly["a_gu"], 2 * ip, _lib.PE_EPI_SWIGLU, outs[ip])
-            gemm(xs[ip], ip, ly["w_down"], ly["a_down"], H, _lib.PE_EPI_RESIDUAL, outs[H], resid=outs[H])
+            gemm(xs[H], H, ly["w_qkv"], ly["a_qkv"], nqkv)
+            gemm(xs[qd], qd, ly["w_o"], ly["a_o"], H)
+            gemm(xs[H], H, ly["w_gu"], ly["a_gu"], 2 * ip)
+            gemm(xs[ip], ip, ly["w_down"], ly["a_down"], H)
 
     seq()
     torch.cuda.synchronize()
@@ -511,8 +513,7 @@ def batch_line(wl, seed: int, steps: int, warmup: int, gemm_reps: int) -> dict:
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    chunks = (M + 63) // 64
-    launches = 4 * shape.num_layers * chunks
+    launches = 4 * shape.num_layers
     gemm_s = e0.elapsed_time(e1) * 1e-3 / gemm_reps
     gemm_flops = 2 * M * sum(n * k for _, n, k in shape.linear_shapes()) * shape.num_layers
     tflops = gemm_flops / gemm_s / 1e12
@@ -534,8 +535,8 @@ def batch_line(wl, seed: int, steps: int, warmup: int, gemm_reps: int) -> dict:
         "accepted": [len(p) for p, _ in res],
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": f"nf4_gemm_kernel (row-major X, {M} rows in {chunks} launches of <= 64 rows per "
-                               f"linear: the {launches} launches of one pass)",
+                     "kernel": f"nf4_gemm_bigm_kernel (A-tiled X, all {M} rows in one launch per linear, each "
+                               f"weight dequantised once; fp32 split partials: the {launches} launches of one pass)",
                      "mean_launch_us": round(gemm_s * 1e6 / launches, 3)},
         "cpu_baseline": None,
     }

@@ -154,8 +154,10 @@ int pe_nf4_gemm_tiled(const void* x_tiled, int M, int K, const uint8_t* w_tiled,
  * sum_s partials[s] = X . deq(W)^T (sum in split order s = 0 .. S-1), written
  * with plain stores and no exchange between workgroups; *splits (host memory)
  * receives S. X row-major (ldx) or A-tiled (x_tiled != 0). M <= 64, K % 128 == 0,
- * N % 32 == 0. Layout variant of pe_nf4_gemm with no reference counterpart: the
- * pass's residual + RMSNorm kernel consumes it (o and down projections). */
+ * N % 32 == 0; or 64 < M <= 256 with A-tiled X and N % 128 == 0 (the many-row
+ * kernel: each weight dequantised once for all rows). Layout variant of
+ * pe_nf4_gemm with no reference counterpart: the pass's residual + RMSNorm,
+ * RoPE and SwiGLU kernels consume it. */
 int64_t pe_nf4_gemm_partials_bytes(int M, int N, int K);
 int pe_nf4_gemm_partials(const void* x, int64_t ldx, int x_tiled, int M, int K, const uint8_t* w_tiled,
                          const uint16_t* absmax_tiled, int N, float* partials, int64_t partial_bytes, int* splits,

@@ -98,18 +98,18 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   __shared__ __align__(16) uint8_t smem[kSmem];
   const int kvh = blockIdx.x, split = blockIdx.y;
   int rt = blockIdx.z, seq = 0;
+  int rbase = 0;  // the sequence's first row in q, bits and out
   if (bt.batch > 0) {
     seq = blockIdx.z / bt.row_tiles;
     rt = blockIdx.z - seq * bt.row_tiles;
-    const int r0 = bt.seq_row0[seq];
-    T = bt.seq_row0[seq + 1] - r0;
+    rbase = bt.seq_row0[seq];
+    T = bt.seq_row0[seq + 1] - rbase;
     P = bt.seq_prefix[seq];
     if (rt * 32 >= T * (nh / nkv) || T <= 0) return;
-    q += (int64_t)r0 * nh * 128;
-    bits += (int64_t)r0 * words;
+    q += (int64_t)rbase * nh * 128;
+    bits += (int64_t)rbase * words;
     kc += seq * bt.seq_stride;
     vc += seq * bt.seq_stride;
-    out = (char*)out + (int64_t)r0 * ld_out * 2;
   }
   const int G = nh / nkv, rows = T * G;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 31, g = lane >> 5;
@@ -397,7 +397,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   const int rr = rt * 32 + row;
   auto write_out = [&](const float (&num)[kDimsT], float den) {
     if (rr >= rows) return;
-    const int tt = rr / G, col0 = (kvh * G + rr % G) * HD + dc;
+    const int tt = rr / G + rbase, col0 = (kvh * G + rr % G) * HD + dc;
     typedef typename Elem<DT>::T Te;
     if (!out_units && ((ld_out & 3) || ((uintptr_t)out & 7))) {  // row-major output not 8-byte aligned
 #pragma unroll
@@ -664,11 +664,12 @@ int64_t pe_internal_attention_batch_bytes(int max_rows, int nh, int nkv, int64_t
 int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
                                      int64_t seq_stride, int nh, int nkv, int max_rows, int64_t max_prefix, int batch,
                                      const int32_t* seq_row0, const int64_t* seq_prefix, const uint64_t* bits,
-                                     int words, float scale, int dtype, void* out, int64_t ld_out, void* workspace,
-                                     int64_t workspace_bytes, int* counters, hipStream_t st) {
+                                     int words, float scale, int dtype, void* out, int64_t ld_out, int out_units,
+                                     void* workspace, int64_t workspace_bytes, int* counters, hipStream_t st) {
   if (!q || !k_cache || !v_cache || !out || !workspace || !seq_row0 || !seq_prefix || !bits) return PE_ERR_ARG;
   if (dtype == PE_DTYPE_F32 || batch <= 0 || max_rows <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || max_prefix < 0)
     return PE_ERR_ARG;
+  if (out_units && out_units * 128 != nh * 128) return PE_ERR_ARG;
   if (max_prefix + max_rows > cache_cap) return PE_ERR_CAPACITY;
   if (words <= 0 || words > PE_TREE_MAX_WORDS || max_rows > 64 * words) return PE_ERR_TREE;
   const int64_t S = max_prefix + max_rows;
@@ -684,12 +685,12 @@ int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const v
     attn_wg_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>(
         (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, max_rows,
         max_prefix, PE_MASK_TREE, bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters,
-        out, ld_out, 0, bt);
+        out, ld_out, out_units, bt);
   else
     attn_wg_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>(
         (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, max_rows,
         max_prefix, PE_MASK_TREE, bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters,
-        out, ld_out, 0, bt);
+        out, ld_out, out_units, bt);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }

@@ -417,7 +417,7 @@ int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, in
                                  int64_t ld_cap_xn, hipStream_t st) {
   if (!h || !w || !xn || M <= 0 || H <= 0 || S < 0 || (S > 0 && !partial)) return PE_ERR_ARG;
   if (H % 4 || H > 4 * kNormThreads * kNormChunks || S > kNormMaxSplits) return PE_ERR_ARG;
-  if (xn_tiled && (H % 128 || M > 64 || dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
+  if (xn_tiled && (H % 128 || dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
   const int ch = (H >> 2) > kNormThreads ? 2 : 1;
   const int smax = S == 0 ? 0 : (S + 3) / 4 * 4;
   PE_DISPATCH_DT(dtype, {
@@ -438,7 +438,7 @@ int pe_internal_embed_rmsnorm(const int64_t* ids, int M, const void* table, int6
                               void* cap_xn, int64_t ld_cap_xn, int32_t* status, hipStream_t st) {
   if (!ids || !table || !h || !w || !xn || M <= 0 || H <= 0 || V <= 0) return PE_ERR_ARG;
   if (H % 4 || H > 4 * kNormThreads * kNormChunks) return PE_ERR_ARG;
-  if (xn_tiled && (H % 128 || M > 64 || dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
+  if (xn_tiled && (H % 128 || dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
   const int ch = (H >> 2) > kNormThreads ? 2 : 1;
   PE_DISPATCH_DT(dtype, {
     typedef typename Elem<DT>::T T;

@@ -695,6 +695,160 @@ __global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_
 }
 
 // ---------------------------------------------------------------------------
+// NF4 GEMM for many rows (the batched pass: M up to 256, A-tiled X)
+// ---------------------------------------------------------------------------
+// One workgroup = 4 waves = one group of four 32-column tiles (128 columns) x
+// one K split. Each 128-wide unit is dequantised once for every row: wave w
+// looks up tile w of the unit (the lane's own table, as in nf4_wave_body)
+// and writes its bf16 MFMA B fragments to a double-buffered LDS tile; after
+// one barrier every wave multiplies its own M tiles (MTW of them) by all four
+// tiles' fragments. Waves split M, not K, so each wave's accumulators hold
+// complete sums over the split's units: no reduction across waves. The
+// result is written as fp32 split partials out[split][row][col] (plain
+// stores), summed by the consumer kernels in split order.
+constexpr int kBigNT = 4;
+constexpr int kBigTab = 16 * 64 * 4;          // one wave's table: 16 codes x 64 lanes x dword (two units)
+constexpr int kBigBufUnit = kBigNT * 8 * 64 * 16;  // B fragments of one unit: 4 tiles x 8 k-steps x 64 lanes x 16 B
+constexpr int kBigSmem = kWaves * kBigTab + 2 * kBigBufUnit;
+
+template <int MTW, int WV>
+__device__ __forceinline__ void nf4_bigm_wave(uint8_t* smem, const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+                                              const uint16_t* __restrict__ Wabs, int NP, int group, int u0, int u1,
+                                              int mt0, int nmt, int mtiles, const EpiArgs& e, int split) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 5, ln = lane & 31;
+  constexpr int TB = WV * kBigTab;  // this wave's table
+  uint8_t* lanetab = smem + lane * 4;
+  uint32_t addr[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) addr[i] = (uint32_t)(lane * 4);
+  u32x4_t* bufs = (u32x4_t*)(smem + kWaves * kBigTab);
+  const int64_t tile = (int64_t)group * kBigNT + WV;
+  auto load_codes = [&](u32x4_t (&q)[2], int p) {
+    const int pc = min(p, u1 - 1);
+    const u32x4_t* wp = (const u32x4_t*)(W + (tile * NP + pc) * 2048 + lane * 16);
+    q[0] = __builtin_nontemporal_load(wp);
+    q[1] = __builtin_nontemporal_load(wp + 64);
+  };
+  auto load_abs = [&](int p) -> uint32_t {
+    return (uint32_t)Wabs[(tile * NP + min(p, u1 - 1)) * 64 + lane];
+  };
+  f32x16_t acc[kBigNT][MTW];
+#pragma unroll
+  for (int nt = 0; nt < kBigNT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.f;
+  // X fragments in a ring of four k-steps, two k-steps ahead of their MFMAs
+  u32x4_t x[4][MTW];
+  auto load_x = [&](int p, int s) {
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt) {
+      const int m = min(mt0 + mt, mtiles - 1);  // waves with fewer M tiles read a valid tile
+      x[s & 3][mt] = *(const u32x4_t*)(X + ((((int64_t)m * NP + p) * 8 + s) * 64 + lane) * 8);
+    }
+  };
+  // dequantise this wave's tile of unit p (table half SL) into buffer slot p & 1
+  auto dequant = [&](const u32x4_t (&q)[2], int p, auto slot_c) {
+    constexpr int SL = decltype(slot_c)::value;
+    u32x4_t* dst = bufs + ((p & 1) * kBigNT + WV) * 8 * 64 + lane;
+    uint32_t r[2][8];
+    nf4_addr8(q[0][0], addr);
+    nf4_read8<TB + SL>(addr, r[0]);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s + 1 < 8) {
+        nf4_addr8(q[(s + 1) >> 2][(s + 1) & 3], addr);
+        nf4_read8<TB + SL>(addr, r[(s + 1) & 1]);
+      }
+      const uint32_t (&cur)[8] = r[s & 1];
+      dst[s * 64] = u32x4_t{pack16(cur[0], cur[1]), pack16(cur[2], cur[3]), pack16(cur[4], cur[5]),
+                            pack16(cur[6], cur[7])};
+    }
+  };
+  // unit p's MFMAs; k-steps 0 and 1 of X were requested before its dequantisation
+  auto multiply = [&](int p) {
+    const u32x4_t* src = bufs + (p & 1) * kBigNT * 8 * 64 + lane;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s + 2 < 8) load_x(p, s + 2);
+#pragma unroll
+      for (int nt = 0; nt < kBigNT; ++nt) {
+        const u32x4_t b = src[(nt * 8 + s) * 64];
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+          if (mt < nmt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(x[s & 3][mt], b, acc[nt][mt]);
+      }
+    }
+  };
+  auto first_x = [&](int p) {
+    load_x(p, 0);
+    load_x(p, 1);
+  };
+  constexpr std::integral_constant<int, 0> kLo{};
+  constexpr std::integral_constant<int, 2> kHi{};
+  u32x4_t qa[2], qb[2];
+  load_codes(qa, u0);
+  load_codes(qb, u0 + 1);
+  uint32_t a0 = load_abs(u0), a1 = load_abs(u0 + 1);
+  for (int p = u0; p < u1; p += 2) {
+    // one table build covers units p (low halves) and p + 1 (high halves)
+    nf4_build_table2<TB, false>(lanetab, a0, a1);
+    a0 = load_abs(p + 2);
+    a1 = load_abs(p + 3);
+    first_x(p);
+    dequant(qa, p, kLo);
+    load_codes(qa, p + 2);
+    lds_barrier();  // unit p's fragments are complete; the other slot is free
+    multiply(p);
+    if (p + 1 < u1) {  // the same for every wave of the workgroup
+      first_x(p + 1);
+      dequant(qb, p + 1, kHi);
+      load_codes(qb, p + 3);
+      lds_barrier();
+      multiply(p + 1);
+    }
+  }
+  // split partials: row 32 mt + 8 q + 4 g + j, column (group * 4 + nt) * 32 + ln
+  float* out = (float*)e.out + (int64_t)split * e.M * e.N;
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt) {
+    if (mt >= nmt) break;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = (mt0 + mt) * 32 + 8 * q4 + 4 * g + j;
+        if (row < e.M)
+#pragma unroll
+          for (int nt = 0; nt < kBigNT; ++nt)
+            out[(int64_t)row * e.N + (group * kBigNT + nt) * 32 + ln] = acc[nt][mt][4 * q4 + j];
+      }
+  }
+}
+
+template <int MTW>
+__global__ __launch_bounds__(kWaves * 64, 2) void nf4_gemm_bigm_kernel(const uint16_t* __restrict__ X,
+                                                                       const uint8_t* __restrict__ W,
+                                                                       const uint16_t* __restrict__ Wabs, int NP,
+                                                                       int pps, int mtiles, EpiArgs e) {
+  __shared__ __align__(256) uint8_t smem[kBigSmem];
+  const int group = blockIdx.x, split = blockIdx.y;
+  const int u0 = split * pps, u1 = min(NP, u0 + pps);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int mt0 = wave * MTW;
+  const int nmt = max(0, min(MTW, mtiles - mt0));
+  if (u0 >= u1) return;  // a whole workgroup: no barrier is left waiting
+  switch (wave) {
+    case 0: nf4_bigm_wave<MTW, 0>(smem, X, W, Wabs, NP, group, u0, u1, mt0, nmt, mtiles, e, split); break;
+    case 1: nf4_bigm_wave<MTW, 1>(smem, X, W, Wabs, NP, group, u0, u1, mt0, nmt, mtiles, e, split); break;
+    case 2: nf4_bigm_wave<MTW, 2>(smem, X, W, Wabs, NP, group, u0, u1, mt0, nmt, mtiles, e, split); break;
+    default: nf4_bigm_wave<MTW, 3>(smem, X, W, Wabs, NP, group, u0, u1, mt0, nmt, mtiles, e, split); break;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Dense 16-bit GEMM: one iteration = 4 MFMA k-steps (64 along K) of NT tiles.
 // Same pipeline as the NF4 kernel; a padded iteration multiplies a zero X.
 // ---------------------------------------------------------------------------
@@ -1212,11 +1366,11 @@ int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int wfmt) {
 int pe_internal_rope_kv_partials(const float* partial, int S, int M, int nh, int nkv, int hd, const void* bias,
                                  const int64_t* positions, const void* cos_sin, int64_t max_pos, void* q_out,
                                  void* k_cache, void* v_cache, int64_t cap, int64_t row0, int32_t* status, int dtype,
-                                 hipStream_t st) {
+                                 hipStream_t st, const int64_t* kv_off) {
   if (!partial || S < 1 || M <= 0 || hd <= 0 || hd % 64 || !positions || !cos_sin || !q_out || !k_cache ||
       !v_cache)
     return PE_ERR_ARG;
-  if (row0 < 0 || row0 + M > cap) return PE_ERR_CAPACITY;
+  if (!kv_off && (row0 < 0 || row0 + M > cap)) return PE_ERR_CAPACITY;
   const int N = (nh + 2 * nkv) * hd;
   EpiArgs e = make_epi(kEpiRopeKV, M, N, bias, nullptr, 0, nullptr, 0);
   e.positions = positions;
@@ -1227,6 +1381,7 @@ int pe_internal_rope_kv_partials(const float* partial, int S, int M, int nh, int
   e.v_cache = v_cache;
   e.cap = cap;
   e.row0 = row0;
+  e.kv_off = kv_off;
   e.nh = nh;
   e.nkv = nkv;
   e.hd = hd;
@@ -1250,6 +1405,47 @@ int pe_internal_swiglu_partials(const float* partial, int S, int M, int N, void*
   if (dtype == PE_DTYPE_BF16) swiglu_partials_kernel<PE_DTYPE_BF16><<<grid, 256, 0, st>>>(partial, S, e);
   else if (dtype == PE_DTYPE_F16) swiglu_partials_kernel<PE_DTYPE_F16><<<grid, 256, 0, st>>>(partial, S, e);
   else return PE_ERR_ARG;
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+// The many-row NF4 GEMM (A-tiled X of M rows, 64 < M <= 256, N % 128 == 0):
+// split partials [S][M][N]; S chosen for about two workgroups per CU.
+namespace {
+struct BigPlan {
+  int groups, units, S, pps;
+};
+BigPlan big_plan(int N, int K) {
+  BigPlan p;
+  p.groups = N / (32 * kBigNT);
+  p.units = K / 128;
+  int S = (2 * cu_count() + p.groups - 1) / p.groups;
+  if (S > kMaxSplits) S = kMaxSplits;
+  if (S > p.units) S = p.units;
+  if (S < 1) S = 1;
+  p.pps = (p.units + S - 1) / S;
+  p.S = (p.units + p.pps - 1) / p.pps;
+  return p;
+}
+}  // namespace
+
+int64_t pe_internal_nf4_bigm_partials_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K < 128 || N % (32 * kBigNT) || K % 128) return 0;
+  return (int64_t)big_plan(N, K).S * M * N * 4;
+}
+
+int pe_internal_nf4_bigm_partials(const void* x_tiled, int M, int K, const void* w, const void* wabs, int N,
+                                  float* partial, int64_t partial_bytes, int* splits, hipStream_t st) {
+  if (!x_tiled || !w || !wabs || !partial || !splits || M <= 0 || M > 8 * 32 || K % 128 || N % (32 * kBigNT))
+    return PE_ERR_ARG;
+  const BigPlan p = big_plan(N, K);
+  if (partial_bytes < (int64_t)p.S * M * N * 4) return PE_ERR_WORKSPACE;
+  EpiArgs e = make_epi(kEpiPartial, M, N, nullptr, nullptr, 0, partial, N);
+  *splits = p.S;
+  const int mtiles = (M + 31) / 32;
+  nf4_gemm_bigm_kernel<2><<<dim3(p.groups, p.S), kWaves * 64, 0, st>>>((const uint16_t*)x_tiled, (const uint8_t*)w,
+                                                                        (const uint16_t*)wabs, p.units, p.pps, mtiles,
+                                                                        e);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }
@@ -1298,6 +1494,7 @@ extern "C" int pe_nf4_gemm_tiled(const void* x_tiled, int M, int K, const uint8_
 }
 
 extern "C" int64_t pe_nf4_gemm_partials_bytes(int M, int N, int K) {
+  if (M > kMaxChunkRows && M <= 8 * 32) return pe_internal_nf4_bigm_partials_bytes(M, N, K);
   if (M <= 0 || M > kMaxChunkRows || N <= 0 || K < 128) return 0;
   return pe_internal_linear_partials_bytes(M, N, K, PE_WFMT_NF4);
 }
@@ -1305,6 +1502,11 @@ extern "C" int64_t pe_nf4_gemm_partials_bytes(int M, int N, int K) {
 extern "C" int pe_nf4_gemm_partials(const void* x, int64_t ldx, int x_tiled, int M, int K, const uint8_t* w_tiled,
                                     const uint16_t* absmax_tiled, int N, float* partials, int64_t partial_bytes,
                                     int* splits, void* stream) {
+  if (M > kMaxChunkRows) {  // the many-row kernel: A-tiled X, N % 128 == 0
+    if (!x_tiled) return PE_ERR_ARG;
+    return pe_internal_nf4_bigm_partials(x, M, K, w_tiled, absmax_tiled, N, partials, partial_bytes, splits,
+                                         (hipStream_t)stream);
+  }
   return pe_internal_linear_partials(PE_WFMT_NF4, PE_DTYPE_BF16, x, x_tiled ? K : ldx, x_tiled != 0, M, K, w_tiled,
                                      absmax_tiled, N, partials, partial_bytes, splits, (hipStream_t)stream);
 }

@@ -45,7 +45,15 @@ PE_INTERNAL int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int w
 PE_INTERNAL int pe_internal_rope_kv_partials(const float* partial, int S, int M, int nh, int nkv, int hd,
                                              const void* bias, const int64_t* positions, const void* cos_sin,
                                              int64_t max_pos, void* q_out, void* k_cache, void* v_cache, int64_t cap,
-                                             int64_t row0, int32_t* status, int dtype, hipStream_t st);
+                                             int64_t row0, int32_t* status, int dtype, hipStream_t st,
+                                             const int64_t* kv_off = nullptr);
+// pe_gemm.hip: the NF4 GEMM for many rows (A-tiled X, 64 < M <= 256,
+// N % 128 == 0, fp16 absmax): each weight dequantised once for all rows;
+// fp32 split partials [S][M][N] (*splits receives S).
+PE_INTERNAL int64_t pe_internal_nf4_bigm_partials_bytes(int M, int N, int K);
+PE_INTERNAL int pe_internal_nf4_bigm_partials(const void* x_tiled, int M, int K, const void* w, const void* wabs,
+                                              int N, float* partial, int64_t partial_bytes, int* splits,
+                                              hipStream_t st);
 PE_INTERNAL int pe_internal_swiglu_partials(const float* partial, int S, int M, int N, void* out, int64_t ld_out,
                                             int out_units, int dtype, hipStream_t st);
 
@@ -86,14 +94,16 @@ PE_INTERNAL int64_t attention_workspace_bytes(int T, int nh, int nkv, int hd, in
 // pe_attn.hip: tree attention of `batch` sequences in one launch (16-bit,
 // hd == 128): sequence b's query rows are [seq_row0[b], seq_row0[b+1]) of q,
 // bits and out (row-major), its cache kc / vc + b * seq_stride elements with
-// seq_prefix[b] cached rows; max_prefix and max_rows size the launch.
+// seq_prefix[b] cached rows; max_prefix and max_rows size the launch; with
+// out_units > 0 out is A-tiled over all rows (K = 128 * out_units).
 PE_INTERNAL int64_t pe_internal_attention_batch_bytes(int max_rows, int nh, int nkv, int64_t max_kv_len, int batch);
 PE_INTERNAL int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const void* v_cache,
                                                  int64_t cache_cap, int64_t seq_stride, int nh, int nkv, int max_rows,
                                                  int64_t max_prefix, int batch, const int32_t* seq_row0,
                                                  const int64_t* seq_prefix, const uint64_t* bits, int words,
-                                                 float scale, int dtype, void* out, int64_t ld_out, void* workspace,
-                                                 int64_t workspace_bytes, int* counters, hipStream_t st);
+                                                 float scale, int dtype, void* out, int64_t ld_out, int out_units,
+                                                 void* workspace, int64_t workspace_bytes, int* counters,
+                                                 hipStream_t st);
 // pe_elem.hip: per-row K/V slot offsets of a batched pass (see EpiArgs::kv_off):
 // off[r] = b * seq_stride + (seq_prefix[b] + r - seq_row0[b]) * hd for row r of
 // sequence b, or -1 (and PE_ERR_CAPACITY in *status) past the sequence's cache.

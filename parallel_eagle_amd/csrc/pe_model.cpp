@@ -480,8 +480,21 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
 // row-major (the A-tiled handoff is for single 64-row passes).
 // ---------------------------------------------------------------------------
 struct BatchLayout {
-  int64_t gemm, gemm_bytes, h, xn, q, attn, act, kvoff, attn_ws, attn_ws_bytes, total;
+  int64_t gemm, gemm_bytes, h, xn, q, attn, act, kvoff, attn_ws, attn_ws_bytes;
+  bool big;                                   // the many-row NF4 path (A-tiled activations, split partials)
+  int64_t xn_t, attn_t, act_t, part, part_bytes;
+  int64_t total;
 };
+
+// The batched NF4 pass over 65..256 rows dequantises each weight once for all
+// rows (pe_internal_nf4_bigm_partials) and hands A-tiled activations between
+// the kernels; other batches run each linear in 64-row launches on row-major X.
+bool batch_big_path(const pe_model_desc* m, int M) {
+  const int H = m->hidden, qd = m->num_heads * m->head_dim, ip = m->intermediate_padded;
+  const int nqkv = qd + 2 * m->num_kv_heads * m->head_dim;
+  return m->weight_format == PE_WFMT_NF4 && M > kFusedChunk && M <= 256 && H % 128 == 0 && qd % 128 == 0 &&
+         ip % 128 == 0 && nqkv % 128 == 0;
+}
 
 BatchLayout make_batch_layout(const pe_model_desc* m, int M, int max_rows, int64_t max_kv_len, int batch) {
   BatchLayout L;
@@ -512,6 +525,19 @@ BatchLayout make_batch_layout(const pe_model_desc* m, int M, int max_rows, int64
   L.attn_ws_bytes =
       align_up(pe_internal_attention_batch_bytes(max_rows, m->num_heads, m->num_kv_heads, max_kv_len, batch));
   L.attn_ws = take(L.attn_ws_bytes);
+  L.big = batch_big_path(m, M);
+  L.xn_t = L.attn_t = L.act_t = L.part = L.part_bytes = 0;
+  if (L.big) {
+    L.xn_t = take(xtile_bytes(M, H));
+    L.attn_t = take(xtile_bytes(M, qd));
+    L.act_t = take(xtile_bytes(M, ip));
+    const int64_t pb[4] = {pe_internal_nf4_bigm_partials_bytes(M, nqkv, H), pe_internal_nf4_bigm_partials_bytes(M, H, qd),
+                           pe_internal_nf4_bigm_partials_bytes(M, 2 * ip, H), pe_internal_nf4_bigm_partials_bytes(M, H, ip)};
+    for (int i = 0; i < 4; ++i)
+      if (pb[i] > L.part_bytes) L.part_bytes = pb[i];
+    L.part_bytes = align_up(L.part_bytes);
+    L.part = take(L.part_bytes);
+  }
   L.total = off;
   return L;
 }
@@ -557,12 +583,52 @@ int forward_batched(const pe_model_desc* m, const pe_pass_args* a, const BatchLa
   };
   PE_TRY(pe_internal_kv_offsets(a->seq_row0, a->seq_prefix, a->batch, M, a->cache_seq_stride, a->cache_capacity, hd,
                                 kvoff, a->status, st));
+  char* xn_t = Lb.big ? ws + Lb.xn_t : nullptr;
   {
     const int f0 = slot_of(0);
     PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, embed_rows(m), h, H, m->attn_norm[0], m->rms_eps,
-                                     m->norm_mode, m->dtype, xn, nullptr, slot_ptr(f0), fused_ld, nullptr, 0,
+                                     m->norm_mode, m->dtype, xn, xn_t, slot_ptr(f0), fused_ld, nullptr, 0,
                                      a->status, st));
     PE_TRY(copy_repeats(0, f0));
+  }
+  if (Lb.big) {
+    // every linear: one launch over all M rows (split partials), consumed by
+    // the RoPE + K/V append, SwiGLU and residual + RMSNorm kernels
+    char* attn_t = ws + Lb.attn_t;
+    char* act_t = ws + Lb.act_t;
+    float* part = (float*)(ws + Lb.part);
+    const int nqkv = (nh + 2 * nkv) * hd;
+    int S = 0;
+    for (int l = 0; l < L; ++l) {
+      char* kc = (char*)a->k_cache + l * layer_stride;
+      char* vc = (char*)a->v_cache + l * layer_stride;
+      PE_TRY(pe_internal_nf4_bigm_partials(xn_t, M, H, m->w_qkv[l], m->a_qkv[l], nqkv, part, Lb.part_bytes, &S, st));
+      PE_TRY(pe_internal_rope_kv_partials(part, S, M, nh, nkv, hd, m->b_qkv ? m->b_qkv[l] : nullptr, a->positions,
+                                          m->rope_cos_sin, m->max_positions, q, kc, vc, a->cache_capacity, 0,
+                                          a->status, m->dtype, st, kvoff));
+      PE_TRY(pe_internal_tree_attention_batch(q, kc, vc, a->cache_capacity, a->cache_seq_stride, nh, nkv,
+                                              a->max_seq_rows, a->prefix_len, a->batch, a->seq_row0, a->seq_prefix,
+                                              a->tree_bits, a->bits_words, scale, m->dtype, attn_t, qd, qd / 128,
+                                              ws + Lb.attn_ws, Lb.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st));
+      PE_TRY(pe_internal_nf4_bigm_partials(attn_t, M, qd, m->w_o[l], m->a_o[l], H, part, Lb.part_bytes, &S, st));
+      PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn,
+                                          xn_t, nullptr, 0, nullptr, 0, st));
+      PE_TRY(pe_internal_nf4_bigm_partials(xn_t, M, H, m->w_gu[l], m->a_gu[l], 2 * ip, part, Lb.part_bytes, &S, st));
+      PE_TRY(pe_internal_swiglu_partials(part, S, M, 2 * ip, act_t, ip, ip / 128, m->dtype, st));
+      PE_TRY(pe_internal_nf4_bigm_partials(act_t, M, ip, m->w_down[l], m->a_down[l], H, part, Lb.part_bytes, &S, st));
+      const bool last = l + 1 == L;
+      const int fh = last ? -1 : slot_of(l + 1);
+      const int fx = last ? slot_of(L) : -1;
+      const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
+      const int next_mode = last ? PE_NORM_HF : m->norm_mode;
+      PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn,
+                                          last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
+      PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
+    }
+    if (a->logits)
+      PE_TRY(pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
+                           m->vocab, gws, gwsb, st));
+    return PE_OK;
   }
   for (int l = 0; l < L; ++l) {
     char* kc = (char*)a->k_cache + l * layer_stride;
@@ -578,7 +644,7 @@ int forward_batched(const pe_model_desc* m, const pe_pass_args* a, const BatchLa
     }
     PE_TRY(pe_internal_tree_attention_batch(q, kc, vc, a->cache_capacity, a->cache_seq_stride, nh, nkv,
                                             a->max_seq_rows, a->prefix_len, a->batch, a->seq_row0, a->seq_prefix,
-                                            a->tree_bits, a->bits_words, scale, m->dtype, attn, qd, ws + Lb.attn_ws,
+                                            a->tree_bits, a->bits_words, scale, m->dtype, attn, qd, 0, ws + Lb.attn_ws,
                                             Lb.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st));
     const void* a_o = m->a_o ? m->a_o[l] : nullptr;
     PE_TRY(pe_internal_linear(wf, m->dtype, attn, qd, false, M, qd, m->w_o[l], a_o, H, PE_EPI_RESIDUAL, nullptr, h, H,
