@@ -1419,7 +1419,17 @@ BigPlan big_plan(int N, int K) {
   BigPlan p;
   p.groups = N / (32 * kBigNT);
   p.units = K / 128;
-  int S = (2 * cu_count() + p.groups - 1) / p.groups;
+  // About one workgroup per CU: every further split adds M x N x 4 bytes of
+  // partials that the consuming kernel re-reads, while a second workgroup on a
+  // CU shares its matrix cores (the 14B shapes at 208 rows measured no faster
+  // past one workgroup per CU). Column groups short of the CUs by more than a
+  // tenth take one split more (gate/up: 216 groups -> 2 splits).
+  static const int forced = env_int("PE_BIGM_SPLITS", 0);
+  const int cu = cu_count();
+  int S = cu / p.groups;
+  if (S < 1) S = 1;
+  if (10 * p.groups * S < 9 * cu && p.groups * (S + 1) <= 2 * cu) ++S;
+  if (forced > 0) S = forced;
   if (S > kMaxSplits) S = kMaxSplits;
   if (S > p.units) S = p.units;
   if (S < 1) S = 1;
