@@ -35,6 +35,9 @@ COMMON = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # buffers are reinterpreted between element types throughout (tables
+    # written as dwords and read as halves, bf16 rows moved as 16-byte vectors)
+    "-fno-strict-aliasing",
     f"-I{INCLUDE}",
     "-Wno-unused-result",
 ]

@@ -233,12 +233,20 @@ __device__ __forceinline__ void nf4_addr8(uint32_t q, uint32_t (&a)[8]) {
 #undef PE_SDWA_HI
 #undef PE_SDWA_LO
 
-typedef __attribute__((address_space(3))) const uint16_t lds_u16_t;
+// The table is written as dwords (two 16-bit slots) and read as 16-bit
+// entries: the read type is may_alias (and the library is built with
+// -fno-strict-aliasing), and the address is formed from the kernel's LDS
+// array itself (smem + the address register + OFF), not from a bare integer.
+// Otherwise the compiler may take the reads as independent of the table
+// builds and move the next build's stores above reads of the current table.
+typedef __attribute__((address_space(3), may_alias)) const uint16_t lds_u16_t;
+typedef __attribute__((address_space(3))) const uint8_t lds_u8_t;
 
 template <int OFF>
-__device__ __forceinline__ void nf4_read8(const uint32_t (&a)[8], uint32_t (&r)[8]) {
+__device__ __forceinline__ void nf4_read8(const uint8_t* smem, const uint32_t (&a)[8], uint32_t (&r)[8]) {
+  const lds_u8_t* base = (const lds_u8_t*)smem;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = *(lds_u16_t*)(size_t)(a[i] + OFF);
+  for (int i = 0; i < 8; ++i) r[i] = *(lds_u16_t*)(base + a[i] + OFF);
 }
 
 __device__ __forceinline__ uint32_t pack16(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
@@ -528,8 +536,8 @@ __device__ __forceinline__ void nf4_wave_body(f32x16_t (&acc)[NT][MT], uint8_t* 
     auto issue = [&](int b, uint32_t (&rr)[8]) {
       const int s = b / NT, nt = b % NT;
       nf4_addr8(q[nt][s >> 2][s & 3], addr);
-      if (nt == 0) nf4_read8<TB + SL>(addr, rr);
-      else nf4_read8<TB + kTabTile + SL>(addr, rr);
+      if (nt == 0) nf4_read8<TB + SL>(smem, addr, rr);
+      else nf4_read8<TB + kTabTile + SL>(smem, addr, rr);
     };
     issue(0, r[0]);
 #pragma unroll
@@ -701,8 +709,11 @@ __global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_
 // one K split. Each 128-wide unit is dequantised once for every row: wave w
 // looks up tile w of the unit (the lane's own table, as in nf4_wave_body)
 // and writes its bf16 MFMA B fragments to a double-buffered LDS tile; after
-// one barrier every wave multiplies its own M tiles (MTW of them) by all four
-// tiles' fragments. Waves split M, not K, so each wave's accumulators hold
+// one barrier every wave multiplies its own M tiles (up to two) by all four
+// tiles' fragments. (Interleaving the next unit's lookups with the MFMAs
+// measured slower: the B-fragment reads and the lookups share the in-order
+// LDS counter, so each MFMA waited for lookups issued after its operand.)
+// Waves split M, not K, so each wave's accumulators hold
 // complete sums over the split's units: no reduction across waves. The
 // result is written as fp32 split partials out[split][row][col] (plain
 // stores), summed by the consumer kernels in split order.
@@ -711,10 +722,13 @@ constexpr int kBigTab = 16 * 64 * 4;          // one wave's table: 16 codes x 64
 constexpr int kBigBufUnit = kBigNT * 8 * 64 * 16;  // B fragments of one unit: 4 tiles x 8 k-steps x 64 lanes x 16 B
 constexpr int kBigSmem = kWaves * kBigTab + 2 * kBigBufUnit;
 
-template <int MTW, int WV>
+// NMT: the M tiles this wave multiplies (compile time, so the MFMA stream has
+// no branches); a wave with none still looks up its tile for the others.
+template <int NMT, int WV>
 __device__ __forceinline__ void nf4_bigm_wave(uint8_t* smem, const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
                                               const uint16_t* __restrict__ Wabs, int NP, int group, int u0, int u1,
-                                              int mt0, int nmt, int mtiles, const EpiArgs& e, int split) {
+                                              int mt0, const EpiArgs& e, int split) {
+  constexpr int MA = NMT > 0 ? NMT : 1;  // array extents
   const int lane = threadIdx.x & 63;
   const int g = lane >> 5, ln = lane & 31;
   constexpr int TB = WV * kBigTab;  // this wave's table
@@ -733,21 +747,19 @@ __device__ __forceinline__ void nf4_bigm_wave(uint8_t* smem, const uint16_t* __r
   auto load_abs = [&](int p) -> uint32_t {
     return (uint32_t)Wabs[(tile * NP + min(p, u1 - 1)) * 64 + lane];
   };
-  f32x16_t acc[kBigNT][MTW];
+  f32x16_t acc[kBigNT][MA];
 #pragma unroll
   for (int nt = 0; nt < kBigNT; ++nt)
 #pragma unroll
-    for (int mt = 0; mt < MTW; ++mt)
+    for (int mt = 0; mt < MA; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.f;
   // X fragments in a ring of four k-steps, two k-steps ahead of their MFMAs
-  u32x4_t x[4][MTW];
+  u32x4_t x[4][MA];
   auto load_x = [&](int p, int s) {
 #pragma unroll
-    for (int mt = 0; mt < MTW; ++mt) {
-      const int m = min(mt0 + mt, mtiles - 1);  // waves with fewer M tiles read a valid tile
-      x[s & 3][mt] = *(const u32x4_t*)(X + ((((int64_t)m * NP + p) * 8 + s) * 64 + lane) * 8);
-    }
+    for (int mt = 0; mt < NMT; ++mt)
+      x[s & 3][mt] = *(const u32x4_t*)(X + ((((int64_t)(mt0 + mt) * NP + p) * 8 + s) * 64 + lane) * 8);
   };
   // dequantise this wave's tile of unit p (table half SL) into buffer slot p & 1
   auto dequant = [&](const u32x4_t (&q)[2], int p, auto slot_c) {
@@ -755,12 +767,12 @@ __device__ __forceinline__ void nf4_bigm_wave(uint8_t* smem, const uint16_t* __r
     u32x4_t* dst = bufs + ((p & 1) * kBigNT + WV) * 8 * 64 + lane;
     uint32_t r[2][8];
     nf4_addr8(q[0][0], addr);
-    nf4_read8<TB + SL>(addr, r[0]);
+    nf4_read8<TB + SL>(smem, addr, r[0]);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       if (s + 1 < 8) {
         nf4_addr8(q[(s + 1) >> 2][(s + 1) & 3], addr);
-        nf4_read8<TB + SL>(addr, r[(s + 1) & 1]);
+        nf4_read8<TB + SL>(smem, addr, r[(s + 1) & 1]);
       }
       const uint32_t (&cur)[8] = r[s & 1];
       dst[s * 64] = u32x4_t{pack16(cur[0], cur[1]), pack16(cur[2], cur[3]), pack16(cur[4], cur[5]),
@@ -777,8 +789,7 @@ __device__ __forceinline__ void nf4_bigm_wave(uint8_t* smem, const uint16_t* __r
       for (int nt = 0; nt < kBigNT; ++nt) {
         const u32x4_t b = src[(nt * 8 + s) * 64];
 #pragma unroll
-        for (int mt = 0; mt < MTW; ++mt)
-          if (mt < nmt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(x[s & 3][mt], b, acc[nt][mt]);
+        for (int mt = 0; mt < NMT; ++mt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(x[s & 3][mt], b, acc[nt][mt]);
       }
     }
   };
@@ -813,8 +824,7 @@ __device__ __forceinline__ void nf4_bigm_wave(uint8_t* smem, const uint16_t* __r
   // split partials: row 32 mt + 8 q + 4 g + j, column (group * 4 + nt) * 32 + ln
   float* out = (float*)e.out + (int64_t)split * e.M * e.N;
 #pragma unroll
-  for (int mt = 0; mt < MTW; ++mt) {
-    if (mt >= nmt) break;
+  for (int mt = 0; mt < NMT; ++mt) {
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4)
 #pragma unroll
@@ -840,12 +850,22 @@ __global__ __launch_bounds__(kWaves * 64, 2) void nf4_gemm_bigm_kernel(const uin
   const int mt0 = wave * MTW;
   const int nmt = max(0, min(MTW, mtiles - mt0));
   if (u0 >= u1) return;  // a whole workgroup: no barrier is left waiting
-  switch (wave) {
-    case 0: nf4_bigm_wave<MTW, 0>(smem, X, W, Wabs, NP, group, u0, u1, mt0, nmt, mtiles, e, split); break;
-    case 1: nf4_bigm_wave<MTW, 1>(smem, X, W, Wabs, NP, group, u0, u1, mt0, nmt, mtiles, e, split); break;
-    case 2: nf4_bigm_wave<MTW, 2>(smem, X, W, Wabs, NP, group, u0, u1, mt0, nmt, mtiles, e, split); break;
-    default: nf4_bigm_wave<MTW, 3>(smem, X, W, Wabs, NP, group, u0, u1, mt0, nmt, mtiles, e, split); break;
+  static_assert(MTW == 2, "the dispatch below instantiates 0, 1 or 2 M tiles per wave");
+#define PE_BIGM_WAVE(N)                                                                          \
+  switch (wave) {                                                                                \
+    case 0: nf4_bigm_wave<N, 0>(smem, X, W, Wabs, NP, group, u0, u1, mt0, e, split); break;      \
+    case 1: nf4_bigm_wave<N, 1>(smem, X, W, Wabs, NP, group, u0, u1, mt0, e, split); break;      \
+    case 2: nf4_bigm_wave<N, 2>(smem, X, W, Wabs, NP, group, u0, u1, mt0, e, split); break;      \
+    default: nf4_bigm_wave<N, 3>(smem, X, W, Wabs, NP, group, u0, u1, mt0, e, split); break;     \
   }
+  if (nmt == 2) {
+    PE_BIGM_WAVE(2)
+  } else if (nmt == 1) {
+    PE_BIGM_WAVE(1)
+  } else {
+    PE_BIGM_WAVE(0)
+  }
+#undef PE_BIGM_WAVE
 }
 
 // ---------------------------------------------------------------------------
