@@ -46,6 +46,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 / fp16
+DTYPE_NAMES = {"bfloat16": "bf16", "float16": "f16", "float32": "f32"}
 METRIC = "tree-verify pass latency + HBM GB/s (% peak), 7B-int4 T=26 KV=2048 bs=1"
 DEFAULT_WORKLOAD = "llama2-7b-nf4-T26-P2048"
 
@@ -152,6 +154,22 @@ def time_pass(step, steps: int, warmup: int):
     return total_ms / steps, statistics.median(per), wall
 
 
+def mfma_flops_per_pass(shape, T: int, P: int) -> int:
+    """MFMA FLOPs one single-sequence pass issues, counted on the launch shapes
+    (the v_mfma_f32_32x32x16 tiles: rows padded to 32; attention over the
+    key blocks of 32 and the row tiles of the T x heads-per-KV-head query
+    rows). The rocprofv3 counter SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 of the
+    GEMM launches equals the GEMM part exactly."""
+    mp = -(-T // 32) * 32
+    lin = sum(n * k for _, n, k in shape.linear_shapes())
+    gemm = 2 * mp * lin * shape.num_layers + 2 * mp * shape.vocab * shape.hidden
+    g = shape.num_heads // shape.num_kv_heads
+    rows = -(-T * g // 32) * 32
+    keys = -(-(P + T) // 32) * 32
+    attn = 4 * rows * keys * shape.head_dim * shape.num_kv_heads * shape.num_layers
+    return gemm + attn
+
+
 def nf4_gemm_roofline(tm, wl, reps: int):
     """Mean duration and algorithmic bytes per launch of the NF4 dequant-GEMM
     kernel as the pass runs it: the 4 * L launches of one pass on A-tiled
@@ -238,11 +256,15 @@ def nf4_gemm_roofline(tm, wl, reps: int):
 # ---------------------------------------------------------------- CPU path
 def cpu_baseline(wl, seed, n_layers: int, runs: int):
     """The reference path on the host cores (the oracle restatement, timed):
-    tree mask + additive bias, forward with per-call NF4 dequantise, bf16
-    matmuls and masked SDPA, the acceptance walk, and the index_select commit
-    over every layer's cache, on an ``n_layers`` slice of the shape at full
-    width, P and T. Per-layer time is scaled to the full layer count; the
-    embedding/lm_head/mask/walk part is counted once."""
+    tree mask + additive bias, forward with per-call NF4 dequantise, matmuls
+    and masked SDPA, the acceptance walk, and the index_select commit over
+    every layer's cache, on an ``n_layers`` slice of the shape at full width,
+    P and T (the whole model when it has no more layers). Stages are timed
+    separately (median of ``runs`` warm runs): mask, dequant, matmul (the
+    lm_head apart), sdpa, the rest of the forward (norms, RoPE, SwiGLU, KV
+    concatenation), walk and commit; per-layer stages are scaled to the full
+    layer count. A second timing with every linear dequantised once beforehand
+    is the lower bound of the same path without per-call dequantisation."""
     import torch
 
     from oracle import masks as om
@@ -255,13 +277,19 @@ def cpu_baseline(wl, seed, n_layers: int, runs: int):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     full = wl.model
-    fl = tuple(min(f, n_layers) for f in (1, n_layers, n_layers))
-    shape = full.reduced(n_layers, feature_layers=fl)
+    n_layers = min(n_layers, full.num_layers)
+    scale = full.num_layers / n_layers
+    if n_layers < full.num_layers:
+        fl = tuple(min(f, n_layers) for f in (1, n_layers, n_layers))
+        shape = full.reduced(n_layers, feature_layers=fl)
+    else:
+        shape = full
     dm = DeviceModel.synthetic(shape, seed, "cuda:0", keep_logical=True)
     hw = dm.host_weights()
     del dm
     torch.cuda.empty_cache()
     orc = OracleTarget(shape, hw)
+    orc.timer.enabled = True
     P, T = wl.prefix_len, wl.tree_nodes
     dt = orc.dtype
     g = torch.Generator().manual_seed(seed)
@@ -271,46 +299,65 @@ def cpu_baseline(wl, seed, n_layers: int, runs: int):
     tokens, parents = synth.tree_for_seed(seed, full.vocab, wl.depth, wl.widths, wl.top_k)
 
     def one():
+        orc.timer.seconds.clear()
         t0 = time.perf_counter()
         allow = om.tree_allow_mask(parents, P)
         bias = om.to_additive_bias(allow[P:, :], dt)
         pos = om.tree_position_ids(parents, P)[P:]
-        t_mask = time.perf_counter() - t0
         t1 = time.perf_counter()
         lg, _, cache = orc.forward(tokens, pos, kv, bias)
-        t_fwd = time.perf_counter() - t1
         t2 = time.perf_counter()
         path, _ = ov.accept_tree_cached(root, lg[0], tokens, parents)
+        t3 = time.perf_counter()
         keep = torch.tensor(list(range(P)) + [P + t for t in path])
         for k_, v_ in cache:
             k_.index_select(2, keep).contiguous()
             v_.index_select(2, keep).contiguous()
-        t_walk = time.perf_counter() - t2
-        return t_mask, t_fwd, t_walk
+        t4 = time.perf_counter()
+        st = dict(orc.timer.seconds)
+        return {"mask": t1 - t0, "forward": t2 - t1, "walk": t3 - t2, "commit": t4 - t3,
+                "dequant": st.get("dequant", 0.0), "matmul": st.get("matmul", 0.0), "sdpa": st.get("sdpa", 0.0)}
+
+    def median_of(samples, key):
+        return statistics.median(smp[key] for smp in samples)
 
     one()  # warm-up
     samples = [one() for _ in range(runs)]
-    t_mask = statistics.median(s[0] for s in samples)
-    t_fwd = statistics.median(s[1] for s in samples)
-    t_walk = statistics.median(s[2] for s in samples)
-    # lm_head + final norm + embedding, timed alone, is the per-pass fixed part of the forward
+    # the lm_head product alone: the per-pass (unscaled) part of "matmul"
     x = torch.randn((1, T, full.hidden)).to(dt)
     lm = hw["lm_head"]
-    fixed = []
+    heads = []
     for _ in range(runs + 1):
         t0 = time.perf_counter()
         torch.nn.functional.linear(x, lm)
-        fixed.append(time.perf_counter() - t0)
-    t_head = statistics.median(fixed[1:])
-    per_layer_fwd = max(0.0, t_fwd - t_head) / n_layers
-    # compaction cost scales with the layer count too
-    t_pass = t_mask + t_head + per_layer_fwd * full.num_layers + t_walk * full.num_layers / n_layers
+        heads.append(time.perf_counter() - t0)
+    t_head = statistics.median(heads[1:])
+
+    def full_pass(smp):
+        st = {k: median_of(smp, k) for k in ("mask", "forward", "walk", "commit", "dequant", "matmul", "sdpa")}
+        mm_layers = max(0.0, st["matmul"] - t_head)
+        other = max(0.0, st["forward"] - st["dequant"] - st["matmul"] - st["sdpa"])
+        stages = {"mask": st["mask"], "dequant": st["dequant"] * scale, "matmul": mm_layers * scale + t_head,
+                  "sdpa": st["sdpa"] * scale, "other_forward": other * scale, "walk": st["walk"],
+                  "commit": st["commit"] * scale}
+        return stages, sum(stages.values())
+
+    stages, t_pass = full_pass(samples)
+    # lower bound: the same forward with every linear dequantised once beforehand
+    orc.cache_dequant = True
+    one()
+    pre = [one() for _ in range(runs)]
+    _, t_pre = full_pass(pre)
     pass_bytes = algorithmic_bytes(full, [P] * wl.batch, T)
+    nf4 = full.weight_format == "nf4"
     return {"value": round(pass_bytes / t_pass / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "ms_per_pass": round(t_pass * 1e3, 1),
-            "sample": (f"oracle forward of a {n_layers}-layer slice at full width (H={full.hidden}, "
-                       f"I={full.intermediate}, V={full.vocab}, P={P}, T={T}; per-call NF4 dequantise in torch), "
-                       f"median of {runs} runs after 1 warm-up, per-layer part scaled x{full.num_layers / n_layers:g}; "
+            "stages_ms": {k: round(v * 1e3, 2) for k, v in stages.items()},
+            "ms_per_pass_predequantised": round(t_pre * 1e3, 1) if nf4 else None,
+            "sample": (f"oracle forward of {'a ' + str(n_layers) + '-layer slice' if scale > 1 else 'the whole model'}"
+                       f" at full width (H={full.hidden}, I={full.intermediate}, V={full.vocab}, P={P}, T={T}"
+                       f"{'; per-call NF4 dequantise in torch' if nf4 else ''}), median of {runs} runs after "
+                       f"1 warm-up{', per-layer stages scaled x' + format(scale, 'g') if scale > 1 else ''}; "
                        f"torch threads = {cores}")}
 
 
@@ -410,7 +457,6 @@ def draft_line(wl, seed: int, reps: int = 10) -> dict:
                        "drafter_layers": 2, "eager": True}}
 
 
-MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def batch_line(wl, seed: int, steps: int, warmup: int, gemm_reps: int) -> dict:
@@ -591,6 +637,12 @@ def main(argv=None) -> int:
                 "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(wl.name),
                 "kernel": r["kernel"], "mean_launch_us": r["mean_launch_us"],
                 "bytes_per_launch": r["bytes_per_launch"]}
+    mfma = None
+    if wl.model.dtype != "float32":  # the fp32 path runs on the VALU
+        fl = mfma_flops_per_pass(wl.model, wl.tree_nodes, wl.prefix_len)
+        tf = fl / (ms * 1e-3) / 1e12
+        mfma = {"flops_per_pass": fl, "tflops": round(tf, 1), "util": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                "peak_tflops": MFMA_BF16_PEAK_TFLOPS}
     cpu = None
     if not a.no_cpu_baseline:
         del step
@@ -602,7 +654,7 @@ def main(argv=None) -> int:
     out = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "vs_baseline": None, "dtype": DTYPE_NAMES[wl.model.dtype], "data": "synthetic",
         "config": {"workload": wl.name, "layers": wl.model.num_layers, "hidden": wl.model.hidden,
                    "heads": f"{wl.model.num_heads}/{wl.model.num_kv_heads}", "intermediate": wl.model.intermediate,
                    "vocab": wl.model.vocab, "weights": wl.model.weight_format, "tree_nodes": wl.tree_nodes,
@@ -611,6 +663,7 @@ def main(argv=None) -> int:
         "latency_ms_median": round(med_ms, 4),
         "pass_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
         "accepted": len(path),
+        "mfma": mfma,
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -77,7 +77,18 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("kind,shape", CASES, ids=[c[1].name for c in CASES])
+# Llama-2-7B's real width (H=4096, 32 heads of 128, I=11008, V=32000) at two
+# layers: the GEMM reduction lengths, head count and vocabulary the GPU path
+# runs at, in fp32 and in bf16.
+WIDE = [
+    ("llama", ModelShape("llama7b-width-2l-f32", 2, 4096, 32, 32, 128, 11008, 32000, rms_eps=1e-5, rope_theta=1e4,
+                         dtype="float32", feature_layers=(0, 1, 2))),
+    ("llama", ModelShape("llama7b-width-2l-bf16", 2, 4096, 32, 32, 128, 11008, 32000, rms_eps=1e-5,
+                         rope_theta=1e4, dtype="bfloat16", feature_layers=(0, 1, 2))),
+]
+
+
+@pytest.mark.parametrize("kind,shape", CASES + WIDE, ids=[c[1].name for c in CASES + WIDE])
 def test_oracle_matches_transformers(kind, shape):
     model, dt = _hf_model(kind, shape, seed=7)
     prompt = [3, 17, 250, 9, 44, 101, 7, 300, 12, 5, 77]
