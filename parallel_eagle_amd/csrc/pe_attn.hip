@@ -499,13 +499,17 @@ __global__ __launch_bounds__(128) void attn_generic_kernel(
   const typename E::T* qr = q + ((int64_t)t * nh + hq) * hd;
   float* sc = scores + ((int64_t)t * nh + hq) * S;
   __shared__ float red[2];
+  __shared__ float qs[256];  // the query row, read by every thread
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = E::load(qr, d);
+  __syncthreads();
   float lmax = kInitMax;
   for (int64_t j = threadIdx.x; j < S; j += blockDim.x) {
     float v = kMaskedScore;
     if (key_allowed(j, P, t, mask_mode, nb)) {
       const typename E::T* kr = kc + ((int64_t)kvh * cap + j) * hd;
       float acc = 0.f;
-      for (int d = 0; d < hd; ++d) acc = fmaf(E::load(qr, d), E::load(kr, d), acc);
+#pragma unroll 8
+      for (int d = 0; d < hd; ++d) acc = fmaf(qs[d], E::load(kr, d), acc);
       v = eager ? E::round(__fdiv_rn(E::round(acc), sqrtf((float)hd))) : acc * scale;
     }
     sc[j] = v;
@@ -529,12 +533,14 @@ __global__ __launch_bounds__(128) void attn_generic_kernel(
   const float invL = 1.0f / L;
   for (int d = threadIdx.x; d < hd; d += blockDim.x) {
     float acc = 0.f;
+    // every key row below S is cache memory, so the loads are unconditional
+    // (independent, several in flight); masked keys (p == 0) add nothing
+#pragma unroll 8
     for (int64_t j = 0; j < S; ++j) {
       const float p = sc[j];
-      if (p != 0.f) {
-        const float pr = eager ? E::round(__fmul_rn(p, invL)) : E::round(p);
-        acc = fmaf(pr, E::load(vc + ((int64_t)kvh * cap + j) * hd, d), acc);
-      }
+      const float v = E::load(vc + ((int64_t)kvh * cap + j) * hd, d);
+      const float pr = eager ? E::round(__fmul_rn(p, invL)) : E::round(p);
+      acc = p != 0.f ? fmaf(pr, v, acc) : acc;
     }
     E::store(out, (int64_t)t * ld_out + (int64_t)hq * hd + d, eager ? acc : acc / L);
   }

@@ -947,34 +947,44 @@ __global__ __launch_bounds__(kWaves * 64, 3) void dense_gemm_kernel(const uint16
   finish_tile<FMT, NT, MT>(acc, red, group, split, S, partial, counters, e);
 }
 
-// fp32 linear on VALU: thread = output column, 8 rows per block row.
-__global__ __launch_bounds__(64) void f32_gemm_kernel(const float* __restrict__ X, int64_t ldx, int M, int K,
-                                                      const float* __restrict__ W, int n_out, EpiArgs e) {
-  const int col = blockIdx.x * 64 + threadIdx.x;
+// fp32 linear (VALU): one wave per output column (with SwiGLU, the column's
+// gate and up weight rows), lanes strided across K so that every weight and X
+// load is 256 contiguous bytes; 8 rows per workgroup, each row's 64 lane sums
+// reduced across the wave.
+template <bool SW>
+__global__ __launch_bounds__(256) void f32_gemm_kernel(const float* __restrict__ X, int64_t ldx, int M, int K,
+                                                       const float* __restrict__ W, int n_out, EpiArgs e) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = blockIdx.x * 4 + wave;
   const int m0 = blockIdx.y * 8;
-  if (col >= n_out) return;
-  const bool swiglu = e.op == PE_EPI_SWIGLU;
-  const int wrow = swiglu ? (col >> 5) * 64 + (col & 31) : col;
+  if (col >= n_out) return;  // no workgroup barrier below
+  const int wrow = SW ? (col >> 5) * 64 + (col & 31) : col;
   const float* wg = W + (int64_t)wrow * K;
   const float* wu = W + (int64_t)(wrow + 32) * K;
+  const int nrow = min(8, M - m0);
   float a[8], b[8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) { a[r] = 0.f; b[r] = 0.f; }
-  const int nrow = min(8, M - m0);
-  for (int k = 0; k < K; ++k) {
+  for (int r = 0; r < 8; ++r) a[r] = b[r] = 0.f;
+  for (int k = lane; k < K; k += 64) {
     const float w1 = wg[k];
-    const float w2 = swiglu ? wu[k] : 0.f;
+    const float w2 = SW ? wu[k] : 0.f;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       if (r < nrow) {
         const float x = X[(int64_t)(m0 + r) * ldx + k];
         a[r] = fmaf(x, w1, a[r]);
-        if (swiglu) b[r] = fmaf(x, w2, b[r]);
+        if constexpr (SW) b[r] = fmaf(x, w2, b[r]);
       }
     }
   }
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    a[r] = wave_sum(a[r]);
+    if constexpr (SW) b[r] = wave_sum(b[r]);
+  }
+  if (lane != 0) return;
   for (int r = 0; r < nrow; ++r) {
-    if (swiglu) epi_swiglu<PE_DTYPE_F32>(e, m0 + r, col, a[r], b[r]);
+    if constexpr (SW) epi_swiglu<PE_DTYPE_F32>(e, m0 + r, col, a[r], b[r]);
     else epi_value<PE_DTYPE_F32>(e, m0 + r, col, a[r]);
   }
 }
@@ -1552,8 +1562,11 @@ extern "C" int pe_dense_gemm(const void* x, int64_t ldx, int M, int K, const voi
     if (epilogue == PE_EPI_SWIGLU && N % 64) return PE_ERR_ARG;
     EpiArgs e = make_epi(epilogue, M, N, bias, resid, ld_resid, out, ld_out);
     const int n_out = epilogue == PE_EPI_SWIGLU ? N / 2 : N;
-    dim3 grid((n_out + 63) / 64, (M + 7) / 8);
-    f32_gemm_kernel<<<grid, 64, 0, st>>>((const float*)x, ldx, M, K, (const float*)w, n_out, e);
+    dim3 grid((n_out + 3) / 4, (M + 7) / 8);
+    if (epilogue == PE_EPI_SWIGLU)
+      f32_gemm_kernel<true><<<grid, 256, 0, st>>>((const float*)x, ldx, M, K, (const float*)w, n_out, e);
+    else
+      f32_gemm_kernel<false><<<grid, 256, 0, st>>>((const float*)x, ldx, M, K, (const float*)w, n_out, e);
     PE_CHECK_LAUNCH();
     return PE_OK;
   }
