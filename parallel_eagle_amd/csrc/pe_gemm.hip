@@ -869,6 +869,129 @@ __global__ __launch_bounds__(kWaves * 64, 2) void nf4_gemm_bigm_kernel(const uin
 }
 
 // ---------------------------------------------------------------------------
+// Dense 16-bit GEMM for many rows (the batched pass's lm_head)
+// ---------------------------------------------------------------------------
+// The many-row NF4 kernel's structure on tiled bf16 / fp16 weights: one
+// workgroup = 4 waves = 128 columns x all of K; per 128-wide unit wave w
+// copies tile w's MFMA B fragments of the unit (8 k-steps x 64 lanes x 16 B,
+// requested two units ahead, in the k order of the A-tiled X) into the
+// double-buffered LDS tile, and after one barrier multiplies its own M tiles
+// by all four tiles.
+// Each weight is read from HBM once for every row; the outputs are rounded
+// once and stored in the dtype, row-major with leading dimension ld.
+template <int DT, int NMT, int WV>
+__device__ __forceinline__ void dense_bigm_wave(uint8_t* smem, const uint16_t* __restrict__ X,
+                                                const uint16_t* __restrict__ W, int NP, int group, int mt0, int M,
+                                                void* __restrict__ out, int64_t ld) {
+  constexpr int MA = NMT > 0 ? NMT : 1;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 5, ln = lane & 31;
+  u32x4_t* bufs = (u32x4_t*)smem;
+  const int64_t tile = (int64_t)group * kBigNT + WV;
+  // A-tiled X gives k-step s of a unit the k = 64 g + 8 s + e (lane half g):
+  // the two 64-wide halves interleaved, as the NF4 tiles order them. The dense
+  // tiles hold k = 16 ks + 8 (lane / 32) + e, so lane (n, g) fetches its
+  // fragment from k-step 8 p + 4 g + s / 2, lane n + 32 (s % 2) of the tile:
+  // two 512-byte contiguous runs per load instruction.
+  auto load_b = [&](u32x4_t (&b)[8], int p) {
+    const int pc = min(p, NP - 1);
+    const u32x4_t* src = (const u32x4_t*)(W + ((tile * NP * 8 + 8 * pc + 4 * g) * 64 + ln) * 8);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) b[s] = __builtin_nontemporal_load(src + (s >> 1) * 64 + 32 * (s & 1));
+  };
+  auto store_b = [&](const u32x4_t (&b)[8], int p) {
+    u32x4_t* dst = bufs + ((p & 1) * kBigNT + WV) * 8 * 64 + lane;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) dst[s * 64] = b[s];
+  };
+  f32x16_t acc[kBigNT][MA];
+#pragma unroll
+  for (int nt = 0; nt < kBigNT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MA; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.f;
+  u32x4_t x[4][MA];
+  auto load_x = [&](int p, int s) {
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+      x[s & 3][mt] = *(const u32x4_t*)(X + ((((int64_t)(mt0 + mt) * NP + p) * 8 + s) * 64 + lane) * 8);
+  };
+  auto multiply = [&](int p) {
+    const u32x4_t* src = bufs + (p & 1) * kBigNT * 8 * 64 + lane;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s + 2 < 8) load_x(p, s + 2);
+#pragma unroll
+      for (int nt = 0; nt < kBigNT; ++nt) {
+        const u32x4_t b = src[(nt * 8 + s) * 64];
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) acc[nt][mt] = mfma16<DT>(x[s & 3][mt], b, acc[nt][mt]);
+      }
+    }
+  };
+  u32x4_t ba[8], bb[8];
+  load_b(ba, 0);
+  load_b(bb, 1);
+  for (int p = 0; p < NP; p += 2) {
+    load_x(p, 0);
+    load_x(p, 1);
+    store_b(ba, p);
+    load_b(ba, p + 2);
+    lds_barrier();  // unit p's fragments are complete; the other slot is free
+    multiply(p);
+    if (p + 1 < NP) {  // the same for every wave of the workgroup
+      load_x(p + 1, 0);
+      load_x(p + 1, 1);
+      store_b(bb, p + 1);
+      load_b(bb, p + 3);
+      lds_barrier();
+      multiply(p + 1);
+    }
+  }
+  typedef typename Elem<DT>::T Te;
+#pragma unroll
+  for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = (mt0 + mt) * 32 + 8 * q4 + 4 * g + j;
+        if (row < M)
+#pragma unroll
+          for (int nt = 0; nt < kBigNT; ++nt)
+            Elem<DT>::store((Te*)out, (int64_t)row * ld + (group * kBigNT + nt) * 32 + ln, acc[nt][mt][4 * q4 + j]);
+      }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kWaves * 64, 2) void dense_gemm_bigm_kernel(const uint16_t* __restrict__ X,
+                                                                        const uint16_t* __restrict__ W, int NP,
+                                                                        int mtiles, int M, void* __restrict__ out,
+                                                                        int64_t ld) {
+  __shared__ __align__(256) uint8_t smem[2 * kBigBufUnit];
+  const int group = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int mt0 = wave * 2;
+  const int nmt = max(0, min(2, mtiles - mt0));
+#define PE_DBIGM_WAVE(N)                                                                       \
+  switch (wave) {                                                                              \
+    case 0: dense_bigm_wave<DT, N, 0>(smem, X, W, NP, group, mt0, M, out, ld); break;          \
+    case 1: dense_bigm_wave<DT, N, 1>(smem, X, W, NP, group, mt0, M, out, ld); break;          \
+    case 2: dense_bigm_wave<DT, N, 2>(smem, X, W, NP, group, mt0, M, out, ld); break;          \
+    default: dense_bigm_wave<DT, N, 3>(smem, X, W, NP, group, mt0, M, out, ld); break;         \
+  }
+  if (nmt == 2) {
+    PE_DBIGM_WAVE(2)
+  } else if (nmt == 1) {
+    PE_DBIGM_WAVE(1)
+  } else {
+    PE_DBIGM_WAVE(0)
+  }
+#undef PE_DBIGM_WAVE
+}
+
+// ---------------------------------------------------------------------------
 // Dense 16-bit GEMM: one iteration = 4 MFMA k-steps (64 along K) of NT tiles.
 // Same pipeline as the NF4 kernel; a padded iteration multiplies a zero X.
 // ---------------------------------------------------------------------------
@@ -1472,6 +1595,25 @@ BigPlan big_plan(int N, int K) {
 int64_t pe_internal_nf4_bigm_partials_bytes(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K < 128 || N % (32 * kBigNT) || K % 128) return 0;
   return (int64_t)big_plan(N, K).S * M * N * 4;
+}
+
+int pe_internal_dense_bigm(const void* x_tiled, int M, int K, const void* w, int dtype, int N, void* out,
+                           int64_t ld_out, hipStream_t st) {
+  if (!x_tiled || !w || !out || M <= 0 || M > 8 * 32 || K % 128 || N % (32 * kBigNT) || ld_out < N)
+    return PE_ERR_ARG;
+  const int np = K / 128;
+  const dim3 grid(N / (32 * kBigNT));
+  const int mtiles = (M + 31) / 32;
+  if (dtype == PE_DTYPE_BF16)
+    dense_gemm_bigm_kernel<PE_DTYPE_BF16><<<grid, kWaves * 64, 0, st>>>((const uint16_t*)x_tiled,
+                                                                         (const uint16_t*)w, np, mtiles, M, out, ld_out);
+  else if (dtype == PE_DTYPE_F16)
+    dense_gemm_bigm_kernel<PE_DTYPE_F16><<<grid, kWaves * 64, 0, st>>>((const uint16_t*)x_tiled,
+                                                                        (const uint16_t*)w, np, mtiles, M, out, ld_out);
+  else
+    return PE_ERR_ARG;
+  PE_CHECK_LAUNCH();
+  return PE_OK;
 }
 
 int pe_internal_nf4_bigm_partials(const void* x_tiled, int M, int K, const void* w, const void* wabs, int N,

@@ -50,6 +50,11 @@ PE_INTERNAL int pe_internal_rope_kv_partials(const float* partial, int S, int M,
 // pe_gemm.hip: the NF4 GEMM for many rows (A-tiled X, 64 < M <= 256,
 // N % 128 == 0, fp16 absmax): each weight dequantised once for all rows;
 // fp32 split partials [S][M][N] (*splits receives S).
+// Dense 16-bit Y[M][N] = X . W^T for 64 < M <= 256 rows (X A-tiled, W in the
+// MFMA-tiled layout, K % 128 == 0, N % 128 == 0), each weight read once for all
+// rows; Y row-major in the dtype (leading dimension ld_out).
+PE_INTERNAL int pe_internal_dense_bigm(const void* x_tiled, int M, int K, const void* w, int dtype, int N, void* out,
+                                       int64_t ld_out, hipStream_t st);
 PE_INTERNAL int64_t pe_internal_nf4_bigm_partials_bytes(int M, int N, int K);
 PE_INTERNAL int pe_internal_nf4_bigm_partials(const void* x_tiled, int M, int K, const void* w, const void* wabs,
                                               int N, float* partial, int64_t partial_bytes, int* splits,

@@ -598,6 +598,7 @@ int forward_batched(const pe_model_desc* m, const pe_pass_args* a, const BatchLa
     char* act_t = ws + Lb.act_t;
     float* part = (float*)(ws + Lb.part);
     const int nqkv = (nh + 2 * nkv) * hd;
+    const bool big_head = m->vocab % 128 == 0 && (m->dtype == PE_DTYPE_BF16 || m->dtype == PE_DTYPE_F16);
     int S = 0;
     for (int l = 0; l < L; ++l) {
       char* kc = (char*)a->k_cache + l * layer_stride;
@@ -622,10 +623,13 @@ int forward_batched(const pe_model_desc* m, const pe_pass_args* a, const BatchLa
       const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
       const int next_mode = last ? PE_NORM_HF : m->norm_mode;
       PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn,
-                                          last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
+                                          last && !big_head ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx),
+                                          fused_ld, st));
       PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
     }
-    if (a->logits)
+    if (a->logits && big_head)  // every lm_head weight read once for all rows
+      PE_TRY(pe_internal_dense_bigm(xn_t, M, H, m->lm_head, m->dtype, m->vocab, a->logits, m->vocab, st));
+    else if (a->logits)
       PE_TRY(pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
                            m->vocab, gws, gwsb, st));
     return PE_OK;
