@@ -162,6 +162,17 @@ int64_t pe_nf4_gemm_partials_bytes(int M, int N, int K);
 int pe_nf4_gemm_partials(const void* x, int64_t ldx, int x_tiled, int M, int K, const uint8_t* w_tiled,
                          const uint16_t* absmax_tiled, int N, float* partials, int64_t partial_bytes, int* splits,
                          void* stream);
+/* pe_dense_gemm with PE_EPI_STORE (16-bit dtypes, no bias) that also writes,
+ * per output row and column group g, the argmax key of the group's stored
+ * values: keys[row * groups + g] = (order-preserving value bits << 32) |
+ * (0xFFFFFFFF - column), so the largest key of a row names its largest value
+ * at its lowest column (NaN largest), torch.argmax's result. groups =
+ * pe_dense_gemm_argmax_groups(M, N, K). The reference's walk takes
+ * logits.argmax(-1) of each node row after the lm_head (verify.py:52,120;
+ * HF modeling_llama.py:480); this folds that argmax into the lm_head. */
+int pe_dense_gemm_argmax_groups(int M, int N, int K);
+int pe_dense_gemm_argmax(const void* x, int64_t ldx, int M, int K, const void* w, int dtype, int N, void* out,
+                         int64_t ld_out, uint64_t* keys, void* workspace, int64_t workspace_bytes, void* stream);
 /* Dense linear in dtype (bf16/fp16 MFMA on tiled weights, fp32 VALU on row-major).
  * Replaces F.linear in HF modeling_llama.py:175,254-256,280,480. */
 int pe_dense_gemm(const void* x, int64_t ldx, int M, int K, const void* w, int dtype, int N,
@@ -235,6 +246,14 @@ int pe_argmax_rows(const void* x, int64_t ld, int rows, int64_t V, int dtype, in
 int pe_accept_tree(const void* root_logit, const void* node_logits, int64_t ld, int T, int64_t V,
                    int dtype, const int64_t* node_tokens, const int32_t* parents, int32_t* out,
                    int32_t* scratch, void* stream);
+/* accept_tree_cached (src/pe/decode/verify.py:104-125) with each node row's
+ * argmax (verify.py:120) taken from the argmax keys that pe_dense_gemm_argmax
+ * (or pe_forward with node_keys) wrote with the logits, [T][groups], instead of
+ * re-reading the T node rows; the root row is read as in pe_accept_tree.
+ * Same outputs, scratch and limits as pe_accept_tree. */
+int pe_accept_tree_keys(const void* root_logit, int64_t V, int dtype, const uint64_t* node_keys, int groups,
+                        int T, const int64_t* node_tokens, const int32_t* parents, int32_t* out,
+                        int32_t* scratch, void* stream);
 /* pe_accept_tree without a scratch argument and without any allocation: the
  * scratch is a library-owned device array of PE_ACCEPT_NOALLOC_MAX_NODES + 2
  * int32 per GPU (held until the process ends), its counter cleared by a small
@@ -372,6 +391,10 @@ typedef struct pe_pass_args {
   const int32_t* seq_row0;
   const int64_t* seq_prefix;
   int64_t cache_seq_stride;
+  /* Optional (single-sequence 16-bit passes with logits): the lm_head also
+   * writes each row's argmax keys, [M][pe_dense_gemm_argmax_groups(M, vocab,
+   * hidden)] (see pe_dense_gemm_argmax), for pe_accept_tree_keys. NULL: none. */
+  uint64_t* node_keys;
 } pe_pass_args;
 
 /* Workspace for pe_forward with up to M rows and kv_len = P + M keys. */

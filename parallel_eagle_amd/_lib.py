@@ -87,6 +87,7 @@ class PassArgs(C.Structure):
         ("_pad", i32), ("k_cache", vp), ("v_cache", vp), ("cache_capacity", i64), ("logits", vp),
         ("fused", vp), ("workspace", vp), ("workspace_bytes", i64), ("status", vp),
         ("batch", i32), ("max_seq_rows", i32), ("seq_row0", vp), ("seq_prefix", vp), ("cache_seq_stride", i64),
+        ("node_keys", vp),
     ]
 
 
@@ -129,6 +130,9 @@ SIGNATURES: dict[str, tuple] = {
                                     C.c_int, f32, C.c_int, vp, i64, vp, i64, vp]),
     "pe_argmax_rows": (C.c_int, [vp, i64, C.c_int, i64, C.c_int, vp, vp]),
     "pe_accept_tree": (C.c_int, [vp, vp, i64, C.c_int, i64, C.c_int, vp, vp, vp, vp, vp]),
+    "pe_accept_tree_keys": (C.c_int, [vp, i64, C.c_int, vp, C.c_int, C.c_int, vp, vp, vp, vp, vp]),
+    "pe_dense_gemm_argmax_groups": (C.c_int, [C.c_int, C.c_int, C.c_int]),
+    "pe_dense_gemm_argmax": (C.c_int, [vp, i64, C.c_int, C.c_int, vp, C.c_int, C.c_int, vp, i64, vp, vp, i64, vp]),
     "pe_accept_tree_noalloc": (C.c_int, [vp, vp, i64, C.c_int, i64, C.c_int, vp, vp, vp, vp]),
     "pe_propose_tree": (C.c_int, [vp, i64, C.c_int, i64, C.c_int, C.POINTER(C.c_int32), C.c_int, vp, vp,
                                   C.POINTER(C.c_int32), vp, vp, vp]),

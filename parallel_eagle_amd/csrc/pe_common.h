@@ -93,6 +93,24 @@ __device__ __constant__ static const float kNF4[16] = {
     0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
 
 // Wave-level reductions (wave64) through DPP-free shuffles.
+// Order-preserving key of a value for torch.argmax's semantics: larger value
+// -> larger key, every NaN -> the largest key, -0 and +0 -> the same key (they
+// compare equal).
+__device__ __forceinline__ uint32_t arg_key(float f) {
+  if (f != f) return 0xFFFFFFFFu;
+  const uint32_t u = f == 0.f ? 0u : __float_as_uint(f);
+  return (u >> 31) ? ~u : (u | 0x80000000u);
+}
+// (value key, column) as one 64-bit key whose maximum is the largest value at
+// the lowest column
+__device__ __forceinline__ uint64_t arg_key64(float f, int col) {
+  return ((uint64_t)arg_key(f) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)col);
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, o, 64), hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -52,6 +52,9 @@ namespace {
 // by the kernel that consumes them.
 constexpr int kEpiRopeKV = 4;
 constexpr int kEpiPartial = 5;
+// PE_EPI_STORE plus, per row and column group, the argmax key of the group's
+// stored values (amax_keys[row * amax_groups + group], arg_key64)
+constexpr int kEpiArgmax = 6;
 
 struct EpiArgs {
   int op;
@@ -80,6 +83,8 @@ struct EpiArgs {
   const int64_t* kv_off;
   int nh, nkv, hd;
   int32_t* status;
+  uint64_t* amax_keys;  // kEpiArgmax: [M][amax_groups]
+  int amax_groups;
 };
 
 __device__ __forceinline__ int64_t kv_row_elem(const EpiArgs& e, int row) {
@@ -443,6 +448,28 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
       }
       epilogue_row<ADT, NT>(e, group, row, ln, v[mt][j]);
     }
+  if (e.op == kEpiArgmax) {
+    // the group's largest stored value of each row: the lane's NT columns, then
+    // the 32 lanes of its half-wave (the row's 32 * NT columns)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const uint64_t k = arg_key64(Elem<ADT>::round(v[mt][j][nt]), (group * NT + nt) * 32 + ln);
+          best = k > best ? k : best;
+        }
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) {
+          const uint64_t k = shfl_xor_u64(best, o);
+          best = k > best ? k : best;
+        }
+        const int row = mt * 32 + 8 * wave + 4 * g + j;
+        if (ln == 0 && row < e.M) e.amax_keys[(int64_t)row * e.amax_groups + group] = best;
+      }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1403,6 +1430,8 @@ EpiArgs make_epi(int epi, int mc, int N, const void* bias, const void* resid, in
   e.kv_off = nullptr;
   e.nh = e.nkv = e.hd = 0;
   e.status = nullptr;
+  e.amax_keys = nullptr;
+  e.amax_groups = 0;
   return e;
 }
 
@@ -1410,21 +1439,28 @@ EpiArgs make_epi(int epi, int mc, int N, const void* bias, const void* resid, in
 // x_tiled: X is A-tiled (M <= 64, one launch); out_units > 0: out is A-tiled.
 int mfma_gemm(int fmt, const void* x, int64_t ldx, int M, int K, const void* w, const void* wabs, int N,
               int epi, const void* bias, const void* resid, int64_t ld_resid, void* out, int64_t ld_out,
-              void* ws, int64_t ws_bytes, hipStream_t st, bool x_tiled = false, int out_units = 0) {
+              void* ws, int64_t ws_bytes, hipStream_t st, bool x_tiled = false, int out_units = 0,
+              uint64_t* amax_keys = nullptr) {
   int rc = check_gemm_args(x, M, K, w, N, epi, resid, out);
   if (rc != PE_OK) return rc;
+  if (amax_keys && (epi != PE_EPI_STORE || out_units)) return PE_ERR_ARG;
   const bool nf4 = fmt < 0;
   if ((x_tiled || out_units) && M > kMaxChunkRows) return PE_ERR_ARG;
   if (out_units && epi == PE_EPI_RESIDUAL) return PE_ERR_ARG;
   int done = 0;
   while (done < M) {
     const int mc = (M - done > kMaxChunkRows) ? kMaxChunkRows : (M - done);
-    Plan p = make_plan(mc, N, K, nf4, epi);
+    Plan p = make_plan(mc, N, K, nf4, amax_keys ? kEpiArgmax : epi);
     if (!ws || ws_bytes < workspace_of(p)) return PE_ERR_WORKSPACE;
     const size_t esz = 2;
     EpiArgs e = make_epi(epi, mc, N, bias, resid ? (const char*)resid + (size_t)done * ld_resid * esz : nullptr,
                          ld_resid, (char*)out + (size_t)done * ld_out * esz, ld_out);
     e.out_units = out_units;
+    if (amax_keys) {
+      e.op = kEpiArgmax;
+      e.amax_groups = p.groups;
+      e.amax_keys = amax_keys + (int64_t)done * p.groups;
+    }
     const uint16_t* xc = x_tiled ? (const uint16_t*)x : (const uint16_t*)x + (size_t)done * ldx;
     rc = launch_gemm(fmt, p, st, xc, ldx, x_tiled, K, w, wabs, ws, e);
     if (rc != PE_OK) return rc;
@@ -1691,6 +1727,19 @@ extern "C" int pe_nf4_gemm_partials(const void* x, int64_t ldx, int x_tiled, int
   }
   return pe_internal_linear_partials(PE_WFMT_NF4, PE_DTYPE_BF16, x, x_tiled ? K : ldx, x_tiled != 0, M, K, w_tiled,
                                      absmax_tiled, N, partials, partial_bytes, splits, (hipStream_t)stream);
+}
+
+extern "C" int pe_dense_gemm_argmax_groups(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K < 128 || K % 128 || N % 32) return 0;
+  return make_plan(M > kMaxChunkRows ? kMaxChunkRows : M, N, K, false, kEpiArgmax).groups;
+}
+
+extern "C" int pe_dense_gemm_argmax(const void* x, int64_t ldx, int M, int K, const void* w, int dtype, int N,
+                                    void* out, int64_t ld_out, uint64_t* keys, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+  if (!keys || (dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16)) return PE_ERR_ARG;
+  return mfma_gemm(dtype, x, ldx, M, K, w, nullptr, N, PE_EPI_STORE, nullptr, nullptr, 0, out, ld_out, workspace,
+                   workspace_bytes, (hipStream_t)stream, false, 0, keys);
 }
 
 extern "C" int pe_dense_gemm(const void* x, int64_t ldx, int M, int K, const void* w, int dtype, int N,

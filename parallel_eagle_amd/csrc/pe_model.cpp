@@ -224,6 +224,18 @@ rocblas_handle blas_handle() {
 }
 
 // y[M][N] (fp32) = x[M][K] . w[N][K]^T, bf16 operands, fp32 accumulation.
+// The lm_head over the final normed rows (row-major xn); with a->node_keys
+// (single-sequence 16-bit passes) the GEMM also writes each row's argmax keys.
+int lm_head(const pe_model_desc* m, const pe_pass_args* a, const void* xn, int M, void* ws, int64_t wsb,
+            hipStream_t st) {
+  const int H = m->hidden;
+  if (a->node_keys)
+    return pe_dense_gemm_argmax(xn, H, M, H, m->lm_head, m->dtype, m->vocab, a->logits, m->vocab, a->node_keys, ws,
+                                wsb, st);
+  return pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
+                       m->vocab, ws, wsb, st);
+}
+
 int blas_gemm(hipStream_t st, int M, int N, int K, const void* x, const void* w, float* y, void* bws,
               int64_t bws_bytes) {
   rocblas_handle hd = blas_handle();
@@ -323,9 +335,7 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
                                         fused_ld, slot_ptr(fx), fused_ld, st));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
-  if (a->logits)
-    PE_TRY(pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
-                         m->vocab, ws + Lp.gemm, Lp.gemm_bytes, st));
+  if (a->logits) PE_TRY(lm_head(m, a, xn, M, ws + Lp.gemm, Lp.gemm_bytes, st));
 #undef PE_TRY
   return PE_OK;
 }
@@ -464,9 +474,7 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     }
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
-  if (a->logits)
-    PE_TRY(pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
-                         m->vocab, gws, gwsb, st));
+  if (a->logits) PE_TRY(lm_head(m, a, xn, M, gws, gwsb, st));
 #undef PE_TRY
   return PE_OK;
 }
@@ -700,6 +708,8 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
   if (m->attn_mode == PE_ATTN_EAGER && pe_wfmt_nf4(m->weight_format)) return PE_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   if (a->batch < 0) return PE_ERR_ARG;
+  // argmax keys: single-sequence 16-bit passes that write logits
+  if (a->node_keys && (a->batch > 0 || !a->logits || m->dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
   if (a->batch > 0) {
     if (a->mask_mode != PE_MASK_TREE || !a->tree_bits || !a->seq_row0 || !a->seq_prefix) return PE_ERR_ARG;
     if (m->dtype == PE_DTYPE_F32 || m->head_dim != 128 || m->qkv_layout != PE_QKV_ROPE_PAIRED ||
@@ -803,9 +813,7 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
   }
   PE_TRY(pe_rmsnorm(h, H, M, H, m->final_norm, m->rms_eps, m->dtype, xn, H, st));
   PE_TRY(capture(m->num_layers, xn));
-  if (a->logits)
-    PE_TRY(pe_dense_gemm(xn, H, M, H, m->lm_head, m->dtype, m->vocab, PE_EPI_STORE, nullptr, nullptr, 0, a->logits,
-                         m->vocab, gws, gwsb, st));
+  if (a->logits) PE_TRY(lm_head(m, a, xn, M, gws, gwsb, st));
 #undef PE_TRY
   return PE_OK;
 }

@@ -120,14 +120,6 @@ __global__ __launch_bounds__(256) void bias_to_bits_kernel(const typename Elem<D
 // every number, and among equal maxima (or NaNs) the lowest index wins.
 constexpr int kArgThreads = 1024;
 
-// Order-preserving key of a value for the argmax: larger value -> larger key,
-// every NaN -> the largest key, -0 and +0 -> the same key (they compare equal).
-__device__ __forceinline__ uint32_t arg_key(float f) {
-  if (f != f) return 0xFFFFFFFFu;
-  const uint32_t u = f == 0.f ? 0u : __float_as_uint(f);
-  return (u >> 31) ? ~u : (u | 0x80000000u);
-}
-
 // One block of kArgThreads per row. Thread t scans 16-byte vectors t,
 // t + kArgThreads, ... in increasing index order (all loads issued first)
 // keeping the first element of the largest key; the block then reduces with
@@ -206,6 +198,32 @@ __device__ int row_argmax(const typename Elem<DT>::T* __restrict__ x, int64_t V,
   return i1;
 }
 
+// Row argmax from per-column-group keys (arg_key64, written by the lm_head
+// GEMM's argmax epilogue): the largest key and its column; the result is
+// valid in thread 0.
+__device__ int row_argmax_keys(const uint64_t* __restrict__ keys, int groups) {
+  uint64_t best = 0;  // below every real key
+  for (int i = threadIdx.x; i < groups; i += kArgThreads) {
+    const uint64_t k = keys[i];
+    best = k > best ? k : best;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t k = shfl_xor_u64(best, o);
+    best = k > best ? k : best;
+  }
+  __shared__ uint64_t wk[kArgThreads / 64];
+  if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = best;
+  __syncthreads();
+  int idx = -1;
+  if (threadIdx.x == 0) {
+    uint64_t b = wk[0];
+    for (int w = 1; w < kArgThreads / 64; ++w) b = wk[w] > b ? wk[w] : b;
+    idx = b ? (int)(0xFFFFFFFFu - (uint32_t)b) : -1;
+  }
+  return idx;
+}
+
 template <int DT>
 __global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const typename Elem<DT>::T* __restrict__ x,
                                                                   int64_t ld, int64_t V, int32_t* __restrict__ out) {
@@ -234,7 +252,8 @@ __global__ __launch_bounds__(kArgThreads) void accept_kernel(const typename Elem
                                                              int T, const int32_t* __restrict__ seq_row0,
                                                              const int64_t* __restrict__ tokens,
                                                              const int32_t* __restrict__ parents,
-                                                             int32_t* __restrict__ out) {
+                                                             int32_t* __restrict__ out,
+                                                             const uint64_t* __restrict__ node_keys, int groups) {
   if (seq_row0) {
     const int b = blockIdx.y, r0 = seq_row0[b];
     root += b * ld_root;
@@ -250,7 +269,9 @@ __global__ __launch_bounds__(kArgThreads) void accept_kernel(const typename Elem
   int32_t* const amax = work + 1;
   const int r = blockIdx.x;
   const typename Elem<DT>::T* x = (r == 0) ? root : nodes + (int64_t)(r - 1) * ld;
-  const int best = row_argmax<DT>(x, V, nullptr);
+  // node rows from the lm_head's argmax keys when the caller has them
+  const int best = (node_keys && r > 0) ? row_argmax_keys(node_keys + (int64_t)(r - 1) * groups, groups)
+                                        : row_argmax<DT>(x, V, nullptr);
   __shared__ int s_last;
   if (threadIdx.x == 0) {
     __hip_atomic_store(amax + r, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -612,23 +633,26 @@ namespace {
 // node rows into trees of at most T nodes each.
 int launch_accept(const void* root_logit, int64_t ld_root, const void* node_logits, int64_t ld, int T, int64_t V,
                   int dtype, const int32_t* seq_row0, int batch, const int64_t* node_tokens, const int32_t* parents,
-                  int32_t* out, int32_t* work, hipStream_t st) {
+                  int32_t* out, int32_t* work, hipStream_t st, const uint64_t* node_keys = nullptr,
+                  int groups = 0) {
   const dim3 grid(T + 1, batch > 0 ? batch : 1);
   switch (dtype) {
     case PE_DTYPE_F32:
       accept_kernel<PE_DTYPE_F32><<<grid, kArgThreads, 0, st>>>((const float*)root_logit, ld_root,
                                                                 (const float*)node_logits, ld, V, work, T, seq_row0,
-                                                                node_tokens, parents, out);
+                                                                node_tokens, parents, out, node_keys, groups);
       break;
     case PE_DTYPE_BF16:
       accept_kernel<PE_DTYPE_BF16><<<grid, kArgThreads, 0, st>>>((const uint16_t*)root_logit, ld_root,
                                                                  (const uint16_t*)node_logits, ld, V, work, T,
-                                                                 seq_row0, node_tokens, parents, out);
+                                                                 seq_row0, node_tokens, parents, out, node_keys,
+                                                                 groups);
       break;
     case PE_DTYPE_F16:
       accept_kernel<PE_DTYPE_F16><<<grid, kArgThreads, 0, st>>>((const uint16_t*)root_logit, ld_root,
                                                                 (const uint16_t*)node_logits, ld, V, work, T,
-                                                                seq_row0, node_tokens, parents, out);
+                                                                seq_row0, node_tokens, parents, out, node_keys,
+                                                                groups);
       break;
     default:
       return PE_ERR_ARG;
@@ -679,6 +703,17 @@ extern "C" int pe_accept_tree(const void* root_logit, const void* node_logits, i
   if (!work) return PE_ERR_ARG;
   return launch_accept(root_logit, 0, node_logits, ld, T, V, dtype, nullptr, 0, node_tokens, parents, out, work,
                        (hipStream_t)stream);
+}
+
+extern "C" int pe_accept_tree_keys(const void* root_logit, int64_t V, int dtype, const uint64_t* node_keys,
+                                   int groups, int T, const int64_t* node_tokens, const int32_t* parents, int32_t* out,
+                                   int32_t* scratch, void* stream) {
+  if (!root_logit || !out || !scratch || T < 0 || V <= 0) return PE_ERR_ARG;
+  if (dtype != PE_DTYPE_F32 && dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16) return PE_ERR_ARG;
+  if (T > 0 && (!node_keys || groups <= 0 || !node_tokens || !parents)) return PE_ERR_ARG;
+  if (T > kWalkMax) return PE_ERR_TREE;
+  return launch_accept(root_logit, 0, nullptr, 0, T, V, dtype, nullptr, 0, node_tokens, parents, out, scratch,
+                       (hipStream_t)stream, node_keys, groups);
 }
 
 extern "C" int pe_accept_tree_batch(const void* root_logits, int64_t ld_root, const void* node_logits, int64_t ld,

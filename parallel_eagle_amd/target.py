@@ -403,8 +403,10 @@ class VerifyStep:
        parent list (masks.py:118-156 without the dense (P+T)^2 matrix),
     2. ``pe_forward``: the masked verification forward over the cache with the
        in-place K/V append (target.py:203-224),
-    3. ``pe_accept_tree``: the greedy walk against the root logit
-       (decode/verify.py:104-125),
+    3. ``pe_accept_tree_keys``: the greedy walk against the root logit
+       (decode/verify.py:104-125), each node row's argmax taken from the keys
+       the lm_head wrote with the logits (16-bit models; fp32 models re-read
+       the rows with ``pe_accept_tree``),
     4. ``pe_kv_compact``: the accepted rows move to P, P+1, ... in place
        (target.py:194-201 with the keep index of serve.py:308-309).
 
@@ -434,6 +436,11 @@ class VerifyStep:
         self.accept_scratch = torch.zeros(self.T + 2, dtype=torch.int32, device=dev)
         self.ws = torch.zeros(target.model.workspace_bytes(self.T, self.P + self.T), dtype=torch.uint8,
                               device=dev)
+        # the lm_head's per-row argmax keys (16-bit models): [T][groups] uint64
+        self.key_groups = 0 if target.dtype == torch.float32 else int(
+            _lib.load().pe_dense_gemm_argmax_groups(self.T, s.vocab, s.hidden))
+        self.node_keys = (torch.zeros((self.T, self.key_groups), dtype=torch.int64, device=dev)
+                          if self.key_groups > 0 else None)
         self.graph = None
         a = _lib.PassArgs()
         a.input_ids, a.positions, a.M, a.mask_mode, a.prefix_len = (self.ids.data_ptr(), self.pos.data_ptr(),
@@ -447,6 +454,7 @@ class VerifyStep:
         a.logits, a.fused = self.logits.data_ptr(), self.fused.data_ptr()
         a.workspace, a.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
         a.status = target.status.data_ptr()
+        a.node_keys = self.node_keys.data_ptr() if self.node_keys is not None else None
         self._args = a
         self._buffers = cache.buffers()
 
@@ -474,10 +482,16 @@ class VerifyStep:
                                    self.pos.data_ptr(), self.depth.data_ptr(), self.tm.status.data_ptr(), st),
                    "pe_tree_masks")
         _lib.check(L.pe_forward(C.byref(self.tm.model.desc()), C.byref(self._args), st), "pe_forward")
-        _lib.check(L.pe_accept_tree(self.root_logit.data_ptr(), self.logits.data_ptr(), s.vocab, self.T, s.vocab,
-                                    ops.dcode(self.tm.dtype), self.ids.data_ptr(), self.parents.data_ptr(),
-                                    self.accept_out.data_ptr(), self.accept_scratch.data_ptr(), st),
-                   "pe_accept_tree")
+        if self.node_keys is not None:
+            _lib.check(L.pe_accept_tree_keys(self.root_logit.data_ptr(), s.vocab, ops.dcode(self.tm.dtype),
+                                             self.node_keys.data_ptr(), self.key_groups, self.T, self.ids.data_ptr(),
+                                             self.parents.data_ptr(), self.accept_out.data_ptr(),
+                                             self.accept_scratch.data_ptr(), st), "pe_accept_tree_keys")
+        else:
+            _lib.check(L.pe_accept_tree(self.root_logit.data_ptr(), self.logits.data_ptr(), s.vocab, self.T,
+                                        s.vocab, ops.dcode(self.tm.dtype), self.ids.data_ptr(),
+                                        self.parents.data_ptr(), self.accept_out.data_ptr(),
+                                        self.accept_scratch.data_ptr(), st), "pe_accept_tree")
         _lib.check(L.pe_kv_compact(c.k.data_ptr(), c.v.data_ptr(), s.num_layers, s.num_kv_heads, c.capacity,
                                    s.head_dim, ops.dcode(self.tm.dtype), self.P, self.accept_out.data_ptr(), st),
                    "pe_kv_compact")

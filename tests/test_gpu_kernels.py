@@ -341,6 +341,86 @@ def test_argmax_rows_first_index_and_nan():
     assert got == [7, 10, 0]
 
 
+def _argmax_gemm(x, w_tiled, n, dtype):
+    L = _lib.load()
+    m, k = x.shape
+    groups = int(L.pe_dense_gemm_argmax_groups(m, n, k))
+    out = torch.empty((m, n), dtype=dtype, device=DEV)
+    keys = torch.zeros((m, groups), dtype=torch.int64, device=DEV)
+    wsb = int(L.pe_gemm_workspace_bytes(m, n, k, _lib.PE_WFMT_DENSE, ops.dcode(dtype), _lib.PE_EPI_STORE))
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=DEV)
+    _lib.check(L.pe_dense_gemm_argmax(x.data_ptr(), k, m, k, w_tiled.data_ptr(), ops.dcode(dtype), n, out.data_ptr(),
+                                      n, keys.data_ptr(), ws.data_ptr(), wsb, ops.stream_ptr()), "pe_dense_gemm_argmax")
+    return out, keys, groups
+
+
+def _tied_lm_head(n, k, dtype, m, seed):
+    """Weights whose rows 5, 900 and n - 1 are identical and carry a feature X
+    has at 10 in every row: those three columns tie exactly at (nearly always)
+    the row's maximum."""
+    g = torch.Generator().manual_seed(seed)
+    w = 0.02 * torch.randn(n, k, generator=g)
+    w[:, 0] = 0.0
+    w[5, 0] = 1.0
+    w[900] = w[5]
+    w[n - 1] = w[5]
+    x = torch.randn(m, k, generator=g)
+    x[:, 0] = 10.0
+    return x.to(dtype), w.to(dtype)
+
+
+@pytest.mark.parametrize("dtype,m", [(torch.bfloat16, 26), (torch.float16, 26), (torch.bfloat16, 100)])
+def test_lm_head_argmax_keys_name_each_rows_first_maximum(dtype, m):
+    """pe_dense_gemm_argmax at the 7B lm_head's shape (K = 4096, N = 32000; 100
+    rows run as two launches): the logits equal pe_dense_gemm's bit for bit, and
+    each row's largest key names the first maximum of that row's stored logits
+    (np.argmax), here mostly a three-way exact tie."""
+    n, k = 32000, 4096
+    x, w = _tied_lm_head(n, k, dtype, m, seed=m)
+    wt = ops.dense_repack(w.to(DEV))
+    out, keys, groups = _argmax_gemm(x.to(DEV), wt, n, dtype)
+    assert groups == n // 64
+    ref = ops.linear(x.to(DEV), n, dense=wt)
+    assert torch.equal(out, ref)
+    logits = out.float().cpu().numpy()
+    kk = keys.cpu().numpy().view(np.uint64)
+    best = kk.max(axis=1)
+    got = (np.uint64(0xFFFFFFFF) - (best & np.uint64(0xFFFFFFFF))).astype(np.int64)
+    want = logits.argmax(axis=1)
+    assert np.array_equal(got, want)
+    assert np.mean(want == 5) > 0.9  # the planted tie decides most rows
+
+
+def test_accept_tree_from_argmax_keys_equals_the_logit_walk():
+    """pe_accept_tree_keys (node argmaxes from the lm_head's keys) returns what
+    pe_accept_tree returns on the same logits, with a chain of node tokens
+    planted on the rows' argmaxes so the walk goes deep."""
+    n, k, dtype = 32000, 4096, torch.bfloat16
+    parents = [-1, 0, 0, 1, 1, 2, 3, 3, 4, 6, 6, 9]
+    T = len(parents)
+    x, w = _tied_lm_head(n, k, dtype, T, seed=11)
+    x[1:, 0] = 0.0  # most rows without the tie feature: their own argmaxes
+    logits, keys, groups = _argmax_gemm(x.to(DEV), ops.dense_repack(w.to(DEV)), n, dtype)
+    root = torch.randn(n, generator=torch.Generator().manual_seed(4)).to(dtype).to(DEV)
+    amax = [int(root.float().argmax())] + [int(r) for r in logits.float().argmax(dim=1).cpu()]
+    tokens = [0] * T
+    for node in (0, 1, 3, 6, 9):  # a chain through the tree
+        tokens[node] = amax[0] if parents[node] < 0 else amax[1 + parents[node]]
+    tok = torch.tensor(tokens, dtype=torch.int64, device=DEV)
+    par = torch.tensor(parents, dtype=torch.int32, device=DEV)
+    want = ops.accept_tree(root, logits, tok, par).cpu().tolist()
+    L = _lib.load()
+    out = torch.zeros(T + 2, dtype=torch.int32, device=DEV)
+    scratch = torch.zeros(T + 2, dtype=torch.int32, device=DEV)
+    _lib.check(L.pe_accept_tree_keys(root.data_ptr(), n, ops.dcode(dtype), keys.data_ptr(), groups, T, tok.data_ptr(),
+                                     par.data_ptr(), out.data_ptr(), scratch.data_ptr(), ops.stream_ptr()),
+               "pe_accept_tree_keys")
+    got = out.cpu().tolist()
+    assert got[: 2 + got[0]] == want[: 2 + want[0]]
+    assert got[0] >= 5
+    assert scratch[0].item() == 0
+
+
 @pytest.mark.parametrize("path", [[], [0], [1, 3, 7], [0, 1, 2, 3, 4]])
 def test_kv_compact_matches_gather_semantics(path):
     L, nkv, cap, hd, P, T = 3, 2, 64, 128, 20, 9
