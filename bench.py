@@ -29,6 +29,7 @@ by the measured pass time (GB/s), ``ms_per_step`` = pass latency, plus
   workload.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload NAME] [--no-cpu-baseline]
+       python bench.py --loop    (decode-loop tokens/s)
        python bench.py --calibrate-copy
 """
 
@@ -66,6 +67,8 @@ def parse_args(argv=None):
     p.add_argument("--prefill", action="store_true",
                    help="instead of the verification pass: time a causal prefill of the workload's prefix length "
                         "from an empty cache and a one-token continuation (eager forward_cached calls)")
+    p.add_argument("--loop", action="store_true",
+                   help="tokens/s of the decode loop (greedy and the device-resident speculative loop)")
     p.add_argument("--draft", action="store_true",
                    help="instead of the verification pass: time the drafting step before it (a 2-layer drafter's "
                         "draft_logits over the workload's prefix plus k - 1 mask slots, then the beam tree proposal)")
@@ -399,6 +402,100 @@ def prefill_line(wl, seed: int, reps: int = 3) -> dict:
                        "weights": shape.weight_format, "eager": True}}
 
 
+def loop_line(wl, seed: int, new_tokens: int = 96) -> dict:
+    """Tokens/s of the whole decode loop on the workload's model (synthetic
+    weights, all layers) over a P-token random prompt: greedy decoding through
+    the reference-shaped API (vanilla_generate_cached, one forward per token)
+    and the device-resident speculative loop (SpeculativeDecoder: drafter,
+    device beam, verification pass, walk, compaction, one host read per step)
+    with (a) a random 2-layer device drafter (nothing is accepted: every step
+    is the miss path) and (b) the same drafter told the greedy continuation
+    (every depth the greedy decode chose). Each run reports whether it emitted
+    exactly the greedy tokens. On random weights the logits are flat (about 30%
+    of greedy steps have a top-1 / top-2 margin under 0.1, a few bf16 ulps),
+    and a tree pass over 20 rows rounds differently from a one-token pass, so
+    the hint is rejected at such near ties and the output can part from greedy
+    decoding there; the loop's exactness is tested on the fp32 model."""
+    import torch
+
+    from parallel_eagle_amd import synth
+    from parallel_eagle_amd.drafter import DeviceDrafter
+    from parallel_eagle_amd.serve import SpeculativeDecoder, vanilla_generate_cached
+    from parallel_eagle_amd.target import TargetModel
+    from parallel_eagle_amd.tree import beam_width
+
+    shape, P, k = wl.model, wl.prefix_len, wl.depth
+    top_k, max_nodes = wl.top_k, wl.tree_nodes
+    T = beam_width(k, top_k, max_nodes) * k
+    cap = P + new_tokens + T + 64
+    tm = TargetModel.synthetic(shape, seed=seed, device="cuda:0", cache_capacity=cap)
+    H, nfl = shape.hidden, len(shape.resolved_feature_layers())
+    g = torch.Generator(device="cuda:0").manual_seed(seed)
+
+    def r(*sz, std=shape.init_std):
+        return (torch.randn(*sz, generator=g, device="cuda:0") * std).to(tm.dtype)
+
+    from dataclasses import replace
+    layers = []
+    for _ in range(2):
+        lw = {n: r(o, i) for n, o, i in replace(shape, qkv_bias=False).linear_shapes()}
+        lw["attn_norm"] = torch.ones(H, dtype=tm.dtype, device="cuda:0")
+        lw["mlp_norm"] = torch.ones(H, dtype=tm.dtype, device="cuda:0")
+        layers.append(lw)
+    w = {"feat_norm": torch.ones(H, dtype=tm.dtype, device="cuda:0"), "feat_proj": r(H, nfl * H),
+         "in_proj": r(H, 2 * H), "mask_emb": r(H), "h_shared": r(H), "layers": layers}
+    drafter = DeviceDrafter(tm, w, max_depth=k, capacity=cap)
+    prompt = synth.uniform_int(seed, synth.STREAM_PROMPT, P, shape.vocab).tolist()
+
+    class GreedyHint:
+        """The drafter, its logits replaced by a peak at the greedy token of each depth."""
+
+        def __init__(self, inner, greedy):
+            self.inner, self.greedy = inner, greedy
+
+        def draft_logits(self, ctx, feats, kk):
+            return self._hint(self.inner.draft_logits(ctx, feats, kk), ctx, kk)
+
+        def draft_logits_extend(self, ctx, feats, kk):
+            return self._hint(self.inner.draft_logits_extend(ctx, feats, kk), ctx, kk)
+
+        def _hint(self, lg, ctx, kk):
+            lg = lg.clone()
+            n = ctx.numel()
+            for d in range(kk):
+                if n + d < len(self.greedy):
+                    lg[d] = lg[d].min()
+                    lg[d, self.greedy[n + d]] = 30.0
+            return lg
+
+    vanilla_generate_cached(tm, prompt, 4)  # warm-up (kernel loads, caches)
+    torch.cuda.synchronize()
+    greedy = vanilla_generate_cached(tm, prompt, new_tokens)
+    full = prompt + greedy.output_ids
+    runs = {}
+    for name, dr in (("random_drafter", drafter), ("greedy_hint_drafter", GreedyHint(drafter, full))):
+        dec = SpeculativeDecoder(tm, dr, k=k, tree_top_k=top_k, tree_max_nodes=max_nodes)
+        dec.generate(prompt, 8)  # warm-up
+        res = dec.generate(prompt, new_tokens)
+        same = res.output_ids == greedy.output_ids
+        first = next((i for i, (x, y) in enumerate(zip(res.output_ids, greedy.output_ids)) if x != y), None)
+        runs[name] = {"tokens_per_s": round(res.tokens_per_second, 1), "steps": res.steps,
+                      "tokens_per_step": round(res.acceptance_length, 3), "target_calls": res.target_calls,
+                      "equal_to_greedy": same, "first_difference": first}
+        log(f"loop ({name}): {res.tokens_per_second:.1f} tokens/s, {res.acceptance_length:.2f} tokens per step, "
+            f"equal to greedy decoding: {same}" + ("" if same else f" (first difference at token {first})"))
+    log(f"greedy decoding through the same API: {greedy.tokens_per_second:.1f} tokens/s")
+    best = runs["greedy_hint_drafter"]
+    return {
+        "metric": "decode loop tokens/s (device-resident speculative loop, synthetic weights)",
+        "value": best["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": DTYPE_NAMES[shape.dtype], "data": "synthetic",
+        "config": {"workload": wl.name, "layers": shape.num_layers, "prompt_len": P, "new_tokens": new_tokens,
+                   "depth": k, "tree_nodes": T, "drafter_layers": 2},
+        "greedy_tokens_per_s": round(greedy.tokens_per_second, 1), "speculative": runs,
+    }
+
+
 def draft_line(wl, seed: int, reps: int = 10) -> dict:
     """Latency of one drafting step at the workload's shape: DeviceDrafter.draft_logits
     (2 dense decoder layers, the reference's default depth, over the P context rows
@@ -615,6 +712,9 @@ def main(argv=None) -> int:
         return 0
     if a.draft:
         print(json.dumps(draft_line(wl, a.seed)))
+        return 0
+    if a.loop:
+        print(json.dumps(loop_line(wl, a.seed)))
         return 0
     if wl.batch != 1:
         print(json.dumps(batch_line(wl, a.seed, a.steps, a.warmup, a.gemm_reps)), flush=True)

@@ -96,6 +96,7 @@ class DeviceDrafter:
         self.runner = TargetModel(core, cache_capacity=capacity)
         self.cache = TreeKVCache(self.shape, dt, dev, capacity)
         self.rows = torch.arange(capacity, dtype=torch.int64, device=dev)
+        self._valid = 0  # context rows of the last call whose K/V are in self.cache
 
     # nn.Module-style calls the reference's callers chain after load_drafter
     # (bench/run_bench.py:57: ``load_drafter(path, target).to(device, dtype).eval()``):
@@ -137,6 +138,20 @@ class DeviceDrafter:
     def draft_logits(self, context_ids: torch.Tensor, context_feats: torch.Tensor, k: int) -> torch.Tensor:
         """Logits (k, V) for the k tokens after ``context_ids``: row 0 from the last
         real slot, row d from mask slot d."""
+        return self._draft(context_ids, context_feats, k, reuse=False)
+
+    @torch.no_grad()
+    def draft_logits_extend(self, context_ids: torch.Tensor, context_feats: torch.Tensor, k: int) -> torch.Tensor:
+        """``draft_logits`` for a context that extends the previous call's (its
+        tokens and features are the previous context's, followed by new ones, as
+        in a decode loop): the K/V rows of the previous context stay in the
+        drafter's cache (the attention is causal, so a row's K/V depend only on
+        the rows before it) and only the new rows and the k query slots run. The
+        caller guarantees the prefix; the logits equal a full recomputation up to
+        the rounding of the different launch shapes (exactly, in fp32)."""
+        return self._draft(context_ids, context_feats, k, reuse=True)
+
+    def _draft(self, context_ids, context_feats, k: int, reuse: bool) -> torch.Tensor:
         ids = torch.as_tensor(context_ids, device=self.device).reshape(-1)
         p = ids.numel()
         m = p + k - 1
@@ -144,20 +159,26 @@ class DeviceDrafter:
             raise ValueError("draft_logits needs a context and k >= 1")
         if m > self.capacity:
             raise ValueError(f"{m} drafter rows exceed the capacity {self.capacity}")
+        # rows [0, kept) of the cache hold this context's K/V from the previous call
+        kept = min(self._valid, p - 1) if reuse else 0
         x = self.core.embed
-        x[:p].copy_(self.real_input(ids, context_feats))
+        x[kept:p].copy_(self.real_input(ids[kept:], context_feats[kept:p]))
         if k > 1:
             x[p:m].copy_(self.mask_vec.expand(k - 1, -1))
-        # rows [0, p - 1) only fill the cache (no lm_head); the k rows whose logits
-        # are read continue it causally: the same attention as one pass over m rows
+        # rows [kept, p - 1) only fill the cache (no lm_head); the k rows whose
+        # logits are read continue it causally: the same attention as one pass
+        # over m rows
         rows = self.rows
-        self.cache.seq_len = 0
-        if p > 1:
-            self.runner.run_pass(rows[: p - 1], rows[: p - 1], self.cache, _lib.PE_MASK_CAUSAL, None, None, None)
+        self.cache.seq_len = kept
+        self._valid = 0  # until this call has written its rows
+        if p - 1 > kept:
+            self.runner.run_pass(rows[kept: p - 1], rows[kept: p - 1], self.cache, _lib.PE_MASK_CAUSAL, None, None,
+                                 None)
             self.cache.seq_len = p - 1
         logits = torch.empty((k, self.shape.vocab), dtype=self.dtype, device=self.device)
         self.runner.run_pass(rows[p - 1: m], rows[p - 1: m], self.cache, _lib.PE_MASK_CAUSAL, None, logits, None)
         ops.read_status(self.runner.status, "draft_logits")
+        self._valid = p  # rows [0, p) are this context's (the mask slots after it are not)
         return logits
 
 

@@ -198,6 +198,9 @@ class SpeculativeDecoder:
         seq.append(bonus)
         stop = eos_token_id is not None and bonus == eos_token_id
         T, V = self.T, tm.shape.vocab
+        # the context only grows, so a drafter that can keep its cache across
+        # calls (DeviceDrafter.draft_logits_extend) runs only the new rows
+        draft = getattr(self.drafter, "draft_logits_extend", None) or self.drafter.draft_logits
         vlogits = torch.empty((T, V), dtype=tm.dtype, device=dev)
         vfused = torch.empty((T, tm.feature_dim), dtype=tm.dtype, device=dev)
         acc_out = torch.zeros(2 + T, dtype=torch.int32, device=dev)
@@ -205,7 +208,7 @@ class SpeculativeDecoder:
         t0 = time.perf_counter()
         while len(seq) - base < max_new_tokens and not stop:
             ctx = torch.tensor(seq[:cache_len], device=dev)
-            dl = self.drafter.draft_logits(ctx, feats, self.k)
+            dl = draft(ctx, feats, self.k)
             drafter_calls += 1
             tokens, parents, pstatus = propose_tree_device(dl, self.widths, self.top_k)
             words = max(1, (T + 63) // 64)

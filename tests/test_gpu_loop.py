@@ -78,6 +78,23 @@ def test_tree_loop_is_lossless_on_the_tiny_fp32_model(p):
           f"{res.acceptance_length:.2f}; device loop {dev.steps} steps")
 
 
+def test_drafter_extend_equals_a_full_recomputation():
+    """DeviceDrafter.draft_logits_extend (the previous context's K/V rows kept in
+    the drafter's cache, only the new rows and the query slots run) returns the
+    logits of draft_logits over the whole context, bit for bit on the fp32
+    model, for contexts that grow by 1 and 3 rows and stay the same."""
+    tm, dr = _tiny()
+    V, F = tm.shape.vocab, dr.feat_dim
+    g = torch.Generator().manual_seed(7)
+    ids = torch.randint(0, V, (40,), generator=g).to(DEV)
+    feats = torch.randn(40, F, generator=g).to(tm.dtype).to(DEV)
+    want = {n: dr.draft_logits(ids[:n], feats[:n], 4).clone() for n in (20, 21, 24)}
+    dr.draft_logits(ids[:20], feats[:20], 4)
+    for n in (21, 24, 24):
+        got = dr.draft_logits_extend(ids[:n], feats[:n], 4)
+        assert torch.equal(got, want[n]), n
+
+
 def test_tree_loop_unknown_mode_is_refused():
     tm, dr = _tiny()
     with pytest.raises(ValueError):
