@@ -678,8 +678,9 @@ def batch_line(wl, seed: int, steps: int, warmup: int, gemm_reps: int) -> dict:
         "accepted": [len(p) for p, _ in res],
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": f"nf4_gemm_bigm_kernel (A-tiled X, all {M} rows in one launch per linear, each "
-                               f"weight dequantised once; fp32 split partials: the {launches} launches of one pass)",
+                     "kernel": f"nf4_gemm_bigws_kernel (A-tiled X, all {M} rows in one launch per linear, each "
+                               f"weight dequantised once by producer waves for the consumer waves' MFMAs; fp32 "
+                               f"split partials: the {launches} launches of one pass)",
                      "mean_launch_us": round(gemm_s * 1e6 / launches, 3)},
         "cpu_baseline": None,
     }

@@ -730,34 +730,34 @@ __global__ __launch_bounds__(KW * 64, KW == 8 ? 1 : (MT == 1 ? 3 : 2)) void nf4_
 }
 
 // ---------------------------------------------------------------------------
-// NF4 GEMM for many rows (the batched pass: M up to 256, A-tiled X)
+// NF4 GEMM for many rows (the batched pass: 64 < M <= 256, A-tiled X)
 // ---------------------------------------------------------------------------
-// One workgroup = 4 waves = one group of four 32-column tiles (128 columns) x
-// one K split. Each 128-wide unit is dequantised once for every row: wave w
-// looks up tile w of the unit (the lane's own table, as in nf4_wave_body)
-// and writes its bf16 MFMA B fragments to a double-buffered LDS tile; after
-// one barrier every wave multiplies its own M tiles (up to two) by all four
-// tiles' fragments. (Interleaving the next unit's lookups with the MFMAs
-// measured slower: the B-fragment reads and the lookups share the in-order
-// LDS counter, so each MFMA waited for lookups issued after its operand.)
-// Waves split M, not K, so each wave's accumulators hold
-// complete sums over the split's units: no reduction across waves. The
+// One workgroup = 8 waves = one group of four 32-column tiles (128 columns) x
+// one K split; each 128-wide unit is dequantised once for every row.
+// Waves 0-3 (producers) each dequantise tile w of every unit (the lane's own
+// table, as in nf4_wave_body) into a two-slot LDS ring of bf16 MFMA B
+// fragments; waves 4-7 (consumers) each multiply up to two M tiles by all
+// four tiles of the unit in the other slot. Round t: the consumers multiply
+// unit t (slot t % 2) while the producers fill unit t + 1 (slot (t + 1) % 2);
+// one workgroup barrier ends the round. A SIMD holds one wave of each kind,
+// so the lookups' VALU and LDS work and the matrix cores run at the same
+// time, and each wave's in-order LDS counter covers one kind of access only
+// (with both jobs in the same four waves, each MFMA waited for lookups issued
+// after its operand). Both kinds run the same 1 + n barriers (n units; every
+// condition below is uniform over the workgroup). Consumers split M, not K,
+// so each accumulator holds the complete sum over the split's units; the
 // result is written as fp32 split partials out[split][row][col] (plain
 // stores), summed by the consumer kernels in split order.
 constexpr int kBigNT = 4;
-constexpr int kBigTab = 16 * 64 * 4;          // one wave's table: 16 codes x 64 lanes x dword (two units)
+constexpr int kBigTab = 16 * 64 * 4;          // one producer's table: 16 codes x 64 lanes x dword (two units)
 constexpr int kBigBufUnit = kBigNT * 8 * 64 * 16;  // B fragments of one unit: 4 tiles x 8 k-steps x 64 lanes x 16 B
 constexpr int kBigSmem = kWaves * kBigTab + 2 * kBigBufUnit;
 
-// NMT: the M tiles this wave multiplies (compile time, so the MFMA stream has
-// no branches); a wave with none still looks up its tile for the others.
-template <int NMT, int WV>
-__device__ __forceinline__ void nf4_bigm_wave(uint8_t* smem, const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
-                                              const uint16_t* __restrict__ Wabs, int NP, int group, int u0, int u1,
-                                              int mt0, const EpiArgs& e, int split) {
-  constexpr int MA = NMT > 0 ? NMT : 1;  // array extents
+template <int WV>
+__device__ __forceinline__ void bigws_producer(uint8_t* smem, const uint8_t* __restrict__ W,
+                                               const uint16_t* __restrict__ Wabs, int NP, int group, int u0, int u1) {
+  const int n = u1 - u0;
   const int lane = threadIdx.x & 63;
-  const int g = lane >> 5, ln = lane & 31;
   constexpr int TB = WV * kBigTab;  // this wave's table
   uint8_t* lanetab = smem + lane * 4;
   uint32_t addr[8];
@@ -766,32 +766,15 @@ __device__ __forceinline__ void nf4_bigm_wave(uint8_t* smem, const uint16_t* __r
   u32x4_t* bufs = (u32x4_t*)(smem + kWaves * kBigTab);
   const int64_t tile = (int64_t)group * kBigNT + WV;
   auto load_codes = [&](u32x4_t (&q)[2], int p) {
-    const int pc = min(p, u1 - 1);
-    const u32x4_t* wp = (const u32x4_t*)(W + (tile * NP + pc) * 2048 + lane * 16);
+    const u32x4_t* wp = (const u32x4_t*)(W + (tile * NP + min(p, u1 - 1)) * 2048 + lane * 16);
     q[0] = __builtin_nontemporal_load(wp);
     q[1] = __builtin_nontemporal_load(wp + 64);
   };
-  auto load_abs = [&](int p) -> uint32_t {
-    return (uint32_t)Wabs[(tile * NP + min(p, u1 - 1)) * 64 + lane];
-  };
-  f32x16_t acc[kBigNT][MA];
-#pragma unroll
-  for (int nt = 0; nt < kBigNT; ++nt)
-#pragma unroll
-    for (int mt = 0; mt < MA; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.f;
-  // X fragments in a ring of four k-steps, two k-steps ahead of their MFMAs
-  u32x4_t x[4][MA];
-  auto load_x = [&](int p, int s) {
-#pragma unroll
-    for (int mt = 0; mt < NMT; ++mt)
-      x[s & 3][mt] = *(const u32x4_t*)(X + ((((int64_t)(mt0 + mt) * NP + p) * 8 + s) * 64 + lane) * 8);
-  };
-  // dequantise this wave's tile of unit p (table half SL) into buffer slot p & 1
-  auto dequant = [&](const u32x4_t (&q)[2], int p, auto slot_c) {
+  auto load_abs = [&](int p) -> uint32_t { return (uint32_t)Wabs[(tile * NP + min(p, u1 - 1)) * 64 + lane]; };
+  // relative unit t (table half SL) into ring slot t % 2
+  auto dequant = [&](const u32x4_t (&q)[2], int t, auto slot_c) {
     constexpr int SL = decltype(slot_c)::value;
-    u32x4_t* dst = bufs + ((p & 1) * kBigNT + WV) * 8 * 64 + lane;
+    u32x4_t* dst = bufs + ((t & 1) * kBigNT + WV) * 8 * 64 + lane;
     uint32_t r[2][8];
     nf4_addr8(q[0][0], addr);
     nf4_read8<TB + SL>(smem, addr, r[0]);
@@ -806,46 +789,97 @@ __device__ __forceinline__ void nf4_bigm_wave(uint8_t* smem, const uint16_t* __r
                             pack16(cur[6], cur[7])};
     }
   };
-  // unit p's MFMAs; k-steps 0 and 1 of X were requested before its dequantisation
-  auto multiply = [&](int p) {
-    const u32x4_t* src = bufs + (p & 1) * kBigNT * 8 * 64 + lane;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      if (s + 2 < 8) load_x(p, s + 2);
-#pragma unroll
-      for (int nt = 0; nt < kBigNT; ++nt) {
-        const u32x4_t b = src[(nt * 8 + s) * 64];
-#pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(x[s & 3][mt], b, acc[nt][mt]);
-      }
+  constexpr std::integral_constant<int, 0> kLo{};
+  constexpr std::integral_constant<int, 2> kHi{};
+  // qa holds the even relative units, qb the odd ones; a table build covers
+  // an even unit (low halves) and the next (high halves)
+  u32x4_t qa[2], qb[2];
+  load_codes(qa, u0);
+  load_codes(qb, u0 + 1);
+  uint32_t a0 = load_abs(u0), a1 = load_abs(u0 + 1);
+  nf4_build_table2<TB, false>(lanetab, a0, a1);
+  a0 = load_abs(u0 + 2);
+  a1 = load_abs(u0 + 3);
+  dequant(qa, 0, kLo);
+  load_codes(qa, u0 + 2);
+  lds_barrier();
+  for (int t = 0; t < n; t += 2) {
+    if (t + 1 < n) {
+      dequant(qb, t + 1, kHi);
+      load_codes(qb, u0 + t + 3);
     }
+    lds_barrier();
+    if (t + 1 < n) {
+      if (t + 2 < n) {
+        nf4_build_table2<TB, false>(lanetab, a0, a1);  // the reads of units t, t + 1 are issued
+        a0 = load_abs(u0 + t + 4);
+        a1 = load_abs(u0 + t + 5);
+        dequant(qa, t + 2, kLo);
+        load_codes(qa, u0 + t + 4);
+      }
+      lds_barrier();
+    }
+  }
+}
+
+template <int NMT>
+__device__ __forceinline__ void bigws_consumer(uint8_t* smem, const uint16_t* __restrict__ X, int NP, int group,
+                                               int u0, int u1, int mt0, const EpiArgs& e, int split) {
+  const int n = u1 - u0;
+  constexpr int MA = NMT > 0 ? NMT : 1;  // array extents
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 5, ln = lane & 31;
+  const u32x4_t* bufs = (const u32x4_t*)(smem + kWaves * kBigTab);
+  f32x16_t acc[kBigNT][MA];
+#pragma unroll
+  for (int nt = 0; nt < kBigNT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MA; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[nt][mt][r] = 0.f;
+  // X fragments in a ring of four k-steps, two k-steps ahead of their MFMAs
+  u32x4_t x[4][MA];
+  auto load_x = [&](int p, int s) {
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+      x[s & 3][mt] = *(const u32x4_t*)(X + ((((int64_t)(mt0 + mt) * NP + p) * 8 + s) * 64 + lane) * 8);
   };
   auto first_x = [&](int p) {
     load_x(p, 0);
     load_x(p, 1);
   };
-  constexpr std::integral_constant<int, 0> kLo{};
-  constexpr std::integral_constant<int, 2> kHi{};
-  u32x4_t qa[2], qb[2];
-  load_codes(qa, u0);
-  load_codes(qb, u0 + 1);
-  uint32_t a0 = load_abs(u0), a1 = load_abs(u0 + 1);
-  for (int p = u0; p < u1; p += 2) {
-    // one table build covers units p (low halves) and p + 1 (high halves)
-    nf4_build_table2<TB, false>(lanetab, a0, a1);
-    a0 = load_abs(p + 2);
-    a1 = load_abs(p + 3);
-    first_x(p);
-    dequant(qa, p, kLo);
-    load_codes(qa, p + 2);
-    lds_barrier();  // unit p's fragments are complete; the other slot is free
-    multiply(p);
-    if (p + 1 < u1) {  // the same for every wave of the workgroup
-      first_x(p + 1);
-      dequant(qb, p + 1, kHi);
-      load_codes(qb, p + 3);
+  // relative unit t from ring slot t % 2: the four B fragments of k-step
+  // s + 1 are requested before the MFMAs of k-step s; the next unit's first
+  // X k-steps are requested before the round's barrier
+  auto multiply = [&](int t) {
+    const u32x4_t* src = bufs + (t & 1) * kBigNT * 8 * 64 + lane;
+    u32x4_t b[2][kBigNT];
+    auto load_b = [&](int s) {
+#pragma unroll
+      for (int nt = 0; nt < kBigNT; ++nt) b[s & 1][nt] = src[(nt * 8 + s) * 64];
+    };
+    if (NMT > 0) load_b(0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (NMT > 0 && s + 1 < 8) load_b(s + 1);
+      if (s + 2 < 8) load_x(u0 + t, s + 2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int nt = 0; nt < kBigNT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) acc[nt][mt] = mfma16<PE_DTYPE_BF16>(x[s & 3][mt], b[s & 1][nt], acc[nt][mt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (t + 1 < n) first_x(u0 + t + 1);
+  };
+  first_x(u0);
+  lds_barrier();
+  for (int t = 0; t < n; t += 2) {
+    multiply(t);
+    lds_barrier();
+    if (t + 1 < n) {
+      multiply(t + 1);
       lds_barrier();
-      multiply(p + 1);
     }
   }
   // split partials: row 32 mt + 8 q + 4 g + j, column (group * 4 + nt) * 32 + ln
@@ -865,41 +899,38 @@ __device__ __forceinline__ void nf4_bigm_wave(uint8_t* smem, const uint16_t* __r
   }
 }
 
-template <int MTW>
-__global__ __launch_bounds__(kWaves * 64, 2) void nf4_gemm_bigm_kernel(const uint16_t* __restrict__ X,
-                                                                       const uint8_t* __restrict__ W,
-                                                                       const uint16_t* __restrict__ Wabs, int NP,
-                                                                       int pps, int mtiles, EpiArgs e) {
+constexpr int kWsWaves = 2 * kWaves;  // producers + consumers
+
+__global__ __launch_bounds__(kWsWaves * 64, 1) void nf4_gemm_bigws_kernel(const uint16_t* __restrict__ X,
+                                                                          const uint8_t* __restrict__ W,
+                                                                          const uint16_t* __restrict__ Wabs, int NP,
+                                                                          int pps, int mtiles, EpiArgs e) {
   __shared__ __align__(256) uint8_t smem[kBigSmem];
   const int group = blockIdx.x, split = blockIdx.y;
   const int u0 = split * pps, u1 = min(NP, u0 + pps);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int mt0 = wave * MTW;
-  const int nmt = max(0, min(MTW, mtiles - mt0));
   if (u0 >= u1) return;  // a whole workgroup: no barrier is left waiting
-  static_assert(MTW == 2, "the dispatch below instantiates 0, 1 or 2 M tiles per wave");
-#define PE_BIGM_WAVE(N)                                                                          \
-  switch (wave) {                                                                                \
-    case 0: nf4_bigm_wave<N, 0>(smem, X, W, Wabs, NP, group, u0, u1, mt0, e, split); break;      \
-    case 1: nf4_bigm_wave<N, 1>(smem, X, W, Wabs, NP, group, u0, u1, mt0, e, split); break;      \
-    case 2: nf4_bigm_wave<N, 2>(smem, X, W, Wabs, NP, group, u0, u1, mt0, e, split); break;      \
-    default: nf4_bigm_wave<N, 3>(smem, X, W, Wabs, NP, group, u0, u1, mt0, e, split); break;     \
+  if (wave < kWaves) {
+    switch (wave) {
+      case 0: bigws_producer<0>(smem, W, Wabs, NP, group, u0, u1); break;
+      case 1: bigws_producer<1>(smem, W, Wabs, NP, group, u0, u1); break;
+      case 2: bigws_producer<2>(smem, W, Wabs, NP, group, u0, u1); break;
+      default: bigws_producer<3>(smem, W, Wabs, NP, group, u0, u1); break;
+    }
+    return;
   }
-  if (nmt == 2) {
-    PE_BIGM_WAVE(2)
-  } else if (nmt == 1) {
-    PE_BIGM_WAVE(1)
-  } else {
-    PE_BIGM_WAVE(0)
-  }
-#undef PE_BIGM_WAVE
+  const int mt0 = (wave - kWaves) * 2;
+  const int nmt = max(0, min(2, mtiles - mt0));
+  if (nmt == 2) bigws_consumer<2>(smem, X, NP, group, u0, u1, mt0, e, split);
+  else if (nmt == 1) bigws_consumer<1>(smem, X, NP, group, u0, u1, mt0, e, split);
+  else bigws_consumer<0>(smem, X, NP, group, u0, u1, mt0, e, split);
 }
 
 // ---------------------------------------------------------------------------
 // Dense 16-bit GEMM for many rows (the batched pass's lm_head)
 // ---------------------------------------------------------------------------
-// The many-row NF4 kernel's structure on tiled bf16 / fp16 weights: one
-// workgroup = 4 waves = 128 columns x all of K; per 128-wide unit wave w
+// Tiled bf16 / fp16 weights need no lookups, so the waves are not
+// specialised: one workgroup = 4 waves = 128 columns x all of K; per 128-wide unit wave w
 // copies tile w's MFMA B fragments of the unit (8 k-steps x 64 lanes x 16 B,
 // requested two units ahead, in the k order of the A-tiled X) into the
 // double-buffered LDS tile, and after one barrier multiplies its own M tiles
@@ -1608,16 +1639,15 @@ BigPlan big_plan(int N, int K) {
   BigPlan p;
   p.groups = N / (32 * kBigNT);
   p.units = K / 128;
-  // About one workgroup per CU: every further split adds M x N x 4 bytes of
-  // partials that the consuming kernel re-reads, while a second workgroup on a
-  // CU shares its matrix cores (the 14B shapes at 208 rows measured no faster
-  // past one workgroup per CU). Column groups short of the CUs by more than a
-  // tenth take one split more (gate/up: 216 groups -> 2 splits).
+  // At most one workgroup per CU (one eight-wave workgroup fills a CU's
+  // registers), all resident at once: every further split adds M x N x 4
+  // bytes of partials that the consuming kernel re-reads, and a launch past
+  // the CU count runs a second, mostly idle round (gate/up at 216 groups
+  // takes one split).
   static const int forced = env_int("PE_BIGM_SPLITS", 0);
   const int cu = cu_count();
   int S = cu / p.groups;
   if (S < 1) S = 1;
-  if (10 * p.groups * S < 9 * cu && p.groups * (S + 1) <= 2 * cu) ++S;
   if (forced > 0) S = forced;
   if (S > kMaxSplits) S = kMaxSplits;
   if (S > p.units) S = p.units;
@@ -1661,9 +1691,8 @@ int pe_internal_nf4_bigm_partials(const void* x_tiled, int M, int K, const void*
   EpiArgs e = make_epi(kEpiPartial, M, N, nullptr, nullptr, 0, partial, N);
   *splits = p.S;
   const int mtiles = (M + 31) / 32;
-  nf4_gemm_bigm_kernel<2><<<dim3(p.groups, p.S), kWaves * 64, 0, st>>>((const uint16_t*)x_tiled, (const uint8_t*)w,
-                                                                        (const uint16_t*)wabs, p.units, p.pps, mtiles,
-                                                                        e);
+  nf4_gemm_bigws_kernel<<<dim3(p.groups, p.S), kWsWaves * 64, 0, st>>>((const uint16_t*)x_tiled, (const uint8_t*)w,
+                                                                       (const uint16_t*)wabs, p.units, p.pps, mtiles, e);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }
