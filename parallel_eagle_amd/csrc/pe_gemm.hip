@@ -793,36 +793,34 @@ __device__ __forceinline__ void bigws_producer(uint8_t* smem, const uint8_t* __r
   constexpr std::integral_constant<int, 2> kHi{};
   // qa holds the even relative units, qb the odd ones; a table build covers
   // an even unit (low halves) and the next (high halves)
+  // Round r (r = 0 .. n, each ending with a barrier) fills relative unit r
+  // while the consumers multiply unit r - 1.
   u32x4_t qa[2], qb[2];
   load_codes(qa, u0);
   load_codes(qb, u0 + 1);
   uint32_t a0 = load_abs(u0), a1 = load_abs(u0 + 1);
-  nf4_build_table2<TB, false>(lanetab, a0, a1);
-  a0 = load_abs(u0 + 2);
-  a1 = load_abs(u0 + 3);
-  dequant(qa, 0, kLo);
-  load_codes(qa, u0 + 2);
-  lds_barrier();
-  for (int t = 0; t < n; t += 2) {
-    if (t + 1 < n) {
-      dequant(qb, t + 1, kHi);
-      load_codes(qb, u0 + t + 3);
+  for (int r = 0; r <= n; r += 2) {
+    if (r < n) {
+      nf4_build_table2<TB, false>(lanetab, a0, a1);  // the reads of units r - 2, r - 1 are issued
+      a0 = load_abs(u0 + r + 2);
+      a1 = load_abs(u0 + r + 3);
+      dequant(qa, r, kLo);
+      load_codes(qa, u0 + r + 2);
     }
     lds_barrier();
-    if (t + 1 < n) {
-      if (t + 2 < n) {
-        nf4_build_table2<TB, false>(lanetab, a0, a1);  // the reads of units t, t + 1 are issued
-        a0 = load_abs(u0 + t + 4);
-        a1 = load_abs(u0 + t + 5);
-        dequant(qa, t + 2, kLo);
-        load_codes(qa, u0 + t + 4);
+    if (r + 1 <= n) {
+      if (r + 1 < n) {
+        dequant(qb, r + 1, kHi);
+        load_codes(qb, u0 + r + 3);
       }
       lds_barrier();
     }
   }
 }
 
-template <int NMT>
+// SW: the launch has one split and stores the SwiGLU activation (a separate
+// instance, so the split-partial launches carry no epilogue code)
+template <int NMT, bool SW>
 __device__ __forceinline__ void bigws_consumer(uint8_t* smem, const uint16_t* __restrict__ X, int NP, int group,
                                                int u0, int u1, int mt0, const EpiArgs& e, int split) {
   const int n = u1 - u0;
@@ -882,25 +880,56 @@ __device__ __forceinline__ void bigws_consumer(uint8_t* smem, const uint16_t* __
       lds_barrier();
     }
   }
-  // split partials: row 32 mt + 8 q + 4 g + j, column (group * 4 + nt) * 32 + ln
-  float* out = (float*)e.out + (int64_t)split * e.M * e.N;
+  // row 32 mt + 8 q + 4 g + j, column (group * 4 + nt) * 32 + ln
+  if constexpr (SW) {
+    // One split (complete sums): tiles 2 p and 2 p + 1 are the gate and up
+    // columns of activation columns (2 group + p) * 32 + c. After the last
+    // barrier the LDS is free: each M tile goes through this wave's 16 KiB
+    // (32 rows x 128 columns, fp32), and a rolled loop stores the activations.
+    float* stage = (float*)smem + (threadIdx.x / 64 - kWaves) * 32 * 128;
 #pragma unroll
-  for (int mt = 0; mt < NMT; ++mt) {
+    for (int mt = 0; mt < NMT; ++mt) {
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4)
+      for (int nt = 0; nt < kBigNT; ++nt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = (mt0 + mt) * 32 + 8 * q4 + 4 * g + j;
+        for (int r = 0; r < 16; ++r) stage[(8 * (r >> 2) + 4 * g + (r & 3)) * 128 + nt * 32 + ln] = acc[nt][mt][r];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll 1
+      for (int it = 0; it < 32; ++it) {
+        const int rr = it, c = lane;  // row of the tile, activation column of the group (pair c / 32)
+        const int row = (mt0 + mt) * 32 + rr;
+        const int pr = c >> 5, cl = c & 31;
         if (row < e.M)
-#pragma unroll
-          for (int nt = 0; nt < kBigNT; ++nt)
-            out[(int64_t)row * e.N + (group * kBigNT + nt) * 32 + ln] = acc[nt][mt][4 * q4 + j];
+          epi_swiglu<PE_DTYPE_BF16>(e, row, (2 * group + pr) * 32 + cl, stage[rr * 128 + 64 * pr + cl],
+                                    stage[rr * 128 + 64 * pr + 32 + cl]);
       }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    }
+  } else {
+    // split partials
+    float* out = (float*)e.out + (int64_t)split * e.M * e.N;
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = (mt0 + mt) * 32 + 8 * q4 + 4 * g + j;
+          if (row < e.M)
+#pragma unroll
+            for (int nt = 0; nt < kBigNT; ++nt)
+              out[(int64_t)row * e.N + (group * kBigNT + nt) * 32 + ln] = acc[nt][mt][4 * q4 + j];
+        }
   }
 }
 
 constexpr int kWsWaves = 2 * kWaves;  // producers + consumers
 
+template <bool SW>
 __global__ __launch_bounds__(kWsWaves * 64, 1) void nf4_gemm_bigws_kernel(const uint16_t* __restrict__ X,
                                                                           const uint8_t* __restrict__ W,
                                                                           const uint16_t* __restrict__ Wabs, int NP,
@@ -921,9 +950,9 @@ __global__ __launch_bounds__(kWsWaves * 64, 1) void nf4_gemm_bigws_kernel(const 
   }
   const int mt0 = (wave - kWaves) * 2;
   const int nmt = max(0, min(2, mtiles - mt0));
-  if (nmt == 2) bigws_consumer<2>(smem, X, NP, group, u0, u1, mt0, e, split);
-  else if (nmt == 1) bigws_consumer<1>(smem, X, NP, group, u0, u1, mt0, e, split);
-  else bigws_consumer<0>(smem, X, NP, group, u0, u1, mt0, e, split);
+  if (nmt == 2) bigws_consumer<2, SW>(smem, X, NP, group, u0, u1, mt0, e, split);
+  else if (nmt == 1) bigws_consumer<1, SW>(smem, X, NP, group, u0, u1, mt0, e, split);
+  else bigws_consumer<0, SW>(smem, X, NP, group, u0, u1, mt0, e, split);
 }
 
 // ---------------------------------------------------------------------------
@@ -1691,8 +1720,27 @@ int pe_internal_nf4_bigm_partials(const void* x_tiled, int M, int K, const void*
   EpiArgs e = make_epi(kEpiPartial, M, N, nullptr, nullptr, 0, partial, N);
   *splits = p.S;
   const int mtiles = (M + 31) / 32;
-  nf4_gemm_bigws_kernel<<<dim3(p.groups, p.S), kWsWaves * 64, 0, st>>>((const uint16_t*)x_tiled, (const uint8_t*)w,
-                                                                       (const uint16_t*)wabs, p.units, p.pps, mtiles, e);
+  nf4_gemm_bigws_kernel<false><<<dim3(p.groups, p.S), kWsWaves * 64, 0, st>>>(
+      (const uint16_t*)x_tiled, (const uint8_t*)w, (const uint16_t*)wabs, p.units, p.pps, mtiles, e);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+int pe_internal_nf4_bigm_swiglu(const void* x_tiled, int M, int K, const void* w, const void* wabs, int N, void* out,
+                                int out_units, int dtype, float* partial, int64_t partial_bytes, int* splits,
+                                hipStream_t st) {
+  if (!x_tiled || !w || !wabs || !out || !splits || M <= 0 || M > 8 * 32 || K % 128 || N % (32 * kBigNT) ||
+      out_units * 128 != N / 2)
+    return PE_ERR_ARG;
+  const BigPlan p = big_plan(N, K);
+  if (p.S > 1 || dtype != PE_DTYPE_BF16)
+    return pe_internal_nf4_bigm_partials(x_tiled, M, K, w, wabs, N, partial, partial_bytes, splits, st);
+  EpiArgs e = make_epi(PE_EPI_SWIGLU, M, N, nullptr, nullptr, 0, out, 0);
+  e.out_units = out_units;
+  *splits = 0;
+  const int mtiles = (M + 31) / 32;
+  nf4_gemm_bigws_kernel<true><<<dim3(p.groups, 1), kWsWaves * 64, 0, st>>>(
+      (const uint16_t*)x_tiled, (const uint8_t*)w, (const uint16_t*)wabs, p.units, p.pps, mtiles, e);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }

@@ -59,6 +59,13 @@ PE_INTERNAL int64_t pe_internal_nf4_bigm_partials_bytes(int M, int N, int K);
 PE_INTERNAL int pe_internal_nf4_bigm_partials(const void* x_tiled, int M, int K, const void* w, const void* wabs,
                                               int N, float* partial, int64_t partial_bytes, int* splits,
                                               hipStream_t st);
+// The gate/up linear of the many-row pass with its SwiGLU: when the plan has
+// one split (and bf16 compute) the GEMM stores the A-tiled activation itself
+// and *splits = 0; otherwise it writes split partials (*splits = S) for
+// pe_internal_swiglu_partials.
+PE_INTERNAL int pe_internal_nf4_bigm_swiglu(const void* x_tiled, int M, int K, const void* w, const void* wabs, int N,
+                                            void* out, int out_units, int dtype, float* partial, int64_t partial_bytes,
+                                            int* splits, hipStream_t st);
 PE_INTERNAL int pe_internal_swiglu_partials(const float* partial, int S, int M, int N, void* out, int64_t ld_out,
                                             int out_units, int dtype, hipStream_t st);
 

@@ -601,7 +601,8 @@ int forward_batched(const pe_model_desc* m, const pe_pass_args* a, const BatchLa
   }
   if (Lb.big) {
     // every linear: one launch over all M rows (split partials), consumed by
-    // the RoPE + K/V append, SwiGLU and residual + RMSNorm kernels
+    // the RoPE + K/V append, SwiGLU and residual + RMSNorm kernels; an
+    // unsplit gate/up launch stores the SwiGLU activation itself
     char* attn_t = ws + Lb.attn_t;
     char* act_t = ws + Lb.act_t;
     float* part = (float*)(ws + Lb.part);
@@ -622,8 +623,9 @@ int forward_batched(const pe_model_desc* m, const pe_pass_args* a, const BatchLa
       PE_TRY(pe_internal_nf4_bigm_partials(attn_t, M, qd, m->w_o[l], m->a_o[l], H, part, Lb.part_bytes, &S, st));
       PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn,
                                           xn_t, nullptr, 0, nullptr, 0, st));
-      PE_TRY(pe_internal_nf4_bigm_partials(xn_t, M, H, m->w_gu[l], m->a_gu[l], 2 * ip, part, Lb.part_bytes, &S, st));
-      PE_TRY(pe_internal_swiglu_partials(part, S, M, 2 * ip, act_t, ip, ip / 128, m->dtype, st));
+      PE_TRY(pe_internal_nf4_bigm_swiglu(xn_t, M, H, m->w_gu[l], m->a_gu[l], 2 * ip, act_t, ip / 128, m->dtype, part,
+                                         Lb.part_bytes, &S, st));
+      if (S > 0) PE_TRY(pe_internal_swiglu_partials(part, S, M, 2 * ip, act_t, ip, ip / 128, m->dtype, st));
       PE_TRY(pe_internal_nf4_bigm_partials(act_t, M, ip, m->w_down[l], m->a_down[l], H, part, Lb.part_bytes, &S, st));
       const bool last = l + 1 == L;
       const int fh = last ? -1 : slot_of(l + 1);
