@@ -146,7 +146,9 @@ int pe_nf4_gemm_f32abs(const void* x, int64_t ldx, int M, int K, const uint8_t* 
  * PE_EPI_STORE, N/256 for PE_EPI_SWIGLU) the output is A-tiled too (not with
  * PE_EPI_RESIDUAL). Same kernels and results as pe_nf4_gemm; no counterpart in
  * the reference (a layout variant of its dequantize + F.linear, used by the
- * pass and timed on its own by the benchmark). */
+ * pass and timed on its own by the benchmark). 64 < M <= 256: PE_EPI_SWIGLU
+ * with an A-tiled output (out_units = N/256) only, the batched pass's gate/up
+ * linear (the many-row kernel; workspace of pe_gemm_workspace_bytes). */
 int pe_nf4_gemm_tiled(const void* x_tiled, int M, int K, const uint8_t* w_tiled, const uint16_t* absmax_tiled,
                       int N, int epilogue, const void* bias, const void* resid, int64_t ld_resid, void* out,
                       int64_t ld_out, int out_units, void* workspace, int64_t workspace_bytes, void* stream);

@@ -1749,8 +1749,12 @@ extern "C" int64_t pe_gemm_workspace_bytes(int M, int N, int K, int wfmt, int dt
   if (dtype == PE_DTYPE_F32 && wfmt == PE_WFMT_DENSE) return 0;
   if (M <= 0 || N <= 0 || K < 128) return kCounterBytes;
   // M runs as 64-row launches plus a shorter last one, whose plan (one M tile
-  // instead of two) can need more split partials
+  // instead of two) can need more split partials; the many-row SwiGLU linear
+  // of pe_nf4_gemm_tiled needs its split partials when its plan splits K
   const bool nf4 = pe_wfmt_nf4(wfmt);
+  const int64_t big = nf4 && epilogue == PE_EPI_SWIGLU && M > kMaxChunkRows && M <= 8 * 32
+                          ? pe_internal_nf4_bigm_partials_bytes(M, N, K)
+                          : 0;
   const int mc = M > kMaxChunkRows ? kMaxChunkRows : M;
   int64_t w = workspace_of(make_plan(mc, N, K, nf4, epilogue));
   const int rem = M % kMaxChunkRows;
@@ -1758,7 +1762,7 @@ extern "C" int64_t pe_gemm_workspace_bytes(int M, int N, int K, int wfmt, int dt
     const int64_t wr = workspace_of(make_plan(rem, N, K, nf4, epilogue));
     if (wr > w) w = wr;
   }
-  return w;
+  return w > big ? w : big;
 }
 
 extern "C" int pe_nf4_gemm(const void* x, int64_t ldx, int M, int K, const uint8_t* w_tiled,
@@ -1783,7 +1787,18 @@ extern "C" int pe_nf4_gemm_tiled(const void* x_tiled, int M, int K, const uint8_
                                  const uint16_t* absmax_tiled, int N, int epilogue, const void* bias,
                                  const void* resid, int64_t ld_resid, void* out, int64_t ld_out, int out_units,
                                  void* workspace, int64_t workspace_bytes, void* stream) {
-  if (!absmax_tiled || M > kMaxChunkRows || out_units < 0) return PE_ERR_ARG;
+  if (!absmax_tiled || out_units < 0) return PE_ERR_ARG;
+  if (M > kMaxChunkRows) {
+    // many rows: the gate/up linear of the batched pass (A-tiled activation out)
+    if (M > 8 * 32 || epilogue != PE_EPI_SWIGLU || bias || out_units * 256 != N) return PE_ERR_ARG;
+    int S = 0;
+    const hipStream_t st = (hipStream_t)stream;
+    int rc = pe_internal_nf4_bigm_swiglu(x_tiled, M, K, w_tiled, absmax_tiled, N, out, out_units, PE_DTYPE_BF16,
+                                         (float*)workspace, workspace_bytes, &S, st);
+    if (rc == PE_OK && S > 0)
+      rc = pe_internal_swiglu_partials((const float*)workspace, S, M, N, out, ld_out, out_units, PE_DTYPE_BF16, st);
+    return rc;
+  }
   return mfma_gemm(kFmtNF4, x_tiled, K, M, K, w_tiled, absmax_tiled, N, epilogue, bias, resid, ld_resid, out, ld_out,
                    workspace, workspace_bytes, (hipStream_t)stream, true, out_units);
 }

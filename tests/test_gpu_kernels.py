@@ -146,6 +146,37 @@ def test_nf4_partials_sum_to_the_product(m, n, k, tiled):
     assert torch.all(err <= 1e-4 * (1 + ref32.abs()) * (k / 1024)), err.max()
 
 
+@pytest.mark.parametrize("m,n,k", [(208, 27648, 5120), (97, 22016, 4096), (130, 5120, 4096)])
+def test_many_row_swiglu_equals_the_swiglu_of_the_split_partials(m, n, k):
+    """pe_nf4_gemm_tiled with 64 < M <= 256 rows and the SwiGLU epilogue (the
+    batched pass's gate/up linear) against the SwiGLU of the same kernel's fp32
+    split partials, summed in split order on the host with the rounding points
+    of HF LlamaMLP (modeling_llama.py:174-176 in the dtype: gate and up rounded,
+    act(gate) rounded, the product rounded). The first two shapes plan one K
+    split, so the kernel stores the A-tiled activation itself; the third splits
+    K and takes the partials + SwiGLU kernel. Every element is equal or one
+    bf16 step apart (the device's expf and torch's exp may differ in the last
+    fp32 bit), at most 0.1% of them one step apart: a wrong row, column or
+    gate/up pairing would miss by far more."""
+    (tiled_w, tabs), _ = _nf4_weight(n, k, seed=m + n + k + 5)
+    x = torch.from_numpy(synth.normal(m, 38, m * k, 1.0).reshape(m, k)).to(torch.bfloat16)
+    xt = ops.to_xtile(x.to(DEV))
+    act = ops.from_xtile(ops.linear_tiled(xt, m, k, n, (tiled_w, tabs), epilogue=_lib.PE_EPI_SWIGLU,
+                                          out_tiled=True), m, n // 2).cpu()
+    parts, s = ops.nf4_linear_partials(xt, m, k, n, (tiled_w, tabs), x_tiled=True)
+    tot = parts[0].clone()
+    for i in range(1, s):
+        tot += parts[i]
+    gu = tot.cpu().view(m, n // 64, 2, 32)  # each 64-column group: 32 gate, then 32 up columns
+    g = gu[:, :, 0, :].reshape(m, n // 2).to(torch.bfloat16).float()
+    u = gu[:, :, 1, :].reshape(m, n // 2).to(torch.bfloat16).float()
+    act_g = (g / (1.0 + torch.exp(-g))).to(torch.bfloat16).float()
+    ref = (act_g * u).to(torch.bfloat16)
+    steps = (act.view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+    assert int(steps.max()) <= 1, int(steps.max())
+    assert int((steps == 1).sum()) <= m * (n // 2) // 1000, int((steps == 1).sum())
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("epi", ["store", "bias", "residual", "swiglu"])
 def test_dense_linear_epilogues(dtype, epi):
