@@ -228,7 +228,9 @@ int64_t pe_attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_
  * with the tree bias of masks.py:127-147. q [T][nh][hd], caches [nkv][cap][hd],
  * out [T][ld_out] with head h at columns [h*hd, (h+1)*hd). The workspace's
  * first 4 KiB are arrival counters: zero before the first call; every call
- * leaves them multiples of 16. */
+ * leaves them multiples of 16. bf16 / fp16 with hd = 128 (the matrix-core
+ * path) requires scale > 0 (1/sqrt(hd) in every model) and cache_cap < 2^24
+ * rows, else PE_ERR_ARG. */
 int pe_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
                       int nh, int nkv, int hd, int T, int64_t P, int mask_mode,
                       const uint64_t* bits, int words, float scale, int dtype, void* out,

@@ -70,6 +70,9 @@ constexpr int kQStride = 128 + 8;  // LDS row stride of the staged Q tile (eleme
 constexpr int kVRow = 128 + 32;    // LDS row stride of a wave's V tile (elements): 320 B, rows 16 banks apart
 constexpr int kCmbRow = 128 + 4;   // LDS row stride of the wave merge (floats; 16-byte aligned rows)
 constexpr int kAttnMaxSplits = 16;
+// a head's cache rows (256 bytes each at hd 128) are addressed with 32-bit
+// byte offsets
+constexpr int64_t kAttnMaxCap = int64_t(1) << 24;
 
 // Batched attention (batch >= 1): grid.z runs over (sequence, row tile);
 // sequence b's query rows are rows [seq_row0[b], seq_row0[b+1]) of q, bits
@@ -129,54 +132,30 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   // cap * 256 bytes < 4 GiB), so each load is base + one offset register
   const char* kbase = (const char*)(kc + (int64_t)kvh * cap * HD);
   const char* vbase = (const char*)(vc + (int64_t)kvh * cap * HD);
+  // Rows past the wave's last key (or, for a wave without keys, row 0) are
+  // clamped to it. The loads of the rounds after the first pair are
+  // unconditional, so each wait there is an exact count of the loads issued
+  // after the awaited one.
+  const int jcl = (int)max(jlast, (int64_t)0);  // a row index of one head: below cap < 2^24
   u32x4_t kf[2][8], vf[2][8];
-  auto load_pair = [&](int64_t jb) {
-    const int nsb = jb + 32 < j1 ? 2 : 1;  // a wave's last block may be a single one
+  auto load_k = [&](int64_t jb, int slot) {
+    const uint32_t ko = (uint32_t)min((int)jb + ln, jcl) * (HD * 2) + 16 * g;
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      if (sb == 1 && nsb == 1) break;
-      const uint32_t ko = (uint32_t)min(jb + 32 * sb + ln, jlast) * (HD * 2) + 16 * g;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) kf[sb][j] = *(const u32x4_t*)(kbase + ko + 32 * j);
-    }
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      if (sb == 1 && nsb == 1) break;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        // 32 keys x 16 chunks of 8 dims: lane covers key 4c + lane / 16, chunk lane % 16
-        const uint32_t vo = (uint32_t)min(jb + 32 * sb + 4 * c + (lane >> 4), jlast) * (HD * 2) + (lane & 15) * 16;
-        vf[sb][c] = *(const u32x4_t*)(vbase + vo);
-      }
-    }
+    for (int j = 0; j < 8; ++j) kf[slot][j] = *(const u32x4_t*)(kbase + ko + 32 * j);
   };
-  // one block into the first slots (later rounds, while O is live)
-  auto load_one = [&](int64_t jb) {
-    const uint32_t ko = (uint32_t)min(jb + ln, jlast) * (HD * 2) + 16 * g;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) kf[0][j] = *(const u32x4_t*)(kbase + ko + 32 * j);
+  auto load_v = [&](int64_t jb, int slot) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const uint32_t vo = (uint32_t)min(jb + 4 * c + (lane >> 4), jlast) * (HD * 2) + (lane & 15) * 16;
-      vf[0][c] = *(const u32x4_t*)(vbase + vo);
+      // 32 keys x 16 chunks of 8 dims: lane covers key 4c + lane / 16, chunk lane % 16
+      const uint32_t vo = (uint32_t)min((int)jb + 4 * c + (lane >> 4), jcl) * (HD * 2) + (lane & 15) * 16;
+      vf[slot][c] = *(const u32x4_t*)(vbase + vo);
     }
   };
-  // the row tile's Q (rows past `rows` are zero) is requested first, so
-  // staging it waits for Q alone and not for the KV stream behind it
   // the row's ancestor bits, then Q (rows past `rows` read row rows - 1 and
-  // stage zeros), then K and V: all requested before anything waits
+  // stage zeros), then the first pair's K and V: all requested before
+  // anything waits, and staging Q waits for Q alone
   const int r = rt * 32 + ln;
-  const bool rvalid = r < rows;
-  const int t = rvalid ? r / G : 0;
-  uint64_t nbits[PE_TREE_MAX_WORDS];
-  if (mask_mode == PE_MASK_TREE) {
-    // a visible tree key u < T <= 64 * words only reads words below `words`
-#pragma unroll
-    for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = bits[(int64_t)t * words + min(w, words - 1)];
-  } else {
-#pragma unroll
-    for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = 0ull;
-  }
+  const int t = r < rows ? r / G : 0;
   constexpr int kQChunks = 512 / (64 * kAttnWaves);  // 32 rows x 16 chunks of 8 dims
   const u32x4_t zero4 = {0u, 0u, 0u, 0u};
   u32x4_t qv[kQChunks];
@@ -190,7 +169,23 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
     const int rr = min(rr0, rows - 1);
     qv[c] = *(const u32x4_t*)(q + ((int64_t)(rr / G) * nh + kvh * G + rr % G) * HD + dc * 8);
   }
-  if (b0 < b1) load_pair(ks0 + 32 * (int64_t)b0);
+  uint64_t nbits[PE_TREE_MAX_WORDS];
+  if (mask_mode == PE_MASK_TREE) {
+    // a visible tree key u < T <= 64 * words only reads words below `words`
+#pragma unroll
+    for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = bits[(int64_t)t * words + min(w, words - 1)];
+  } else {
+#pragma unroll
+    for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = 0ull;
+  }
+  // the first pair (a wave's last block may be a single one: then only its
+  // first block is requested, and staging Q waits for that block too)
+  const bool pair2 = b0 + 1 < b1;
+  load_k(ks0 + 32 * (int64_t)b0, 0);
+  if (pair2) load_k(ks0 + 32 * (int64_t)b0 + 32, 1);
+  load_v(ks0 + 32 * (int64_t)b0, 0);
+  if (pair2) load_v(ks0 + 32 * (int64_t)b0 + 32, 1);
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before staging Q waits for Q
 #pragma unroll
   for (int c = 0; c < kQChunks; ++c) {
     const int chunk = c * 64 * kAttnWaves + threadIdx.x;
@@ -205,10 +200,19 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   __syncthreads();  // Q staged
 
   const float scale2 = scale * 1.44269504088896341f;  // natural-log scores -> base 2
-  auto process = [&](int64_t jb, auto first_c, auto pair_c) {
+  // kPair: the block pair in K and V slots 0 and 1, else one block in K slot
+  // KS and V slot 0. kNext: requests the block after this one, K into the
+  // other K slot (a pair's: into slot 0 once its QK products have read both)
+  // and V into V slot 0 once this block's V is in LDS; a pair that
+  // prefetches has two blocks.
+  auto process = [&](int64_t jb, auto first_c, auto pair_c, auto ks_c, auto next_c) {
     constexpr bool kFirst = decltype(first_c)::value;
     constexpr bool kPair = decltype(pair_c)::value;
-    const bool two = kPair && jb + 32 < j1;  // wave-uniform: the pair's second block has keys
+    constexpr int KS = decltype(ks_c)::value;
+    constexpr bool kNext = decltype(next_c)::value;
+    const bool two = kPair && (kNext || jb + 32 < j1);  // wave-uniform: the pair's second block has keys
+    const int64_t jn = jb + (kPair ? 64 : 32);          // the next block
+    if constexpr (kNext && !kPair) load_k(jn, 1 - KS);
     // ---- S^T = K Q^T over hd, two 32-key halves
     f32x16_t sc[2];
 #pragma unroll
@@ -222,15 +226,20 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
       for (int sb = 0; sb < 2; ++sb) {
         if (sb == 1 && !two) break;
         if constexpr (DT == PE_DTYPE_F16)
-          sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[sb][j]),
+          sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[KS + sb][j]),
                                                           __builtin_bit_cast(f16x8_t, qf), sc[sb], 0, 0, 0);
         else
-          sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[sb][j]),
+          sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[KS + sb][j]),
                                                            __builtin_bit_cast(bf16x8_t, qf), sc[sb], 0, 0, 0);
       }
     }
-    // ---- scale + mask, pair max (sc[sb][i] holds key jb + 32 sb + 8*(i/4) + 4*g + (i%4) of row ln)
-    float bmax = kInitMax;
+    if constexpr (kNext && kPair) load_k(jn, 0);
+    // ---- mask, pair max (sc[sb][i] holds key jb + 32 sb + 8*(i/4) + 4*g + (i%4) of row ln).
+    // The max is taken over the unscaled products (scale2 > 0, so it commutes
+    // with the scaling) and each exponent is one fma; a masked key is -inf,
+    // its probability exactly zero. Padding rows (past `rows`, zero Q) are
+    // computed like the others and never stored.
+    float bmax = -INFINITY;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       if (sb == 1 && !two) break;
@@ -238,21 +247,18 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
       if (kb + 32 <= min(P, j1) && (mask_mode == PE_MASK_TREE || kb + 32 <= P + 1)) {
         // a whole 32-key half of prefix keys: every key is visible to every node
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          sc[sb][i] = rvalid ? sc[sb][i] * scale2 : kMaskedScore;
-          bmax = fmaxf(bmax, sc[sb][i]);
-        }
+        for (int i = 0; i < 16; ++i) bmax = fmaxf(bmax, sc[sb][i]);
       } else {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int64_t kj = kb + 8 * (i >> 2) + 4 * g + (i & 3);
-          const bool ok = rvalid && kj < j1 && key_allowed(kj, P, t, mask_mode, nbits);
-          sc[sb][i] = ok ? sc[sb][i] * scale2 : kMaskedScore;
+          const bool ok = kj < j1 && key_allowed(kj, P, t, mask_mode, nbits);
+          sc[sb][i] = ok ? sc[sb][i] : -INFINITY;
           bmax = fmaxf(bmax, sc[sb][i]);
         }
       }
     }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * scale2;
     const float mnew = fmaxf(m, bmax);
     const float alpha = __builtin_amdgcn_exp2f(m - mnew);
     float psum = 0.f;
@@ -265,7 +271,8 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
           pb[sb][i >> 1] = 0u;
           continue;
         }
-        const float p0 = __builtin_amdgcn_exp2f(sc[sb][i] - mnew), p1 = __builtin_amdgcn_exp2f(sc[sb][i + 1] - mnew);
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[sb][i], scale2, -mnew));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[sb][i + 1], scale2, -mnew));
         psum += p0 + p1;
         pb[sb][i >> 1] = (DT == PE_DTYPE_F16)
                              ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
@@ -298,6 +305,8 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
       }
 #pragma unroll
       for (int c = 0; c < 8; ++c) *(u32x4_t*)&vs[4 * c + (lane >> 4)][(lane & 15) * 8] = vf[sb][c];
+      if constexpr (kNext)
+        if (sb == (kPair ? 1 : 0)) load_v(jn, 0);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -344,17 +353,30 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
 
-  if (b0 < b1) {
-    process(ks0 + 32 * (int64_t)b0, std::true_type(), std::true_type());
+  constexpr std::integral_constant<int, 0> kK0{};
+  constexpr std::integral_constant<int, 1> kK1{};
+  if (b0 + 2 < b1) {
+    // more blocks after the first pair: one block per round, the next block's
+    // K and V in flight during each round (K slots alternate)
+    process(ks0 + 32 * (int64_t)b0, std::true_type(), std::true_type(), kK0, std::true_type());
+    int b = b0 + 2;
+    for (; b + 2 < b1; b += 2) {
+      process(ks0 + 32 * (int64_t)b, std::false_type(), std::false_type(), kK0, std::true_type());
+      process(ks0 + 32 * (int64_t)b + 32, std::false_type(), std::false_type(), kK1, std::true_type());
+    }
+    if (b + 1 < b1) {
+      process(ks0 + 32 * (int64_t)b, std::false_type(), std::false_type(), kK0, std::true_type());
+      process(ks0 + 32 * (int64_t)b + 32, std::false_type(), std::false_type(), kK1, std::false_type());
+    } else {
+      process(ks0 + 32 * (int64_t)b, std::false_type(), std::false_type(), kK0, std::false_type());
+    }
+  } else if (b0 < b1) {
+    process(ks0 + 32 * (int64_t)b0, std::true_type(), std::true_type(), kK0, std::false_type());
   } else {
 #pragma unroll
     for (int h = 0; h < 4; ++h)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
-  }
-  for (int b = b0 + 2; b < b1; ++b) {  // caches longer than one pair: one block per round
-    load_one(ks0 + 32 * (int64_t)b);
-    process(ks0 + 32 * (int64_t)b, std::false_type(), std::false_type());
   }
 
   // ---- merge the waves (wave order) with all threads: thread (row, kDimsT-dim
@@ -451,14 +473,15 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   for (int k = 0; k < kDimsT; ++k) num[k] = 0.f;
   for (int c0 = 0; c0 < splits; c0 += 8) {  // up to 8 splits' loads in flight
     f32x4_t ov[8][kDimsT / 4], mv[8];
+    // every load unconditional (a split past the last reads this workgroup's
+    // own partial, a padding row its own slot; neither value is used), so all
+    // of them are in flight together
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const int sp = c0 + c;
-      if (sp < splits && sp != split && rr < rows) {
+      const int sp = c0 + c < splits ? c0 + c : split;
 #pragma unroll
-        for (int k = 0; k < kDimsT / 4; ++k) ov[c][k] = load_agent_x4(ro, (prow(sp) * HD + dc) * 4 + 16 * k);
-        mv[c] = load_agent_x4(rm, prow(sp) * 16);
-      }
+      for (int k = 0; k < kDimsT / 4; ++k) ov[c][k] = load_agent_x4(ro, (prow(sp) * HD + dc) * 4 + 16 * k);
+      mv[c] = load_agent_x4(rm, prow(sp) * 16);
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
@@ -612,6 +635,7 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
   if (eager && out_units) return PE_ERR_ARG;
   if (workspace_bytes < attention_workspace_bytes(T, nh, nkv, hd, S, dtype, attn_mode)) return PE_ERR_WORKSPACE;
   if (dtype != PE_DTYPE_F32 && hd == 128 && !eager) {
+    if (!(scale > 0.f) || cache_cap >= kAttnMaxCap) return PE_ERR_ARG;
     AttnPlan p = attn_plan(T, nh, nkv, S);
     if (p.splits > 1 && (int64_t)nkv * p.row_tiles * 4 > kAttnCounterBytes) return PE_ERR_ARG;
     if (!counters) counters = (int*)workspace;
@@ -675,6 +699,7 @@ int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const v
   if (!q || !k_cache || !v_cache || !out || !workspace || !seq_row0 || !seq_prefix || !bits) return PE_ERR_ARG;
   if (dtype == PE_DTYPE_F32 || batch <= 0 || max_rows <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || max_prefix < 0)
     return PE_ERR_ARG;
+  if (!(scale > 0.f) || cache_cap >= kAttnMaxCap) return PE_ERR_ARG;
   if (out_units && out_units * 128 != nh * 128) return PE_ERR_ARG;
   if (max_prefix + max_rows > cache_cap) return PE_ERR_CAPACITY;
   if (words <= 0 || words > PE_TREE_MAX_WORDS || max_rows > 64 * words) return PE_ERR_TREE;
