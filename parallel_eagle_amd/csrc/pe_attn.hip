@@ -46,11 +46,13 @@ __device__ __forceinline__ bool key_allowed(int64_t key, int64_t P, int t, int m
 // One workgroup = 8 waves = one (KV head, key split, 32-row tile); each wave
 // takes a contiguous run of the split's 32-key blocks. Its first two blocks
 // are loaded and processed together as one 64-key block (a run of one block
-// processes half of it); a longer run continues one block per round, so the
-// O accumulators never share the register file with a second pair in flight
-// and a wave stays within 240 VGPRs without spilling. The row's ancestor
-// bits, the row tile's Q and the first pair's K and V are the first loads of
-// the wave, so at the 7B shape the whole KV stream is in flight at once. V
+// processes half of it); a longer run continues one block per round, the
+// next block's K (into the other of two K slots) and V (into the one V slot,
+// once this block's V is in LDS) in flight during the round: with the O
+// accumulators live, a wave holds three block slots, not four, and stays
+// within 256 VGPRs without spilling. The row tile's Q, the row's ancestor
+// bits and the first pair's K and V are the first loads of the wave, so at
+// the 7B shape the whole KV stream is in flight at once. V
 // goes to a wave-private LDS transpose before S = K Q^T is formed, the row
 // tile's Q is staged once per workgroup in LDS (the B operand of S^T is read
 // from there per k-step); the LDS footprint (about 89 KiB) allows one
