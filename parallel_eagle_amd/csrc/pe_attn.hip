@@ -76,7 +76,8 @@ constexpr int kAttnMaxSplits = 16;
 // byte offsets
 constexpr int64_t kAttnMaxCap = int64_t(1) << 24;
 
-// Batched attention (batch >= 1): grid.z runs over (sequence, row tile);
+// Batched attention (batch >= 1): grid.z runs over (sequence, row tile), the
+// sequences in order of decreasing prefix length;
 // sequence b's query rows are rows [seq_row0[b], seq_row0[b+1]) of q, bits
 // and out, its keys the seq_prefix[b] cached rows plus its own node rows of
 // the cache at kc / vc + b * seq_stride. Row tiles past a sequence's rows
@@ -105,8 +106,27 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   int rt = blockIdx.z, seq = 0;
   int rbase = 0;  // the sequence's first row in q, bits and out
   if (bt.batch > 0) {
-    seq = blockIdx.z / bt.row_tiles;
-    rt = blockIdx.z - seq * bt.row_tiles;
+    const int pos = blockIdx.z / bt.row_tiles;
+    rt = blockIdx.z - pos * bt.row_tiles;
+    seq = pos;
+    if (bt.batch <= 64) {
+      // Workgroups are dispatched in grid order and a launch may hold more of
+      // them than there are CUs, so the sequences go longest prefix first
+      // (ties by index): those dispatched last, when CUs free up, are the
+      // shortest. Lane b ranks sequence b; the lane whose rank is `pos` names
+      // the sequence (the ranks are a permutation of 0 .. batch - 1).
+      const int lane = threadIdx.x & 63;
+      int rank = -1;
+      if (lane < bt.batch) {
+        const int64_t pl = bt.seq_prefix[lane];
+        rank = 0;
+        for (int j = 0; j < bt.batch; ++j) {
+          const int64_t pj = bt.seq_prefix[j];
+          rank += (pj > pl || (pj == pl && j < lane)) ? 1 : 0;
+        }
+      }
+      seq = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(rank == pos));
+    }
     rbase = bt.seq_row0[seq];
     T = bt.seq_row0[seq + 1] - rbase;
     P = bt.seq_prefix[seq];
