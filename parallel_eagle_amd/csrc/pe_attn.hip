@@ -125,7 +125,8 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
           rank += (pj > pl || (pj == pl && j < lane)) ? 1 : 0;
         }
       }
-      seq = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(rank == pos));
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(rank == pos);
+      seq = hit ? (int)__builtin_ctzll(hit) : pos;
     }
     rbase = bt.seq_row0[seq];
     T = bt.seq_row0[seq + 1] - rbase;
