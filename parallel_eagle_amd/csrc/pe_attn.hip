@@ -522,6 +522,274 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   write_out(num, den);
 }
 
+// Eager attention on the matrix cores (PE_ATTN_EAGER, the drafter's attention,
+// src/pe/nn.py:84-87) for launches whose plan has one key split, so that a
+// workgroup sees every key of its rows: one workgroup = 8 waves = one (KV head,
+// 32-row tile), each wave a contiguous run of the tile's 32-key blocks, walked
+// twice.
+//   Pass 1: S^T = K Q^T on MFMA; each score rounded as the reference rounds it
+//   (the product to the dtype, divided by sqrt(hd), to the dtype again; a
+//   masked key is -inf); the row's max and the fp32 sum of exp(s - max) kept
+//   online; the waves' (max, sum) merged in LDS in wave order.
+//   Pass 2: the same scores again; each probability exp(s - M) / L rounded to
+//   the dtype, as softmax(...).to(q.dtype) leaves it, and multiplied by V on
+//   MFMA (fp32 accumulation and no rescaling: M is the row's final max); the
+//   waves' sums added in wave order and rounded once.
+// The next block's K (both passes) and V (pass 2) are in flight during each
+// block; every load of those rounds is unconditional (rows clamped to the
+// wave's last key), so the waits are exact counts.
+template <int DT>
+__global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_eager_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
+    int nh, int nkv, int T, int64_t P, int mask_mode, const uint64_t* __restrict__ bits, int words,
+    void* __restrict__ out, int64_t ld_out) {
+  typedef Elem<DT> E;
+  constexpr int HD = 128;
+  constexpr int kQBytes = 32 * kQStride * 2;
+  constexpr int kVtBytes = 32 * kVRow * 2;
+  constexpr int kCmbBytes = kAttnWaves * 32 * kCmbRow * 4;
+  constexpr int kMain = kQBytes + kAttnWaves * kVtBytes;
+  constexpr int kSmem = (kMain > kCmbBytes) ? kMain : kCmbBytes;
+  __shared__ __align__(16) uint8_t smem[kSmem];
+  __shared__ float s_ml[kAttnWaves][32][2];
+  const int kvh = blockIdx.x, rt = blockIdx.z;
+  const int G = nh / nkv, rows = T * G;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ln = lane & 31, g = lane >> 5;
+  const int64_t S = P + T;
+  const int64_t kvis = mask_mode == PE_MASK_CAUSAL ? P + min(T - 1, (rt * 32 + 31) / G) + 1 : S;
+  const int64_t ks1 = min(S, kvis);
+  const int nb = (int)((ks1 + 31) / 32);
+  const int b0 = (nb * wave) / kAttnWaves, b1 = (nb * (wave + 1)) / kAttnWaves;
+  const int64_t j1 = min(ks1, 32 * (int64_t)b1);  // end of this wave's keys
+  const int jcl = (int)max(j1 - 1, (int64_t)0);    // a row index of one head: below cap < 2^24
+  uint16_t(*qs)[kQStride] = (uint16_t(*)[kQStride])smem;
+  uint16_t(*vs)[kVRow] = (uint16_t(*)[kVRow])(smem + kQBytes + wave * kVtBytes);
+  const char* kbase = (const char*)(kc + (int64_t)kvh * cap * HD);
+  const char* vbase = (const char*)(vc + (int64_t)kvh * cap * HD);
+  u32x4_t kf[2][8], vf[8];
+  auto load_k = [&](int jb, int slot) {
+    const uint32_t ko = (uint32_t)min(jb + ln, jcl) * (HD * 2) + 16 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kf[slot][j] = *(const u32x4_t*)(kbase + ko + 32 * j);
+  };
+  auto load_v = [&](int jb) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t vo = (uint32_t)min(jb + 4 * c + (lane >> 4), jcl) * (HD * 2) + (lane & 15) * 16;
+      vf[c] = *(const u32x4_t*)(vbase + vo);
+    }
+  };
+  // the row's ancestor bits and the row tile's Q (rows past `rows` read row
+  // rows - 1 and stage zeros; their outputs are never stored)
+  const int r = rt * 32 + ln;
+  const int t = r < rows ? r / G : 0;
+  uint64_t nbits[PE_TREE_MAX_WORDS];
+  if (mask_mode == PE_MASK_TREE) {
+#pragma unroll
+    for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = bits[(int64_t)t * words + min(w, words - 1)];
+  } else {
+#pragma unroll
+    for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = 0ull;
+  }
+  constexpr int kQChunks = 512 / (64 * kAttnWaves);
+  {
+    u32x4_t qv[kQChunks];
+    bool qok[kQChunks];
+#pragma unroll
+    for (int c = 0; c < kQChunks; ++c) {
+      const int chunk = c * 64 * kAttnWaves + threadIdx.x;
+      const int qr = chunk >> 4, dc = chunk & 15;
+      const int rr0 = rt * 32 + qr;
+      qok[c] = rr0 < rows;
+      const int rr = min(rr0, rows - 1);
+      qv[c] = *(const u32x4_t*)(q + ((int64_t)(rr / G) * nh + kvh * G + rr % G) * HD + dc * 8);
+    }
+    const u32x4_t zero4 = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int c = 0; c < kQChunks; ++c) {
+      const int chunk = c * 64 * kAttnWaves + threadIdx.x;
+      *(u32x4_t*)&qs[chunk >> 4][(chunk & 15) * 8] = qok[c] ? qv[c] : zero4;
+    }
+  }
+  __syncthreads();  // Q staged
+
+  const float sqrt_hd = sqrtf((float)HD);
+  // the rounded scores of one block (s[i]: key jb + 8*(i/4) + 4*g + (i%4) of row ln)
+  auto scores = [&](int jb, int slot, float (&s)[16]) {
+    f32x16_t sc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sc[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const u32x4_t qf = *(const u32x4_t*)&qs[ln][16 * j + 8 * g];
+      if constexpr (DT == PE_DTYPE_F16)
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[slot][j]),
+                                                    __builtin_bit_cast(f16x8_t, qf), sc, 0, 0, 0);
+      else
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[slot][j]),
+                                                     __builtin_bit_cast(bf16x8_t, qf), sc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t kj = jb + 8 * (i >> 2) + 4 * g + (i & 3);
+      const bool ok = kj < j1 && key_allowed(kj, P, t, mask_mode, nbits);
+      s[i] = ok ? E::round(__fdiv_rn(E::round(sc[i]), sqrt_hd)) : -INFINITY;
+    }
+  };
+  constexpr std::integral_constant<int, 0> kK0{};
+  constexpr std::integral_constant<int, 1> kK1{};
+
+  // ---- pass 1: the row's max and sum
+  float m = kInitMax, l = 0.f;
+  auto pass1 = [&](int jb, auto ks_c, auto next_c) {
+    constexpr int KS = decltype(ks_c)::value;
+    if constexpr (decltype(next_c)::value) load_k(jb + 32, 1 - KS);
+    float s[16];
+    scores(jb, KS, s);
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bmax = fmaxf(bmax, s[i]);
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    const float mnew = fmaxf(m, bmax);
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) psum += expf(s[i] - mnew);
+    psum += __shfl_xor(psum, 32, 64);
+    l = l * expf(m - mnew) + psum;
+    m = mnew;
+  };
+  if (b0 < b1) {
+    load_k(32 * b0, 0);
+    int b = b0;
+    for (; b + 2 < b1; b += 2) {
+      pass1(32 * b, kK0, std::true_type());
+      pass1(32 * b + 32, kK1, std::true_type());
+    }
+    if (b + 1 < b1) {
+      pass1(32 * b, kK0, std::true_type());
+      pass1(32 * b + 32, kK1, std::false_type());
+    } else {
+      pass1(32 * b, kK0, std::false_type());
+    }
+  }
+  if (g == 0) {
+    s_ml[wave][ln][0] = m;
+    s_ml[wave][ln][1] = l;
+  }
+  __syncthreads();
+  float M = kInitMax;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, s_ml[w][ln][0]);
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) L += s_ml[w][ln][1] * expf(s_ml[w][ln][0] - M);
+  const float invL = 1.0f / L;
+
+  // ---- pass 2: O = sum_j round(exp(s_j - M) / L) v_j
+  f32x16_t o[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
+  const int qg = lane >> 4, jl = lane & 15;
+  auto pass2 = [&](int jb, auto ks_c, auto next_c) {
+    constexpr int KS = decltype(ks_c)::value;
+    constexpr bool kNext = decltype(next_c)::value;
+    if constexpr (kNext) load_k(jb + 32, 1 - KS);
+    float s[16];
+    scores(jb, KS, s);
+    uint32_t pb[8];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = E::round(expf(s[i] - M) * invL), p1 = E::round(expf(s[i + 1] - M) * invL);
+      pb[i >> 1] = (DT == PE_DTYPE_F16) ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
+                                        : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) *(u32x4_t*)&vs[4 * c + (lane >> 4)][(lane & 15) * 8] = vf[c];
+    if constexpr (kNext) load_v(jb + 32);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int cq = 0; cq < 2; ++cq) {
+      u32x4_t bp;
+      bp[0] = pb[4 * cq + 0];
+      bp[1] = pb[4 * cq + 1];
+      bp[2] = pb[4 * cq + 2];
+      bp[3] = pb[4 * cq + 3];
+      const int kb = 16 * cq + 4 * (qg >> 1) + (jl >> 2);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int db = 32 * h + 16 * (qg & 1) + 4 * (jl & 3);
+        typedef short s4v_t __attribute__((__vector_size__(4 * sizeof(short))));
+        typedef __attribute__((address_space(3))) s4v_t lds_s4v_t;
+        const s4v_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb][db]);
+        const s4v_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb + 8][db]);
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        u32x4_t a;
+        a[0] = l2.x;
+        a[1] = l2.y;
+        a[2] = h2.x;
+        a[3] = h2.y;
+        if constexpr (DT == PE_DTYPE_F16)
+          o[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                        __builtin_bit_cast(f16x8_t, bp), o[h], 0, 0, 0);
+        else
+          o[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                         __builtin_bit_cast(bf16x8_t, bp), o[h], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  if (b0 < b1) {
+    load_k(32 * b0, 0);
+    load_v(32 * b0);
+    int b = b0;
+    for (; b + 2 < b1; b += 2) {
+      pass2(32 * b, kK0, std::true_type());
+      pass2(32 * b + 32, kK1, std::true_type());
+    }
+    if (b + 1 < b1) {
+      pass2(32 * b, kK0, std::true_type());
+      pass2(32 * b + 32, kK1, std::false_type());
+    } else {
+      pass2(32 * b, kK0, std::false_type());
+    }
+  }
+
+  // ---- the waves' sums, in wave order, rounded once
+  __syncthreads();  // every wave is done with Q and its V^T tile
+  float* cmb = (float*)smem;  // [wave][row][kCmbRow]
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *(f32x4_t*)&cmb[(wave * 32 + ln) * kCmbRow + h * 32 + 8 * c + 4 * g] =
+          f32x4_t{o[h][4 * c], o[h][4 * c + 1], o[h][4 * c + 2], o[h][4 * c + 3]};
+  __syncthreads();
+  constexpr int kDimsT = HD * 32 / (64 * kAttnWaves);
+  const int row = threadIdx.x / (HD / kDimsT), dc = (threadIdx.x % (HD / kDimsT)) * kDimsT;
+  const int rr = rt * 32 + row;
+  if (rr >= rows) return;
+  float acc[kDimsT];
+#pragma unroll
+  for (int k = 0; k < kDimsT; ++k) acc[k] = 0.f;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w)
+#pragma unroll
+    for (int k4 = 0; k4 < kDimsT / 4; ++k4) {
+      const f32x4_t cv = *(const f32x4_t*)&cmb[(w * 32 + row) * kCmbRow + dc + 4 * k4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[4 * k4 + k] += cv[k];
+    }
+  const int tt = rr / G, col0 = (kvh * G + rr % G) * HD + dc;
+#pragma unroll
+  for (int k = 0; k < kDimsT; ++k) E::store((typename E::T*)out, (int64_t)tt * ld_out + col0 + k, acc[k]);
+}
+
 // Generic path (fp32, any hd <= 256; and the eager semantics in any dtype):
 // one block per (row t, query head), all keys.
 // eager (PE_ATTN_EAGER, the drafter's attention, src/pe/nn.py:84-87): the
@@ -680,6 +948,23 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
     }
     PE_CHECK_LAUNCH();
     return PE_OK;
+  }
+  if (eager && dtype != PE_DTYPE_F32 && hd == 128 && cache_cap < kAttnMaxCap) {
+    // every key of a row tile in one workgroup: the matrix-core eager kernel
+    const AttnPlan p = attn_plan(T, nh, nkv, S);
+    if (p.splits == 1) {
+      const dim3 grid(nkv, 1, p.row_tiles);
+      if (dtype == PE_DTYPE_BF16)
+        attn_eager_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>(
+            (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
+            mask_mode, bits, words, out, ld_out);
+      else
+        attn_eager_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>(
+            (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
+            mask_mode, bits, words, out, ld_out);
+      PE_CHECK_LAUNCH();
+      return PE_OK;
+    }
   }
   dim3 grid(T, nh);
   float* scores = (float*)workspace;
