@@ -523,7 +523,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
 }
 
 // Eager attention on the matrix cores (PE_ATTN_EAGER, the drafter's attention,
-// src/pe/nn.py:84-87) for launches whose plan has one key split, so that a
+// src/pe/nn.py:84-87, 16-bit with hd = 128), one key split, so that a
 // workgroup sees every key of its rows: one workgroup = 8 waves = one (KV head,
 // 32-row tile), each wave a contiguous run of the tile's 32-key blocks, walked
 // twice.
@@ -790,8 +790,9 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_eager_kernel(
   for (int k = 0; k < kDimsT; ++k) E::store((typename E::T*)out, (int64_t)tt * ld_out + col0 + k, acc[k]);
 }
 
-// Generic path (fp32, any hd <= 256; and the eager semantics in any dtype):
-// one block per (row t, query head), all keys.
+// Generic path (fp32, any hd <= 256; and the eager semantics where
+// attn_eager_kernel does not apply: fp32, or hd != 128): one block per (row t,
+// query head), all keys.
 // eager (PE_ATTN_EAGER, the drafter's attention, src/pe/nn.py:84-87): the
 // score is the dot product rounded to the dtype, divided by sqrt(hd) and
 // rounded again (the masked keys' -inf bias leaves them out); softmax in fp32;
@@ -898,7 +899,8 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S, int batch = 1) {
 
 int64_t attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_len, int dtype, int attn_mode) {
   if (T <= 0 || nh <= 0 || nkv <= 0 || kv_len <= 0) return 0;
-  if (dtype != PE_DTYPE_F32 && hd == 128 && attn_mode != PE_ATTN_EAGER) {
+  if (dtype != PE_DTYPE_F32 && hd == 128) {
+    if (attn_mode == PE_ATTN_EAGER) return kAttnCounterBytes;  // attn_eager_kernel: no scratch
     AttnPlan p = attn_plan(T, nh, nkv, kv_len);
     return kAttnCounterBytes + p.opart_bytes + p.ml_bytes;
   }
@@ -949,22 +951,20 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
     PE_CHECK_LAUNCH();
     return PE_OK;
   }
-  if (eager && dtype != PE_DTYPE_F32 && hd == 128 && cache_cap < kAttnMaxCap) {
-    // every key of a row tile in one workgroup: the matrix-core eager kernel
-    const AttnPlan p = attn_plan(T, nh, nkv, S);
-    if (p.splits == 1) {
-      const dim3 grid(nkv, 1, p.row_tiles);
-      if (dtype == PE_DTYPE_BF16)
-        attn_eager_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>(
-            (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
-            mask_mode, bits, words, out, ld_out);
-      else
-        attn_eager_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>(
-            (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
-            mask_mode, bits, words, out, ld_out);
-      PE_CHECK_LAUNCH();
-      return PE_OK;
-    }
+  if (eager && dtype != PE_DTYPE_F32 && hd == 128) {
+    // the matrix-core eager kernel: every key of a row tile in one workgroup
+    if (cache_cap >= kAttnMaxCap) return PE_ERR_ARG;
+    const dim3 grid(nkv, 1, (T * (nh / nkv) + 31) / 32);
+    if (dtype == PE_DTYPE_BF16)
+      attn_eager_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
+          mask_mode, bits, words, out, ld_out);
+    else
+      attn_eager_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P,
+          mask_mode, bits, words, out, ld_out);
+    PE_CHECK_LAUNCH();
+    return PE_OK;
   }
   dim3 grid(T, nh);
   float* scores = (float*)workspace;

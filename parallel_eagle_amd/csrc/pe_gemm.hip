@@ -1348,7 +1348,10 @@ int cu_count() {
 }
 
 Plan make_plan(int M, int N, int K, bool nf4, int epi) {
-  static const int wave_slots = env_int("PE_GEMM_WAVE_SLOTS", 3072);
+  // dense linears: about 1792 waves' worth of units per launch (the 14B fp16
+  // linears then run 400-480 workgroups in 4-6 K splits; 3072 gave 7-9
+  // splits and a pass 6% slower)
+  static const int wave_slots = env_int("PE_GEMM_WAVE_SLOTS", 1792);
   static const int nf4_min_wgs = env_int("PE_NF4_MIN_WGS", 128);
   static const int nf4_min_units = env_int("PE_NF4_MIN_UNITS", 2);
   static const int min_units = env_int("PE_GEMM_MIN_UNITS", 2);
