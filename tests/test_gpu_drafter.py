@@ -6,7 +6,7 @@ import torch
 
 from oracle import drafter as od
 from parallel_eagle_amd import tree as ptree
-from parallel_eagle_amd.config import LLAMA2_7B_NF4
+from parallel_eagle_amd.config import LLAMA2_7B_NF4, QWEN25_14B_FP16
 from parallel_eagle_amd.drafter import DeviceDrafter
 from parallel_eagle_amd.target import TargetModel
 from tests.test_oracle_pins import _drafter_weights
@@ -24,21 +24,43 @@ def target():
     return tm, shared
 
 
+@pytest.fixture(scope="module")
+def target_fp16():
+    # the 14B shape's grouped-query heads (40 query / 8 KV) in fp16, one layer,
+    # a smaller vocabulary for the CPU oracle
+    shape = QWEN25_14B_FP16.reduced(1, vocab=16384, feature_layers=(1, 1, 1))
+    tm = TargetModel.synthetic(shape, seed=5, device=DEV, keep_logical=True, norm_noise=0.1)
+    hw = tm.model.host_weights()
+    shared = {"embed": hw["embed"], "final_norm": hw["final_norm"], "lm_head": hw["lm_head"]}
+    return tm, shared
+
+
 @pytest.mark.parametrize("n_layers,p,k", [(1, 40, 5), (2, 300, 6), (1, 1, 1)])
 def test_draft_logits_match_oracle(target, n_layers, p, k):
-    tm, shared = target
+    _check_draft_logits(*target, n_layers, p, k)
+
+
+def test_draft_logits_fp16_grouped_query_heads_match_oracle(target_fp16):
+    """An fp16 drafter with grouped-query heads: the eager attention's fp16
+    matrix-core instance, its 32-row tiles spanning G = 5 query heads per KV
+    head (130 context rows, 26 nodes' worth), against the oracle."""
+    _check_draft_logits(*target_fp16, 1, 130, 5)
+
+
+def _check_draft_logits(tm, shared, n_layers, p, k):
     shape = tm.shape
+    dt = tm.dtype
     # weights at the target's init scale: larger ones make attention so sharp that
     # bf16 rounding alone (the oracle's too) moves logits by more than the tolerance
-    w, _ = _drafter_weights(shape, n_layers, 3, torch.bfloat16, seed=p + n_layers, std=shape.init_std)
-    w["feat_norm"] = w["feat_norm"].float().clamp(min=0.5).to(torch.bfloat16)
+    w, _ = _drafter_weights(shape, n_layers, 3, dt, seed=p + n_layers, std=shape.init_std)
+    w["feat_norm"] = w["feat_norm"].float().clamp(min=0.5).to(dt)
     gen = torch.Generator().manual_seed(p)
     ids = torch.randint(0, shape.vocab, (p,), generator=gen)
-    feats = (torch.randn(p, 3 * shape.hidden, generator=gen) * 4).to(torch.bfloat16)
+    feats = (torch.randn(p, 3 * shape.hidden, generator=gen) * 4).to(dt)
     dr = DeviceDrafter(tm, w, max_depth=k, capacity=512)
     got = dr.draft_logits(ids.to(DEV), feats.to(DEV), k).cpu()
     assert got.shape == (k, shape.vocab)
-    want = od.OracleDrafter(shape, w, shared, torch.bfloat16).draft_logits(ids, feats, k)
+    want = od.OracleDrafter(shape, w, shared, dt).draft_logits(ids, feats, k)
     f32 = lambda d: {kk: (vv.float() if torch.is_tensor(vv) else [{a: b.float() for a, b in x.items()} for x in vv])
                      for kk, vv in d.items()}
     ref32 = od.OracleDrafter(shape, f32(w), f32(shared), torch.float32).draft_logits(ids, feats.float(), k)
