@@ -7,9 +7,10 @@
 // ancestor of t), which is the (T, P+T) additive bias of the reference
 // (src/pe/masks.py:127-147 + to_additive_bias :29-33) without materialising it.
 //
-// 16-bit path (hd = 128): one wave per (KV head, key split, 32-row tile).
+// 16-bit path (hd = 128): one workgroup of 8 waves per (KV head, key split,
+// 32-row tile), each wave a run of the split's 32-key blocks.
 //   S^T = K Q^T with v_mfma_f32_32x32x16 (A = 32 keys x 16 dims of K straight
-//   from the cache, B = Q^T held in registers), so every lane owns one query
+//   from the cache, B = Q^T from the tile staged in LDS), so every lane owns one query
 //   row (column) and 16 of the 32 keys: the online-softmax max/sum of a row is
 //   a 16-value in-lane reduction plus one exchange with lane^32.
 //   O^T += V^T P^T (A = V^T from a wave-private LDS transpose of the 32-key V
@@ -24,6 +25,8 @@
 // exponential is one v_exp_f32 (2^x) and the running maxima and split partials
 // are in base 2 as well.
 //
+// The drafter's eager rounding (PE_ATTN_EAGER) at 16 bits: attn_eager_kernel,
+// the same tiles in two passes over the keys.
 // fp32 path: one block per (row, query head), scores in LDS, VALU arithmetic.
 
 #include "pe_common.h"
