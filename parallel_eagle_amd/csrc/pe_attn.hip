@@ -46,6 +46,16 @@ __device__ __forceinline__ bool key_allowed(int64_t key, int64_t P, int t, int m
   return (nb[u >> 6] >> (u & 63)) & 1ull;
 }
 
+// tree mask of one key, the word chosen by selects (no indexed read of the
+// register array)
+__device__ __forceinline__ bool tree_key_allowed(int64_t key, int64_t P, const uint64_t* nb) {
+  if (key < P) return true;
+  const int u = (int)(key - P);
+  static_assert(PE_TREE_MAX_WORDS == 4, "one select per word");
+  const uint64_t w = u < 64 ? nb[0] : u < 128 ? nb[1] : u < 192 ? nb[2] : nb[3];
+  return (w >> (u & 63)) & 1ull;
+}
+
 // One workgroup = 8 waves = one (KV head, key split, 32-row tile); each wave
 // takes a contiguous run of the split's 32-key blocks. Its first two blocks
 // are loaded and processed together as one 64-key block (a run of one block
@@ -523,6 +533,332 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
     }
   }
   write_out(num, den);
+}
+
+// Batched attention with two row tiles per wave. One workgroup = 4 waves (one
+// per SIMD, so a wave may hold up to 512 VGPRs) = one (KV head, sequence,
+// pair of 32-row tiles); every key of the sequence in one split, each wave a
+// quarter of the key blocks. Every K fragment feeds the S^T products of both
+// tiles and every transposed V read the PV products of both, so each K/V byte
+// a CU reads serves 64 query rows instead of 32, and a (sequence, KV head)
+// with five row tiles (G = 5 query heads x 26 nodes) needs three workgroups
+// instead of five. A pair's second tile may lie past the sequence's rows (the
+// fifth of five): then only the first is computed. Each round: the next
+// block's K (into the other of two K slots) and V (once this block's V is in
+// LDS) in flight, every load unconditional (rows clamped to the wave's last
+// key), so the waits are exact counts. The softmax arithmetic is
+// attn_wg_kernel's; the waves' (O, m, l) are merged per tile in LDS in wave
+// order.
+constexpr int kPairWaves = 4;
+
+template <int DT>
+__global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
+    int nh, int nkv, const uint64_t* __restrict__ bits, int words, float scale, void* __restrict__ out,
+    int64_t ld_out, int out_units, AttnBatch bt) {
+  constexpr int HD = 128;
+  constexpr int kQBytes = 32 * kQStride * 2;
+  constexpr int kVtBytes = 32 * kVRow * 2;
+  constexpr int kCmbBytes = kPairWaves * 32 * (kCmbRow + 2) * 4;
+  constexpr int kMain = 2 * kQBytes + kPairWaves * kVtBytes;
+  constexpr int kSmem = (kMain > kCmbBytes) ? kMain : kCmbBytes;
+  __shared__ __align__(16) uint8_t smem[kSmem];
+  const int kvh = blockIdx.x;
+  const int tpairs = (bt.row_tiles + 1) / 2;
+  const int pos = blockIdx.z / tpairs, tp = blockIdx.z - pos * tpairs;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ln = lane & 31, g = lane >> 5;
+  int seq = pos;
+  if (bt.batch <= 64) {  // longest prefix first, as attn_wg_kernel orders them
+    int rank = -1;
+    if (lane < bt.batch) {
+      const int64_t pl = bt.seq_prefix[lane];
+      rank = 0;
+      for (int j = 0; j < bt.batch; ++j) {
+        const int64_t pj = bt.seq_prefix[j];
+        rank += (pj > pl || (pj == pl && j < lane)) ? 1 : 0;
+      }
+    }
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(rank == pos);
+    seq = hit ? (int)__builtin_ctzll(hit) : pos;
+  }
+  const int rbase = bt.seq_row0[seq];
+  const int T = bt.seq_row0[seq + 1] - rbase;
+  const int64_t P = bt.seq_prefix[seq];
+  const int G = nh / nkv, rows = T * G;
+  const int rtA = 2 * tp, rtB = 2 * tp + 1;
+  if (T <= 0 || rtA * 32 >= rows) return;
+  const bool two = rtB * 32 < rows;  // workgroup-uniform: one body per case
+  auto body = [&](auto two_c) {
+  constexpr bool TWO = decltype(two_c)::value;
+  q += (int64_t)rbase * nh * HD;
+  bits += (int64_t)rbase * words;
+  kc += seq * bt.seq_stride;
+  vc += seq * bt.seq_stride;
+  const int64_t S = P + T;
+  const int nb = (int)((S + 31) / 32);
+  const int b0 = (nb * wave) / kPairWaves, b1 = (nb * (wave + 1)) / kPairWaves;
+  const int64_t j1 = min(S, 32 * (int64_t)b1);
+  const int jcl = (int)max(j1 - 1, (int64_t)0);  // a row index of one head: below cap < 2^24
+  uint16_t(*qsA)[kQStride] = (uint16_t(*)[kQStride])smem;
+  uint16_t(*qsB)[kQStride] = (uint16_t(*)[kQStride])(smem + kQBytes);
+  uint16_t(*vs)[kVRow] = (uint16_t(*)[kVRow])(smem + 2 * kQBytes + wave * kVtBytes);
+  const char* kbase = (const char*)(kc + (int64_t)kvh * cap * HD);
+  const char* vbase = (const char*)(vc + (int64_t)kvh * cap * HD);
+  u32x4_t kf[2][8], vf[8];
+  auto load_k = [&](int jb, int slot) {
+    const uint32_t ko = (uint32_t)min(jb + ln, jcl) * (HD * 2) + 16 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kf[slot][j] = *(const u32x4_t*)(kbase + ko + 32 * j);
+  };
+  auto load_v = [&](int jb) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t vo = (uint32_t)min(jb + 4 * c + (lane >> 4), jcl) * (HD * 2) + (lane & 15) * 16;
+      vf[c] = *(const u32x4_t*)(vbase + vo);
+    }
+  };
+  // each lane's row in the two tiles, their ancestor bits, both tiles' Q
+  // (rows past `rows` read row rows - 1 and stage zeros; never stored), then
+  // the first block: all requested before anything waits
+  const int rA = rtA * 32 + ln, rB = rtB * 32 + ln;
+  const int tA = rA < rows ? rA / G : 0, tB = rB < rows ? rB / G : 0;
+  uint64_t nbA[PE_TREE_MAX_WORDS], nbB[PE_TREE_MAX_WORDS];
+#pragma unroll
+  for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) {
+    nbA[w] = bits[(int64_t)tA * words + min(w, words - 1)];
+    nbB[w] = bits[(int64_t)tB * words + min(w, words - 1)];
+  }
+  constexpr int kQChunks = 512 / (64 * kPairWaves);
+  u32x4_t qv[2][kQChunks];
+  bool qok[2][kQChunks];
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+    for (int c = 0; c < kQChunks; ++c) {
+      const int chunk = c * 64 * kPairWaves + threadIdx.x;
+      const int qr = chunk >> 4, dc = chunk & 15;
+      const int rr0 = (tile ? rtB : rtA) * 32 + qr;
+      qok[tile][c] = rr0 < rows;
+      const int rr = min(rr0, rows - 1);
+      qv[tile][c] = *(const u32x4_t*)(q + ((int64_t)(rr / G) * nh + kvh * G + rr % G) * HD + dc * 8);
+    }
+  load_k(32 * b0, 0);
+  load_v(32 * b0);
+  __builtin_amdgcn_sched_barrier(0);
+  const u32x4_t zero4 = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+    for (int c = 0; c < kQChunks; ++c) {
+      const int chunk = c * 64 * kPairWaves + threadIdx.x;
+      uint16_t(*qs)[kQStride] = tile ? qsB : qsA;
+      *(u32x4_t*)&qs[chunk >> 4][(chunk & 15) * 8] = qok[tile][c] ? qv[tile][c] : zero4;
+    }
+  f32x16_t oA[4], oB[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) oA[h][i] = oB[h][i] = 0.f;
+  float mA = kInitMax, lA = 0.f, mB = kInitMax, lB = 0.f;
+  __syncthreads();  // both Q tiles staged
+
+  const float scale2 = scale * 1.44269504088896341f;  // natural-log scores -> base 2
+  const int qg = lane >> 4, jl = lane & 15;
+  // online softmax of one tile's 32 keys: returns the packed probabilities
+  auto softmax = [&](f32x16_t& sc, int64_t jb, bool whole, int t, const uint64_t (&nb)[PE_TREE_MAX_WORDS],
+                     float& m, float& l, f32x16_t (&o)[4], uint32_t (&pb)[8]) {
+    float bmax = -INFINITY;
+    if (whole) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) bmax = fmaxf(bmax, sc[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t kj = jb + 8 * (i >> 2) + 4 * g + (i & 3);
+        const bool ok = kj < j1 && tree_key_allowed(kj, P, nb);
+        sc[i] = ok ? sc[i] : -INFINITY;
+        bmax = fmaxf(bmax, sc[i]);
+      }
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * scale2;
+    // a row keeps its running max until a block's exceeds it by more than
+    // 2^8: its probabilities stay below 2^8 and O (held in the matrix-core
+    // accumulators) is rescaled in a few rounds only
+    const float mnew = bmax > m + 8.f ? bmax : m;
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[i], scale2, -mnew));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[i + 1], scale2, -mnew));
+      psum += p0 + p1;
+      pb[i >> 1] = (DT == PE_DTYPE_F16) ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
+                                        : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
+    }
+    psum += __shfl_xor(psum, 32, 64);
+    l = l * alpha + psum;
+    // rescale O only if some row's running max moved (alpha == 1 leaves O as is)
+    if (__builtin_amdgcn_ballot_w64(mnew != m) != 0ull) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[h][i] *= alpha;
+    }
+    m = mnew;
+  };
+  auto process = [&](int jb, auto ks_c, auto next_c) {
+    constexpr int KS = decltype(ks_c)::value;
+    constexpr bool kNext = decltype(next_c)::value;
+    if constexpr (kNext) load_k(jb + 32, 1 - KS);
+    f32x16_t scA, scB;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) scA[i] = scB[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const u32x4_t qa = *(const u32x4_t*)&qsA[ln][16 * j + 8 * g];
+      const u32x4_t qb = *(const u32x4_t*)&qsB[ln][16 * j + 8 * g];
+      if constexpr (DT == PE_DTYPE_F16) {
+        scA = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[KS][j]),
+                                                     __builtin_bit_cast(f16x8_t, qa), scA, 0, 0, 0);
+        if constexpr (TWO)
+          scB = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf[KS][j]),
+                                                       __builtin_bit_cast(f16x8_t, qb), scB, 0, 0, 0);
+      } else {
+        scA = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[KS][j]),
+                                                      __builtin_bit_cast(bf16x8_t, qa), scA, 0, 0, 0);
+        if constexpr (TWO)
+          scB = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[KS][j]),
+                                                        __builtin_bit_cast(bf16x8_t, qb), scB, 0, 0, 0);
+      }
+    }
+    // a whole 32-key block of prefix keys: every key is visible to every node
+    const bool whole = jb + 32 <= min(P, j1);
+    uint32_t pbA[8], pbB[8] = {};
+    softmax(scA, jb, whole, tA, nbA, mA, lA, oA, pbA);
+    if constexpr (TWO) softmax(scB, jb, whole, tB, nbB, mB, lB, oB, pbB);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) *(u32x4_t*)&vs[4 * c + (lane >> 4)][(lane & 15) * 8] = vf[c];
+    if constexpr (kNext) load_v(jb + 32);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int cq = 0; cq < 2; ++cq) {
+      u32x4_t bpA, bpB;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bpA[e] = pbA[4 * cq + e];
+        bpB[e] = pbB[4 * cq + e];
+      }
+      const int kb = 16 * cq + 4 * (qg >> 1) + (jl >> 2);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int db = 32 * h + 16 * (qg & 1) + 4 * (jl & 3);
+        typedef short s4v_t __attribute__((__vector_size__(4 * sizeof(short))));
+        typedef __attribute__((address_space(3))) s4v_t lds_s4v_t;
+        const s4v_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb][db]);
+        const s4v_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb + 8][db]);
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        u32x4_t a;
+        a[0] = l2.x;
+        a[1] = l2.y;
+        a[2] = h2.x;
+        a[3] = h2.y;
+        if constexpr (DT == PE_DTYPE_F16) {
+          oA[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                         __builtin_bit_cast(f16x8_t, bpA), oA[h], 0, 0, 0);
+          if constexpr (TWO)
+            oB[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                           __builtin_bit_cast(f16x8_t, bpB), oB[h], 0, 0, 0);
+        } else {
+          oA[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                          __builtin_bit_cast(bf16x8_t, bpA), oA[h], 0, 0, 0);
+          if constexpr (TWO)
+            oB[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                            __builtin_bit_cast(bf16x8_t, bpB), oB[h], 0, 0, 0);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  constexpr std::integral_constant<int, 0> kK0{};
+  constexpr std::integral_constant<int, 1> kK1{};
+  if (b0 < b1) {
+    int b = b0;
+    for (; b + 2 < b1; b += 2) {
+      process(32 * b, kK0, std::true_type());
+      process(32 * b + 32, kK1, std::true_type());
+    }
+    if (b + 1 < b1) {
+      process(32 * b, kK0, std::true_type());
+      process(32 * b + 32, kK1, std::false_type());
+    } else {
+      process(32 * b, kK0, std::false_type());
+    }
+  }
+
+  // ---- per tile: merge the waves (wave order) and write the rows
+  constexpr int kDimsT = HD * 32 / (64 * kPairWaves);  // output dims per thread
+  const int row = threadIdx.x / (HD / kDimsT), dc = (threadIdx.x % (HD / kDimsT)) * kDimsT;
+  float* cmb = (float*)smem;                     // [wave][row][kCmbRow]
+  float* mlw = cmb + kPairWaves * 32 * kCmbRow;  // [wave][row][2]
+  typedef typename Elem<DT>::T Te;
+  auto merge_tile = [&](const f32x16_t (&o)[4], float m, float l, int rt) {
+    __syncthreads();  // every wave is done with Q, its V^T tile and the previous merge
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *(f32x4_t*)&cmb[(wave * 32 + ln) * kCmbRow + h * 32 + 8 * c + 4 * g] =
+            f32x4_t{o[h][4 * c], o[h][4 * c + 1], o[h][4 * c + 2], o[h][4 * c + 3]};
+    if (g == 0) {
+      mlw[(wave * 32 + ln) * 2] = m;
+      mlw[(wave * 32 + ln) * 2 + 1] = l;
+    }
+    __syncthreads();
+    float M = kInitMax;
+#pragma unroll
+    for (int w = 0; w < kPairWaves; ++w) M = fmaxf(M, mlw[(w * 32 + row) * 2]);
+    float L = 0.f, acc[kDimsT];
+#pragma unroll
+    for (int k = 0; k < kDimsT; ++k) acc[k] = 0.f;
+#pragma unroll
+    for (int w = 0; w < kPairWaves; ++w) {
+      const float wt = __builtin_amdgcn_exp2f(mlw[(w * 32 + row) * 2] - M);
+      L += wt * mlw[(w * 32 + row) * 2 + 1];
+#pragma unroll
+      for (int k4 = 0; k4 < kDimsT / 4; ++k4) {
+        const f32x4_t cv = *(const f32x4_t*)&cmb[(w * 32 + row) * kCmbRow + dc + 4 * k4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[4 * k4 + k] += wt * cv[k];
+      }
+    }
+    const int rr = rt * 32 + row;
+    if (rr >= rows) return;
+    const int tt = rr / G + rbase, col0 = (kvh * G + rr % G) * HD + dc;
+    if (!out_units && ((ld_out & 3) || ((uintptr_t)out & 7))) {  // row-major output not 8-byte aligned
+#pragma unroll
+      for (int k = 0; k < kDimsT; ++k) Elem<DT>::store((Te*)out, (int64_t)tt * ld_out + col0 + k, acc[k] / L);
+      return;
+    }
+#pragma unroll
+    for (int k4 = 0; k4 < kDimsT / 4; ++k4) {
+      float o4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o4[i] = acc[4 * k4 + i] / L;
+      const int col = col0 + 4 * k4;
+      Vec4<DT>::store((Te*)out + (out_units ? xtile_index(tt, col, out_units) : (int64_t)tt * ld_out + col), o4);
+    }
+  };
+  merge_tile(oA, mA, lA, rtA);
+  if constexpr (TWO) merge_tile(oB, mB, lB, rtB);
+  };
+  if (two)
+    body(std::true_type());
+  else
+    body(std::false_type());
 }
 
 // Eager attention on the matrix cores (PE_ATTN_EAGER, the drafter's attention,
@@ -1021,8 +1357,23 @@ int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const v
   if (!counters) counters = (int*)workspace;
   float* opart = (float*)((char*)workspace + kAttnCounterBytes);
   float* ml = (float*)((char*)workspace + kAttnCounterBytes + p.opart_bytes);
-  const dim3 grid(nkv, p.splits, batch * p.row_tiles);
   const AttnBatch bt{batch, p.row_tiles, seq_row0, seq_prefix, seq_stride};
+  const int tpairs = (p.row_tiles + 1) / 2;
+  if (p.row_tiles >= 2 && (int64_t)batch * nkv * tpairs >= 128) {
+    // two row tiles per wave: each K/V block read once for both
+    const dim3 gridp(nkv, 1, batch * tpairs);
+    if (dtype == PE_DTYPE_BF16)
+      attn_pair_kernel<PE_DTYPE_BF16><<<gridp, 64 * kPairWaves, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, bits, words,
+          scale, out, ld_out, out_units, bt);
+    else
+      attn_pair_kernel<PE_DTYPE_F16><<<gridp, 64 * kPairWaves, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, bits, words,
+          scale, out, ld_out, out_units, bt);
+    PE_CHECK_LAUNCH();
+    return PE_OK;
+  }
+  const dim3 grid(nkv, p.splits, batch * p.row_tiles);
   if (dtype == PE_DTYPE_BF16)
     attn_wg_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>(
         (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, max_rows,
