@@ -305,6 +305,45 @@ def test_tree_attention_matches_sdpa(dtype, hd, nh, nkv, P, parents, causal):
     assert torch.allclose(out.float(), ref.float(), rtol=tol, atol=tol), (out.float() - ref.float()).abs().max()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("nh,nkv,T,P", [
+    (4, 4, 64, 2000),   # two row tiles, key splits; the last split holds node keys only
+    (10, 2, 26, 1000),  # five row tiles per KV head, the last with two rows
+    (2, 1, 26, 5000),   # two row tiles in 16 key splits
+    (8, 8, 40, 0),      # node keys only, one split, the second tile 8 rows
+])
+def test_multi_tile_attention_with_key_splits_matches_sdpa(dtype, nh, nkv, T, P):
+    """Tree attention over more than 32 query rows per KV head (several row
+    tiles, split keys combined by the last workgroup to arrive): against SDPA
+    with the reference's additive tree bias; a call repeated on the same
+    workspace after a causal call (the same arrival counters) is equal."""
+    hd = 128
+    rng = np.random.default_rng(1000 * T + P)
+    parents = [-1] + [int(rng.integers(-1, t)) for t in range(1, T)]
+    S = P + T
+    cap = S + 5
+    q = torch.from_numpy(synth.normal(4, 60, T * nh * hd).reshape(T, nh, hd)).to(dtype)
+    k = torch.from_numpy(synth.normal(5, 61, nkv * S * hd).reshape(nkv, S, hd)).to(dtype)
+    v = torch.from_numpy(synth.normal(6, 62, nkv * S * hd).reshape(nkv, S, hd)).to(dtype)
+    kc = torch.zeros((nkv, cap, hd), dtype=dtype)
+    vc = torch.zeros((nkv, cap, hd), dtype=dtype)
+    kc[:, :S], vc[:, :S] = k, v
+    qd, kd, vd = q.to(DEV), kc.to(DEV), vc.to(DEV)
+    scale = hd ** -0.5
+    st = _status()
+    bits, _, _ = ops.tree_masks(torch.tensor(parents, dtype=torch.int32, device=DEV), P, (T + 63) // 64, st)
+    need = int(ops.lib().pe_attention_workspace_bytes(T, nh, nkv, hd, S, ops.dcode(dtype)))
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    out = ops.tree_attention(qd, kd, vd, P, _lib.PE_MASK_TREE, bits, scale, workspace=ws).cpu()
+    causal = ops.tree_attention(qd, kd, vd, P, _lib.PE_MASK_CAUSAL, None, scale, workspace=ws).cpu()
+    again = ops.tree_attention(qd, kd, vd, P, _lib.PE_MASK_TREE, bits, scale, workspace=ws).cpu()
+    assert torch.equal(out, again)
+    ref = _attn_ref(q, k, v, P, parents, False, scale, dtype)
+    assert torch.allclose(out.float(), ref.float(), rtol=2e-2, atol=2e-2), (out.float() - ref.float()).abs().max()
+    ref_c = _attn_ref(q, k, v, P, None, True, scale, dtype)
+    assert torch.allclose(causal.float(), ref_c.float(), rtol=2e-2, atol=2e-2)
+
+
 # ------------------------------------------------------------------ acceptance and compaction
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("seed", range(6))
