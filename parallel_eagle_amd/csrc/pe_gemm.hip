@@ -1332,8 +1332,10 @@ struct Plan {
 // (one CU pulls under 1/128 of the HBM bandwidth), keeping every wave at least
 // `min_units` units; at the 7B shapes q/k/v and gate/up get one split (the
 // epilogue runs in the GEMM, no exchange).
-// Dense: S spreads the work over about `wave_slots` waves (256 CUs x 3
-// four-wave workgroups), a wave getting at least 2 units.
+// Dense q/k/v (split exchange) and o/down (split partials): as many splits as
+// keep the launch within one workgroup per CU. Other dense launches: S spreads
+// the work over about `wave_slots` waves (256 CUs x 3 four-wave workgroups), a
+// wave getting at least 2 units.
 // Either way the splits are balanced to differ by at most one unit per wave.
 // CUs of the current device (256 on MI355X), queried once.
 int cu_count() {
@@ -1373,6 +1375,13 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   } else if (nf4) {
     S = (nf4_min_wgs + p.groups - 1) / p.groups;
     const int s_units = p.units / (kWaves * nf4_min_units);
+    if (S > s_units) S = s_units;
+  } else if (epi == kEpiRopeKV || epi == kEpiPartial) {
+    // dense split exchange (q/k/v) or split partials (o, down): at most one
+    // round of one workgroup per CU; a second, partly filled round costs more
+    // than the splits save
+    S = cu_count() / p.groups;
+    const int s_units = p.units / (kWaves * min_units);
     if (S > s_units) S = s_units;
   } else {
     const int64_t total = (int64_t)p.groups * p.units;

@@ -94,6 +94,8 @@ Layout make_layout(const pe_model_desc* m, int M, int64_t kv_len) {
     L.xn_t = off; off += align_up(xtile_bytes(M, H));
     L.attn_t = off; off += align_up(xtile_bytes(M, qd));
     L.act_t = off; off += align_up(xtile_bytes(M, ip));
+  }
+  if (fused_path(m, M)) {  // o and down write split partials (NF4 and dense)
     const int wf = m->weight_format;
     const int64_t pb[2] = {pe_internal_linear_partials_bytes(M, H, qd, wf),
                            pe_internal_linear_partials_bytes(M, H, ip, wf)};
@@ -361,9 +363,9 @@ extern "C" int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int
 // The 16-bit pass: per layer
 //   q/k/v GEMM with bias + RoPE + in-place K/V append in its epilogue
 //   -> tree attention (split-KV) -> combine
-//   -> o GEMM with the residual add in its epilogue -> post-attention RMSNorm
+//   -> o GEMM (fp32 split partials) -> residual add + post-attention RMSNorm
 //   -> gate/up GEMM with SwiGLU epilogue
-//   -> down GEMM with the residual add in its epilogue -> next RMSNorm
+//   -> down GEMM (fp32 split partials) -> residual add + next RMSNorm
 // The RMSNorm after the down projection is the next layer's input norm, or the
 // final norm after the last layer; hidden-state captures ride on it.
 int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& Lo, hipStream_t st) {
@@ -420,11 +422,13 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
                                      m->norm_mode, m->dtype, xn, xn_t, slot_ptr(f0), fused_ld, nullptr, 0, a->status, st));
     PE_TRY(copy_repeats(0, f0));
   }
-  // The tiled (NF4) pass: q/k/v and gate/up run unsplit with their RoPE + KV
-  // append / SwiGLU epilogues in the GEMM; o and down write split partials
-  // with plain stores that the residual + RMSNorm kernel sums, so no GEMM
-  // waits on another workgroup of its own launch.
-  float* part = tiled ? (float*)(ws + Lo.part) : nullptr;
+  // q/k/v and gate/up run with their RoPE + KV append / SwiGLU epilogues in
+  // the GEMM (unsplit in the tiled NF4 pass); o and down write split partials
+  // with plain stores that the residual + RMSNorm kernel sums, so no o or down
+  // workgroup waits on another of its own launch (NF4 and dense alike: for
+  // the dense 14B shapes the partials and one round of workgroups made the
+  // pass 7.9% faster than the in-launch exchange).
+  float* part = (float*)(ws + Lo.part);
   const int nqkv = (nh + 2 * nkv) * hd;
   int S = 0;
   for (int l = 0; l < L; ++l) {
@@ -439,17 +443,10 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
                                       a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
                                       Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st, m->attn_mode));
     const void* a_o = m->a_o ? m->a_o[l] : nullptr;
-    if (tiled) {
-      PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, true, M, qd, m->w_o[l], a_o, H, part,
-                                         Lo.part_bytes, &S, st));
-      PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, xn_t, nullptr,
-                                          0, nullptr, 0, st));
-    } else {
-      PE_TRY(pe_internal_linear(wf, m->dtype, x_attn, qd, false, M, qd, m->w_o[l], a_o, H, PE_EPI_RESIDUAL, nullptr,
-                                h, H, h, H, 0, gws, gwsb, st));
-      PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, nullptr,
-                                          nullptr, 0, nullptr, 0, st));
-    }
+    PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, tiled, M, qd, m->w_o[l], a_o, H, part,
+                                       Lo.part_bytes, &S, st));
+    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, xn_t,
+                                        nullptr, 0, nullptr, 0, st));
     const void* a_gu = m->a_gu ? m->a_gu[l] : nullptr;
     const void* a_down = m->a_down ? m->a_down[l] : nullptr;
     const bool last = l + 1 == L;
@@ -457,21 +454,12 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     const int fx = last ? slot_of(L) : -1;
     const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
     const int next_mode = last ? PE_NORM_HF : m->norm_mode;
-    if (tiled) {
-      PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, true, M, H, m->w_gu[l], a_gu, 2 * ip, PE_EPI_SWIGLU,
-                                nullptr, nullptr, 0, x_act, ip, act_units, gws, gwsb, st));
-      PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_act, ip, true, M, ip, m->w_down[l], a_down, H, part,
-                                         Lo.part_bytes, &S, st));
-      PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn,
-                                          last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
-    } else {
-      PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, false, M, H, m->w_gu[l], a_gu, 2 * ip, PE_EPI_SWIGLU,
-                                nullptr, nullptr, 0, x_act, ip, 0, gws, gwsb, st));
-      PE_TRY(pe_internal_linear(wf, m->dtype, x_act, ip, false, M, ip, m->w_down[l], a_down, H, PE_EPI_RESIDUAL,
-                                nullptr, h, H, h, H, 0, gws, gwsb, st));
-      PE_TRY(pe_internal_residual_rmsnorm(nullptr, 0, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn, nullptr,
-                                          slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
-    }
+    PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, tiled, M, H, m->w_gu[l], a_gu, 2 * ip, PE_EPI_SWIGLU, nullptr,
+                              nullptr, 0, x_act, ip, act_units, gws, gwsb, st));
+    PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_act, ip, tiled, M, ip, m->w_down[l], a_down, H, part,
+                                       Lo.part_bytes, &S, st));
+    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn,
+                                        last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
   if (a->logits) PE_TRY(lm_head(m, a, xn, M, gws, gwsb, st));
