@@ -1327,7 +1327,8 @@ struct Plan {
 };
 
 // units: 128-wide K units (NF4) or 64-wide K steps (dense).
-// NF4 split partials (one M tile): K / 1024 splits, two units per wave.
+// NF4 split partials (one M tile): K / 1024 splits, two units per wave, at
+// most one workgroup per CU.
 // NF4 otherwise: the fewest splits that give at least `min_wgs` workgroups
 // (one CU pulls under 1/128 of the HBM bandwidth), keeping every wave at least
 // `min_units` units; at the 7B shapes q/k/v and gate/up get one split (the
@@ -1372,6 +1373,10 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
     // split partials, at most two units per wave: the wave issues all of its
     // loads at once
     S = (p.units + kWaves * nf4_upw - 1) / (kWaves * nf4_upw);
+    // within one round of one workgroup per CU (the 7B down projection: 4
+    // splits of five or six units per wave instead of 11 of two, 256
+    // workgroups instead of 704; 3% of the pass)
+    if (S * p.groups > cu_count() && cu_count() >= p.groups) S = cu_count() / p.groups;
   } else if (nf4) {
     S = (nf4_min_wgs + p.groups - 1) / p.groups;
     const int s_units = p.units / (kWaves * nf4_min_units);
