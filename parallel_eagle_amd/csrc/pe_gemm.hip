@@ -1327,8 +1327,9 @@ struct Plan {
 };
 
 // units: 128-wide K units (NF4) or 64-wide K steps (dense).
-// NF4 split partials (one M tile): K / 1024 splits, two units per wave, at
-// most one workgroup per CU.
+// NF4 split partials: as many splits as one round of one workgroup per CU
+// holds (at least two units per wave); with more column groups than CUs (one
+// M tile) K / 1024 splits, two units per wave.
 // NF4 otherwise: the fewest splits that give at least `min_wgs` workgroups
 // (one CU pulls under 1/128 of the HBM bandwidth), keeping every wave at least
 // `min_units` units; at the 7B shapes q/k/v and gate/up get one split (the
@@ -1369,14 +1370,19 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   p.groups = N / (32 * p.NT);
   p.units = nf4 ? K / 128 : K / 64;
   int S;
-  if (nf4 && p.MT == 1 && epi == kEpiPartial && p.units <= kMaxSplits * kWaves * nf4_upw) {
+  if (nf4 && epi == kEpiPartial && p.groups <= cu_count()) {
+    // split partials: as many splits as fill one round of one workgroup per
+    // CU, each wave at least two units (the 7B o and down projections at 26
+    // and at 64 rows: 4 splits, 256 workgroups; down had 11 splits of two units
+    // per wave, 704 workgroups, at 26 rows and 2 at 64: 3% and 6% of the
+    // passes)
+    S = cu_count() / p.groups;
+    const int s_units = p.units / (kWaves * nf4_min_units);
+    if (S > s_units) S = s_units;
+  } else if (nf4 && p.MT == 1 && epi == kEpiPartial && p.units <= kMaxSplits * kWaves * nf4_upw) {
     // split partials, at most two units per wave: the wave issues all of its
     // loads at once
     S = (p.units + kWaves * nf4_upw - 1) / (kWaves * nf4_upw);
-    // within one round of one workgroup per CU (the 7B down projection: 4
-    // splits of five or six units per wave instead of 11 of two, 256
-    // workgroups instead of 704; 3% of the pass)
-    if (S * p.groups > cu_count() && cu_count() >= p.groups) S = cu_count() / p.groups;
   } else if (nf4) {
     S = (nf4_min_wgs + p.groups - 1) / p.groups;
     const int s_units = p.units / (kWaves * nf4_min_units);
@@ -1409,7 +1415,7 @@ Plan make_plan(int M, int N, int K, bool nf4, int epi) {
   // more or fewer whole groups measured slower in the 7B pass.)
   p.nl = p.tS = p.tpps = 0;
   const int ncu = cu_count();
-  if (nf4 && p.MT == 1 && p.NT == 2 && p.S == 1 && epi != kEpiPartial && nf4_hybrid && p.groups > ncu &&
+  if (nf4 && p.NT == 2 && p.S == 1 && epi != kEpiPartial && nf4_hybrid && p.groups > ncu &&
       p.groups < 2 * ncu && p.units >= 4 * kWaves) {
     p.nl = ncu - nf4_hybrid_less;
     p.tS = nf4_hybrid_ts;
