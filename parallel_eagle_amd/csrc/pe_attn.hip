@@ -493,17 +493,17 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
   }
   // the stores are acknowledged at agent scope before this workgroup counts itself
   __builtin_amdgcn_s_waitcnt(0);
-  // Each workgroup adds kAttnMaxSplits / splits (splits is a power of two), so
-  // a launch adds kAttnMaxSplits to the pair's counter and the workgroup that
-  // brings it to a multiple of kAttnMaxSplits is the last of this launch; the
-  // counter is never reset (wrap-around keeps the multiples).
-  const int inc = kAttnMaxSplits / splits;
+  // Each workgroup adds one to the pair's counter; the one that brings it to
+  // `splits` is the last of this launch and, once it has written the output,
+  // sets it back to zero (every other split has counted itself by then, so
+  // nothing of this launch adds to it again, and the next launch starts after
+  // this one ends; issued last, the store delays none of the combine's loads).
   __shared__ int s_arrived;
   __syncthreads();
   if (threadIdx.x == 0)
-    s_arrived = __hip_atomic_fetch_add(counters + pair, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_arrived = __hip_atomic_fetch_add(counters + pair, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  if (((s_arrived + inc) & (kAttnMaxSplits - 1)) != 0) return;
+  if (s_arrived + 1 != splits) return;
   float Mx = kInitMax, den = 0.f, num[kDimsT];
 #pragma unroll
   for (int k = 0; k < kDimsT; ++k) num[k] = 0.f;
@@ -533,6 +533,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
     }
   }
   write_out(num, den);
+  if (threadIdx.x == 0) __hip_atomic_store(counters + pair, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Batched attention with two row tiles per wave. One workgroup = 4 waves (one
@@ -1200,8 +1201,7 @@ __global__ __launch_bounds__(128) void attn_generic_kernel(
   }
 }
 
-// per-pair arrival counters: zero before first use, multiples of
-// kAttnMaxSplits between launches
+// per-pair arrival counters: zero before first use and between launches
 constexpr int64_t kAttnCounterBytes = 4096;
 
 struct AttnPlan {
@@ -1222,9 +1222,7 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S, int batch = 1) {
   int64_t cap_splits = 256 / pairs;
   if (cap_splits > kAttnMaxSplits) cap_splits = kAttnMaxSplits;
   if (want > cap_splits) want = cap_splits;
-  // a power of two (the arrival count is kept modulo kAttnMaxSplits)
-  int64_t pw = 1;
-  while (pw * 2 <= want) pw *= 2;
+  const int64_t pw = want > 1 ? want : 1;
   int64_t kps = (S + pw - 1) / pw;
   kps = ((kps + 31) / 32) * 32;
   p.keys_per_split = (int)kps;
