@@ -666,7 +666,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(
   const float scale2 = scale * 1.44269504088896341f;  // natural-log scores -> base 2
   const int qg = lane >> 4, jl = lane & 15;
   // online softmax of one tile's 32 keys: returns the packed probabilities
-  auto softmax = [&](f32x16_t& sc, int64_t jb, bool whole, int t, const uint64_t (&nb)[PE_TREE_MAX_WORDS],
+  auto softmax = [&](f32x16_t& sc, int64_t jb, bool whole, const uint64_t (&nb)[PE_TREE_MAX_WORDS],
                      float& m, float& l, f32x16_t (&o)[4], uint32_t (&pb)[8]) {
     float bmax = -INFINITY;
     if (whole) {
@@ -735,8 +735,8 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(
     // a whole 32-key block of prefix keys: every key is visible to every node
     const bool whole = jb + 32 <= min(P, j1);
     uint32_t pbA[8], pbB[8] = {};
-    softmax(scA, jb, whole, tA, nbA, mA, lA, oA, pbA);
-    if constexpr (TWO) softmax(scB, jb, whole, tB, nbB, mB, lB, oB, pbB);
+    softmax(scA, jb, whole, nbA, mA, lA, oA, pbA);
+    if constexpr (TWO) softmax(scB, jb, whole, nbB, mB, lB, oB, pbB);
 #pragma unroll
     for (int c = 0; c < 8; ++c) *(u32x4_t*)&vs[4 * c + (lane >> 4)][(lane & 15) * 8] = vf[c];
     if constexpr (kNext) load_v(jb + 32);

@@ -429,7 +429,6 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   // the dense 14B shapes the partials and one round of workgroups made the
   // pass 7.9% faster than the in-launch exchange).
   float* part = (float*)(ws + Lo.part);
-  const int nqkv = (nh + 2 * nkv) * hd;
   int S = 0;
   for (int l = 0; l < L; ++l) {
     void* kc = (char*)a->k_cache + l * layer_stride;

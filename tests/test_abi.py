@@ -91,3 +91,20 @@ def test_xtile_round_trip():
     t = ops.to_xtile(x)
     assert t.numel() == 64 * 256
     assert torch.equal(ops.from_xtile(t, 40, 256), x)
+
+
+@pytest.mark.parametrize("m", [1, 26, 33, 64])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (4096, 11008), (5120, 13824), (5120, 5120), (32000, 4096)])
+def test_nf4_split_partials_fill_one_round(lib, m, n, k):
+    """Split count of an NF4 split-partial launch, read from its workspace size:
+    as many K splits as one round of one workgroup per CU holds (256 CUs, also
+    the count the library assumes without a device) while every wave keeps at
+    least two 128-wide units; with more 64-column groups than CUs, at least one
+    split."""
+    s, rem = divmod(int(lib.pe_nf4_gemm_partials_bytes(m, n, k)), m * n * 4)
+    assert rem == 0
+    groups, units = n // 64, k // 128
+    if groups <= 256:
+        assert s == max(1, min(256 // groups, units // 8))
+    else:
+        assert 1 <= s <= 16
