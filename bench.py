@@ -67,6 +67,9 @@ def parse_args(argv=None):
     p.add_argument("--prefill", action="store_true",
                    help="instead of the verification pass: time a causal prefill of the workload's prefix length "
                         "from an empty cache and a one-token continuation (eager forward_cached calls)")
+    p.add_argument("--prefill-weights", action="store_true",
+                   help="with --prefill: keep row-major 16-bit copies of the linears on the device "
+                        "(pe_prefill_weights_fill) instead of dequantising them per prefill")
     p.add_argument("--loop", action="store_true",
                    help="tokens/s of the decode loop (greedy and the device-resident speculative loop)")
     p.add_argument("--draft", action="store_true",
@@ -365,7 +368,7 @@ def cpu_baseline(wl, seed, n_layers: int, runs: int):
 
 
 # ---------------------------------------------------------------- main
-def prefill_line(wl, seed: int, reps: int = 3) -> dict:
+def prefill_line(wl, seed: int, reps: int = 3, weight_copy: bool = False) -> dict:
     """Latency of the causal prefill of the workload's prefix (P tokens from an empty
     cache, the prompt step before the first verification) and of a one-token
     continuation (the miss path), eager forward_cached calls after a warm-up call
@@ -377,6 +380,7 @@ def prefill_line(wl, seed: int, reps: int = 3) -> dict:
 
     shape, P = wl.model, wl.prefix_len
     tm = TargetModel.synthetic(shape, seed=seed, device="cuda:0", cache_capacity=P + 64)
+    copy_bytes = tm.model.enable_prefill_weights() if weight_copy else 0
     ids = torch.tensor([synth.uniform_int(seed, synth.STREAM_PROMPT, P, shape.vocab).tolist()])
     pos = torch.arange(P).unsqueeze(0)
     pre, one = [], []
@@ -399,7 +403,7 @@ def prefill_line(wl, seed: int, reps: int = 3) -> dict:
             "ms_prefill": round(ms, 3), "ms_one_token": round(statistics.median(one) * 1e3, 3),
             "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
             "config": {"workload": wl.name, "prefill_tokens": P, "layers": shape.num_layers,
-                       "weights": shape.weight_format, "eager": True}}
+                       "weights": shape.weight_format, "eager": True, "prefill_weight_copy_bytes": copy_bytes}}
 
 
 def loop_line(wl, seed: int, new_tokens: int = 96) -> dict:
@@ -709,7 +713,7 @@ def main(argv=None) -> int:
         return 1
     wl = WORKLOADS[a.workload]
     if a.prefill:
-        print(json.dumps(prefill_line(wl, a.seed)))
+        print(json.dumps(prefill_line(wl, a.seed, weight_copy=a.prefill_weights)))
         return 0
     if a.draft:
         print(json.dumps(draft_line(wl, a.seed)))

@@ -260,6 +260,23 @@ int dequant(const pe_model_desc* m, const void* w, const void* a, int64_t N, int
   return pe_nf4_dequant((const uint8_t*)w, (const uint16_t*)a, N, K, (uint16_t*)out, st);
 }
 
+// The prefill weight copy: per layer q/k/v [nqkv][H], o [H][qd], gate/up
+// [2 ip][H], down [H][ip], row-major 16-bit, layer after layer.
+struct PrefillCopy {
+  int64_t off[4], layer;  // elements
+};
+PrefillCopy prefill_copy_layout(const pe_model_desc* m) {
+  const int64_t H = m->hidden, qd = (int64_t)m->num_heads * m->head_dim;
+  const int64_t nqkv = qd + 2ll * m->num_kv_heads * m->head_dim, ip = m->intermediate_padded;
+  PrefillCopy c;
+  c.off[0] = 0;
+  c.off[1] = c.off[0] + nqkv * H;
+  c.off[2] = c.off[1] + H * qd;
+  c.off[3] = c.off[2] + 2 * ip * H;
+  c.layer = c.off[3] + H * ip;
+  return c;
+}
+
 int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const PrefillLayout& Lp, hipStream_t st) {
   const int M = a->M;
   char* ws = (char*)a->workspace;
@@ -300,7 +317,12 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
     }
     return PE_OK;
   };
-  auto linear = [&](const void* x, int K, const void* w, const void* ab, int N) -> int {
+  const PrefillCopy pc = prefill_copy_layout(m);
+  // `which`: 0 q/k/v, 1 o, 2 gate/up, 3 down of layer l
+  auto linear = [&](const void* x, int K, const void* w, const void* ab, int N, int l, int which) -> int {
+    if (m->prefill_weights)
+      return blas_gemm(st, M, N, K, x, (const uint16_t*)m->prefill_weights + l * pc.layer + pc.off[which], y, bws,
+                       Lp.blas_bytes);
     int r = dequant(m, w, ab, N, K, wdeq, st);
     if (r != PE_OK) return r;
     return blas_gemm(st, M, N, K, x, wdeq, y, bws, Lp.blas_bytes);
@@ -315,19 +337,19 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
   for (int l = 0; l < L; ++l) {
     void* kc = (char*)a->k_cache + l * layer_stride;
     void* vc = (char*)a->v_cache + l * layer_stride;
-    PE_TRY(linear(xn, H, m->w_qkv[l], m->a_qkv[l], nqkv));
+    PE_TRY(linear(xn, H, m->w_qkv[l], m->a_qkv[l], nqkv, l, 0));
     PE_TRY(pe_internal_rope_kv_partials(y, 1, M, nh, nkv, hd, m->b_qkv ? m->b_qkv[l] : nullptr, a->positions,
                                         m->rope_cos_sin, m->max_positions, q, kc, vc, a->cache_capacity,
                                         a->prefix_len, a->status, m->dtype, st));
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, PE_MASK_CAUSAL,
                                       nullptr, 0, scale, m->dtype, attn, qd, 0, ws + Lp.attn_ws, Lp.attn_ws_bytes,
                                       (int*)(ws + Lp.gemm) + kPassAttnCounterInt, st, m->attn_mode));
-    PE_TRY(linear(attn, qd, m->w_o[l], m->a_o[l], H));
+    PE_TRY(linear(attn, qd, m->w_o[l], m->a_o[l], H, l, 1));
     PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, nullptr, nullptr, 0,
                                         nullptr, 0, st));
-    PE_TRY(linear(xn, H, m->w_gu[l], m->a_gu[l], 2 * ip));
+    PE_TRY(linear(xn, H, m->w_gu[l], m->a_gu[l], 2 * ip, l, 2));
     PE_TRY(pe_internal_swiglu_partials(y, 1, M, 2 * ip, act, ip, 0, m->dtype, st));
-    PE_TRY(linear(act, ip, m->w_down[l], m->a_down[l], H));
+    PE_TRY(linear(act, ip, m->w_down[l], m->a_down[l], H, l, 3));
     const bool last = l + 1 == L;
     const int fh = last ? -1 : slot_of(l + 1);
     const int fx = last ? slot_of(L) : -1;
@@ -339,6 +361,31 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
   }
   if (a->logits) PE_TRY(lm_head(m, a, xn, M, ws + Lp.gemm, Lp.gemm_bytes, st));
 #undef PE_TRY
+  return PE_OK;
+}
+
+extern "C" int64_t pe_prefill_weights_bytes(const pe_model_desc* m) {
+  if (!m || m->num_layers <= 0 || m->dtype == PE_DTYPE_F32) return 0;
+  return prefill_copy_layout(m).layer * m->num_layers * 2;
+}
+
+extern "C" int pe_prefill_weights_fill(const pe_model_desc* m, void* out, int64_t bytes, void* stream) {
+  if (!m || !out || m->num_layers <= 0 || m->dtype == PE_DTYPE_F32) return PE_ERR_ARG;
+  if (bytes < pe_prefill_weights_bytes(m)) return PE_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  const PrefillCopy pc = prefill_copy_layout(m);
+  const int64_t H = m->hidden, qd = (int64_t)m->num_heads * m->head_dim;
+  const int64_t nqkv = qd + 2ll * m->num_kv_heads * m->head_dim, ip = m->intermediate_padded;
+  const int64_t N[4] = {nqkv, H, 2 * ip, H}, K[4] = {H, qd, H, ip};
+  for (int l = 0; l < m->num_layers; ++l) {
+    const void* w[4] = {m->w_qkv[l], m->w_o[l], m->w_gu[l], m->w_down[l]};
+    const void* ab[4] = {m->a_qkv ? m->a_qkv[l] : nullptr, m->a_o ? m->a_o[l] : nullptr,
+                         m->a_gu ? m->a_gu[l] : nullptr, m->a_down ? m->a_down[l] : nullptr};
+    for (int i = 0; i < 4; ++i) {
+      const int rc = dequant(m, w[i], ab[i], N[i], K[i], (uint16_t*)out + l * pc.layer + pc.off[i], st);
+      if (rc != PE_OK) return rc;
+    }
+  }
   return PE_OK;
 }
 

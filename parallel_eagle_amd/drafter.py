@@ -92,6 +92,11 @@ class DeviceDrafter:
         core.norm_mode = _lib.PE_NORM_FP32_WEIGHT
         core.attn_mode = _lib.PE_ATTN_EAGER
         core._finish()
+        if dt == torch.bfloat16:
+            # context passes of more than 256 rows multiply row-major copies of
+            # the layer weights (2 bytes per weight) instead of untiling every
+            # linear per call
+            core.enable_prefill_weights()
         self.core = core
         self.runner = TargetModel(core, cache_capacity=capacity)
         self.cache = TreeKVCache(self.shape, dt, dev, capacity)

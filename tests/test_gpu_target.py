@@ -232,6 +232,31 @@ def test_llama7b_nf4_width_prefill_longer_than_a_chunk(P):
     print(f"P={P}: {v}, accepted {n}, max |dlogit| {err:.3g}")
 
 
+@pytest.mark.parametrize("shape", [LLAMA2_7B_NF4.reduced(2),
+                                   replace(QWEN25_14B_FP16.reduced(1, vocab=16384), dtype="bfloat16")],
+                         ids=["nf4", "dense-bf16"])
+def test_prefill_weight_copy_gives_the_same_prefill(shape):
+    """pe_prefill_weights_fill keeps every linear as a row-major 16-bit copy and
+    the prefill multiplies it instead of dequantising (NF4) or untiling (dense)
+    per call: the same bf16 / fp16 operands, so the logits and the K/V rows the
+    prefill appends are bit-identical to a prefill without the copy."""
+    P = 300
+    tm = TargetModel.synthetic(shape, seed=3, device=DEV, cache_capacity=P + 8)
+    ids = torch.tensor([synth.uniform_int(3, synth.STREAM_PROMPT, P, shape.vocab).tolist()])
+    pos = torch.arange(P).unsqueeze(0)
+    c1 = tm.make_cache(P + 8)
+    l1, _, c1 = tm.forward_cached(ids, c1, pos)
+    nbytes = tm.model.enable_prefill_weights()
+    s = shape
+    per_weight = ((s.num_heads + 2 * s.num_kv_heads) * s.head_dim + s.num_heads * s.head_dim) * s.hidden \
+        + 3 * tm.model.ipad * s.hidden
+    assert nbytes == 2 * per_weight * s.num_layers
+    c2 = tm.make_cache(P + 8)
+    l2, _, c2 = tm.forward_cached(ids, c2, pos)
+    assert torch.equal(l1, l2)
+    assert torch.equal(c1.k[..., :P, :], c2.k[..., :P, :]) and torch.equal(c1.v[..., :P, :], c2.v[..., :P, :])
+
+
 def test_llama7b_nf4_width_long_random_prefix():
     wl = WORKLOADS["llama2-7b-nf4-T26-P2048"]
     shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
