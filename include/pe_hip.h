@@ -415,8 +415,9 @@ int64_t pe_forward_batch_workspace_bytes(const pe_model_desc* m, int M, int max_
  * (src/pe/target.py:203-224 -> HF LlamaForCausalLM / Qwen2ForCausalLM forward,
  * modeling_llama.py:347-490): embeddings, L decoder layers with in-place KV
  * append, final norm, lm_head over all M rows, fused features.
- * A causal pass of more than 256 rows on an NF4 model (a prefill) dequantises
- * each linear once and multiplies it with rocBLAS (bf16, fp32 accumulation);
+ * A causal pass of more than 256 rows of a bf16 model, NF4 or dense (a
+ * prefill), dequantises or untiles each linear once (or reads the copy at
+ * m->prefill_weights) and multiplies it with rocBLAS (bf16, fp32 accumulation);
  * rocBLAS gets its workspace from the pass workspace, and the library keeps one
  * rocBLAS handle per device, made on the first such pass (the handle's own
  * state is rocBLAS's). Set PE_PREFILL_GEMM=0 to run such passes in 64-row
