@@ -87,7 +87,7 @@ PE_INTERNAL int pe_internal_embed_rmsnorm(const int64_t* ids, int M, const void*
 // The pass workspace's first 32 KiB hold arrival counters: GEMM column
 // groups use ints [0, kGemmCounterInts) and return them to zero; attention
 // (head, row tile) pairs use the 1024 ints from kPassAttnCounterInt on, which
-// stay multiples of 16.
+// the last workgroup of each pair also returns to zero.
 constexpr int kGemmCounterInts = 7168;
 constexpr int kPassAttnCounterInt = 7168;
 

@@ -179,8 +179,8 @@ PrefillLayout make_prefill_layout(const pe_model_desc* m, int M, int64_t kv_len)
   const int64_t H = m->hidden, qd = (int64_t)m->num_heads * m->head_dim;
   const int64_t nqkv = qd + 2ll * m->num_kv_heads * m->head_dim, ip = m->intermediate_padded;
   // offset 0: the pass's counters and the lm_head GEMM's workspace, as in the
-  // fused layout (the GEMM and attention counter slices rest at zero or at
-  // multiples of 16 between passes, whichever path ran last)
+  // fused layout (the GEMM and attention counter slices rest at zero between
+  // passes, whichever path ran last)
   L.gemm = 0;
   L.gemm_bytes = align_up(std::max<int64_t>(
       kCounterBytes, pe_gemm_workspace_bytes(kFusedChunk, m->vocab, m->hidden, PE_WFMT_DENSE, m->dtype, PE_EPI_STORE)));
