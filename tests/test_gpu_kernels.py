@@ -206,6 +206,30 @@ def test_dense_linear_epilogues(dtype, epi):
     assert torch.allclose(y.float(), ref.float(), rtol=tol, atol=tol), (y.float() - ref.float()).abs().max()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [26, 40])
+def test_dense_swiglu_at_the_14b_shape(dtype, m):
+    """The dense gate/up at the Qwen2.5-14B shape (K = 5120, 2 x 13824 columns:
+    432 column groups, between one and two per CU, one unsplit launch).
+    Every column against the fp32 product with HF LlamaMLP's rounding points
+    (modeling_llama.py:174-176: gate and up rounded, silu rounded, the product
+    rounded) within a few 16-bit ulps, and equal for almost every column."""
+    n, k = 2 * 13824, 5120
+    w = torch.from_numpy(synth.normal(5, 44, n * k, 0.02).reshape(n, k)).to(dtype)
+    x = torch.from_numpy(synth.normal(6, 45, m * k, 1.0).reshape(m, k)).to(dtype)
+    g, u = w[: n // 2], w[n // 2:]
+    inter = torch.stack([g.view(-1, 32, k), u.view(-1, 32, k)], 1).reshape(n, k).contiguous()
+    y = ops.linear(x.to(DEV), n, dense=ops.dense_repack(inter.to(DEV)), epilogue=_lib.PE_EPI_SWIGLU).cpu().float()
+    gf = (x.float() @ g.float().t()).to(dtype)
+    uf = (x.float() @ u.float().t()).to(dtype)
+    ref = (torch.nn.functional.silu(gf.float()).to(dtype).float() * uf.float()).to(dtype).float()
+    err = (y - ref).abs()
+    # the fp32 accumulation order may move a rounding of gate or up by one
+    # 16-bit ulp, which moves the output by a few ulps of itself at most
+    assert torch.all(err <= 4 * torch.finfo(dtype).eps * ref.abs() + 1e-3), err.max()
+    assert float((err > 0).float().mean()) < 0.02
+
+
 # ------------------------------------------------------------------ masks
 TREES = [
     [-1, 0, -1],
