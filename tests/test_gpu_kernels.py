@@ -108,7 +108,7 @@ def test_nf4_linear_tiled_x_equals_row_major(m, epi):
     assert torch.equal(got, ref)
 
 
-@pytest.mark.parametrize("m", [1, 26, 32])
+@pytest.mark.parametrize("m", [1, 26, 32, 48, 64])
 @pytest.mark.parametrize("n,k", [(12288, 4096), (8192, 1024), (16384, 512), (22016, 4096), (20480, 1024),
                                  (24576, 2560)])
 def test_nf4_tiled_unsplit_wide_workgroups(m, n, k):
