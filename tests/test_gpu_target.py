@@ -286,13 +286,16 @@ def test_qwen14b_width_one_layer(shape):
 
 @pytest.mark.parametrize("shape,P,plant", [(WORKLOADS["tiny-fp32-T8-P64"].model, 64, 2),
                                            (LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2)), 300, 2),
-                                           (LLAMA2_7B_NF4, 2048, 5)],
-                         ids=["tiny-fp32", "llama7b-nf4-2layers", "llama7b-nf4-32layers-P2048"])
+                                           (LLAMA2_7B_NF4, 2048, 5),
+                                           (QWEN25_14B_FP16.reduced(1, vocab=16384), 1200, 2)],
+                         ids=["tiny-fp32", "llama7b-nf4-2layers", "llama7b-nf4-32layers-P2048",
+                              "qwen14b-fp16-1layer-P1200"])
 def test_verify_step_graph_replays_match_eager_api(shape, P, plant):
     """The device-resident step (masks -> forward -> acceptance -> compaction),
     eager and replayed from a HIP graph, equals forward_cached + accept_tree_cached
     + gather_cache on the same inputs, bit for bit, on every replay with eager
-    work in between. The full 32-layer 7B model (the benchmark's workload, too
+    work in between (the GQA case: two row tiles per KV head in 5 key splits,
+    whose arrival counters return to zero after every launch). The full 32-layer 7B model (the benchmark's workload, too
     deep for the CPU oracle) is held to properties: every logit finite, and a
     chain of the device's own greedy tokens planted to the tree's full depth is
     accepted to that depth with the greedy bonus."""
