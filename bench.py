@@ -253,8 +253,8 @@ def nf4_gemm_roofline(tm, wl, reps: int):
     per_layer = sum(nf4_bytes(n, k) + 2 * M * k + 2 * M * n for n, k in ((nqkv, H), (H, qd), (2 * I, H), (H, I)))
     bytes_per_launch = per_layer * s.num_layers / launches
     gbs = bytes_per_launch / (mean_us * 1e-6) / 1e9
-    return {"kernel": "nf4_gemm_kernel (A-tiled X; q/k/v and gate/up unsplit, o and down fp32 split partials: "
-                      "the 4 x L launches of one pass)",
+    return {"kernel": "nf4_gemm_kernel (A-tiled X; q/k/v unsplit, gate/up as whole column groups plus halves, "
+                      "o and down fp32 split partials in one round of workgroups: the 4 x L launches of one pass)",
             "mean_launch_us": round(mean_us, 3), "bytes_per_launch": int(bytes_per_launch),
             "achieved": round(gbs, 1)}
 
