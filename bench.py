@@ -409,9 +409,10 @@ def prefill_line(wl, seed: int, reps: int = 3, weight_copy: bool = False) -> dic
 def loop_line(wl, seed: int, new_tokens: int = 96) -> dict:
     """Tokens/s of the whole decode loop on the workload's model (synthetic
     weights, all layers) over a P-token random prompt: greedy decoding through
-    the reference-shaped API (vanilla_generate_cached, one forward per token)
-    and the device-resident speculative loop (SpeculativeDecoder: drafter,
-    device beam, verification pass, walk, compaction, one host read per step)
+    forward_cached (greedy_decode, one one-token pass per token) and the
+    device-resident speculative loop (SpeculativeDecoder: drafter, device beam,
+    then one recorded step replayed: masks, verification pass, walk,
+    compaction, commit; one host read per step)
     with (a) a random 2-layer device drafter (nothing is accepted: every step
     is the miss path) and (b) the same drafter told the greedy continuation
     (every depth the greedy decode chose). Each run reports whether it emitted
@@ -424,7 +425,7 @@ def loop_line(wl, seed: int, new_tokens: int = 96) -> dict:
 
     from parallel_eagle_amd import synth
     from parallel_eagle_amd.drafter import DeviceDrafter
-    from parallel_eagle_amd.serve import SpeculativeDecoder, vanilla_generate_cached
+    from parallel_eagle_amd.serve import SpeculativeDecoder, greedy_decode
     from parallel_eagle_amd.target import TargetModel
     from parallel_eagle_amd.tree import beam_width
 
@@ -456,6 +457,18 @@ def loop_line(wl, seed: int, new_tokens: int = 96) -> dict:
 
         def __init__(self, inner, greedy):
             self.inner, self.greedy = inner, greedy
+            self.status = inner.status
+
+        @property
+        def sync_status(self):
+            return self.inner.sync_status
+
+        @sync_status.setter
+        def sync_status(self, v):
+            self.inner.sync_status = v
+
+        def reset(self):
+            self.inner.reset()
 
         def draft_logits(self, ctx, feats, kk):
             return self._hint(self.inner.draft_logits(ctx, feats, kk), ctx, kk)
@@ -472,21 +485,24 @@ def loop_line(wl, seed: int, new_tokens: int = 96) -> dict:
                     lg[d, self.greedy[n + d]] = 30.0
             return lg
 
-    vanilla_generate_cached(tm, prompt, 4)  # warm-up (kernel loads, caches)
+    greedy_decode(tm, prompt, 4)  # warm-up (kernel loads, caches)
     torch.cuda.synchronize()
-    greedy = vanilla_generate_cached(tm, prompt, new_tokens)
-    full = prompt + greedy.output_ids
+    greedy = greedy_decode(tm, prompt, new_tokens)
+    full = prompt + greedy.tokens
     runs = {}
     for name, dr in (("random_drafter", drafter), ("greedy_hint_drafter", GreedyHint(drafter, full))):
         dec = SpeculativeDecoder(tm, dr, k=k, tree_top_k=top_k, tree_max_nodes=max_nodes)
         dec.generate(prompt, 8)  # warm-up
         res = dec.generate(prompt, new_tokens)
-        same = res.output_ids == greedy.output_ids
-        first = next((i for i, (x, y) in enumerate(zip(res.output_ids, greedy.output_ids)) if x != y), None)
+        same = res.tokens == greedy.tokens
+        first = next((i for i, (x, y) in enumerate(zip(res.tokens, greedy.tokens)) if x != y), None)
         runs[name] = {"tokens_per_s": round(res.tokens_per_second, 1), "steps": res.steps,
-                      "tokens_per_step": round(res.acceptance_length, 3), "target_calls": res.target_calls,
+                      "ms_per_step": round(res.seconds * 1e3 / max(1, res.steps), 3),
+                      "tokens_per_step": round(res.tokens_per_step, 3), "target_passes": res.target_passes,
+                      "host_reads": res.host_reads, "recorded_steps": dec.device_prefix,
                       "equal_to_greedy": same, "first_difference": first}
-        log(f"loop ({name}): {res.tokens_per_second:.1f} tokens/s, {res.acceptance_length:.2f} tokens per step, "
+        log(f"loop ({name}): {res.tokens_per_second:.1f} tokens/s, {res.tokens_per_step:.2f} tokens per step, "
+            f"{runs[name]['ms_per_step']} ms per step, {res.host_reads} host reads in {res.steps} steps, "
             f"equal to greedy decoding: {same}" + ("" if same else f" (first difference at token {first})"))
     log(f"greedy decoding through the same API: {greedy.tokens_per_second:.1f} tokens/s")
     best = runs["greedy_hint_drafter"]

@@ -330,6 +330,36 @@ int pe_propose_tree(const void* logits, int64_t ld, int k, int64_t V, int dtype,
                     int64_t* node_tokens, int32_t* parents, int32_t* n_nodes, void* scratch, int32_t* status,
                     void* stream);
 
+/* ------------------------------------------------------------ decode loop */
+/* The bookkeeping that ends one step of the reference's one-forward tree loop
+ * (src/pe/serve.py:305-343: the accepted path's features appended with
+ * torch.cat, the tokens emitted, root_logit re-rooted, the pending bonus),
+ * kept in device memory so that a recorded step needs no host value:
+ * state (int64 [2]) = {P: tokens cached and featurised, the pending bonus};
+ * ids (int64 [cap]) the context tokens with the pending one at ids[P]; feats
+ * ([cap][feat_dim] in dtype) their fused features; root ([V]) the logit row
+ * that predicted ids[P]. With a walk's result [n, bonus, path...]
+ * (pe_accept_tree*): feats / ids rows P + i take node path[i]'s fused row and
+ * token (i < n), root takes node path[n-1]'s logit row, ids[P + n] = bonus
+ * becomes pending and P += n; n == 0 changes nothing (the caller then runs the
+ * one-node miss pass of serve.py:315-328 and pe_loop_miss_commit). rec (int32,
+ * read by the host once per step): rec[0] = n, rec[1] = bonus, rec[2] |= the
+ * status words given (each cleared; NULL entries skipped), rec[4 + i] (i <
+ * rec_path) the accepted tokens, -1 past n. */
+#define PE_LOOP_REC_HEAD 4
+int pe_loop_commit(const int32_t* accept_out, int T, const int64_t* node_tokens, const void* node_fused,
+                   int feat_dim, const void* node_logits, int64_t V, int dtype, void* feats, int64_t* ids,
+                   void* root, int64_t cap, int64_t* state, int32_t* rec, int rec_path, int32_t* status0,
+                   int32_t* status1, int32_t* status2, void* stream);
+/* After the miss pass (the pending token at position P, its logit row written
+ * to root): feats row P takes its fused row, its argmax (from the lm_head's
+ * argmax keys [groups], or from row_argmax[0] as pe_argmax_rows wrote it:
+ * exactly one of the two) becomes the pending bonus at ids[P + 1], P += 1;
+ * rec[3] = that bonus, rec[2] |= the status words. */
+int pe_loop_miss_commit(const void* fused_row, int feat_dim, const uint64_t* keys, int groups,
+                        const int32_t* row_argmax, int dtype, void* feats, int64_t* ids, int64_t cap, int64_t* state,
+                        int32_t* rec, int32_t* status0, int32_t* status1, int32_t* status2, void* stream);
+
 /* ---------------------------------------------------------------- whole pass */
 typedef struct pe_model_desc {
   int32_t num_layers, hidden, num_heads, num_kv_heads, head_dim, intermediate, vocab;
@@ -392,16 +422,24 @@ typedef struct pe_pass_args {
    * with seq_prefix[b] rows cached (device int64 [batch]); tree_bits of a row
    * name nodes of its own sequence (pe_tree_masks_batch). prefix_len is the
    * largest seq_prefix and max_seq_rows the largest row count: they size the
-   * launches. A row's K/V land at its sequence's rows [prefix, prefix + rows).
-   * 16-bit models with hd 128 and RoPE-paired q/k/v, PE_MASK_TREE. */
+   * launches; a sequence whose device prefix or row count exceeds them sets
+   * PE_ERR_CAPACITY / PE_ERR_TREE in status and is skipped (no K/V written,
+   * no key read past the bounds). A row's K/V land at its sequence's rows
+   * [prefix, prefix + rows). 16-bit models with hd 128 and RoPE-paired q/k/v,
+   * PE_MASK_TREE. batch == 1 with M <= 64 rows (max_seq_rows == M) runs the
+   * single-sequence pass with its prefix read from seq_prefix[0] on the
+   * device: one recorded launch sequence (a HIP graph) serves every prefix up
+   * to prefix_len, and for seq_prefix[0] == prefix_len the result equals the
+   * batch == 0 pass bit for bit. */
   int32_t batch;
   int32_t max_seq_rows;
   const int32_t* seq_row0;
   const int64_t* seq_prefix;
   int64_t cache_seq_stride;
-  /* Optional (single-sequence 16-bit passes with logits): the lm_head also
-   * writes each row's argmax keys, [M][pe_dense_gemm_argmax_groups(M, vocab,
-   * hidden)] (see pe_dense_gemm_argmax), for pe_accept_tree_keys. NULL: none. */
+  /* Optional (single-sequence 16-bit passes of at most 64 rows with logits,
+   * batch 0 or 1): the lm_head also writes each row's argmax keys,
+   * [M][pe_dense_gemm_argmax_groups(M, vocab, hidden)] (see
+   * pe_dense_gemm_argmax), for pe_accept_tree_keys. NULL: none. */
   uint64_t* node_keys;
 } pe_pass_args;
 

@@ -36,6 +36,7 @@ PE_ATTN_SDPA, PE_ATTN_EAGER = 0, 1
 PE_TREE_MAX_WORDS = 4
 PE_PROPOSE_MAX_DEPTH, PE_PROPOSE_MAX_WIDTH, PE_PROPOSE_SCRATCH_PER_DEPTH = 16, 64, 512
 PE_ACCEPT_NOALLOC_MAX_NODES = 64 * PE_TREE_MAX_WORDS
+PE_LOOP_REC_HEAD = 4
 
 _ERR_NAMES = {
     PE_ERR_ARG: "invalid argument",
@@ -148,6 +149,9 @@ SIGNATURES: dict[str, tuple] = {
     "pe_accept_tree_batch": (C.c_int, [vp, i64, vp, i64, i64, C.c_int, vp, C.c_int, C.c_int, vp, vp, vp, vp, vp]),
     "pe_kv_compact_batch": (C.c_int, [vp, vp, C.c_int, i64, C.c_int, C.c_int, i64, C.c_int, C.c_int, vp, vp,
                                       C.c_int, vp]),
+    "pe_loop_commit": (C.c_int, [vp, C.c_int, vp, vp, C.c_int, vp, i64, C.c_int, vp, vp, vp, i64, vp, vp, C.c_int,
+                                 vp, vp, vp, vp]),
+    "pe_loop_miss_commit": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, C.c_int, vp, vp, i64, vp, vp, vp, vp, vp, vp]),
 }
 
 _lib = None

@@ -25,6 +25,7 @@ SOURCES = [
     "pe_elem.hip",
     "pe_attn.hip",
     "pe_tree.hip",
+    "pe_loop.hip",
     "pe_model.cpp",
 ]
 

@@ -95,11 +95,19 @@ constexpr int64_t kAttnMaxCap = int64_t(1) << 24;
 // and out, its keys the seq_prefix[b] cached rows plus its own node rows of
 // the cache at kc / vc + b * seq_stride. Row tiles past a sequence's rows
 // leave at once (all splits of such a tile alike, so no arrival is awaited).
+// A sequence whose device prefix or row count exceeds the bounds the launch
+// was sized for (max_prefix, max_rows) is skipped by every workgroup alike
+// (the K/V offsets kernel reports it), so no key past them is read. With
+// dyn_split the key splits of a sequence cover its own P + T keys
+// (round32(ceil((P + T) / splits)) each), the split count fixed by the launch.
 struct AttnBatch {
   int batch, row_tiles;
   const int32_t* seq_row0;
   const int64_t* seq_prefix;
   int64_t seq_stride;  // elements
+  int64_t max_prefix;
+  int max_rows;
+  int dyn_split;
 };
 
 template <int DT>
@@ -144,7 +152,8 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_wg_kernel(
     rbase = bt.seq_row0[seq];
     T = bt.seq_row0[seq + 1] - rbase;
     P = bt.seq_prefix[seq];
-    if (rt * 32 >= T * (nh / nkv) || T <= 0) return;
+    if (rt * 32 >= T * (nh / nkv) || T <= 0 || T > bt.max_rows || P < 0 || P > bt.max_prefix) return;
+    if (bt.dyn_split) keys_per_split = (int)((((P + T) + splits - 1) / splits + 31) / 32 * 32);
     q += (int64_t)rbase * nh * 128;
     bits += (int64_t)rbase * words;
     kc += seq * bt.seq_stride;
@@ -587,7 +596,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(
   const int64_t P = bt.seq_prefix[seq];
   const int G = nh / nkv, rows = T * G;
   const int rtA = 2 * tp, rtB = 2 * tp + 1;
-  if (T <= 0 || rtA * 32 >= rows) return;
+  if (T <= 0 || rtA * 32 >= rows || T > bt.max_rows || P < 0 || P > bt.max_prefix) return;
   const bool two = rtB * 32 < rows;  // workgroup-uniform: one body per case
   auto body = [&](auto two_c) {
   constexpr bool TWO = decltype(two_c)::value;
@@ -1276,12 +1285,12 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
       attn_wg_kernel<PE_DTYPE_BF16><<<grid, 64 * kAttnWaves, 0, st>>>(
           (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P, mask_mode,
           bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters, out, ld_out, out_units,
-          AttnBatch{0, 0, nullptr, nullptr, 0});
+          AttnBatch{0, 0, nullptr, nullptr, 0, 0, 0, 0});
     } else if (dtype == PE_DTYPE_F16) {
       attn_wg_kernel<PE_DTYPE_F16><<<grid, 64 * kAttnWaves, 0, st>>>(
           (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P, mask_mode,
           bits, words, scale, p.keys_per_split, p.splits, p.rows_pad, opart, ml, counters, out, ld_out, out_units,
-          AttnBatch{0, 0, nullptr, nullptr, 0});
+          AttnBatch{0, 0, nullptr, nullptr, 0, 0, 0, 0});
     } else {
       return PE_ERR_ARG;
     }
@@ -1340,7 +1349,8 @@ int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const v
                                      int64_t seq_stride, int nh, int nkv, int max_rows, int64_t max_prefix, int batch,
                                      const int32_t* seq_row0, const int64_t* seq_prefix, const uint64_t* bits,
                                      int words, float scale, int dtype, void* out, int64_t ld_out, int out_units,
-                                     void* workspace, int64_t workspace_bytes, int* counters, hipStream_t st) {
+                                     void* workspace, int64_t workspace_bytes, int* counters, hipStream_t st,
+                                     int dyn_split) {
   if (!q || !k_cache || !v_cache || !out || !workspace || !seq_row0 || !seq_prefix || !bits) return PE_ERR_ARG;
   if (dtype == PE_DTYPE_F32 || batch <= 0 || max_rows <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || max_prefix < 0)
     return PE_ERR_ARG;
@@ -1355,7 +1365,7 @@ int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const v
   if (!counters) counters = (int*)workspace;
   float* opart = (float*)((char*)workspace + kAttnCounterBytes);
   float* ml = (float*)((char*)workspace + kAttnCounterBytes + p.opart_bytes);
-  const AttnBatch bt{batch, p.row_tiles, seq_row0, seq_prefix, seq_stride};
+  const AttnBatch bt{batch, p.row_tiles, seq_row0, seq_prefix, seq_stride, max_prefix, max_rows, dyn_split};
   const int tpairs = (p.row_tiles + 1) / 2;
   if (p.row_tiles >= 2 && (int64_t)batch * nkv * tpairs >= 128) {
     // two row tiles per wave: each K/V block read once for both

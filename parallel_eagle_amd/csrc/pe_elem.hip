@@ -302,22 +302,30 @@ extern "C" int pe_embed(const int64_t* ids, int M, const void* table, int64_t V,
 }
 
 __global__ void kv_offsets_kernel(const int32_t* __restrict__ seq_row0, const int64_t* __restrict__ seq_prefix,
-                                  int batch, int M, int64_t seq_stride, int64_t cap, int hd, int64_t* __restrict__ off,
-                                  int32_t* status) {
+                                  int batch, int M, int64_t seq_stride, int64_t cap, int hd, int64_t max_prefix,
+                                  int max_rows, int64_t* __restrict__ off, int32_t* status) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= M) return;
   int b = 0;
   while (b + 1 < batch && seq_row0[b + 1] <= r) ++b;
-  const int64_t slot = seq_prefix[b] + (r - seq_row0[b]);
-  const bool ok = r >= seq_row0[b] && r < seq_row0[b + 1] && seq_prefix[b] >= 0 && slot < cap;
-  if (!ok && status) atomicOr(status, PE_ERR_CAPACITY);
+  const int64_t pre = seq_prefix[b];
+  const int rows = seq_row0[b + 1] - seq_row0[b];
+  const int64_t slot = pre + (r - seq_row0[b]);
+  // the launches were sized for prefixes up to max_prefix and max_rows rows
+  // per sequence: a sequence beyond either is not appended (and attention
+  // skips it)
+  const bool fits = pre >= 0 && pre <= max_prefix && rows <= max_rows;
+  const bool ok = fits && r >= seq_row0[b] && r < seq_row0[b + 1] && slot < cap;
+  if (!ok && status) atomicOr(status, rows > max_rows ? PE_ERR_TREE : PE_ERR_CAPACITY);
   off[r] = ok ? b * seq_stride + slot * hd : -1;
 }
 
 int pe_internal_kv_offsets(const int32_t* seq_row0, const int64_t* seq_prefix, int batch, int M, int64_t seq_stride,
-                           int64_t cap, int hd, int64_t* off, int32_t* status, hipStream_t st) {
+                           int64_t cap, int hd, int64_t max_prefix, int max_rows, int64_t* off, int32_t* status,
+                           hipStream_t st) {
   if (!seq_row0 || !seq_prefix || !off || batch <= 0 || M <= 0) return PE_ERR_ARG;
-  kv_offsets_kernel<<<(M + 255) / 256, 256, 0, st>>>(seq_row0, seq_prefix, batch, M, seq_stride, cap, hd, off, status);
+  kv_offsets_kernel<<<(M + 255) / 256, 256, 0, st>>>(seq_row0, seq_prefix, batch, M, seq_stride, cap, hd, max_prefix,
+                                                     max_rows, off, status);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }

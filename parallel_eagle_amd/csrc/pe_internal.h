@@ -106,8 +106,14 @@ PE_INTERNAL int64_t attention_workspace_bytes(int T, int nh, int nkv, int hd, in
 // pe_attn.hip: tree attention of `batch` sequences in one launch (16-bit,
 // hd == 128): sequence b's query rows are [seq_row0[b], seq_row0[b+1]) of q,
 // bits and out (row-major), its cache kc / vc + b * seq_stride elements with
-// seq_prefix[b] cached rows; max_prefix and max_rows size the launch; with
-// out_units > 0 out is A-tiled over all rows (K = 128 * out_units).
+// seq_prefix[b] cached rows; max_prefix and max_rows size the launch (a
+// sequence whose device prefix or row count exceeds them is skipped: no key is
+// read past them, and pe_internal_kv_offsets reports it); with out_units > 0
+// out is A-tiled over all rows (K = 128 * out_units). dyn_split: each
+// sequence's key splits cover its own prefix + rows (round32(ceil(S / splits))
+// keys each, the split count fixed by the launch), so a launch sized for a
+// longer prefix than the device holds keeps its splits balanced, and a
+// single sequence gets the key ranges pe_internal_tree_attention gives it.
 PE_INTERNAL int64_t pe_internal_attention_batch_bytes(int max_rows, int nh, int nkv, int64_t max_kv_len, int batch);
 PE_INTERNAL int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const void* v_cache,
                                                  int64_t cache_cap, int64_t seq_stride, int nh, int nkv, int max_rows,
@@ -115,13 +121,16 @@ PE_INTERNAL int pe_internal_tree_attention_batch(const void* q, const void* k_ca
                                                  const int64_t* seq_prefix, const uint64_t* bits, int words,
                                                  float scale, int dtype, void* out, int64_t ld_out, int out_units,
                                                  void* workspace, int64_t workspace_bytes, int* counters,
-                                                 hipStream_t st);
+                                                 hipStream_t st, int dyn_split = 0);
 // pe_elem.hip: per-row K/V slot offsets of a batched pass (see EpiArgs::kv_off):
 // off[r] = b * seq_stride + (seq_prefix[b] + r - seq_row0[b]) * hd for row r of
-// sequence b, or -1 (and PE_ERR_CAPACITY in *status) past the sequence's cache.
+// sequence b, or -1 (and PE_ERR_CAPACITY in *status) past the sequence's cache
+// or when seq_prefix[b] exceeds max_prefix (the bound the launches were sized
+// for); a sequence of more than max_rows rows sets PE_ERR_TREE and drops its
+// rows' K/V.
 PE_INTERNAL int pe_internal_kv_offsets(const int32_t* seq_row0, const int64_t* seq_prefix, int batch, int M,
-                                       int64_t seq_stride, int64_t cap, int hd, int64_t* off, int32_t* status,
-                                       hipStream_t st);
+                                       int64_t seq_stride, int64_t cap, int hd, int64_t max_prefix, int max_rows,
+                                       int64_t* off, int32_t* status, hipStream_t st);
 
 // MFMA-tiled 16-bit weights [N][K] back to row-major (the inverse of pe_dense_repack)
 int pe_internal_dense_untile(const void* tiled, int64_t N, int64_t K, void* out, hipStream_t st);

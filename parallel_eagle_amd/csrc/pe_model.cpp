@@ -44,6 +44,7 @@ struct Layout {
   int64_t h, xn, qkv, q, attn, act, attn_ws, attn_ws_bytes;
   int64_t xn_t, attn_t, act_t;  // A-tiled GEMM inputs of the fused NF4 pass
   int64_t part, part_bytes;      // split partials of the fused NF4 pass's GEMMs
+  int64_t kvoff;                 // per-row K/V slots of a pass whose prefix is read on the device
   int64_t total;
 };
 
@@ -108,6 +109,8 @@ Layout make_layout(const pe_model_desc* m, int M, int64_t kv_len) {
   L.attn_ws_bytes = align_up(attention_workspace_bytes(M, m->num_heads, m->num_kv_heads, m->head_dim, kv_len,
                                                        m->dtype, m->attn_mode));
   off += L.attn_ws_bytes;
+  L.kvoff = off;
+  off += align_up((int64_t)M * 8);
   L.total = off;
   return L;
 }
@@ -439,12 +442,21 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   const float scale = (float)(1.0 / std::sqrt((double)hd));
   const int64_t layer_stride = (int64_t)nkv * a->cache_capacity * hd * es;
   const int64_t fused_ld = (int64_t)a->num_features * H;  // elements
+  // A batch of one: the sequence's prefix P is read on the device
+  // (seq_prefix[0]); a->prefix_len bounds it and sizes the launches. K/V land
+  // at per-row slots P + row, and attention takes its keys and splits from the
+  // device P (for P == prefix_len the same key splits as a host-P pass).
+  const bool devp = a->batch == 1;
+  int64_t* kvoff = devp ? (int64_t*)(ws + Lo.kvoff) : nullptr;
   int rc;
 #define PE_TRY(expr)            \
   do {                          \
     rc = (expr);                \
     if (rc != PE_OK) return rc; \
   } while (0)
+  if (devp)
+    PE_TRY(pe_internal_kv_offsets(a->seq_row0, a->seq_prefix, 1, M, a->cache_seq_stride, a->cache_capacity, hd,
+                                  a->prefix_len, M, kvoff, a->status, st));
   // first fused-feature slot capturing `layer` (or -1), and extra copies for repeated layers
   auto slot_of = [&](int layer) -> int {
     if (!a->fused) return -1;
@@ -484,10 +496,16 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     const void* b_qkv = m->b_qkv ? m->b_qkv[l] : nullptr;
     PE_TRY(pe_internal_gemm_rope_kv(wf, m->dtype, x_norm, H, M, H, m->w_qkv[l], a_qkv, nh, nkv, hd, b_qkv,
                                     a->positions, m->rope_cos_sin, m->max_positions, q, kc, vc, a->cache_capacity,
-                                    a->prefix_len, a->status, gws, gwsb, tiled, st));
-    PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
-                                      a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
-                                      Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st, m->attn_mode));
+                                    a->prefix_len, a->status, gws, gwsb, tiled, st, kvoff));
+    if (devp)
+      PE_TRY(pe_internal_tree_attention_batch(q, kc, vc, a->cache_capacity, a->cache_seq_stride, nh, nkv, M,
+                                              a->prefix_len, 1, a->seq_row0, a->seq_prefix, a->tree_bits,
+                                              a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
+                                              Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st, 1));
+    else
+      PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, a->mask_mode,
+                                        a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
+                                        Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st, m->attn_mode));
     const void* a_o = m->a_o ? m->a_o[l] : nullptr;
     PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, tiled, M, qd, m->w_o[l], a_o, H, part,
                                        Lo.part_bytes, &S, st));
@@ -624,7 +642,7 @@ int forward_batched(const pe_model_desc* m, const pe_pass_args* a, const BatchLa
     return PE_OK;
   };
   PE_TRY(pe_internal_kv_offsets(a->seq_row0, a->seq_prefix, a->batch, M, a->cache_seq_stride, a->cache_capacity, hd,
-                                kvoff, a->status, st));
+                                a->prefix_len, a->max_seq_rows, kvoff, a->status, st));
   char* xn_t = Lb.big ? ws + Lb.xn_t : nullptr;
   {
     const int f0 = slot_of(0);
@@ -724,7 +742,12 @@ int forward_batched(const pe_model_desc* m, const pe_pass_args* a, const BatchLa
 extern "C" int64_t pe_forward_batch_workspace_bytes(const pe_model_desc* m, int M, int max_seq_rows,
                                                     int64_t max_kv_len, int batch) {
   if (!m || M <= 0 || max_seq_rows <= 0 || max_kv_len <= 0 || batch <= 0) return 0;
-  return make_batch_layout(m, M, max_seq_rows, max_kv_len, batch).total;
+  const int64_t b = make_batch_layout(m, M, max_seq_rows, max_kv_len, batch).total;
+  if (batch == 1 && fused_path(m, M)) {  // the single-sequence pass with a device prefix
+    const int64_t f = make_layout(m, M, max_kv_len).total;
+    return f > b ? f : b;
+  }
+  return b;
 }
 
 extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* stream) {
@@ -744,8 +767,10 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
   if (m->attn_mode == PE_ATTN_EAGER && pe_wfmt_nf4(m->weight_format)) return PE_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   if (a->batch < 0) return PE_ERR_ARG;
-  // argmax keys: single-sequence 16-bit passes that write logits
-  if (a->node_keys && (a->batch > 0 || !a->logits || m->dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
+  // argmax keys: single-sequence 16-bit passes of at most one chunk that write
+  // logits (a batch of one included)
+  if (a->node_keys && (a->batch > 1 || !a->logits || m->dtype == PE_DTYPE_F32 || M > kFusedChunk))
+    return PE_ERR_ARG;
   if (a->batch > 0) {
     if (a->mask_mode != PE_MASK_TREE || !a->tree_bits || !a->seq_row0 || !a->seq_prefix) return PE_ERR_ARG;
     if (m->dtype == PE_DTYPE_F32 || m->head_dim != 128 || m->qkv_layout != PE_QKV_ROPE_PAIRED ||
@@ -756,6 +781,15 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
       return PE_ERR_TREE;
     const int64_t per_seq = (int64_t)m->num_layers * m->num_kv_heads * a->cache_capacity * m->head_dim;
     if (a->cache_seq_stride < per_seq) return PE_ERR_ARG;
+    if (a->batch == 1 && fused_path(m, M)) {
+      // one sequence of at most one chunk: the single-sequence pass with its
+      // prefix read on the device
+      if (a->max_seq_rows != M) return PE_ERR_ARG;
+      const Layout Lo = make_layout(m, M, a->prefix_len + M);
+      if (a->workspace_bytes < Lo.total) return PE_ERR_WORKSPACE;
+      return forward_fused(m, a, Lo, st);
+    }
+    if (a->node_keys) return PE_ERR_ARG;
     const BatchLayout Lb = make_batch_layout(m, M, a->max_seq_rows, a->prefix_len + a->max_seq_rows, a->batch);
     if (a->workspace_bytes < Lb.total) return PE_ERR_WORKSPACE;
     return forward_batched(m, a, Lb, st);

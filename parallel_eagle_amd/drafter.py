@@ -102,6 +102,19 @@ class DeviceDrafter:
         self.cache = TreeKVCache(self.shape, dt, dev, capacity)
         self.rows = torch.arange(capacity, dtype=torch.int64, device=dev)
         self._valid = 0  # context rows of the last call whose K/V are in self.cache
+        # False: calls leave their status word for the caller to read (a decode
+        # loop folds it into its one read per step) instead of synchronising
+        self.sync_status = True
+
+    @property
+    def status(self) -> torch.Tensor:
+        """The device int32 status word the drafter's kernels report errors in."""
+        return self.runner.status
+
+    def reset(self) -> None:
+        """Forget the cached context: the next ``draft_logits_extend`` runs its whole
+        context (a new prompt is not an extension of the last one)."""
+        self._valid = 0
 
     # nn.Module-style calls the reference's callers chain after load_drafter
     # (bench/run_bench.py:57: ``load_drafter(path, target).to(device, dtype).eval()``):
@@ -152,8 +165,9 @@ class DeviceDrafter:
         in a decode loop): the K/V rows of the previous context stay in the
         drafter's cache (the attention is causal, so a row's K/V depend only on
         the rows before it) and only the new rows and the k query slots run. The
-        caller guarantees the prefix; the logits equal a full recomputation up to
-        the rounding of the different launch shapes (exactly, in fp32)."""
+        caller guarantees the prefix (``reset`` before a context that does not
+        extend the last one); the logits equal a full recomputation up to the
+        rounding of the different launch shapes (exactly, in fp32)."""
         return self._draft(context_ids, context_feats, k, reuse=True)
 
     def _draft(self, context_ids, context_feats, k: int, reuse: bool) -> torch.Tensor:
@@ -182,7 +196,8 @@ class DeviceDrafter:
             self.cache.seq_len = p - 1
         logits = torch.empty((k, self.shape.vocab), dtype=self.dtype, device=self.device)
         self.runner.run_pass(rows[p - 1: m], rows[p - 1: m], self.cache, _lib.PE_MASK_CAUSAL, None, logits, None)
-        ops.read_status(self.runner.status, "draft_logits")
+        if self.sync_status:
+            ops.read_status(self.runner.status, "draft_logits")
         self._valid = p  # rows [0, p) are this context's (the mask slots after it are not)
         return logits
 

@@ -1,253 +1,357 @@
-"""The reference's decode loops over this package's target, drafter and acceptance.
+"""Decoding loops over the device path.
 
-``generate_speculative_cached`` follows the shipped one-forward loop of
-src/pe/serve.py:221-355 (tree mode) step for step: prefill, the pending bonus
-re-confirmed at depth 0, one tree verification per step through
-``forward_cached`` with the dense tree bias of masks.py, ``accept_tree_cached``,
-the commit by ``gather_cache`` with keep = [0, P) + [P + t for t in path], the
-fused features of the accepted path appended, and on a miss ``crop`` plus a
-one-token forward of the pending bonus. ``vanilla_generate_cached`` is the
-greedy baseline of src/pe/decode/baselines.py:49-94 (one incremental forward
-per token). Both loops only call the reference-shaped API (TargetModel,
-propose_tree, accept_tree_cached, the mask helpers), so they are the proof that
-a serve.py-style caller runs unchanged on the device path: their outputs must
-be equal (the reference's lossless invariant, tests/test_lossless.py:56-62).
+``greedy_decode`` is the target alone: one prefill, then one one-token
+``forward_cached`` pass per new token. It is the yardstick of the reference's
+lossless invariant (tests/test_lossless.py:56-62): speculative decoding must
+emit exactly its tokens.
 
-``SpeculativeDecoder`` is the same loop with the step's device work kept on the
-device: the tree goes from the drafter's logits to the verification pass as
-device tensors (no per-depth host reads), the masks come from the parent list
-on the device, the acceptance walk and the compaction of the accepted rows run
-there too, and the host reads one small vector per step (the accepted path and
-the bonus), which it needs to emit tokens anyway.
+``SpeculativeDecoder`` runs the reference's one-forward tree loop
+(src/pe/serve.py:221-355, tree mode): a prefill, then per step a tree drafted
+from the confirmed context, one verification pass over it against the cache,
+the greedy walk, the accepted path's rows kept; on a miss, one one-token pass
+of the pending bonus. Its design is not the reference's host loop:
+
+- the loop's state lives on the device (``pe_loop_commit``): the context ids,
+  the fused feature rows, the root logit row, the prefix length P and the
+  pending bonus; nothing is re-uploaded or concatenated per step;
+- for 16-bit models the verification step (masks -> pass -> walk ->
+  compaction -> commit) and the miss pass are each recorded once as a HIP
+  graph whose kernels read P from device memory (``pe_forward`` with a batch
+  of one), so every step replays the same two graphs;
+- the host reads one small record per step (the accepted length, the bonus,
+  the accepted tokens and every status word); the bonus of a miss pass is
+  read with the next step's record.
+
+Other models (fp32) run the same kernels eagerly with P passed from the host.
 """
 
 from __future__ import annotations
 
+import ctypes as C
+import math
 import time
-from collections.abc import Callable
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
 from . import _lib, ops
-from .masks import to_additive_bias, tree_allow_mask, tree_position_ids
-from .tree import beam_width, propose_tree, propose_tree_device
-from .verify import accept_tree_cached
+from .target import TargetModel, TreeKVCache
+from .tree import beam_width
 
 
 @dataclass
-class GenResult:
-    """src/pe/decode/result.py: the loop's output and counters."""
+class LoopStats:
+    """What a decode produced and what it cost."""
 
-    output_ids: list[int]
-    steps: int
-    target_calls: int
-    drafter_calls: int
-    accepted_tokens: int
-    num_generated: int
-    seconds: float
-
-    @property
-    def acceptance_length(self) -> float:
-        return self.num_generated / max(1, self.steps)
+    tokens: list[int]
+    steps: int = 0          # loop iterations after the prefill
+    target_passes: int = 1  # verification and one-token passes, the prefill included
+    draft_calls: int = 0
+    accepted: int = 0       # drafted tokens accepted beyond the re-confirmed pending one
+    host_reads: int = 0     # device-to-host reads inside the timed loop
+    seconds: float = 0.0
+    per_step: list[int] = field(default_factory=list)  # tokens each step committed
 
     @property
     def tokens_per_second(self) -> float:
-        return self.num_generated / self.seconds if self.seconds > 0 else 0.0
+        return len(self.tokens) / self.seconds if self.seconds > 0 else 0.0
+
+    @property
+    def tokens_per_step(self) -> float:
+        return len(self.tokens) / max(1, self.steps)
 
 
-def _argmax(row: torch.Tensor) -> int:
+def _first_argmax(row: torch.Tensor) -> int:
     return int(ops.argmax_rows(row.reshape(1, -1).contiguous())[0])
 
 
 @torch.no_grad()
-def vanilla_generate_cached(target, prompt_ids: list[int], max_new_tokens: int, eos_token_id: int | None = None,
-                            on_commit: Callable[[list[int]], None] | None = None) -> GenResult:
-    """Greedy decoding with a KV cache (src/pe/decode/baselines.py:49-94)."""
+def greedy_decode(target: TargetModel, prompt_ids: list[int], max_new_tokens: int,
+                  eos_token_id: int | None = None) -> LoopStats:
+    """Greedy decoding through ``forward_cached``: the prompt as one causal pass,
+    then the argmax of the last logit row is emitted and fed back as a
+    one-token pass at the next position, until ``max_new_tokens`` tokens or
+    ``eos_token_id`` (emitted, then stop)."""
     dev = target.device
-    seq = list(prompt_ids)
-    base = len(seq)
-    cache = target.make_cache()
-    pos = torch.arange(len(seq), device=dev).unsqueeze(0)
-    logits, _, cache = target.forward_cached(torch.tensor(seq, device=dev).unsqueeze(0), cache, pos)
-    nxt = _argmax(logits[0, -1])
-    target_calls = 1
+    n0 = len(prompt_ids)
+    cache = target.make_cache(n0 + max_new_tokens + 1)
+    logits, _, cache = target.forward_cached(torch.tensor([list(prompt_ids)], device=dev), cache,
+                                             torch.arange(n0, device=dev)[None])
+    stats = LoopStats(tokens=[])
     t0 = time.perf_counter()
-    while len(seq) - base < max_new_tokens:
-        seq.append(nxt)
-        if on_commit is not None:
-            on_commit([nxt])
-        if eos_token_id is not None and nxt == eos_token_id:
+    while max_new_tokens > 0:
+        tok = _first_argmax(logits[0, -1])
+        stats.tokens.append(tok)
+        stats.host_reads += 1
+        if len(stats.tokens) >= max_new_tokens or tok == eos_token_id:
             break
-        if len(seq) - base >= max_new_tokens:
-            break
-        npos = torch.tensor([[len(seq) - 1]], device=dev)
-        logits, _, cache = target.forward_cached(torch.tensor([[nxt]], device=dev), cache, npos)
-        target_calls += 1
-        nxt = _argmax(logits[0, -1])
+        pos = n0 + len(stats.tokens) - 1
+        logits, _, cache = target.forward_cached(torch.tensor([[tok]], device=dev), cache,
+                                                 torch.tensor([[pos]], device=dev))
+        stats.target_passes += 1
+        stats.steps += 1
     torch.cuda.synchronize(dev)
-    n = len(seq) - base
-    return GenResult(seq[base:], n, target_calls, 0, 0, n, time.perf_counter() - t0)
+    stats.seconds = time.perf_counter() - t0
+    return stats
 
 
-@torch.no_grad()
-def generate_speculative_cached(target, drafter, prompt_ids: list[int], *, k: int, mode: str = "tree",
-                                max_new_tokens: int = 256, tree_top_k: int = 3, tree_max_nodes: int = 24,
-                                eos_token_id: int | None = None,
-                                on_commit: Callable[[list[int]], None] | None = None) -> GenResult:
-    """One-forward KV-cache speculative decoding, tree mode (src/pe/serve.py:221-355)."""
-    if mode != "tree":
-        raise ValueError(f"unknown mode {mode!r}: the device path verifies trees")
-    dev = target.device
-    seq = list(prompt_ids)
-    base = len(seq)
-    cache = target.make_cache()
-    pos = torch.arange(len(seq), device=dev).unsqueeze(0)
-    logits, fused, cache = target.forward_cached(torch.tensor(seq, device=dev).unsqueeze(0), cache, pos)
-    feats = fused[0]
-    cache_len = len(seq)
-    root_logit = logits[0, -1]
-    target_calls, drafter_calls, accepted, steps = 1, 0, 0, 0
-    bonus = _argmax(root_logit)
-    seq.append(bonus)
-    if on_commit is not None:
-        on_commit([bonus])
-    stop = eos_token_id is not None and bonus == eos_token_id
-    t0 = time.perf_counter()
-    while len(seq) - base < max_new_tokens and not stop:
-        ctx = torch.tensor(seq[:cache_len], device=dev)
-        node_tokens, parents = propose_tree(drafter, ctx, feats, k, tree_top_k, tree_max_nodes)
-        drafter_calls += 1
-        allow = tree_allow_mask(parents, cache_len, device=dev)[cache_len:, :]
-        bias = to_additive_bias(allow, target.dtype)
-        npos = tree_position_ids(parents, cache_len, device=dev)[cache_len:].unsqueeze(0)
-        vlogits, vfused, cache = target.forward_cached(torch.tensor(node_tokens, device=dev).unsqueeze(0), cache,
-                                                       npos, attention_mask=bias)
-        target_calls += 1
-        path, new_bonus = accept_tree_cached(root_logit, vlogits[0], node_tokens, parents)
-        acc_tokens = [node_tokens[t] for t in path]
-        if acc_tokens:
-            keep = torch.tensor(list(range(cache_len)) + [cache_len + t for t in path], device=dev)
-            target.gather_cache(cache, keep)
-            feats = torch.cat([feats, vfused[0][path]], dim=0)
-            cache_len += len(acc_tokens)
-            root_logit = vlogits[0][path[-1]]
-            emit = [*acc_tokens[1:], int(new_bonus)]
-            accepted += len(acc_tokens) - 1
+class _Step:
+    """The device buffers and launches of one kind of loop step over ``rows`` rows:
+    the verification step (``rows`` = the tree's node count) or the miss pass
+    (one node, the pending token)."""
+
+    def __init__(self, dec: "SpeculativeDecoder", rows: int):
+        tm, dev = dec.tm, dec.tm.device
+        s = tm.shape
+        self.dec, self.rows = dec, rows
+        self.words = max(1, math.ceil(rows / 64))
+        self.parents = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+        self.tokens = torch.zeros(rows, dtype=torch.int64, device=dev)
+        self.bits = torch.zeros((rows, self.words), dtype=torch.int64, device=dev)
+        self.pos = torch.zeros(rows, dtype=torch.int64, device=dev)
+        self.depth = torch.zeros(rows, dtype=torch.int32, device=dev)
+        self.row0 = torch.tensor([0, rows], dtype=torch.int32, device=dev)
+        self.fused = torch.empty((rows, tm.feature_dim), dtype=tm.dtype, device=dev)
+        # the miss pass writes its logit row straight into the loop's root row
+        self.logits = dec.root.view(1, -1) if rows == 1 else torch.empty((rows, s.vocab), dtype=tm.dtype, device=dev)
+        self.groups = int(_lib.load().pe_dense_gemm_argmax_groups(rows, s.vocab, s.hidden)) if dec.keys else 0
+        self.keys = torch.zeros((rows, max(1, self.groups)), dtype=torch.int64, device=dev)
+        self.acc_out = torch.zeros(2 + rows, dtype=torch.int32, device=dev)
+        self.acc_scratch = torch.zeros(rows + 2, dtype=torch.int32, device=dev)
+        self.amax = torch.zeros(1, dtype=torch.int32, device=dev)
+        cap = dec.cache.capacity
+        if dec.device_prefix:
+            need = tm.model.desc()
+            ws = int(_lib.load().pe_forward_batch_workspace_bytes(C.byref(need), rows, rows, cap, 1))
         else:
-            pending = seq[cache_len]
-            cache.crop(cache_len)
-            blogits, bfused, cache = target.forward_cached(torch.tensor([[pending]], device=dev), cache,
-                                                           torch.tensor([[cache_len]], device=dev))
-            target_calls += 1
-            feats = torch.cat([feats, bfused[0]], dim=0)
-            cache_len += 1
-            root_logit = blogits[0, -1]
-            emit = [_argmax(root_logit)]
-        steps += 1
-        emitted: list[int] = []
-        for tok in emit:
-            seq.append(tok)
-            emitted.append(tok)
-            if eos_token_id is not None and tok == eos_token_id:
-                stop = True
-                break
-            if len(seq) - base >= max_new_tokens:
-                break
-        if on_commit is not None and emitted:
-            on_commit(emitted)
-    torch.cuda.synchronize(dev)
-    return GenResult(seq[base: base + max_new_tokens], steps, target_calls, drafter_calls, accepted,
-                     min(len(seq) - base, max_new_tokens), time.perf_counter() - t0)
+            ws = tm.model.workspace_bytes(rows, cap)
+        self.ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
+        self.graph = None
+
+    def _pass_args(self, P: int) -> _lib.PassArgs:
+        dec, tm = self.dec, self.dec.tm
+        c = dec.cache
+        a = _lib.PassArgs()
+        a.M = self.rows
+        a.mask_mode = _lib.PE_MASK_TREE if (dec.device_prefix or self.rows > 1) else _lib.PE_MASK_CAUSAL
+        a.input_ids = self.tokens.data_ptr() if self.rows > 1 else dec.state.data_ptr() + 8  # the pending token
+        a.positions = self.pos.data_ptr()
+        a.tree_bits = self.bits.data_ptr() if a.mask_mode == _lib.PE_MASK_TREE else None
+        a.bits_words = self.words if a.mask_mode == _lib.PE_MASK_TREE else 0
+        fl = tm.feature_layers
+        a.num_features = len(fl)
+        for i, f in enumerate(fl[:4]):
+            a.feature_layers[i] = f
+        a.k_cache, a.v_cache, a.cache_capacity = c.k.data_ptr(), c.v.data_ptr(), c.capacity
+        a.logits, a.fused = self.logits.data_ptr(), self.fused.data_ptr()
+        a.workspace, a.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
+        a.status = tm.status.data_ptr()
+        a.node_keys = self.keys.data_ptr() if dec.keys else None
+        if dec.device_prefix:
+            # one sequence whose P is state[0], up to the cache's capacity
+            a.batch, a.max_seq_rows = 1, self.rows
+            a.seq_row0, a.seq_prefix = self.row0.data_ptr(), dec.state.data_ptr()
+            a.cache_seq_stride = c.k.numel()
+            a.prefix_len = c.capacity - self.rows
+        else:
+            a.prefix_len = P
+        return a
+
+    def launch(self, P: int) -> None:
+        """Enqueue the step on the current stream (P: the host's prefix, used
+        when the model does not read it on the device)."""
+        dec, tm = self.dec, self.dec.tm
+        L, st = _lib.load(), ops.stream_ptr()
+        s, c, dt = tm.shape, dec.cache, ops.dcode(tm.dtype)
+        status = tm.status.data_ptr()
+        if dec.device_prefix:
+            _lib.check(L.pe_tree_masks_batch(self.parents.data_ptr(), self.row0.data_ptr(), dec.state.data_ptr(), 1,
+                                             self.rows, self.bits.data_ptr(), self.words, self.pos.data_ptr(),
+                                             self.depth.data_ptr(), status, st), "pe_tree_masks_batch")
+        elif self.rows > 1:
+            _lib.check(L.pe_tree_masks(self.parents.data_ptr(), self.rows, P, self.bits.data_ptr(), self.words,
+                                       self.pos.data_ptr(), self.depth.data_ptr(), status, st), "pe_tree_masks")
+        else:
+            self.pos.fill_(P)
+        _lib.check(L.pe_forward(C.byref(tm.model.desc()), C.byref(self._pass_args(P)), st), "pe_forward")
+        stats = (status, dec.draft_status, dec.propose_status.data_ptr())
+        feat = tm.feature_dim
+        if self.rows == 1:  # the miss pass: its bonus is the argmax of the root row
+            if not dec.keys:
+                _lib.check(L.pe_argmax_rows(dec.root.data_ptr(), s.vocab, 1, s.vocab, dt, self.amax.data_ptr(), st),
+                           "pe_argmax_rows")
+            _lib.check(L.pe_loop_miss_commit(self.fused.data_ptr(), feat, self.keys.data_ptr() if dec.keys else None,
+                                             self.groups, None if dec.keys else self.amax.data_ptr(), dt,
+                                             dec.feats.data_ptr(), dec.ids.data_ptr(), c.capacity,
+                                             dec.state.data_ptr(), dec.rec.data_ptr(), *stats, st),
+                       "pe_loop_miss_commit")
+            return
+        if dec.keys:
+            _lib.check(L.pe_accept_tree_keys(dec.root.data_ptr(), s.vocab, dt, self.keys.data_ptr(), self.groups,
+                                             self.rows, self.tokens.data_ptr(), self.parents.data_ptr(),
+                                             self.acc_out.data_ptr(), self.acc_scratch.data_ptr(), st),
+                       "pe_accept_tree_keys")
+        else:
+            _lib.check(L.pe_accept_tree(dec.root.data_ptr(), self.logits.data_ptr(), s.vocab, self.rows, s.vocab, dt,
+                                        self.tokens.data_ptr(), self.parents.data_ptr(), self.acc_out.data_ptr(),
+                                        self.acc_scratch.data_ptr(), st), "pe_accept_tree")
+        if dec.device_prefix:
+            _lib.check(L.pe_kv_compact_batch(c.k.data_ptr(), c.v.data_ptr(), 1, c.k.numel(), s.num_layers,
+                                             s.num_kv_heads, c.capacity, s.head_dim, dt, dec.state.data_ptr(),
+                                             self.acc_out.data_ptr(), self.rows, st), "pe_kv_compact_batch")
+        else:
+            _lib.check(L.pe_kv_compact(c.k.data_ptr(), c.v.data_ptr(), s.num_layers, s.num_kv_heads, c.capacity,
+                                       s.head_dim, dt, P, self.acc_out.data_ptr(), st), "pe_kv_compact")
+        _lib.check(L.pe_loop_commit(self.acc_out.data_ptr(), self.rows, self.tokens.data_ptr(), self.fused.data_ptr(),
+                                    feat, self.logits.data_ptr(), s.vocab, dt, dec.feats.data_ptr(),
+                                    dec.ids.data_ptr(), dec.root.data_ptr(), c.capacity, dec.state.data_ptr(),
+                                    dec.rec.data_ptr(), dec.rec_path, *stats, st), "pe_loop_commit")
+
+    def run(self, P: int) -> None:
+        if self.dec.device_prefix:
+            if self.graph is None:
+                self.graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(self.graph):
+                    self.launch(P)
+            self.graph.replay()
+        else:
+            self.launch(P)
 
 
 class SpeculativeDecoder:
-    """``generate_speculative_cached`` with the step's work resident on the device.
+    """Tree speculative decoding with the step's work and state on the device.
 
-    Per step: the drafter's logits (device) -> ``pe_propose_tree`` (device
-    tokens and parents) -> ``pe_tree_masks`` (bitmasks and positions from the
-    parents) -> ``pe_forward`` over the tree -> ``pe_accept_tree`` against the
-    root logit row -> ``pe_kv_compact`` of the accepted rows, all enqueued
-    without a host read; then one read of (|path|, bonus, path). The root logit
-    and the fused features stay device tensors. The tree's node count is known
-    on the host before the kernels run (the widths fix it).
+    ``drafter``: any object with ``draft_logits(context_ids, context_feats, k)``
+    returning (k, V) device logits (the reference drafter's API); a drafter with
+    ``draft_logits_extend`` (DeviceDrafter) keeps its context K/V across steps,
+    and one with ``sync_status`` / ``status`` lets the loop fold its status word
+    into the step's one read. The tree is the reference's constant-width beam:
+    width max(1, min(tree_top_k, tree_max_nodes // k)) at each of k depths.
+    ``use_graphs``: replay recorded steps (16-bit models with 128-dim heads and
+    trees of at most 64 nodes); otherwise the kernels are launched each step.
     """
 
-    def __init__(self, target, drafter, *, k: int, tree_top_k: int = 3, tree_max_nodes: int = 24):
-        self.tm, self.drafter = target, drafter
-        self.k = k
+    def __init__(self, target: TargetModel, drafter, *, k: int, tree_top_k: int = 3, tree_max_nodes: int = 24,
+                 use_graphs: bool = True):
+        self.tm, self.drafter, self.k = target, drafter, int(k)
         w = beam_width(k, tree_top_k, tree_max_nodes)
-        self.widths = [w] * k
+        self.widths = [w] * self.k
         self.top_k = w
-        self.T = w * k
+        self.T = w * self.k
+        if self.T > 64 * _lib.PE_TREE_MAX_WORDS:
+            raise ValueError(f"a tree of {self.T} nodes exceeds {64 * _lib.PE_TREE_MAX_WORDS}")
+        s = target.shape
+        self.keys = target.dtype != torch.float32 and self.T <= 64
+        self.device_prefix = bool(use_graphs) and self.keys and s.head_dim == 128 and target.model.qkv_paired
+
+    # ------------------------------------------------------------ set-up per generate call
+    def _allocate(self, capacity: int) -> None:
+        tm, dev = self.tm, self.tm.device
+        self.cache = TreeKVCache(tm.shape, tm.dtype, dev, capacity)
+        self.ids = torch.zeros(capacity, dtype=torch.int64, device=dev)
+        self.feats = torch.zeros((capacity, tm.feature_dim), dtype=tm.dtype, device=dev)
+        self.root = torch.zeros(tm.shape.vocab, dtype=tm.dtype, device=dev)
+        self.state = torch.zeros(2, dtype=torch.int64, device=dev)
+        self.rec_path = self.T
+        self.rec = torch.zeros(_lib.PE_LOOP_REC_HEAD + self.rec_path, dtype=torch.int32, device=dev)
+        self.propose_status = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.propose_scratch = torch.zeros(self.k * _lib.PE_PROPOSE_SCRATCH_PER_DEPTH, dtype=torch.uint8, device=dev)
+        st = getattr(self.drafter, "status", None)
+        self.draft_status = st.data_ptr() if isinstance(st, torch.Tensor) else None
+        self.verify = _Step(self, self.T)
+        self.miss = _Step(self, 1)
+
+    def _propose(self, logits: torch.Tensor) -> None:
+        """pe_propose_tree into the verification step's token and parent buffers."""
+        if logits.shape != (self.k, self.tm.shape.vocab) or logits.stride(1) != 1:
+            raise ValueError(f"the drafter must return ({self.k}, V) logits with contiguous rows")
+        n = C.c_int32(0)
+        widths = (C.c_int32 * self.k)(*self.widths)
+        _lib.check(_lib.load().pe_propose_tree(logits.data_ptr(), logits.stride(0), self.k, logits.shape[1],
+                                               ops.dcode(logits.dtype), widths, self.top_k,
+                                               self.verify.tokens.data_ptr(), self.verify.parents.data_ptr(),
+                                               C.byref(n), self.propose_scratch.data_ptr(),
+                                               self.propose_status.data_ptr(), ops.stream_ptr()), "pe_propose_tree")
+        if n.value != self.T:
+            raise RuntimeError(f"the beam proposed {n.value} nodes, expected {self.T}")
 
     @torch.no_grad()
-    def generate(self, prompt_ids: list[int], max_new_tokens: int, eos_token_id: int | None = None) -> GenResult:
+    def generate(self, prompt_ids: list[int], max_new_tokens: int, eos_token_id: int | None = None) -> LoopStats:
         tm, dev = self.tm, self.tm.device
-        seq = list(prompt_ids)
-        base = len(seq)
-        cache = tm.make_cache()
-        cache.ensure_capacity(len(seq) + max_new_tokens + self.T + 1)
-        pos = torch.arange(len(seq), device=dev).unsqueeze(0)
-        logits, fused, cache = tm.forward_cached(torch.tensor(seq, device=dev).unsqueeze(0), cache, pos)
-        feats = fused[0]
-        cache_len = len(seq)
-        root = logits[0, -1].contiguous()
-        target_calls, drafter_calls, accepted, steps = 1, 0, 0, 0
-        bonus = _argmax(root)
-        seq.append(bonus)
-        stop = eos_token_id is not None and bonus == eos_token_id
-        T, V = self.T, tm.shape.vocab
-        # the context only grows, so a drafter that can keep its cache across
-        # calls (DeviceDrafter.draft_logits_extend) runs only the new rows
+        if hasattr(self.drafter, "reset"):
+            self.drafter.reset()  # its cached context belongs to another prompt
+        sync_before = getattr(self.drafter, "sync_status", None)
+        if sync_before is not None:
+            self.drafter.sync_status = False
+        P = len(prompt_ids)
+        self._allocate(P + max_new_tokens + self.T + 2)
+        try:
+            return self._loop(list(prompt_ids), max_new_tokens, eos_token_id)
+        finally:
+            if sync_before is not None:
+                self.drafter.sync_status = sync_before
+            torch.cuda.synchronize(dev)
+
+    def _loop(self, prompt: list[int], max_new: int, eos: int | None) -> LoopStats:
+        tm, dev = self.tm, self.tm.device
+        P = len(prompt)
+        ids_p = torch.tensor(prompt, device=dev)
+        logits, fused, self.cache = tm.forward_cached(ids_p[None], self.cache, torch.arange(P, device=dev)[None])
+        self.ids[:P] = ids_p
+        self.feats[:P] = fused[0]
+        self.root.copy_(logits[0, -1])
+        bonus = _first_argmax(self.root)
+        self.ids[P] = bonus
+        self.state.copy_(torch.tensor([P, bonus], dtype=torch.int64))
+        stats = LoopStats(tokens=[bonus])
         draft = getattr(self.drafter, "draft_logits_extend", None) or self.drafter.draft_logits
-        vlogits = torch.empty((T, V), dtype=tm.dtype, device=dev)
-        vfused = torch.empty((T, tm.feature_dim), dtype=tm.dtype, device=dev)
-        acc_out = torch.zeros(2 + T, dtype=torch.int32, device=dev)
-        acc_scratch = torch.zeros(T + 2, dtype=torch.int32, device=dev)
+        stop = bonus == eos
+        miss_pending = False  # a miss pass ran; its bonus comes with the next record
         t0 = time.perf_counter()
-        while len(seq) - base < max_new_tokens and not stop:
-            ctx = torch.tensor(seq[:cache_len], device=dev)
-            dl = draft(ctx, feats, self.k)
-            drafter_calls += 1
-            tokens, parents, pstatus = propose_tree_device(dl, self.widths, self.top_k)
-            words = max(1, (T + 63) // 64)
-            bits, npos, _ = ops.tree_masks(parents, cache_len, words, tm.status)
-            tm.run_pass(tokens, npos, cache, _lib.PE_MASK_TREE, bits, vlogits, vfused)
-            target_calls += 1
-            ops.accept_tree(root, vlogits, tokens, parents, out=acc_out, scratch=acc_scratch)
-            tm.commit_path(cache, cache_len, acc_out)
-            out = acc_out.cpu().tolist()  # the step's one host read
-            ops.read_status(tm.status, "speculative step")
-            if int(pstatus.item()):
-                raise _lib.PEError(int(pstatus.item()), "propose_tree")
-            n, new_bonus, path = out[0], out[1], out[2: 2 + out[0]]
+        while not stop and len(stats.tokens) + miss_pending < max_new:
+            self._propose(draft(self.ids[:P], self.feats[:P], self.k))
+            stats.draft_calls += 1
+            self.verify.run(P)
+            stats.target_passes += 1
+            rec = self.rec.cpu().tolist()  # the step's one read
+            stats.host_reads += 1
+            if rec[2]:
+                self.rec[2] = 0
+                raise _lib.PEError(rec[2], "speculative step")
+            if miss_pending:
+                miss_pending = False
+                stats.tokens.append(rec[3])
+                if rec[3] == eos or len(stats.tokens) >= max_new:
+                    break  # this step's verification is discarded
+            n = rec[0]
+            stats.steps += 1
             if n:
-                acc_tokens = tokens[torch.tensor(path, device=dev)].tolist()
-                feats = torch.cat([feats, vfused[path]], dim=0)
-                cache_len += n
-                cache.seq_len = cache_len
-                root = vlogits[path[-1]].clone()
-                emit = [*acc_tokens[1:], int(new_bonus)]
-                accepted += n - 1
+                # rec[4] re-confirms the pending bonus (already emitted)
+                emit = rec[_lib.PE_LOOP_REC_HEAD + 1: _lib.PE_LOOP_REC_HEAD + n] + [rec[1]]
+                P += n
+                stats.accepted += n - 1
             else:
-                cache.seq_len = cache_len
-                pending = seq[cache_len]
-                blogits, bfused, cache = tm.forward_cached(torch.tensor([[pending]], device=dev), cache,
-                                                           torch.tensor([[cache_len]], device=dev))
-                target_calls += 1
-                feats = torch.cat([feats, bfused[0]], dim=0)
-                cache_len += 1
-                root = blogits[0, -1].contiguous()
-                emit = [_argmax(root)]
-            steps += 1
+                self.miss.run(P)
+                stats.target_passes += 1
+                P += 1
+                miss_pending, emit = True, []
+            before = len(stats.tokens)
             for tok in emit:
-                seq.append(tok)
-                if eos_token_id is not None and tok == eos_token_id:
+                stats.tokens.append(tok)
+                if tok == eos:
                     stop = True
                     break
-                if len(seq) - base >= max_new_tokens:
+                if len(stats.tokens) >= max_new:
                     break
+            stats.per_step.append(len(stats.tokens) - before + (1 if miss_pending else 0))
+        if miss_pending:
+            rec = self.rec.cpu().tolist()
+            stats.host_reads += 1
+            if rec[2]:
+                raise _lib.PEError(rec[2], "miss pass")
+            stats.tokens.append(rec[3])
         torch.cuda.synchronize(dev)
-        return GenResult(seq[base: base + max_new_tokens], steps, target_calls, drafter_calls, accepted,
-                         min(len(seq) - base, max_new_tokens), time.perf_counter() - t0)
+        stats.seconds = time.perf_counter() - t0
+        self.cache.seq_len = P
+        del stats.tokens[max_new:]
+        return stats

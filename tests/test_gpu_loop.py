@@ -1,14 +1,17 @@
-"""The reference's decode loop and its drafter interface over the device path.
+"""The decode loop and the drafter interface over the device path.
 
-- Losslessness (tests/test_lossless.py:56-62 of the reference): the tree loop
-  of src/pe/serve.py:221-355, driven through forward_cached / propose_tree /
-  accept_tree_cached / gather_cache / crop, emits exactly the tokens of greedy
-  decoding (src/pe/decode/baselines.py:49-94) through the same API: exactly on
-  the tiny fp32 model, and at the 7B width in bf16 up to a near tie of the
-  greedy decode itself. The device-resident loop (SpeculativeDecoder) emits
-  the same tokens. Drafters: an untrained device drafter (the miss path: one
-  token at a time) and one that is told the greedy continuation at some depths
-  (accepted paths of every length, compaction across steps).
+- Losslessness (tests/test_lossless.py:56-62 of the reference): the
+  speculative loop (SpeculativeDecoder: the one-forward tree loop of
+  src/pe/serve.py:221-355 with its state and step on the device) emits exactly
+  the tokens of greedy decoding through forward_cached: exactly on the tiny
+  fp32 model (kernels launched each step, P from the host), and at the 7B width
+  in bf16 (recorded steps replayed, P read on the device) up to a near tie of
+  the greedy decode itself. Drafters: an untrained device drafter (the miss
+  path: one token at a time) and one that is told the greedy continuation at
+  some depths (accepted paths of every length, compaction across steps).
+- One host read per step, and the recorded steps equal the same kernels
+  launched each step.
+- The drafter's cached context is dropped between two prompts.
 - The shared modules a reference drafter calls (src/pe/drafter.py:81-83,120,
   123,161): get_input_embeddings / get_lm_head / get_final_norm are callable
   and agree with the oracle.
@@ -24,7 +27,7 @@ from oracle.model import rms_norm
 from parallel_eagle_amd import ops
 from parallel_eagle_amd.config import LLAMA2_7B_NF4, TINY_LLAMA
 from parallel_eagle_amd.drafter import DeviceDrafter
-from parallel_eagle_amd.serve import SpeculativeDecoder, generate_speculative_cached, vanilla_generate_cached
+from parallel_eagle_amd.serve import SpeculativeDecoder, greedy_decode
 from parallel_eagle_amd.target import TargetModel
 from tests.test_oracle_pins import _drafter_weights
 
@@ -41,6 +44,21 @@ class PeekingDrafter:
     def __init__(self, inner, greedy: list[int], p: float, seed: int):
         self.inner, self.greedy, self.p = inner, greedy, p
         self.rng = random.Random(seed)
+
+    @property
+    def status(self):
+        return self.inner.status
+
+    @property
+    def sync_status(self):
+        return self.inner.sync_status
+
+    @sync_status.setter
+    def sync_status(self, v):
+        self.inner.sync_status = v
+
+    def reset(self):
+        self.inner.reset()
 
     def draft_logits(self, ctx, feats, k):
         lg = self.inner.draft_logits(ctx, feats, k).clone()
@@ -59,23 +77,35 @@ def _tiny():
 
 
 @pytest.mark.parametrize("p", [0.0, 0.6, 0.95])
-def test_tree_loop_is_lossless_on_the_tiny_fp32_model(p):
+def test_speculative_loop_is_lossless_on_the_tiny_fp32_model(p):
     tm, dr = _tiny()
     prompt = [1, 2, 3, 4, 5, 6]
     n = 48
-    ref = vanilla_generate_cached(tm, prompt, n)
-    drafter = PeekingDrafter(dr, prompt + ref.output_ids, p, seed=int(p * 100)) if p else dr
-    res = generate_speculative_cached(tm, drafter, prompt, k=5, mode="tree", max_new_tokens=n, tree_top_k=3,
-                                      tree_max_nodes=15)
-    assert res.output_ids == ref.output_ids
-    assert res.num_generated == n
+    ref = greedy_decode(tm, prompt, n)
+    assert len(ref.tokens) == n
+    drafter = PeekingDrafter(dr, prompt + ref.tokens, p, seed=int(p * 100)) if p else dr
+    dec = SpeculativeDecoder(tm, drafter, k=5, tree_top_k=3, tree_max_nodes=15)
+    assert not dec.device_prefix  # fp32: kernels launched each step
+    res = dec.generate(prompt, n)
+    assert res.tokens == ref.tokens
+    # one read per step, plus one at the end when the last step missed
+    assert res.steps <= res.host_reads <= res.steps + 1
     if p >= 0.95:
-        assert res.acceptance_length > 2.0  # most steps commit several tokens
-    dev = SpeculativeDecoder(tm, PeekingDrafter(dr, prompt + ref.output_ids, p, seed=int(p * 100)) if p else dr,
-                             k=5, tree_top_k=3, tree_max_nodes=15).generate(prompt, n)
-    assert dev.output_ids == ref.output_ids
-    print(f"p={p}: steps {res.steps}, target calls {res.target_calls}, acceptance length "
-          f"{res.acceptance_length:.2f}; device loop {dev.steps} steps")
+        assert res.tokens_per_step > 2.0  # most steps commit several tokens
+    print(f"p={p}: steps {res.steps}, target passes {res.target_passes}, tokens per step "
+          f"{res.tokens_per_step:.2f}, host reads {res.host_reads}")
+
+
+def test_speculative_loop_stops_at_eos():
+    tm, dr = _tiny()
+    prompt = [9, 8, 7]
+    ref = greedy_decode(tm, prompt, 40)
+    eos = ref.tokens[17]
+    want = ref.tokens[: ref.tokens.index(eos) + 1]
+    assert greedy_decode(tm, prompt, 40, eos_token_id=eos).tokens == want
+    dr2 = PeekingDrafter(dr, prompt + ref.tokens, 0.7, seed=4)
+    got = SpeculativeDecoder(tm, dr2, k=4, tree_top_k=2, tree_max_nodes=8).generate(prompt, 40, eos_token_id=eos)
+    assert got.tokens == want
 
 
 def test_drafter_extend_equals_a_full_recomputation():
@@ -95,38 +125,85 @@ def test_drafter_extend_equals_a_full_recomputation():
         assert torch.equal(got, want[n]), n
 
 
-def test_tree_loop_unknown_mode_is_refused():
+class RecordingDrafter:
+    """Passes draft_logits_extend through to ``inner`` and checks every call
+    against a second drafter with the same weights that recomputes the whole
+    context (draft_logits)."""
+
+    def __init__(self, inner, fresh):
+        self.inner, self.fresh, self.calls = inner, fresh, 0
+
+    def reset(self):
+        self.inner.reset()
+
+    def draft_logits(self, ctx, feats, k):
+        return self.inner.draft_logits(ctx, feats, k)
+
+    def draft_logits_extend(self, ctx, feats, k):
+        got = self.inner.draft_logits_extend(ctx, feats, k)
+        want = self.fresh.draft_logits(ctx, feats, k)
+        assert torch.equal(got, want), f"call {self.calls}: the drafter reused another context's rows"
+        self.calls += 1
+        return got
+
+
+def test_a_second_prompt_does_not_reuse_the_first_prompts_drafter_rows():
+    """Two generate() calls on one DeviceDrafter with different prompts: every
+    draft of the second call equals a full recomputation of its context (the
+    loop resets the drafter's cached rows at the start of a call)."""
     tm, dr = _tiny()
-    with pytest.raises(ValueError):
-        generate_speculative_cached(tm, dr, [1, 2], k=3, mode="chain", max_new_tokens=4)
+    w, _ = _drafter_weights(TINY_LLAMA, 2, len(tm.feature_layers), torch.float32, seed=5, std=0.05)
+    fresh = DeviceDrafter(tm, w, max_depth=5, capacity=256)
+    rec = RecordingDrafter(dr, fresh)
+    dec = SpeculativeDecoder(tm, rec, k=4, tree_top_k=2, tree_max_nodes=8)
+    a = dec.generate([3, 1, 4, 1, 5, 9, 2, 6, 5, 3], 12)
+    b = dec.generate([2, 7, 1, 8], 12)
+    assert a.tokens == greedy_decode(tm, [3, 1, 4, 1, 5, 9, 2, 6, 5, 3], 12).tokens
+    assert b.tokens == greedy_decode(tm, [2, 7, 1, 8], 12).tokens
+    assert rec.calls >= 4
 
 
-def test_tree_loop_at_the_7b_width_bf16():
-    """Two 7B-width NF4 layers in bf16. The tree pass and the one-token pass that
-    greedy decoding uses compute the same logits in different row blocks, so a
-    bf16 rounding can flip a near tie; every token must match up to the first
-    such step, and that step's greedy top-1 / top-2 margin must be small."""
+def _near_tie_or_equal(tm, prompt, ref_tokens, got_tokens, bound=0.0625):
+    """``got`` equals greedy decoding, or first differs at a step whose greedy
+    top-1 / top-2 margin is at most ``bound`` (a bf16 rounding of a different
+    row block flips a near tie)."""
+    if got_tokens == ref_tokens:
+        return "equal"
+    j = next(i for i, (a, b) in enumerate(zip(got_tokens, ref_tokens)) if a != b)
+    lg = tm.forward(torch.tensor([prompt + ref_tokens[:j]])).logits[0, -1].float()
+    top = lg.topk(2).values
+    margin = float(top[0] - top[1])
+    assert margin <= bound, f"token {j} differs with a greedy margin of {margin:.4g}"
+    return f"near tie at token {j} (margin {margin:.3g})"
+
+
+def test_speculative_loop_at_the_7b_width_bf16():
+    """Two 7B-width NF4 layers in bf16, recorded steps with P read on the device.
+    The tree pass and the one-token pass that greedy decoding uses compute the
+    same logits in different row blocks, so a bf16 rounding can flip a near
+    tie; every token must match up to the first such step, and that step's
+    greedy top-1 / top-2 margin must be small. The recorded steps emit exactly
+    the tokens of the same kernels launched each step with P from the host."""
     shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
     tm = TargetModel.synthetic(shape, seed=4, device=DEV, norm_noise=0.1, cache_capacity=512)
     w, _ = _drafter_weights(shape, 1, 3, torch.bfloat16, seed=6, std=shape.init_std)
     dr = DeviceDrafter(tm, w, max_depth=5, capacity=512)
     prompt = list(range(100, 140))
     n = 64
-    ref = vanilla_generate_cached(tm, prompt, n)
-    res = generate_speculative_cached(tm, PeekingDrafter(dr, prompt + ref.output_ids, 0.8, seed=3), prompt, k=5,
-                                      max_new_tokens=n, tree_top_k=4, tree_max_nodes=26)
-    dev = SpeculativeDecoder(tm, PeekingDrafter(dr, prompt + ref.output_ids, 0.8, seed=3), k=5, tree_top_k=4,
-                             tree_max_nodes=26).generate(prompt, n)
-    print(f"7B width: acceptance length {res.acceptance_length:.2f}, steps {res.steps}")
-    for got in (res.output_ids, dev.output_ids):
-        if got == ref.output_ids:
-            continue
-        j = next(i for i, (a, b) in enumerate(zip(got, ref.output_ids)) if a != b)
-        lg = tm.forward(torch.tensor([prompt + ref.output_ids[:j]])).logits[0, -1].float()
-        top = lg.topk(2).values
-        margin = float(top[0] - top[1])
-        print(f"first difference at token {j}: greedy margin {margin:.4g}")
-        assert margin <= 0.0625, f"token {j} differs with a greedy margin of {margin:.4g}"
+    ref = greedy_decode(tm, prompt, n)
+    graph = SpeculativeDecoder(tm, PeekingDrafter(dr, prompt + ref.tokens, 0.8, seed=3), k=5, tree_top_k=4,
+                               tree_max_nodes=26)
+    assert graph.device_prefix
+    res = graph.generate(prompt, n)
+    eager = SpeculativeDecoder(tm, PeekingDrafter(dr, prompt + ref.tokens, 0.8, seed=3), k=5, tree_top_k=4,
+                               tree_max_nodes=26, use_graphs=False).generate(prompt, n)
+    assert res.tokens == eager.tokens  # one key split either way at these lengths: the same roundings
+    assert res.steps <= res.host_reads <= res.steps + 1
+    verdict = _near_tie_or_equal(tm, prompt, ref.tokens, res.tokens)
+    print(f"7B width: tokens per step {res.tokens_per_step:.2f}, steps {res.steps}, {verdict}")
+    # an untrained drafter: every step misses and runs the one-token pass
+    miss = SpeculativeDecoder(tm, dr, k=5, tree_top_k=4, tree_max_nodes=26).generate(prompt, 24)
+    print("miss path:", _near_tie_or_equal(tm, prompt, ref.tokens[:24], miss.tokens))
 
 
 # ------------------------------------------------------------------ the shared modules
