@@ -370,36 +370,176 @@ def read_status(status: torch.Tensor, where: str) -> None:
 
 
 # ------------------------------------------------------------------ torch custom ops
+# A target registered here is named by an integer handle in torch.ops.pe.verify_pass
+# (a torch op takes tensors and scalars only; the pass reads the model's weights
+# through its pe_model_desc).
+_MODELS: dict[int, object] = {}
+
+
+def register_model(target) -> int:
+    """Handle of ``target`` (a TargetModel) for ``torch.ops.pe.verify_pass``; the same
+    target gets the same handle."""
+    for h, t in _MODELS.items():
+        if t is target:
+            return h
+    h = len(_MODELS) + 1
+    _MODELS[h] = target
+    return h
+
+
+def _model(handle: int):
+    try:
+        return _MODELS[handle]
+    except KeyError as e:
+        raise ValueError(f"no target registered under handle {handle} (ops.register_model)") from e
+
+
+def verify_pass(target, input_ids: torch.Tensor, positions: torch.Tensor, tree_bits: torch.Tensor,
+                k_cache: torch.Tensor, v_cache: torch.Tensor, prefix_len: int, workspace: torch.Tensor,
+                status: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """TargetModel.forward_cached (src/pe/target.py:203-224) as one pe_forward over
+    preallocated caches [L][nkv][cap][hd]: rows input_ids at positions, their K/V
+    appended at [prefix_len, prefix_len + M), attention over the prefix plus the
+    tree rows of tree_bits [M][words] (empty: a causal continuation). Returns
+    (logits [M][V], fused [M][F]) in the model dtype; device errors go to status."""
+    s = target.shape
+    m = input_ids.numel()
+    _req(positions.numel() == m and input_ids.dtype == torch.int64 and positions.dtype == torch.int64,
+         "input_ids and positions: int64, one position per id")
+    _req(k_cache.shape == v_cache.shape and k_cache.dim() == 4 and k_cache.dtype == target.dtype
+         and k_cache.is_contiguous() and v_cache.is_contiguous(), "caches [L][nkv][cap][hd] in the model dtype")
+    _req(status.dtype == torch.int32 and workspace.dtype == torch.uint8, "status int32, workspace uint8")
+    tree = tree_bits.numel() > 0
+    logits = torch.empty((m, s.vocab), dtype=target.dtype, device=input_ids.device)
+    fused = torch.empty((m, target.feature_dim), dtype=target.dtype, device=input_ids.device)
+    a = _lib.PassArgs()
+    a.input_ids, a.positions, a.M, a.prefix_len = ptr(input_ids), ptr(positions), m, prefix_len
+    a.mask_mode = _lib.PE_MASK_TREE if tree else _lib.PE_MASK_CAUSAL
+    a.tree_bits, a.bits_words = (ptr(tree_bits), tree_bits.shape[1]) if tree else (None, 0)
+    fl = target.feature_layers
+    a.num_features = len(fl)
+    for i, f in enumerate(fl[:4]):
+        a.feature_layers[i] = f
+    a.k_cache, a.v_cache, a.cache_capacity = ptr(k_cache), ptr(v_cache), k_cache.shape[2]
+    a.logits, a.fused = ptr(logits), ptr(fused)
+    a.workspace, a.workspace_bytes = ptr(workspace), workspace.numel()
+    a.status = ptr(status)
+    check(lib().pe_forward(C.byref(target.model.desc()), C.byref(a), stream_ptr()), "pe_forward")
+    return logits, fused
+
+
 _REGISTERED = False
 
 
 def register_torch_ops() -> None:
-    """Expose the functional kernels as torch.ops.pe.* custom ops."""
+    """Register the pass and its steps as torch custom ops (``torch.ops.pe.*``),
+    each with a fake (meta) implementation for tracing and the cache / scratch /
+    status mutations declared in its schema:
+
+    - ``verify_pass(model, input_ids, positions, tree_bits, k_cache!, v_cache!,
+      prefix_len, workspace!, status!) -> (logits, fused)``: the masked
+      verification forward (src/pe/target.py:203-224), ``model`` from
+      ``register_model``;
+    - ``tree_masks(parents, prefix_len, words, status!) -> (bits, positions,
+      depths)``: src/pe/masks.py:118-156;
+    - ``accept_tree(root, node_logits, node_tokens, parents, scratch!) -> out``:
+      src/pe/decode/verify.py:104-125, out = [|path|, bonus, path...];
+    - ``kv_compact(k_cache!, v_cache!, prefix_len, accept_out)`` and
+      ``kv_gather(k_cache!, v_cache!, keep, status!)``: gather_cache
+      (src/pe/target.py:194-201);
+    - ``rmsnorm``, ``argmax_rows``, ``nf4_linear``, ``dense_linear``: the pass's
+      building blocks.
+    """
     global _REGISTERED
     if _REGISTERED:
         return
+    lib_def = torch.library.custom_op
 
-    @torch.library.custom_op("pe::rmsnorm", mutates_args=())
-    def _rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    def op(name, schema, mutates=()):
+        return lambda fn: lib_def(f"pe::{name}", fn, mutates_args=mutates, schema=schema)
+
+    @op("verify_pass", "(int model, Tensor input_ids, Tensor positions, Tensor tree_bits, Tensor(a!) k_cache, "
+        "Tensor(b!) v_cache, int prefix_len, Tensor(c!) workspace, Tensor(d!) status) -> (Tensor, Tensor)",
+        ("k_cache", "v_cache", "workspace", "status"))
+    def _verify_pass(model, input_ids, positions, tree_bits, k_cache, v_cache, prefix_len, workspace, status):
+        return verify_pass(_model(model), input_ids, positions, tree_bits, k_cache, v_cache, prefix_len, workspace,
+                           status)
+
+    @_verify_pass.register_fake
+    def _(model, input_ids, positions, tree_bits, k_cache, v_cache, prefix_len, workspace, status):
+        t = _model(model)
+        m = input_ids.numel()
+        return (input_ids.new_empty((m, t.shape.vocab), dtype=t.dtype),
+                input_ids.new_empty((m, t.feature_dim), dtype=t.dtype))
+
+    @op("tree_masks", "(Tensor parents, int prefix_len, int words, Tensor(a!) status) -> (Tensor, Tensor, Tensor)",
+        ("status",))
+    def _tree_masks(parents, prefix_len, words, status):
+        return tree_masks(parents, prefix_len, words, status)
+
+    @_tree_masks.register_fake
+    def _(parents, prefix_len, words, status):
+        t = parents.numel()
+        return (parents.new_empty((t, words), dtype=torch.int64), parents.new_empty(t, dtype=torch.int64),
+                parents.new_empty(t, dtype=torch.int32))
+
+    @op("accept_tree", "(Tensor root, Tensor node_logits, Tensor node_tokens, Tensor parents, Tensor(a!) scratch) "
+        "-> Tensor", ("scratch",))
+    def _accept(root, node_logits, node_tokens, parents, scratch):
+        return accept_tree(root, node_logits, node_tokens, parents, scratch=scratch)
+
+    @_accept.register_fake
+    def _(root, node_logits, node_tokens, parents, scratch):
+        return root.new_empty(2 + max(node_tokens.numel(), 1), dtype=torch.int32)
+
+    @op("kv_compact", "(Tensor(a!) k_cache, Tensor(b!) v_cache, int prefix_len, Tensor accept_out) -> ()",
+        ("k_cache", "v_cache"))
+    def _kv_compact(k_cache, v_cache, prefix_len, accept_out):
+        kv_compact(k_cache, v_cache, prefix_len, accept_out)
+
+    @_kv_compact.register_fake
+    def _(k_cache, v_cache, prefix_len, accept_out):
+        return None
+
+    @op("kv_gather", "(Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor keep, Tensor(c!) status) -> ()",
+        ("k_cache", "v_cache", "status"))
+    def _kv_gather(k_cache, v_cache, keep, status):
+        kv_gather(k_cache, v_cache, keep, status)
+
+    @_kv_gather.register_fake
+    def _(k_cache, v_cache, keep, status):
+        return None
+
+    @op("rmsnorm", "(Tensor x, Tensor w, float eps) -> Tensor")
+    def _rmsnorm(x, w, eps):
         return rmsnorm(x, w, eps)
 
-    @torch.library.custom_op("pe::argmax_rows", mutates_args=())
-    def _argmax(x: torch.Tensor) -> torch.Tensor:
+    @_rmsnorm.register_fake
+    def _(x, w, eps):
+        return torch.empty_like(x)
+
+    @op("argmax_rows", "(Tensor x) -> Tensor")
+    def _argmax(x):
         return argmax_rows(x)
 
-    @torch.library.custom_op("pe::nf4_linear", mutates_args=())
-    def _nf4_linear(x: torch.Tensor, tiled: torch.Tensor, tabs: torch.Tensor, n: int) -> torch.Tensor:
+    @_argmax.register_fake
+    def _(x):
+        return x.new_empty(x.shape[0], dtype=torch.int32)
+
+    @op("nf4_linear", "(Tensor x, Tensor tiled, Tensor tabs, int n) -> Tensor")
+    def _nf4_linear(x, tiled, tabs, n):
         return linear(x, n, nf4=(tiled, tabs))
 
-    @torch.library.custom_op("pe::dense_linear", mutates_args=())
-    def _dense_linear(x: torch.Tensor, w: torch.Tensor, n: int) -> torch.Tensor:
+    @_nf4_linear.register_fake
+    def _(x, tiled, tabs, n):
+        return x.new_empty((x.shape[0], n))
+
+    @op("dense_linear", "(Tensor x, Tensor w, int n) -> Tensor")
+    def _dense_linear(x, w, n):
         return linear(x, n, dense=w)
 
-    @torch.library.custom_op("pe::accept_tree", mutates_args=())
-    def _accept(root: torch.Tensor, nodes: torch.Tensor, tokens: torch.Tensor, parents: torch.Tensor) -> torch.Tensor:
-        return accept_tree(root, nodes, tokens, parents)
+    @_dense_linear.register_fake
+    def _(x, w, n):
+        return x.new_empty((x.shape[0], n))
 
     _REGISTERED = True
-
-
-_ = C  # ctypes kept importable for callers building descriptors
