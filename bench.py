@@ -67,9 +67,6 @@ def parse_args(argv=None):
     p.add_argument("--prefill", action="store_true",
                    help="instead of the verification pass: time a causal prefill of the workload's prefix length "
                         "from an empty cache and a one-token continuation (eager forward_cached calls)")
-    p.add_argument("--prefill-weights", action="store_true",
-                   help="with --prefill: keep row-major 16-bit copies of the linears on the device "
-                        "(pe_prefill_weights_fill) instead of dequantising them per prefill")
     p.add_argument("--loop", action="store_true",
                    help="tokens/s of the decode loop (greedy and the device-resident speculative loop)")
     p.add_argument("--draft", action="store_true",
@@ -368,11 +365,13 @@ def cpu_baseline(wl, seed, n_layers: int, runs: int):
 
 
 # ---------------------------------------------------------------- main
-def prefill_line(wl, seed: int, reps: int = 3, weight_copy: bool = False) -> dict:
+def prefill_line(wl, seed: int, reps: int = 3) -> dict:
     """Latency of the causal prefill of the workload's prefix (P tokens from an empty
     cache, the prompt step before the first verification) and of a one-token
     continuation (the miss path), eager forward_cached calls after a warm-up call
-    each (the first prefill of a process loads the GEMM library's kernels)."""
+    each. Past 256 tokens the prefill runs every linear once over all rows on the
+    library's many-row MFMA kernels; ``mfma`` is the pass's matrix-core FLOP (the
+    linears and the lm_head, 2 M N K each, plus causal attention) over its time."""
     import torch
 
     from parallel_eagle_amd import synth
@@ -380,7 +379,6 @@ def prefill_line(wl, seed: int, reps: int = 3, weight_copy: bool = False) -> dic
 
     shape, P = wl.model, wl.prefix_len
     tm = TargetModel.synthetic(shape, seed=seed, device="cuda:0", cache_capacity=P + 64)
-    copy_bytes = tm.model.enable_prefill_weights() if weight_copy else 0
     ids = torch.tensor([synth.uniform_int(seed, synth.STREAM_PROMPT, P, shape.vocab).tolist()])
     pos = torch.arange(P).unsqueeze(0)
     pre, one = [], []
@@ -398,12 +396,17 @@ def prefill_line(wl, seed: int, reps: int = 3, weight_copy: bool = False) -> dic
             pre.append(t1 - t0)
             one.append(t2 - t1)
     ms = statistics.median(pre) * 1e3
+    lin = sum(n * k for _, n, k in shape.linear_shapes()) * shape.num_layers + shape.vocab * shape.hidden
+    attn = 2 * 2 * shape.num_heads * shape.head_dim * P * (P + 1) / 2 * shape.num_layers  # causal QK^T and PV
+    flop = 2 * P * lin + attn
     return {"metric": "prefill latency (causal, from an empty cache) and one-token continuation latency",
             "value": round(P / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": reps,
             "ms_prefill": round(ms, 3), "ms_one_token": round(statistics.median(one) * 1e3, 3),
-            "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+            "mfma": {"flop": flop, "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+                     "util": round(flop / (ms * 1e-3) / (MFMA_BF16_PEAK_TFLOPS * 1e12), 4)},
+            "higher_is_better": True, "dtype": DTYPE_NAMES[shape.dtype], "data": "synthetic",
             "config": {"workload": wl.name, "prefill_tokens": P, "layers": shape.num_layers,
-                       "weights": shape.weight_format, "eager": True, "prefill_weight_copy_bytes": copy_bytes}}
+                       "weights": shape.weight_format, "eager": True}}
 
 
 def loop_line(wl, seed: int, new_tokens: int = 96) -> dict:
@@ -729,7 +732,7 @@ def main(argv=None) -> int:
         return 1
     wl = WORKLOADS[a.workload]
     if a.prefill:
-        print(json.dumps(prefill_line(wl, a.seed, weight_copy=a.prefill_weights)))
+        print(json.dumps(prefill_line(wl, a.seed)))
         return 0
     if a.draft:
         print(json.dumps(draft_line(wl, a.seed)))

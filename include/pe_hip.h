@@ -389,10 +389,6 @@ typedef struct pe_model_desc {
   const void* const* a_gu;
   const void* const* w_down; /* K = intermediate_padded */
   const void* const* a_down;
-  /* Optional: every layer's linears as row-major 16-bit [N][K], filled once by
-   * pe_prefill_weights_fill; a prefill (causal pass of more than 256 rows) then
-   * multiplies these instead of dequantising each linear per call. NULL: none. */
-  const void* prefill_weights;
 } pe_model_desc;
 
 typedef struct pe_pass_args {
@@ -453,25 +449,12 @@ int64_t pe_forward_batch_workspace_bytes(const pe_model_desc* m, int M, int max_
  * (src/pe/target.py:203-224 -> HF LlamaForCausalLM / Qwen2ForCausalLM forward,
  * modeling_llama.py:347-490): embeddings, L decoder layers with in-place KV
  * append, final norm, lm_head over all M rows, fused features.
- * A causal pass of more than 256 rows of a bf16 model, NF4 or dense (a
- * prefill), dequantises or untiles each linear once (or reads the copy at
- * m->prefill_weights) and multiplies it with rocBLAS (bf16, fp32 accumulation);
- * rocBLAS gets its workspace from the pass workspace, and the library keeps one
- * rocBLAS handle per device, made on the first such pass (the handle's own
- * state is rocBLAS's). Set PE_PREFILL_GEMM=0 to run such passes in 64-row
- * chunks instead. */
+ * A causal pass of more than 256 rows of a 16-bit model with 128-dim heads, NF4
+ * or dense (a prefill), runs every linear once over all rows in blocks of 256
+ * rows on the matrix cores (each NF4 weight dequantised once per block inside
+ * the GEMM) and attention once over all rows. Set PE_PREFILL_GEMM=0 to run such
+ * passes in 64-row chunks of the fused pass instead. */
 int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* stream);
-
-/* No counterpart in the reference (bitsandbytes' Linear4bit dequantises its
- * weight on every multi-token call, src/pe/target.py:32-38): bytes of the
- * prefill weight copy, every layer's q/k/v, o, gate/up and down as row-major
- * 16-bit [N][K], layer after layer in that order (about 2 bytes per weight:
- * 13.0 GB at the Llama-2-7B shape, a few percent of one GPU's HBM). */
-int64_t pe_prefill_weights_bytes(const pe_model_desc* m);
-/* Fill that copy from the model's linears (NF4 dequantised exactly as
- * pe_nf4_dequant, dense untiled); `bytes` must be at least
- * pe_prefill_weights_bytes(m). Point m->prefill_weights at it afterwards. */
-int pe_prefill_weights_fill(const pe_model_desc* m, void* out, int64_t bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -78,7 +78,6 @@ class ModelDesc(C.Structure):
         ("w_o", C.POINTER(vp)), ("a_o", C.POINTER(vp)),
         ("w_gu", C.POINTER(vp)), ("a_gu", C.POINTER(vp)),
         ("w_down", C.POINTER(vp)), ("a_down", C.POINTER(vp)),
-        ("prefill_weights", vp),
     ]
 
 
@@ -142,8 +141,6 @@ SIGNATURES: dict[str, tuple] = {
     "pe_kv_gather": (C.c_int, [vp, vp, C.c_int, C.c_int, i64, C.c_int, C.c_int, vp, i64, vp, vp]),
     "pe_forward_workspace_bytes": (i64, [C.POINTER(ModelDesc), C.c_int, i64]),
     "pe_forward": (C.c_int, [C.POINTER(ModelDesc), C.POINTER(PassArgs), vp]),
-    "pe_prefill_weights_bytes": (i64, [C.POINTER(ModelDesc)]),
-    "pe_prefill_weights_fill": (C.c_int, [C.POINTER(ModelDesc), vp, i64, vp]),
     "pe_forward_batch_workspace_bytes": (i64, [C.POINTER(ModelDesc), C.c_int, C.c_int, i64, C.c_int]),
     "pe_tree_masks_batch": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, vp, C.c_int, vp, vp, vp, vp]),
     "pe_accept_tree_batch": (C.c_int, [vp, i64, vp, i64, i64, C.c_int, vp, C.c_int, C.c_int, vp, vp, vp, vp, vp]),

@@ -67,10 +67,7 @@ def build(verbose: bool = False) -> Path:
     with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
-    # rocBLAS: the prefill path's bf16 GEMM over all rows (pe_model.cpp)
-    rocm_lib = Path(hipcc()).resolve().parent.parent / "lib"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-           f"-L{rocm_lib}", "-lrocblas", f"-Wl,-rpath,{rocm_lib}"]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr[-6000:]}")

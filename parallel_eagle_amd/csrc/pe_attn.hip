@@ -1262,7 +1262,7 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
                                float scale, int dtype, void* out, int64_t ld_out, int out_units, void* workspace,
                                int64_t workspace_bytes, int* counters, hipStream_t st, int attn_mode) {
   if (!q || !k_cache || !v_cache || !out || !workspace) return PE_ERR_ARG;
-  if (out_units && (dtype == PE_DTYPE_F32 || hd != 128 || T > 64 || out_units * 128 != nh * hd)) return PE_ERR_ARG;
+  if (out_units && (dtype == PE_DTYPE_F32 || hd != 128 || out_units * 128 != nh * hd)) return PE_ERR_ARG;
   if (T <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || hd <= 0 || hd > 256 || P < 0) return PE_ERR_ARG;
   if (P + T > cache_cap) return PE_ERR_CAPACITY;
   if (mask_mode != PE_MASK_TREE && mask_mode != PE_MASK_CAUSAL) return PE_ERR_ARG;

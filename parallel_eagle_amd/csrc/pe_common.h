@@ -92,6 +92,16 @@ __device__ __constant__ static const float kNF4[16] = {
     0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
     0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
 
+// The normalised value of x times the weight w, rounded as PE_NORM_HF (the
+// normalised value rounded, then a rounded multiply by w: HF LlamaRMSNorm,
+// modeling_llama.py:62-67) or PE_NORM_FP32_WEIGHT (x * inv * w in fp32, one
+// rounding: src/pe/nn.py:22-26).
+template <typename E>
+__device__ __forceinline__ float norm_out(int mode, float x, float inv, float w) {
+  const float y = __fmul_rn(x, inv);
+  return mode == PE_NORM_FP32_WEIGHT ? E::round(__fmul_rn(y, w)) : E::round(__fmul_rn(w, E::round(y)));
+}
+
 // Wave-level reductions (wave64) through DPP-free shuffles.
 // Order-preserving key of a value for torch.argmax's semantics: larger value
 // -> larger key, every NaN -> the largest key, -0 and +0 -> the same key (they

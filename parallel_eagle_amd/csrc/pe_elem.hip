@@ -48,16 +48,6 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
   }
 }
 
-// The normalised value of x times the weight w, rounded as PE_NORM_HF (the
-// normalised value rounded, then a rounded multiply by w: HF LlamaRMSNorm,
-// modeling_llama.py:62-67) or PE_NORM_FP32_WEIGHT (x * inv * w in fp32, one
-// rounding: src/pe/nn.py:22-26).
-template <typename E>
-__device__ __forceinline__ float norm_out(int mode, float x, float inv, float w) {
-  const float y = __fmul_rn(x, inv);
-  return mode == PE_NORM_FP32_WEIGHT ? E::round(__fmul_rn(y, w)) : E::round(__fmul_rn(w, E::round(y)));
-}
-
 template <int DT>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const typename Elem<DT>::T* __restrict__ x, int64_t ldx, int H,
                                                       const typename Elem<DT>::T* __restrict__ w, float eps,
@@ -318,6 +308,39 @@ __global__ void kv_offsets_kernel(const int32_t* __restrict__ seq_row0, const in
   const bool ok = fits && r >= seq_row0[b] && r < seq_row0[b + 1] && slot < cap;
   if (!ok && status) atomicOr(status, rows > max_rows ? PE_ERR_TREE : PE_ERR_CAPACITY);
   off[r] = ok ? b * seq_stride + slot * hd : -1;
+}
+
+// One thread per 8 consecutive columns of a row: 16 bytes that are 16
+// contiguous bytes in the A-tiled layout as well.
+__global__ void to_xtile_kernel(const uint16_t* __restrict__ x, int64_t ld, int M, int K, int rows_pad,
+                                uint16_t* __restrict__ out, int vec) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int chunks = K >> 3;
+  if (i >= (int64_t)rows_pad * chunks) return;
+  const int r = (int)(i / chunks), c = (int)(i % chunks) * 8;
+  uint16_t* d = out + xtile_index(r, c, K >> 7);
+  if (r >= M) {  // the last tile's padding rows: zeros
+    *(uint4*)d = uint4{0u, 0u, 0u, 0u};
+    return;
+  }
+  const uint16_t* sp = x + (int64_t)r * ld + c;
+  if (vec) {
+    *(uint4*)d = *(const uint4*)sp;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = sp[e];
+  }
+}
+
+int pe_internal_to_xtile(const void* x, int64_t ld, int M, int K, void* out, hipStream_t st) {
+  if (!x || !out || M <= 0 || K <= 0 || K % 128 || ld < K) return PE_ERR_ARG;
+  const int rows_pad = (M + 31) / 32 * 32;
+  const int64_t n = (int64_t)rows_pad * (K / 8);
+  const int vec = ((((uintptr_t)x) | (uintptr_t)(ld * 2)) & 15) == 0;
+  to_xtile_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>((const uint16_t*)x, ld, M, K, rows_pad,
+                                                                (uint16_t*)out, vec);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
 }
 
 int pe_internal_kv_offsets(const int32_t* seq_row0, const int64_t* seq_prefix, int batch, int M, int64_t seq_stride,

@@ -85,6 +85,9 @@ struct EpiArgs {
   int32_t* status;
   uint64_t* amax_keys;  // kEpiArgmax: [M][amax_groups]
   int amax_groups;
+  // kEpiPartial with tail.w set: the launch's last workgroups apply the
+  // residual + RMSNorm to the summed partials (see partial_norm_tail)
+  PeNormTail tail;
 };
 
 __device__ __forceinline__ int64_t kv_row_elem(const EpiArgs& e, int row) {
@@ -289,7 +292,9 @@ __device__ __forceinline__ void lds_barrier() {
 // ---------------------------------------------------------------------------
 constexpr int kWaves = 4;             // waves per GEMM workgroup (K slices)
 constexpr int kCounterBytes = 32768;  // per-column-group arrival counters at the head of the workspace
-constexpr int kMaxGroups = kGemmCounterInts;  // the rest of the counter area belongs to attention
+// the last two GEMM counters belong to the norm tail of split-partial launches
+// (kTailCounterInt); the rest of the counter area belongs to attention
+constexpr int kMaxGroups = kTailCounterInt;
 constexpr int kMaxSplits = 16;
 
 // Epilogue of one output row of a column group: v[nt] is the lane's column of
@@ -322,6 +327,118 @@ __host__ __device__ constexpr int64_t partial_bytes_of(int S, int groups, int MT
 // accesses of 16 consecutive lanes hit 64 distinct banks.
 constexpr int kRedLane = 20;
 __host__ __device__ constexpr int red_floats(int KW, int NT, int MT) { return KW * NT * MT * 64 * kRedLane; }
+
+// ---------------------------------------------------------------------------
+// Norm tail of a split-partial launch (o and down of the fused pass). The
+// residual + RMSNorm of a row needs every column group's and every split's
+// partial of that row, so it cannot start before the whole launch has stored
+// its partials. The launch holds one round of workgroups, all resident at
+// once; every workgroup stores its partials agent-coherent and counts itself,
+// and the last W = min(M, workgroups) to arrive wait (bounded) for the count
+// to reach every workgroup, then take rows w, w + W, ... each. The arithmetic
+// and its order are residual_rmsnorm_kernel's: the split partials summed in
+// split order, h = round(h + round(sum)), the squares summed per thread of a
+// 1024-thread row (the norm kernel's) as this workgroup's threads replaying
+// those 1024 in turn, wave sums, then the 16 wave sums in order; the results
+// are bit-identical to the norm kernel's. The last waiter sets the two
+// counters back to zero.
+// ---------------------------------------------------------------------------
+constexpr int kTailVT = 1024;       // the norm kernel's threads per row
+constexpr int kTailSpin = 1 << 20;  // polls (about 64 clocks apart) before a wait gives up
+
+template <int DT, int NTHR>
+__device__ void tail_norm_row(const EpiArgs& e, int S, int m, __amdgpu_buffer_rsrc_t rp, float* lds) {
+  typedef Elem<DT> E;
+  typedef typename E::T T;
+  constexpr int J = kTailVT / NTHR;  // norm-kernel threads replayed by each thread
+  const PeNormTail& t = e.tail;
+  const int H = e.N, nchunk = H >> 2;
+  const int chv = (nchunk + kTailVT - 1) / kTailVT;  // 1 or 2 chunks per norm-kernel thread
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  T* hr = (T*)t.h + (int64_t)m * H;
+  float v[J][2][4];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int vt = threadIdx.x + NTHR * j;
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int ch = vt + kTailVT * c;
+      if (c >= chv || ch >= nchunk) continue;
+      float a[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < S; ++sp) {
+        const f32x4_t pv = load_agent_x4(rp, (uint32_t)((((int64_t)sp * e.M + m) * H + 4 * ch) * 4));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[q] = a[q] + pv[q];
+      }
+      float hv[4];
+      Vec4<DT>::load(hr + 4 * ch, hv);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[j][c][q] = E::round(__fadd_rn(hv[q], E::round(a[q])));
+      Vec4<DT>::store(hr + 4 * ch, v[j][c]);
+      if (t.cap_h) Vec4<DT>::store((T*)t.cap_h + (int64_t)m * t.ld_cap_h + 4 * ch, v[j][c]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ss = __fadd_rn(ss, __fmul_rn(v[j][c][q], v[j][c][q]));
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) lds[wave + (NTHR / 64) * j] = ss;
+  }
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kTailVT / 64; ++i) tot += lds[i];
+  const float inv = 1.0f / sqrtf(tot / (float)H + t.eps);
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int vt = threadIdx.x + NTHR * j;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int ch = vt + kTailVT * c;
+      if (c >= chv || ch >= nchunk) continue;
+      float wv[4], o[4];
+      Vec4<DT>::load((const T*)t.w + 4 * ch, wv);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = norm_out<E>(t.mode, v[j][c][q], inv, wv[q]);
+      Vec4<DT>::store((T*)t.xn + (int64_t)m * H + 4 * ch, o);
+      if (t.xn_tiled) Vec4<DT>::store((T*)t.xn_tiled + xtile_index(m, 4 * ch, H >> 7), o);
+      if (t.cap_xn) Vec4<DT>::store((T*)t.cap_xn + (int64_t)m * t.ld_cap_xn + 4 * ch, o);
+    }
+  }
+  __syncthreads();  // lds is reused by the next row
+}
+
+// Called by every thread of the workgroup once its partial stores are issued.
+template <int DT, int NTHR>
+__device__ void partial_norm_tail(const EpiArgs& e, int S, float* lds) {
+  int* flag = (int*)lds;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's agent-coherent stores are acknowledged
+  __syncthreads();
+  const int G = gridDim.x * gridDim.y, W = min(e.M, G);
+  int* const arrived = e.tail.counters;
+  int* const done = e.tail.counters + 1;
+  if (threadIdx.x == 0) flag[0] = __hip_atomic_fetch_add(arrived, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int a = flag[0];
+  if (a < G - W) return;
+  if (threadIdx.x == 0) {
+    int it = 0;
+    while (__hip_atomic_load(arrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < G && ++it < kTailSpin)
+      __builtin_amdgcn_s_sleep(1);
+    flag[1] = it < kTailSpin;
+    if (it >= kTailSpin && e.tail.status) atomicOr(e.tail.status, PE_ERR_LAUNCH);
+  }
+  __syncthreads();
+  const bool ok = flag[1] != 0;
+  __syncthreads();  // flag is overwritten by the rows' sums
+  if (ok) {
+    const __amdgpu_buffer_rsrc_t rp = agent_rsrc(e.out, (uint32_t)((int64_t)S * e.M * e.N * 4));
+    for (int m = a - (G - W); m < e.M; m += W) tail_norm_row<DT, NTHR>(e, S, m, rp, lds);
+  }
+  if (threadIdx.x == 0 && __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == W - 1) {
+    __hip_atomic_store(arrived, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
 
 template <int ADT, int NT, int MT, int KW = kWaves>
 __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red, int group, int split, int S,
@@ -360,16 +477,35 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
     }
 
   if (e.op == kEpiPartial) {
-    float* out = (float*)e.out + (int64_t)split * e.M * e.N;
+    if (e.tail.w) {
+      // agent-coherent stores: the norm tail reads them from other XCDs
+      const __amdgpu_buffer_rsrc_t ro = agent_rsrc(e.out, (uint32_t)((int64_t)S * e.M * e.N * 4));
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = mt * 32 + 8 * wave + 4 * g + j;
-        if (row < e.M)
+        for (int j = 0; j < 4; ++j) {
+          const int row = mt * 32 + 8 * wave + 4 * g + j;
+          if (row < e.M)
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) out[(int64_t)row * e.N + (group * NT + nt) * 32 + ln] = v[mt][j][nt];
-      }
+            for (int nt = 0; nt < NT; ++nt)
+              __builtin_amdgcn_raw_buffer_store_b32(
+                  __float_as_uint(v[mt][j][nt]), ro,
+                  (uint32_t)((((int64_t)split * e.M + row) * e.N + (group * NT + nt) * 32 + ln) * 4), 0, kCpolSC1);
+        }
+      // waves past kWaves of an eight-wave workgroup have left after the reduction
+      partial_norm_tail<ADT, kWaves * 64>(e, S, red);
+    } else {
+      float* out = (float*)e.out + (int64_t)split * e.M * e.N;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = mt * 32 + 8 * wave + 4 * g + j;
+          if (row < e.M)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) out[(int64_t)row * e.N + (group * NT + nt) * 32 + ln] = v[mt][j][nt];
+        }
+    }
     return;
   }
   if (S > 1) {
@@ -948,7 +1084,8 @@ __global__ __launch_bounds__(kWsWaves * 64, 1) void nf4_gemm_bigws_kernel(const 
     }
     return;
   }
-  const int mt0 = (wave - kWaves) * 2;
+  // grid.z: blocks of eight 32-row tiles (a prefill of more than 256 rows)
+  const int mt0 = blockIdx.z * 8 + (wave - kWaves) * 2;
   const int nmt = max(0, min(2, mtiles - mt0));
   if (nmt == 2) bigws_consumer<2, SW>(smem, X, NP, group, u0, u1, mt0, e, split);
   else if (nmt == 1) bigws_consumer<1, SW>(smem, X, NP, group, u0, u1, mt0, e, split);
@@ -966,7 +1103,7 @@ __global__ __launch_bounds__(kWsWaves * 64, 1) void nf4_gemm_bigws_kernel(const 
 // by all four tiles.
 // Each weight is read from HBM once for every row; the outputs are rounded
 // once and stored in the dtype, row-major with leading dimension ld.
-template <int DT, int NMT, int WV>
+template <int DT, int NMT, int WV, bool F32OUT>
 __device__ __forceinline__ void dense_bigm_wave(uint8_t* smem, const uint16_t* __restrict__ X,
                                                 const uint16_t* __restrict__ W, int NP, int group, int mt0, int M,
                                                 void* __restrict__ out, int64_t ld) {
@@ -1046,12 +1183,19 @@ __device__ __forceinline__ void dense_bigm_wave(uint8_t* smem, const uint16_t* _
         const int row = (mt0 + mt) * 32 + 8 * q4 + 4 * g + j;
         if (row < M)
 #pragma unroll
-          for (int nt = 0; nt < kBigNT; ++nt)
-            Elem<DT>::store((Te*)out, (int64_t)row * ld + (group * kBigNT + nt) * 32 + ln, acc[nt][mt][4 * q4 + j]);
+          for (int nt = 0; nt < kBigNT; ++nt) {
+            const int64_t o = (int64_t)row * ld + (group * kBigNT + nt) * 32 + ln;
+            if constexpr (F32OUT)
+              ((float*)out)[o] = acc[nt][mt][4 * q4 + j];
+            else
+              Elem<DT>::store((Te*)out, o, acc[nt][mt][4 * q4 + j]);
+          }
       }
 }
 
-template <int DT>
+// F32OUT: the fp32 sums are stored as they are (one split of partials, for the
+// prefill's epilogue kernels); grid.y runs over blocks of eight 32-row tiles.
+template <int DT, bool F32OUT>
 __global__ __launch_bounds__(kWaves * 64, 2) void dense_gemm_bigm_kernel(const uint16_t* __restrict__ X,
                                                                         const uint16_t* __restrict__ W, int NP,
                                                                         int mtiles, int M, void* __restrict__ out,
@@ -1059,14 +1203,14 @@ __global__ __launch_bounds__(kWaves * 64, 2) void dense_gemm_bigm_kernel(const u
   __shared__ __align__(256) uint8_t smem[2 * kBigBufUnit];
   const int group = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int mt0 = wave * 2;
+  const int mt0 = blockIdx.y * 8 + wave * 2;
   const int nmt = max(0, min(2, mtiles - mt0));
-#define PE_DBIGM_WAVE(N)                                                                       \
-  switch (wave) {                                                                              \
-    case 0: dense_bigm_wave<DT, N, 0>(smem, X, W, NP, group, mt0, M, out, ld); break;          \
-    case 1: dense_bigm_wave<DT, N, 1>(smem, X, W, NP, group, mt0, M, out, ld); break;          \
-    case 2: dense_bigm_wave<DT, N, 2>(smem, X, W, NP, group, mt0, M, out, ld); break;          \
-    default: dense_bigm_wave<DT, N, 3>(smem, X, W, NP, group, mt0, M, out, ld); break;         \
+#define PE_DBIGM_WAVE(N)                                                                            \
+  switch (wave) {                                                                                   \
+    case 0: dense_bigm_wave<DT, N, 0, F32OUT>(smem, X, W, NP, group, mt0, M, out, ld); break;       \
+    case 1: dense_bigm_wave<DT, N, 1, F32OUT>(smem, X, W, NP, group, mt0, M, out, ld); break;       \
+    case 2: dense_bigm_wave<DT, N, 2, F32OUT>(smem, X, W, NP, group, mt0, M, out, ld); break;       \
+    default: dense_bigm_wave<DT, N, 3, F32OUT>(smem, X, W, NP, group, mt0, M, out, ld); break;      \
   }
   if (nmt == 2) {
     PE_DBIGM_WAVE(2)
@@ -1515,6 +1659,7 @@ EpiArgs make_epi(int epi, int mc, int N, const void* bias, const void* resid, in
   e.status = nullptr;
   e.amax_keys = nullptr;
   e.amax_groups = 0;
+  e.tail = PeNormTail{};
   return e;
 }
 
@@ -1614,7 +1759,7 @@ int64_t pe_internal_gemm_rope_kv_bytes(int M, int N, int K, int wfmt) {
 // exchange between workgroups, the consumer sums them); one launch, M <= 64.
 int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M, int K,
                                 const void* w, const void* wabs, int N, float* partial, int64_t partial_bytes,
-                                int* splits, hipStream_t st) {
+                                int* splits, hipStream_t st, const PeNormTail* tail) {
   if (M > kMaxChunkRows || !partial || !splits) return PE_ERR_ARG;
   int rc = check_gemm_args(x, M, K, w, N, PE_EPI_STORE, nullptr, partial);
   if (rc != PE_OK) return rc;
@@ -1624,8 +1769,22 @@ int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx,
   const Plan p = make_plan(M, N, K, nf4, kEpiPartial);
   if (partial_bytes < (int64_t)p.S * M * N * 4) return PE_ERR_WORKSPACE;
   EpiArgs e = make_epi(kEpiPartial, M, N, nullptr, nullptr, 0, partial, N);
+  if (tail) {
+    // the rows are normed by the launch's last workgroups, which wait for all
+    // of them: the launch must be one round, resident at once
+    if (!tail->h || !tail->w || !tail->xn || !tail->counters || N % 4 || N > 4 * kTailVT * 2 ||
+        (tail->xn_tiled && N % 128) || (int64_t)p.groups * p.S > cu_count() || p.nl > 0)
+      return PE_ERR_ARG;
+    e.tail = *tail;
+  }
   *splits = p.S;
   return launch_gemm(nf4 ? nf4_fmt(wfmt) : dtype, p, st, (const uint16_t*)x, ldx, x_tiled, K, w, wabs, nullptr, e);
+}
+
+bool pe_internal_partials_tail_ok(int M, int N, int K, int wfmt) {
+  if (M <= 0 || M > kMaxChunkRows || N % 128 || N > 4 * kTailVT * 2 || K % 128) return false;
+  const Plan p = make_plan(M, N, K, pe_wfmt_nf4(wfmt), kEpiPartial);
+  return p.nl == 0 && (int64_t)p.groups * p.S <= cu_count();
 }
 
 int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int wfmt) {
@@ -1716,20 +1875,49 @@ int64_t pe_internal_nf4_bigm_partials_bytes(int M, int N, int K) {
 }
 
 int pe_internal_dense_bigm(const void* x_tiled, int M, int K, const void* w, int dtype, int N, void* out,
-                           int64_t ld_out, hipStream_t st) {
-  if (!x_tiled || !w || !out || M <= 0 || M > 8 * 32 || K % 128 || N % (32 * kBigNT) || ld_out < N)
-    return PE_ERR_ARG;
+                           int64_t ld_out, hipStream_t st, bool f32_out) {
+  if (!x_tiled || !w || !out || M <= 0 || K % 128 || N % (32 * kBigNT) || ld_out < N) return PE_ERR_ARG;
   const int np = K / 128;
-  const dim3 grid(N / (32 * kBigNT));
   const int mtiles = (M + 31) / 32;
-  if (dtype == PE_DTYPE_BF16)
-    dense_gemm_bigm_kernel<PE_DTYPE_BF16><<<grid, kWaves * 64, 0, st>>>((const uint16_t*)x_tiled,
-                                                                         (const uint16_t*)w, np, mtiles, M, out, ld_out);
+  const dim3 grid(N / (32 * kBigNT), (mtiles + 7) / 8);
+#define PE_DBIGM_LAUNCH(D, F)                                                                             \
+  dense_gemm_bigm_kernel<D, F><<<grid, kWaves * 64, 0, st>>>((const uint16_t*)x_tiled, (const uint16_t*)w, np, \
+                                                             mtiles, M, out, ld_out)
+  if (dtype == PE_DTYPE_BF16 && f32_out)
+    PE_DBIGM_LAUNCH(PE_DTYPE_BF16, true);
+  else if (dtype == PE_DTYPE_BF16)
+    PE_DBIGM_LAUNCH(PE_DTYPE_BF16, false);
+  else if (dtype == PE_DTYPE_F16 && f32_out)
+    PE_DBIGM_LAUNCH(PE_DTYPE_F16, true);
   else if (dtype == PE_DTYPE_F16)
-    dense_gemm_bigm_kernel<PE_DTYPE_F16><<<grid, kWaves * 64, 0, st>>>((const uint16_t*)x_tiled,
-                                                                        (const uint16_t*)w, np, mtiles, M, out, ld_out);
+    PE_DBIGM_LAUNCH(PE_DTYPE_F16, false);
   else
     return PE_ERR_ARG;
+#undef PE_DBIGM_LAUNCH
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
+// The prefill's NF4 linears: all M rows (A-tiled) in blocks of 256 rows on
+// grid.z, one K split, each weight dequantised once per row block. SwiGLU
+// (out_units > 0, bf16): the activation stored A-tiled; otherwise fp32 sums
+// y[M][N] (one split of partials).
+int pe_internal_nf4_prefill(const void* x_tiled, int M, int K, const void* w, const void* wabs, int N, float* y,
+                            void* act, int out_units, hipStream_t st) {
+  if (!x_tiled || !w || !wabs || M <= 0 || K % 128 || N % (32 * kBigNT)) return PE_ERR_ARG;
+  if (out_units ? (!act || out_units * 128 != N / 2) : !y) return PE_ERR_ARG;
+  const int units = K / 128, groups = N / (32 * kBigNT), mtiles = (M + 31) / 32;
+  const dim3 grid(groups, 1, (mtiles + 7) / 8);
+  if (out_units) {
+    EpiArgs e = make_epi(PE_EPI_SWIGLU, M, N, nullptr, nullptr, 0, act, 0);
+    e.out_units = out_units;
+    nf4_gemm_bigws_kernel<true><<<grid, kWsWaves * 64, 0, st>>>((const uint16_t*)x_tiled, (const uint8_t*)w,
+                                                                (const uint16_t*)wabs, units, units, mtiles, e);
+  } else {
+    EpiArgs e = make_epi(kEpiPartial, M, N, nullptr, nullptr, 0, y, N);
+    nf4_gemm_bigws_kernel<false><<<grid, kWsWaves * 64, 0, st>>>((const uint16_t*)x_tiled, (const uint8_t*)w,
+                                                                 (const uint16_t*)wabs, units, units, mtiles, e);
+  }
   PE_CHECK_LAUNCH();
   return PE_OK;
 }
@@ -1768,8 +1956,16 @@ int pe_internal_nf4_bigm_swiglu(const void* x_tiled, int M, int K, const void* w
   return PE_OK;
 }
 
+// A dense 16-bit pe_dense_gemm of more than 256 rows without bias or residual
+// packs X A-tiled into its workspace and runs the many-row kernel.
+static bool dense_many_rows(int M, int N, int K, int epilogue, const void* bias) {
+  return M > 4 * kMaxChunkRows && epilogue == PE_EPI_STORE && !bias && K % 128 == 0 && N % (32 * kBigNT) == 0;
+}
+
 extern "C" int64_t pe_gemm_workspace_bytes(int M, int N, int K, int wfmt, int dtype, int epilogue) {
   if (dtype == PE_DTYPE_F32 && wfmt == PE_WFMT_DENSE) return 0;
+  // the packed rows go after the counters, which other calls sharing the workspace rely on
+  if (wfmt == PE_WFMT_DENSE && dense_many_rows(M, N, K, epilogue, nullptr)) return kCounterBytes + xtile_bytes(M, K);
   if (M <= 0 || N <= 0 || K < 128) return kCounterBytes;
   // M runs as 64-row launches plus a shorter last one, whose plan (one M tile
   // instead of two) can need more split partials; the many-row SwiGLU linear
@@ -1877,6 +2073,15 @@ extern "C" int pe_dense_gemm(const void* x, int64_t ldx, int M, int K, const voi
     return PE_OK;
   }
   if (dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16) return PE_ERR_ARG;
+  if (dense_many_rows(M, N, K, epilogue, bias) && workspace && workspace_bytes >= kCounterBytes + xtile_bytes(M, K)) {
+    // every weight read once per 256 rows instead of once per 64-row launch;
+    // the A-tiled rows after the workspace's counters
+    if (!x || !w || !out || ld_out < N || ldx < K) return PE_ERR_ARG;
+    void* xt = (char*)workspace + kCounterBytes;
+    int rc = pe_internal_to_xtile(x, ldx, M, K, xt, st);
+    if (rc != PE_OK) return rc;
+    return pe_internal_dense_bigm(xt, M, K, w, dtype, N, out, ld_out, st);
+  }
   return mfma_gemm(dtype, x, ldx, M, K, w, nullptr, N, epilogue, bias, resid, ld_resid, out, ld_out, workspace,
                    workspace_bytes, st);
 }

@@ -33,10 +33,32 @@ PE_INTERNAL int pe_internal_linear(int wfmt, int dtype, const void* x, int64_t l
 
 // pe_gemm.hip: Y = X . W^T as split partials partial[S][M][N] fp32 (plain
 // stores, summed by the consumer in split order); *splits receives S. M <= 64.
+// The residual + RMSNorm a split-partial launch can apply itself (see
+// pe_internal_linear_partials): h[m] = round(h[m] + round(sum_s partial[s][m])),
+// then xn / xn_tiled / captures as pe_internal_residual_rmsnorm, with the same
+// arithmetic and summation order (bit-identical results).
+struct PeNormTail {
+  void* h;
+  const void* w;
+  float eps;
+  int mode;
+  void* xn;
+  void* xn_tiled;
+  void* cap_h;
+  int64_t ld_cap_h;
+  void* cap_xn;
+  int64_t ld_cap_xn;
+  int32_t* status;  // PE_ERR_LAUNCH if a waiting workgroup gave up (workgroups not all resident)
+  int* counters;    // two ints, zero before the launch and left zero
+};
 PE_INTERNAL int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M,
                                             int K, const void* w, const void* wabs, int N, float* partial,
-                                            int64_t partial_bytes, int* splits, hipStream_t st);
+                                            int64_t partial_bytes, int* splits, hipStream_t st,
+                                            const PeNormTail* tail = nullptr);
 PE_INTERNAL int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int wfmt);
+// Whether a split-partial launch of this shape can take a PeNormTail (one
+// round of workgroups, resident at once; N within the norm's row size).
+PE_INTERNAL bool pe_internal_partials_tail_ok(int M, int N, int K, int wfmt);
 
 // pe_gemm.hip: the q/k/v epilogue (bias, RoPE, q out, K/V appended at cache rows
 // row0 + row) and the SwiGLU epilogue (N / 2 outputs, A-tiled when out_units)
@@ -50,11 +72,21 @@ PE_INTERNAL int pe_internal_rope_kv_partials(const float* partial, int S, int M,
 // pe_gemm.hip: the NF4 GEMM for many rows (A-tiled X, 64 < M <= 256,
 // N % 128 == 0, fp16 absmax): each weight dequantised once for all rows;
 // fp32 split partials [S][M][N] (*splits receives S).
-// Dense 16-bit Y[M][N] = X . W^T for 64 < M <= 256 rows (X A-tiled, W in the
-// MFMA-tiled layout, K % 128 == 0, N % 128 == 0), each weight read once for all
-// rows; Y row-major in the dtype (leading dimension ld_out).
+// Dense 16-bit Y[M][N] = X . W^T for many rows (X A-tiled, W in the
+// MFMA-tiled layout, K % 128 == 0, N % 128 == 0), one workgroup per 128
+// columns and block of 256 rows, each weight read once per row block; Y
+// row-major (leading dimension ld_out) in the dtype, or the fp32 sums as they
+// are (f32_out: one split of partials for the prefill's epilogue kernels).
 PE_INTERNAL int pe_internal_dense_bigm(const void* x_tiled, int M, int K, const void* w, int dtype, int N, void* out,
-                                       int64_t ld_out, hipStream_t st);
+                                       int64_t ld_out, hipStream_t st, bool f32_out = false);
+// The prefill's NF4 linear over all M rows (A-tiled X, blocks of 256 rows, one
+// K split): fp32 sums y[M][N], or with out_units > 0 (the interleaved gate/up
+// weight, N = 2 * 128 * out_units) the SwiGLU activation stored A-tiled.
+PE_INTERNAL int pe_internal_nf4_prefill(const void* x_tiled, int M, int K, const void* w, const void* wabs, int N,
+                                        float* y, void* act, int out_units, hipStream_t st);
+// Row-major 16-bit [M][K] (leading dimension ld) -> the A-tiled layout
+// (K % 128 == 0; rows past M of the last 32-row tile are written as zeros).
+PE_INTERNAL int pe_internal_to_xtile(const void* x, int64_t ld, int M, int K, void* out, hipStream_t st);
 PE_INTERNAL int64_t pe_internal_nf4_bigm_partials_bytes(int M, int N, int K);
 PE_INTERNAL int pe_internal_nf4_bigm_partials(const void* x_tiled, int M, int K, const void* w, const void* wabs,
                                               int N, float* partial, int64_t partial_bytes, int* splits,
@@ -89,6 +121,7 @@ PE_INTERNAL int pe_internal_embed_rmsnorm(const int64_t* ids, int M, const void*
 // (head, row tile) pairs use the 1024 ints from kPassAttnCounterInt on, which
 // the last workgroup of each pair also returns to zero.
 constexpr int kGemmCounterInts = 7168;
+constexpr int kTailCounterInt = kGemmCounterInts - 2;  // two ints of the GEMM region: the norm tail's
 constexpr int kPassAttnCounterInt = 7168;
 
 // pe_attn.hip: pe_tree_attention whose output is A-tiled when out_units > 0

@@ -15,8 +15,6 @@
 
 #include <hip/hip_runtime.h>
 
-#include <rocblas/rocblas.h>
-
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -150,15 +148,18 @@ extern "C" int pe_version(void) { return 1; }
 constexpr int kFusedChunk = 64;  // rows per fused pass (causal passes are chunked)
 
 // ---------------------------------------------------------------------------
-// Prefill (a causal pass of more than kFusedChunk rows on a bf16 model, NF4 or
-// dense, with RoPE-paired q/k/v): every linear is dequantised (NF4) or untiled
-// (dense) once to row-major bf16 (in its tiled row order) and multiplied over all M rows by a rocBLAS GEMM with fp32
-// output; the fused pass's epilogue kernels then treat that output as one
-// split: RoPE + K/V append for q/k/v, SwiGLU for gate/up, residual + RMSNorm
-// (with the captures) after o and down. Attention runs once over all rows.
-// The weights are read once per pass instead of once per 64-row chunk; the
-// dequantisation costs about as much as four chunked passes, so shorter causal
-// passes stay chunked.
+// Prefill (a causal pass of more than 256 rows of a 16-bit model, NF4 or
+// dense, with RoPE-paired q/k/v and 128-dim heads): every linear runs once
+// over all M rows in blocks of 256 rows on the matrix cores
+// (pe_internal_nf4_prefill: each NF4 weight dequantised once per row block by
+// producer waves; pe_internal_dense_bigm: 16-bit tiled weights), with the
+// activations A-tiled between kernels. The GEMMs write fp32 sums that the
+// fused pass's epilogue kernels treat as one split: RoPE + K/V append for
+// q/k/v, SwiGLU for a dense gate/up (the NF4 gate/up stores the activation
+// itself), residual + RMSNorm (with the captures) after o and down.
+// Attention runs once over all rows, causally. NF4 weights with fp32 absmax
+// (checkpoint imports) are dequantised and tiled to 16-bit once per linear
+// and prefill. Shorter causal passes run as 64-row chunks of the fused pass.
 // ---------------------------------------------------------------------------
 constexpr int kPrefillMinRows = 4 * kFusedChunk + 1;
 bool prefill_path(const pe_model_desc* m, int M, int mask_mode) {
@@ -168,25 +169,24 @@ bool prefill_path(const pe_model_desc* m, int M, int mask_mode) {
   }();
   return on && M >= kPrefillMinRows && mask_mode == PE_MASK_CAUSAL &&
          (pe_wfmt_nf4(m->weight_format) || m->weight_format == PE_WFMT_DENSE) &&
-         m->qkv_layout == PE_QKV_ROPE_PAIRED && m->dtype == PE_DTYPE_BF16 && m->head_dim == 128 &&
-         m->hidden % 128 == 0 && m->intermediate_padded % 128 == 0;
+         m->qkv_layout == PE_QKV_ROPE_PAIRED && m->dtype != PE_DTYPE_F32 && m->head_dim == 128 &&
+         m->hidden % 128 == 0 && m->intermediate_padded % 128 == 0 && (m->num_heads * m->head_dim) % 128 == 0 &&
+         ((m->num_heads + 2 * m->num_kv_heads) * m->head_dim) % 128 == 0 && m->vocab % 128 == 0;
 }
 
 struct PrefillLayout {
-  int64_t h, xn, q, attn, act, y, wdeq, attn_ws, attn_ws_bytes, gemm, gemm_bytes, blas, blas_bytes, total;
+  int64_t h, xn, xn_t, q, attn, attn_t, act_t, y, wdeq, wtile, attn_ws, attn_ws_bytes, gemm, gemm_bytes, total;
 };
-constexpr int64_t kBlasWorkspace = 64ll << 20;
 
 PrefillLayout make_prefill_layout(const pe_model_desc* m, int M, int64_t kv_len) {
   PrefillLayout L;
   const int64_t H = m->hidden, qd = (int64_t)m->num_heads * m->head_dim;
   const int64_t nqkv = qd + 2ll * m->num_kv_heads * m->head_dim, ip = m->intermediate_padded;
-  // offset 0: the pass's counters and the lm_head GEMM's workspace, as in the
-  // fused layout (the GEMM and attention counter slices rest at zero between
-  // passes, whichever path ran last)
+  // offset 0: the pass's arrival counters, as in the fused layout (the GEMM
+  // and attention counter slices rest at zero between passes, whichever path
+  // ran last)
   L.gemm = 0;
-  L.gemm_bytes = align_up(std::max<int64_t>(
-      kCounterBytes, pe_gemm_workspace_bytes(kFusedChunk, m->vocab, m->hidden, PE_WFMT_DENSE, m->dtype, PE_EPI_STORE)));
+  L.gemm_bytes = align_up(kCounterBytes);
   int64_t off = L.gemm_bytes;
   auto take = [&](int64_t bytes) {
     const int64_t o = off;
@@ -195,40 +195,31 @@ PrefillLayout make_prefill_layout(const pe_model_desc* m, int M, int64_t kv_len)
   };
   L.h = take(M * H * 2);
   L.xn = take(M * H * 2);
+  L.xn_t = take(xtile_bytes(M, (int)H));
   L.q = take(M * qd * 2);
   L.attn = take(M * qd * 2);
-  L.act = take(M * ip * 2);
+  L.attn_t = take(xtile_bytes(M, (int)qd));
+  L.act_t = take(xtile_bytes(M, (int)ip));
   int64_t ny = nqkv;
   if (2 * ip > ny) ny = 2 * ip;
   if (H > ny) ny = H;
   L.y = take(M * ny * 4);
-  int64_t nw = nqkv * H;
-  if (2 * ip * H > nw) nw = 2 * ip * H;
-  if (H * ip > nw) nw = H * ip;
-  if (H * qd > nw) nw = H * qd;
-  L.wdeq = take(nw * 2);
+  L.wdeq = L.wtile = 0;
+  if (m->weight_format == PE_WFMT_NF4_F32ABS) {  // one linear dequantised, then tiled
+    int64_t nw = nqkv * H;
+    if (2 * ip * H > nw) nw = 2 * ip * H;
+    if (H * ip > nw) nw = H * ip;
+    if (H * qd > nw) nw = H * qd;
+    L.wdeq = take(nw * 2);
+    L.wtile = take(nw * 2);
+  }
   L.attn_ws_bytes = align_up(attention_workspace_bytes(M, m->num_heads, m->num_kv_heads, m->head_dim, kv_len,
                                                        m->dtype, m->attn_mode));
   L.attn_ws = take(L.attn_ws_bytes);
-  L.blas_bytes = kBlasWorkspace;
-  L.blas = take(L.blas_bytes);
   L.total = off;
   return L;
 }
 
-// One rocBLAS handle per device, made on first use; each call sets the stream
-// and hands rocBLAS its workspace from the pass's workspace.
-rocblas_handle blas_handle() {
-  static std::mutex mu;
-  static rocblas_handle handles[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!handles[dev] && rocblas_create_handle(&handles[dev]) != rocblas_status_success) handles[dev] = nullptr;
-  return handles[dev];
-}
-
-// y[M][N] (fp32) = x[M][K] . w[N][K]^T, bf16 operands, fp32 accumulation.
 // The lm_head over the final normed rows (row-major xn); with a->node_keys
 // (single-sequence 16-bit passes) the GEMM also writes each row's argmax keys.
 int lm_head(const pe_model_desc* m, const pe_pass_args* a, const void* xn, int M, void* ws, int64_t wsb,
@@ -241,45 +232,6 @@ int lm_head(const pe_model_desc* m, const pe_pass_args* a, const void* xn, int M
                        m->vocab, ws, wsb, st);
 }
 
-int blas_gemm(hipStream_t st, int M, int N, int K, const void* x, const void* w, float* y, void* bws,
-              int64_t bws_bytes) {
-  rocblas_handle hd = blas_handle();
-  if (!hd) return PE_ERR_LAUNCH;
-  if (rocblas_set_stream(hd, st) != rocblas_status_success) return PE_ERR_LAUNCH;
-  if (rocblas_set_workspace(hd, bws, (size_t)bws_bytes) != rocblas_status_success) return PE_ERR_LAUNCH;
-  const float alpha = 1.f, beta = 0.f;
-  // column-major: y^T [N][M] = (w viewed K x N)^T . (x viewed K x M)
-  const rocblas_status s = rocblas_gemm_ex(hd, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha,
-                                           w, rocblas_datatype_bf16_r, K, x, rocblas_datatype_bf16_r, K, &beta, y,
-                                           rocblas_datatype_f32_r, N, y, rocblas_datatype_f32_r, N,
-                                           rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-  return s == rocblas_status_success ? PE_OK : PE_ERR_LAUNCH;
-}
-
-int dequant(const pe_model_desc* m, const void* w, const void* a, int64_t N, int64_t K, void* out, hipStream_t st) {
-  if (m->weight_format == PE_WFMT_DENSE) return pe_internal_dense_untile(w, N, K, out, st);
-  if (m->weight_format == PE_WFMT_NF4_F32ABS)
-    return pe_nf4_dequant_f32abs((const uint8_t*)w, (const float*)a, N, K, (uint16_t*)out, st);
-  return pe_nf4_dequant((const uint8_t*)w, (const uint16_t*)a, N, K, (uint16_t*)out, st);
-}
-
-// The prefill weight copy: per layer q/k/v [nqkv][H], o [H][qd], gate/up
-// [2 ip][H], down [H][ip], row-major 16-bit, layer after layer.
-struct PrefillCopy {
-  int64_t off[4], layer;  // elements
-};
-PrefillCopy prefill_copy_layout(const pe_model_desc* m) {
-  const int64_t H = m->hidden, qd = (int64_t)m->num_heads * m->head_dim;
-  const int64_t nqkv = qd + 2ll * m->num_kv_heads * m->head_dim, ip = m->intermediate_padded;
-  PrefillCopy c;
-  c.off[0] = 0;
-  c.off[1] = c.off[0] + nqkv * H;
-  c.off[2] = c.off[1] + H * qd;
-  c.off[3] = c.off[2] + 2 * ip * H;
-  c.layer = c.off[3] + H * ip;
-  return c;
-}
-
 int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const PrefillLayout& Lp, hipStream_t st) {
   const int M = a->M;
   char* ws = (char*)a->workspace;
@@ -289,15 +241,16 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
   const int nqkv = (nh + 2 * nkv) * hd;
   void* h = ws + Lp.h;
   void* xn = ws + Lp.xn;
+  void* xn_t = ws + Lp.xn_t;
   void* q = ws + Lp.q;
   void* attn = ws + Lp.attn;
-  void* act = ws + Lp.act;
+  void* attn_t = ws + Lp.attn_t;
+  void* act_t = ws + Lp.act_t;
   float* y = (float*)(ws + Lp.y);
-  void* wdeq = ws + Lp.wdeq;
-  void* bws = ws + Lp.blas;
   const float scale = (float)(1.0 / std::sqrt((double)hd));
   const int64_t layer_stride = (int64_t)nkv * a->cache_capacity * hd * es;
   const int64_t fused_ld = (int64_t)a->num_features * H;
+  const bool nf4 = m->weight_format == PE_WFMT_NF4;
   int rc;
 #define PE_TRY(expr)            \
   do {                          \
@@ -320,75 +273,62 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
     }
     return PE_OK;
   };
-  const PrefillCopy pc = prefill_copy_layout(m);
-  // `which`: 0 q/k/v, 1 o, 2 gate/up, 3 down of layer l
-  auto linear = [&](const void* x, int K, const void* w, const void* ab, int N, int l, int which) -> int {
-    if (m->prefill_weights)
-      return blas_gemm(st, M, N, K, x, (const uint16_t*)m->prefill_weights + l * pc.layer + pc.off[which], y, bws,
-                       Lp.blas_bytes);
-    int r = dequant(m, w, ab, N, K, wdeq, st);
-    if (r != PE_OK) return r;
-    return blas_gemm(st, M, N, K, x, wdeq, y, bws, Lp.blas_bytes);
+  // y[M][N] (fp32) = x (A-tiled) . W^T over all rows
+  auto linear = [&](const void* xt, int K, const void* w, const void* ab, int N) -> int {
+    if (nf4) return pe_internal_nf4_prefill(xt, M, K, w, ab, N, y, nullptr, 0, st);
+    const void* wt = w;
+    if (m->weight_format == PE_WFMT_NF4_F32ABS) {
+      int r = pe_nf4_dequant_f32abs((const uint8_t*)w, (const float*)ab, N, K, (uint16_t*)(ws + Lp.wdeq), st);
+      if (r != PE_OK) return r;
+      r = pe_dense_repack(ws + Lp.wdeq, N, K, m->dtype, ws + Lp.wtile, st);
+      if (r != PE_OK) return r;
+      wt = ws + Lp.wtile;
+    }
+    return pe_internal_dense_bigm(xt, M, K, wt, m->dtype, N, y, N, st, true);
   };
 
   {
     const int f0 = slot_of(0);
     PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, embed_rows(m), h, H, m->attn_norm[0], m->rms_eps,
-                                     m->norm_mode, m->dtype, xn, nullptr, slot_ptr(f0), fused_ld, nullptr, 0, a->status, st));
+                                     m->norm_mode, m->dtype, xn, xn_t, slot_ptr(f0), fused_ld, nullptr, 0, a->status,
+                                     st));
     PE_TRY(copy_repeats(0, f0));
   }
+  const bool eager = m->attn_mode == PE_ATTN_EAGER;  // writes row-major output, packed afterwards
   for (int l = 0; l < L; ++l) {
     void* kc = (char*)a->k_cache + l * layer_stride;
     void* vc = (char*)a->v_cache + l * layer_stride;
-    PE_TRY(linear(xn, H, m->w_qkv[l], m->a_qkv[l], nqkv, l, 0));
+    PE_TRY(linear(xn_t, H, m->w_qkv[l], m->a_qkv ? m->a_qkv[l] : nullptr, nqkv));
     PE_TRY(pe_internal_rope_kv_partials(y, 1, M, nh, nkv, hd, m->b_qkv ? m->b_qkv[l] : nullptr, a->positions,
                                         m->rope_cos_sin, m->max_positions, q, kc, vc, a->cache_capacity,
                                         a->prefix_len, a->status, m->dtype, st));
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, PE_MASK_CAUSAL,
-                                      nullptr, 0, scale, m->dtype, attn, qd, 0, ws + Lp.attn_ws, Lp.attn_ws_bytes,
-                                      (int*)(ws + Lp.gemm) + kPassAttnCounterInt, st, m->attn_mode));
-    PE_TRY(linear(attn, qd, m->w_o[l], m->a_o[l], H, l, 1));
-    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, nullptr, nullptr, 0,
-                                        nullptr, 0, st));
-    PE_TRY(linear(xn, H, m->w_gu[l], m->a_gu[l], 2 * ip, l, 2));
-    PE_TRY(pe_internal_swiglu_partials(y, 1, M, 2 * ip, act, ip, 0, m->dtype, st));
-    PE_TRY(linear(act, ip, m->w_down[l], m->a_down[l], H, l, 3));
+                                      nullptr, 0, scale, m->dtype, eager ? attn : attn_t, qd, eager ? 0 : qd / 128,
+                                      ws + Lp.attn_ws, Lp.attn_ws_bytes, (int*)(ws + Lp.gemm) + kPassAttnCounterInt,
+                                      st, m->attn_mode));
+    if (eager) PE_TRY(pe_internal_to_xtile(attn, qd, M, qd, attn_t, st));
+    PE_TRY(linear(attn_t, qd, m->w_o[l], m->a_o ? m->a_o[l] : nullptr, H));
+    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, xn_t,
+                                        nullptr, 0, nullptr, 0, st));
+    if (nf4) {
+      PE_TRY(pe_internal_nf4_prefill(xn_t, M, H, m->w_gu[l], m->a_gu[l], 2 * ip, nullptr, act_t, ip / 128, st));
+    } else {
+      PE_TRY(linear(xn_t, H, m->w_gu[l], m->a_gu ? m->a_gu[l] : nullptr, 2 * ip));
+      PE_TRY(pe_internal_swiglu_partials(y, 1, M, 2 * ip, act_t, ip, ip / 128, m->dtype, st));
+    }
+    PE_TRY(linear(act_t, ip, m->w_down[l], m->a_down ? m->a_down[l] : nullptr, H));
     const bool last = l + 1 == L;
     const int fh = last ? -1 : slot_of(l + 1);
     const int fx = last ? slot_of(L) : -1;
     const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
     const int next_mode = last ? PE_NORM_HF : m->norm_mode;
-    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn, nullptr, slot_ptr(fh),
-                                        fused_ld, slot_ptr(fx), fused_ld, st));
+    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn, xn_t,
+                                        slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
-  if (a->logits) PE_TRY(lm_head(m, a, xn, M, ws + Lp.gemm, Lp.gemm_bytes, st));
+  // every lm_head weight read once per 256-row block
+  if (a->logits) PE_TRY(pe_internal_dense_bigm(xn_t, M, H, m->lm_head, m->dtype, m->vocab, a->logits, m->vocab, st));
 #undef PE_TRY
-  return PE_OK;
-}
-
-extern "C" int64_t pe_prefill_weights_bytes(const pe_model_desc* m) {
-  if (!m || m->num_layers <= 0 || m->dtype == PE_DTYPE_F32) return 0;
-  return prefill_copy_layout(m).layer * m->num_layers * 2;
-}
-
-extern "C" int pe_prefill_weights_fill(const pe_model_desc* m, void* out, int64_t bytes, void* stream) {
-  if (!m || !out || m->num_layers <= 0 || m->dtype == PE_DTYPE_F32) return PE_ERR_ARG;
-  if (bytes < pe_prefill_weights_bytes(m)) return PE_ERR_WORKSPACE;
-  hipStream_t st = (hipStream_t)stream;
-  const PrefillCopy pc = prefill_copy_layout(m);
-  const int64_t H = m->hidden, qd = (int64_t)m->num_heads * m->head_dim;
-  const int64_t nqkv = qd + 2ll * m->num_kv_heads * m->head_dim, ip = m->intermediate_padded;
-  const int64_t N[4] = {nqkv, H, 2 * ip, H}, K[4] = {H, qd, H, ip};
-  for (int l = 0; l < m->num_layers; ++l) {
-    const void* w[4] = {m->w_qkv[l], m->w_o[l], m->w_gu[l], m->w_down[l]};
-    const void* ab[4] = {m->a_qkv ? m->a_qkv[l] : nullptr, m->a_o ? m->a_o[l] : nullptr,
-                         m->a_gu ? m->a_gu[l] : nullptr, m->a_down ? m->a_down[l] : nullptr};
-    for (int i = 0; i < 4; ++i) {
-      const int rc = dequant(m, w[i], ab[i], N[i], K[i], (uint16_t*)out + l * pc.layer + pc.off[i], st);
-      if (rc != PE_OK) return rc;
-    }
-  }
   return PE_OK;
 }
 
@@ -489,6 +429,26 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   // pass 7.9% faster than the in-launch exchange).
   float* part = (float*)(ws + Lo.part);
   int S = 0;
+  // x . W^T as split partials, then the residual add and the RMSNorm that
+  // follows: inside the GEMM launch when its workgroups fit one round (its last
+  // workgroups norm the rows once every partial is stored), else as the
+  // residual + RMSNorm kernel
+  static const bool tail_on = [] {
+    const char* v = getenv("PE_GEMM_NORM_TAIL");
+    return v && atoi(v) != 0;
+  }();
+  auto partials_norm = [&](const void* x, int K, const void* w, const void* ab, const void* nw, int nmode,
+                           void* xt_out, void* cap_h, void* cap_xn) -> int {
+    if (tail_on && pe_internal_partials_tail_ok(M, H, K, wf)) {
+      PeNormTail t{h, nw, m->rms_eps, nmode, xn, xt_out, cap_h, fused_ld, cap_xn, fused_ld, a->status,
+                   (int*)gws + kTailCounterInt};
+      return pe_internal_linear_partials(wf, m->dtype, x, K, tiled, M, K, w, ab, H, part, Lo.part_bytes, &S, st, &t);
+    }
+    int r = pe_internal_linear_partials(wf, m->dtype, x, K, tiled, M, K, w, ab, H, part, Lo.part_bytes, &S, st);
+    if (r != PE_OK) return r;
+    return pe_internal_residual_rmsnorm(part, S, M, h, H, nw, m->rms_eps, nmode, m->dtype, xn, xt_out, cap_h,
+                                        fused_ld, cap_xn, fused_ld, st);
+  };
   for (int l = 0; l < L; ++l) {
     void* kc = (char*)a->k_cache + l * layer_stride;
     void* vc = (char*)a->v_cache + l * layer_stride;
@@ -507,10 +467,7 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
                                         a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
                                         Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st, m->attn_mode));
     const void* a_o = m->a_o ? m->a_o[l] : nullptr;
-    PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, tiled, M, qd, m->w_o[l], a_o, H, part,
-                                       Lo.part_bytes, &S, st));
-    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, xn_t,
-                                        nullptr, 0, nullptr, 0, st));
+    PE_TRY(partials_norm(x_attn, qd, m->w_o[l], a_o, m->mlp_norm[l], m->norm_mode, xn_t, nullptr, nullptr));
     const void* a_gu = m->a_gu ? m->a_gu[l] : nullptr;
     const void* a_down = m->a_down ? m->a_down[l] : nullptr;
     const bool last = l + 1 == L;
@@ -520,10 +477,8 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     const int next_mode = last ? PE_NORM_HF : m->norm_mode;
     PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, tiled, M, H, m->w_gu[l], a_gu, 2 * ip, PE_EPI_SWIGLU, nullptr,
                               nullptr, 0, x_act, ip, act_units, gws, gwsb, st));
-    PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_act, ip, tiled, M, ip, m->w_down[l], a_down, H, part,
-                                       Lo.part_bytes, &S, st));
-    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn,
-                                        last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
+    PE_TRY(partials_norm(x_act, ip, m->w_down[l], a_down, next_norm, next_mode, last ? nullptr : xn_t, slot_ptr(fh),
+                         slot_ptr(fx)));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
   if (a->logits) PE_TRY(lm_head(m, a, xn, M, gws, gwsb, st));

@@ -43,8 +43,6 @@ class DeviceDrafter:
     "v", "o", "gate", "up", "down"}]} (host or device tensors, logical [N][K]).
     ``capacity``: the most rows (context + k - 1) one call may run."""
 
-    library_gemm_rows = 256  # longer contexts run the input projections as library GEMMs
-
     def __init__(self, target: TargetModel, weights: dict, max_depth: int, capacity: int = 4096):
         tm = target.model
         s = tm.shape
@@ -73,12 +71,6 @@ class DeviceDrafter:
             raise ValueError("feat_proj's input width must be a multiple of hidden")
         self.feat_proj = tile(weights["feat_proj"])
         self.in_proj = tile(weights["in_proj"])
-        # row-major copies for contexts longer than a few chunks: the two input
-        # projections then run as one library GEMM each (rocBLAS / hipBLASLt, bf16
-        # in, fp32 accumulate, one rounding) instead of re-reading the weights once
-        # per 64-row chunk
-        self.feat_proj_rm = up(weights["feat_proj"]) if dt != torch.float32 else None
-        self.in_proj_rm = up(weights["in_proj"]) if dt != torch.float32 else None
         mask_in = torch.cat([up(weights["mask_emb"]), up(weights["h_shared"])]).view(1, -1)
         self.mask_vec = ops.linear(mask_in, s.hidden, dense=self.in_proj).view(-1)
 
@@ -92,11 +84,6 @@ class DeviceDrafter:
         core.norm_mode = _lib.PE_NORM_FP32_WEIGHT
         core.attn_mode = _lib.PE_ATTN_EAGER
         core._finish()
-        if dt == torch.bfloat16:
-            # context passes of more than 256 rows multiply row-major copies of
-            # the layer weights (2 bytes per weight) instead of untiling every
-            # linear per call
-            core.enable_prefill_weights()
         self.core = core
         self.runner = TargetModel(core, cache_capacity=capacity)
         self.cache = TreeKVCache(self.shape, dt, dev, capacity)
@@ -146,9 +133,8 @@ class DeviceDrafter:
         emb = ops.embed(ids, self.target.model.embed, self.runner.status)
         f = features.to(device=self.device, dtype=self.dtype).reshape(p * (self.feat_dim // H), H).contiguous()
         f = ops.rmsnorm(f, self.feat_norm, self.eps, mode=_lib.PE_NORM_FP32_WEIGHT).view(p, self.feat_dim)
-        if p > self.library_gemm_rows and self.in_proj_rm is not None:
-            feat = torch.nn.functional.linear(f, self.feat_proj_rm)
-            return torch.nn.functional.linear(torch.cat([emb, feat], dim=-1), self.in_proj_rm)
+        # pe_dense_gemm: more than 256 rows run the many-row kernel (each weight
+        # read once per 256 rows)
         feat = ops.linear(f, H, dense=self.feat_proj)
         return ops.linear(torch.cat([emb, feat], dim=-1).contiguous(), H, dense=self.in_proj)
 

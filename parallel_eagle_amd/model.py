@@ -85,7 +85,6 @@ class DeviceModel:
         self.attn_mode = _lib.PE_ATTN_SDPA
         self._desc = None
         self._keep = []
-        self._prefill_weights = None  # see enable_prefill_weights
 
     # ------------------------------------------------------------ construction
     @classmethod
@@ -285,28 +284,8 @@ class DeviceModel:
         d.w_o, d.a_o = parr("w_o"), parr("a_o")
         d.w_gu, d.a_gu = parr("w_gu"), parr("a_gu")
         d.w_down, d.a_down = parr("w_down"), parr("a_down")
-        d.prefill_weights = self._prefill_weights.data_ptr() if self._prefill_weights is not None else None
         self._desc = d
         return d
-
-    def enable_prefill_weights(self) -> int:
-        """Keep every layer's linears as row-major 16-bit copies on the device
-        (about 2 bytes per weight; 13 GB at the Llama-2-7B shape), filled once
-        here, so that prefills (causal passes of more than 256 rows) multiply
-        them directly instead of dequantising or untiling each linear per call.
-        Returns the bytes held."""
-        if self._prefill_weights is None:
-            self._desc = None
-            d = self.desc()
-            nbytes = int(_lib.load().pe_prefill_weights_bytes(C.byref(d)))
-            if nbytes <= 0:
-                raise RuntimeError("prefill weight copy: not available for this model (16-bit activations only)")
-            buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
-            _lib.check(_lib.load().pe_prefill_weights_fill(C.byref(d), buf.data_ptr(), nbytes, ops.stream_ptr()),
-                       "pe_prefill_weights_fill")
-            self._prefill_weights = buf
-            self._desc = None
-        return self._prefill_weights.numel()
 
     def workspace_bytes(self, m: int, kv_len: int) -> int:
         return int(_lib.load().pe_forward_workspace_bytes(C.byref(self.desc()), m, kv_len))

@@ -13,6 +13,8 @@ row), committed rows bit-exact. Ragged tree sizes (up to 64 nodes) and the
 graph-replayed step are checked too.
 """
 
+from dataclasses import replace
+
 import numpy as np
 import pytest
 import torch
@@ -21,8 +23,8 @@ from oracle import masks as om
 from oracle import verify as ov
 from oracle.model import OracleTarget
 from parallel_eagle_amd import batch as pb
-from parallel_eagle_amd import synth
-from parallel_eagle_amd.config import LLAMA2_7B_NF4, QWEN25_14B_NF4, WORKLOADS
+from parallel_eagle_amd import ops, synth
+from parallel_eagle_amd.config import LLAMA2_7B_NF4, QWEN25_14B_FP16, QWEN25_14B_NF4, WORKLOADS
 from parallel_eagle_amd.target import TargetModel
 from tests.test_gpu_target import _check_acceptance, _close, _fp32_oracle
 
@@ -31,22 +33,29 @@ DEV = "cuda"
 STREAM_BATCH_PREFIX = 8
 
 
-def _batch_case(shape, seed, prefixes, trees_spec, plant):
+def _batch_case(shape, seed, prefixes, trees_spec, plant, device_kv=False):
     """trees_spec: per sequence (depth, widths, top_k). Returns everything the
-    checks need, after the batched pass, walk and commit."""
+    checks need, after the batched pass, walk and commit. device_kv: the prefix
+    K/V drawn on the device (no host copy for an oracle; property tests)."""
     B = len(prefixes)
     cap = max(prefixes) + 80
-    tm = TargetModel.synthetic(shape, seed=seed, device=DEV, keep_logical=True, norm_noise=0.1, cache_capacity=cap)
+    tm = TargetModel.synthetic(shape, seed=seed, device=DEV, keep_logical=not device_kv, norm_noise=0.1,
+                               cache_capacity=cap)
     V = shape.vocab
     cache = pb.BatchKVCache(tm, B, cap)
     kv_host = []
+    if device_kv:
+        ops.fill_normal(cache.k, seed, synth.STREAM_KV, 1.0)
+        ops.fill_normal(cache.v, seed, synth.STREAM_KV_V, 1.0)
     for b, P in enumerate(prefixes):
+        cache.seq(b).seq_len = P
+        if device_kv:
+            continue
         g = torch.Generator().manual_seed(1000 * seed + b)
         k = torch.randn(shape.num_layers, shape.num_kv_heads, P, shape.head_dim, generator=g).to(tm.dtype)
         v = torch.randn(shape.num_layers, shape.num_kv_heads, P, shape.head_dim, generator=g).to(tm.dtype)
         cache.k[b, :, :, :P] = k.to(DEV)
         cache.v[b, :, :, :P] = v.to(DEV)
-        cache.seq(b).seq_len = P
         kv_host.append((k, v))
     g = torch.Generator().manual_seed(seed)
     roots = torch.randn(B, V, generator=g).to(tm.dtype)
@@ -68,8 +77,12 @@ def _batch_case(shape, seed, prefixes, trees_spec, plant):
                 row = lg[trees.row0[b] + chains[b][d - 1]]
                 synth.set_token(tokens[b], parents[b], chains[b][d], int(row.float().argmax()), V)
     lg, fu, trees = pb.forward_tree_batch(tm, tokens, parents, cache)
-    pre_k = [cache.k[b, :, :, : prefixes[b] + trees.rows[b]].float().cpu().numpy() for b in range(B)]
-    pre_v = [cache.v[b, :, :, : prefixes[b] + trees.rows[b]].float().cpu().numpy() for b in range(B)]
+    if device_kv:  # pre-commit rows kept on the device
+        pre_k = [cache.k[b, :, :, : prefixes[b] + trees.rows[b]].clone() for b in range(B)]
+        pre_v = [cache.v[b, :, :, : prefixes[b] + trees.rows[b]].clone() for b in range(B)]
+    else:
+        pre_k = [cache.k[b, :, :, : prefixes[b] + trees.rows[b]].float().cpu().numpy() for b in range(B)]
+        pre_v = [cache.v[b, :, :, : prefixes[b] + trees.rows[b]].float().cpu().numpy() for b in range(B)]
     out = pb.accept_batch_device(roots.to(DEV), lg, trees)
     pb.commit_batch(tm, cache, trees, out)
     res = [(row[2: 2 + row[0]], row[1]) for row in out.cpu().tolist()]
@@ -81,7 +94,7 @@ def _check_sequences(shape, c, tol=2e-2):
     hw = c["tm"].model.host_weights()
     orc = OracleTarget(shape, hw)
     orc.cache_dequant = True
-    o32 = _fp32_oracle(shape, hw)
+    o32 = _fp32_oracle(shape, hw, orc)
     verdicts = []
     for b, P in enumerate(c["prefixes"]):
         tokens, parents = c["tokens"][b], c["parents"][b]
@@ -143,22 +156,15 @@ def test_batched_ragged_tree_sizes_7b_width():
     print("verdicts", verdicts, "accepted", [len(r[0]) for r in c["res"]])
 
 
-def test_batch_verify_step_graph_replays_match_eager():
-    """BatchVerifyStep (masks -> batched pass -> walk -> ragged compaction), eager
-    and replayed from a HIP graph, equals the eager batch API bit for bit, with
-    eager work between the replays."""
-    shape = QWEN25_14B_NF4.reduced(2, feature_layers=(1, 2, 2), vocab=16384)
-    prefixes = [700, 1500, 3100, 520]
-    spec = [(5, (4, 5, 5, 6, 6), 4)] * len(prefixes)
-    c = _batch_case(shape, 7, prefixes, spec, plant=lambda b: 2 + b % 3)
+def _graph_replays_equal_eager(c, prefixes):
     cache, tm = c["cache"], c["tm"]
     want = c["res"]
     k_e = [cache.k[b, :, :, : cache.seq(b).seq_len].clone() for b in range(len(prefixes))]
     # restore the pre-commit caches and lengths, then run the step
     for b, P in enumerate(prefixes):
         T = c["trees"].rows[b]
-        cache.k[b, :, :, : P + T] = torch.from_numpy(c["pre_k"][b]).to(tm.dtype).to(DEV)
-        cache.v[b, :, :, : P + T] = torch.from_numpy(c["pre_v"][b]).to(tm.dtype).to(DEV)
+        cache.k[b, :, :, : P + T] = torch.as_tensor(c["pre_k"][b]).to(tm.dtype).to(DEV)
+        cache.v[b, :, :, : P + T] = torch.as_tensor(c["pre_v"][b]).to(tm.dtype).to(DEV)
         cache.seq(b).seq_len = P
     step = pb.BatchVerifyStep(tm, cache, c["tokens"], c["parents"])
     step.root.copy_(c["roots"].to(DEV))
@@ -173,3 +179,62 @@ def test_batch_verify_step_graph_replays_match_eager():
         cache.k[:, :, :, max(prefixes):].normal_()
         step.logits.zero_()
         torch.cuda.synchronize()
+
+
+def test_batch_verify_step_graph_replays_match_eager():
+    """BatchVerifyStep (masks -> batched pass -> walk -> ragged compaction), eager
+    and replayed from a HIP graph, equals the eager batch API bit for bit, with
+    eager work between the replays."""
+    shape = QWEN25_14B_NF4.reduced(2, feature_layers=(1, 2, 2), vocab=16384)
+    prefixes = [700, 1500, 3100, 520]
+    spec = [(5, (4, 5, 5, 6, 6), 4)] * len(prefixes)
+    c = _batch_case(shape, 7, prefixes, spec, plant=lambda b: 2 + b % 3)
+    _graph_replays_equal_eager(c, prefixes)
+
+
+def test_batched_workload_at_full_depth():
+    """The batched workload itself: the 48-layer Qwen2.5-14B-shaped NF4 model
+    with its 152064-token vocabulary, eight sequences over the workload's
+    prefixes (drawn from [512, 4096]), 26-node trees. Held to properties: every
+    logit finite, each sequence's planted chain of the device's own greedy
+    tokens (1 to 5 deep) accepted to its depth, the ragged commit moving exactly
+    the accepted rows, and the recorded step's replays equal to the eager batch
+    API bit for bit."""
+    wl = WORKLOADS["qwen2.5-14b-nf4-B8-T26"]
+    prefixes = (synth.uniform_int(3, STREAM_BATCH_PREFIX, wl.batch, wl.prefix_len - wl.prefix_min + 1)
+                + wl.prefix_min).tolist()
+    spec = [(wl.depth, wl.widths, wl.top_k)] * wl.batch
+    plant = lambda b: 1 + b % 5  # noqa: E731
+    c = _batch_case(wl.model, 3, prefixes, spec, plant=plant, device_kv=True)
+    assert c["trees"].M == 208
+    assert bool(torch.isfinite(c["lg"].float()).all()) and bool(torch.isfinite(c["fu"].float()).all())
+    for b, P in enumerate(prefixes):
+        path = c["res"][b][0]
+        assert path[: len(c["chains"][b])] == c["chains"][b], f"sequence {b}: {path} vs {c['chains'][b]}"
+        n = P + len(path)
+        got = c["cache"].k[b, :, :, :n]
+        assert torch.equal(got[:, :, :P], c["pre_k"][b][:, :, :P])
+        for i, t in enumerate(path):
+            assert torch.equal(got[:, :, P + i], c["pre_k"][b][:, :, P + t])
+    print("prefixes", prefixes, "accepted", [len(r[0]) for r in c["res"]])
+    _graph_replays_equal_eager(c, prefixes)
+
+
+@pytest.mark.parametrize("case", ["nf4-2x26", "dense-bf16-3x26"])
+def test_row_major_batched_branch(case):
+    """Batched passes that take the row-major branch (64-row launches over all
+    sequences' rows, each row's K/V at its own sequence's slot): an NF4 batch of
+    52 rows (two 26-node trees) and a dense bf16 batch (three trees, 78 rows,
+    the GQA 40/8 width with q/k/v bias); each sequence against the oracle's
+    batch-1 step, the ragged commit bit-exact."""
+    spec7 = (5, (4, 5, 5, 6, 6), 4)
+    if case == "nf4-2x26":
+        shape = LLAMA2_7B_NF4.reduced(1, feature_layers=(1, 1, 1))
+        prefixes = [300, 700]
+    else:
+        shape = replace(QWEN25_14B_FP16.reduced(1, feature_layers=(0, 1, 1), vocab=16384), dtype="bfloat16")
+        prefixes = [100, 513, 1024]
+    c = _batch_case(shape, 9, prefixes, [spec7] * len(prefixes), plant=lambda b: 1 + b % 3)
+    assert c["trees"].M == 26 * len(prefixes)
+    verdicts = _check_sequences(shape, c)
+    print(case, "verdicts", verdicts, "accepted", [len(r[0]) for r in c["res"]])

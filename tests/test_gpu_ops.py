@@ -47,6 +47,15 @@ def _eager_ctypes(tm, cache, root, tok, par, P):
     return bits, pos, dep, lg, fu, out
 
 
+def _same(got, want):
+    """(bits, positions, depths, logits, fused, walk result) equal; of the walk's
+    result only [|path|, bonus, path] is written."""
+    for a, b in zip(got[:5], want[:5]):
+        assert torch.equal(a, b)
+    n = int(want[5][0])
+    assert torch.equal(got[5][: 2 + n], want[5][: 2 + n])
+
+
 def _through_ops(h, cache, root, tok, par, P, ws, status, scratch):
     bits, pos, dep = torch.ops.pe.tree_masks(par, P, 1, status)
     lg, fu = torch.ops.pe.verify_pass(h, tok, pos, bits, cache.k, cache.v, P, ws, status)
@@ -75,8 +84,7 @@ def test_torch_ops_equal_the_ctypes_path_eagerly_and_in_a_graph():
     cache.v.copy_(v0)
     got = _through_ops(h, cache, root, tok, par, P, ws, status, scratch)
     torch.cuda.synchronize()
-    for a, b in zip(got, want):
-        assert torch.equal(a, b)
+    _same(got, want)
     assert torch.equal(cache.k, k_want) and torch.equal(cache.v, v_want)
     assert int(status[0]) == 0
     # captured in a HIP graph, replayed with eager work in between
@@ -91,8 +99,7 @@ def test_torch_ops_equal_the_ctypes_path_eagerly_and_in_a_graph():
         cache.v.copy_(v0)
         g.replay()
         torch.cuda.synchronize()
-        for a, b in zip(outs, want):
-            assert torch.equal(a, b), rep
+        _same(outs, want)
         assert torch.equal(cache.k, k_want) and torch.equal(cache.v, v_want), rep
         outs[3].zero_()
         cache.k[:, :, P:].normal_()
