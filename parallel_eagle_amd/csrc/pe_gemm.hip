@@ -85,9 +85,6 @@ struct EpiArgs {
   int32_t* status;
   uint64_t* amax_keys;  // kEpiArgmax: [M][amax_groups]
   int amax_groups;
-  // kEpiPartial with tail.w set: the launch's last workgroups apply the
-  // residual + RMSNorm to the summed partials (see partial_norm_tail)
-  PeNormTail tail;
 };
 
 __device__ __forceinline__ int64_t kv_row_elem(const EpiArgs& e, int row) {
@@ -292,9 +289,7 @@ __device__ __forceinline__ void lds_barrier() {
 // ---------------------------------------------------------------------------
 constexpr int kWaves = 4;             // waves per GEMM workgroup (K slices)
 constexpr int kCounterBytes = 32768;  // per-column-group arrival counters at the head of the workspace
-// the last two GEMM counters belong to the norm tail of split-partial launches
-// (kTailCounterInt); the rest of the counter area belongs to attention
-constexpr int kMaxGroups = kTailCounterInt;
+constexpr int kMaxGroups = kGemmCounterInts;  // the rest of the counter area belongs to attention
 constexpr int kMaxSplits = 16;
 
 // Epilogue of one output row of a column group: v[nt] is the lane's column of
@@ -327,118 +322,6 @@ __host__ __device__ constexpr int64_t partial_bytes_of(int S, int groups, int MT
 // accesses of 16 consecutive lanes hit 64 distinct banks.
 constexpr int kRedLane = 20;
 __host__ __device__ constexpr int red_floats(int KW, int NT, int MT) { return KW * NT * MT * 64 * kRedLane; }
-
-// ---------------------------------------------------------------------------
-// Norm tail of a split-partial launch (o and down of the fused pass). The
-// residual + RMSNorm of a row needs every column group's and every split's
-// partial of that row, so it cannot start before the whole launch has stored
-// its partials. The launch holds one round of workgroups, all resident at
-// once; every workgroup stores its partials agent-coherent and counts itself,
-// and the last W = min(M, workgroups) to arrive wait (bounded) for the count
-// to reach every workgroup, then take rows w, w + W, ... each. The arithmetic
-// and its order are residual_rmsnorm_kernel's: the split partials summed in
-// split order, h = round(h + round(sum)), the squares summed per thread of a
-// 1024-thread row (the norm kernel's) as this workgroup's threads replaying
-// those 1024 in turn, wave sums, then the 16 wave sums in order; the results
-// are bit-identical to the norm kernel's. The last waiter sets the two
-// counters back to zero.
-// ---------------------------------------------------------------------------
-constexpr int kTailVT = 1024;       // the norm kernel's threads per row
-constexpr int kTailSpin = 1 << 20;  // polls (about 64 clocks apart) before a wait gives up
-
-template <int DT, int NTHR>
-__device__ void tail_norm_row(const EpiArgs& e, int S, int m, __amdgpu_buffer_rsrc_t rp, float* lds) {
-  typedef Elem<DT> E;
-  typedef typename E::T T;
-  constexpr int J = kTailVT / NTHR;  // norm-kernel threads replayed by each thread
-  const PeNormTail& t = e.tail;
-  const int H = e.N, nchunk = H >> 2;
-  const int chv = (nchunk + kTailVT - 1) / kTailVT;  // 1 or 2 chunks per norm-kernel thread
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  T* hr = (T*)t.h + (int64_t)m * H;
-  float v[J][2][4];
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int vt = threadIdx.x + NTHR * j;
-    float ss = 0.f;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int ch = vt + kTailVT * c;
-      if (c >= chv || ch >= nchunk) continue;
-      float a[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < S; ++sp) {
-        const f32x4_t pv = load_agent_x4(rp, (uint32_t)((((int64_t)sp * e.M + m) * H + 4 * ch) * 4));
-#pragma unroll
-        for (int q = 0; q < 4; ++q) a[q] = a[q] + pv[q];
-      }
-      float hv[4];
-      Vec4<DT>::load(hr + 4 * ch, hv);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[j][c][q] = E::round(__fadd_rn(hv[q], E::round(a[q])));
-      Vec4<DT>::store(hr + 4 * ch, v[j][c]);
-      if (t.cap_h) Vec4<DT>::store((T*)t.cap_h + (int64_t)m * t.ld_cap_h + 4 * ch, v[j][c]);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) ss = __fadd_rn(ss, __fmul_rn(v[j][c][q], v[j][c][q]));
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) lds[wave + (NTHR / 64) * j] = ss;
-  }
-  __syncthreads();
-  float tot = 0.f;
-#pragma unroll
-  for (int i = 0; i < kTailVT / 64; ++i) tot += lds[i];
-  const float inv = 1.0f / sqrtf(tot / (float)H + t.eps);
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int vt = threadIdx.x + NTHR * j;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int ch = vt + kTailVT * c;
-      if (c >= chv || ch >= nchunk) continue;
-      float wv[4], o[4];
-      Vec4<DT>::load((const T*)t.w + 4 * ch, wv);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) o[q] = norm_out<E>(t.mode, v[j][c][q], inv, wv[q]);
-      Vec4<DT>::store((T*)t.xn + (int64_t)m * H + 4 * ch, o);
-      if (t.xn_tiled) Vec4<DT>::store((T*)t.xn_tiled + xtile_index(m, 4 * ch, H >> 7), o);
-      if (t.cap_xn) Vec4<DT>::store((T*)t.cap_xn + (int64_t)m * t.ld_cap_xn + 4 * ch, o);
-    }
-  }
-  __syncthreads();  // lds is reused by the next row
-}
-
-// Called by every thread of the workgroup once its partial stores are issued.
-template <int DT, int NTHR>
-__device__ void partial_norm_tail(const EpiArgs& e, int S, float* lds) {
-  int* flag = (int*)lds;
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's agent-coherent stores are acknowledged
-  __syncthreads();
-  const int G = gridDim.x * gridDim.y, W = min(e.M, G);
-  int* const arrived = e.tail.counters;
-  int* const done = e.tail.counters + 1;
-  if (threadIdx.x == 0) flag[0] = __hip_atomic_fetch_add(arrived, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  const int a = flag[0];
-  if (a < G - W) return;
-  if (threadIdx.x == 0) {
-    int it = 0;
-    while (__hip_atomic_load(arrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < G && ++it < kTailSpin)
-      __builtin_amdgcn_s_sleep(1);
-    flag[1] = it < kTailSpin;
-    if (it >= kTailSpin && e.tail.status) atomicOr(e.tail.status, PE_ERR_LAUNCH);
-  }
-  __syncthreads();
-  const bool ok = flag[1] != 0;
-  __syncthreads();  // flag is overwritten by the rows' sums
-  if (ok) {
-    const __amdgpu_buffer_rsrc_t rp = agent_rsrc(e.out, (uint32_t)((int64_t)S * e.M * e.N * 4));
-    for (int m = a - (G - W); m < e.M; m += W) tail_norm_row<DT, NTHR>(e, S, m, rp, lds);
-  }
-  if (threadIdx.x == 0 && __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == W - 1) {
-    __hip_atomic_store(arrived, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
 
 template <int ADT, int NT, int MT, int KW = kWaves>
 __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red, int group, int split, int S,
@@ -477,35 +360,16 @@ __device__ __forceinline__ void finish_tile(f32x16_t (&acc)[NT][MT], float* red,
     }
 
   if (e.op == kEpiPartial) {
-    if (e.tail.w) {
-      // agent-coherent stores: the norm tail reads them from other XCDs
-      const __amdgpu_buffer_rsrc_t ro = agent_rsrc(e.out, (uint32_t)((int64_t)S * e.M * e.N * 4));
+    float* out = (float*)e.out + (int64_t)split * e.M * e.N;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int row = mt * 32 + 8 * wave + 4 * g + j;
-          if (row < e.M)
+      for (int j = 0; j < 4; ++j) {
+        const int row = mt * 32 + 8 * wave + 4 * g + j;
+        if (row < e.M)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-              __builtin_amdgcn_raw_buffer_store_b32(
-                  __float_as_uint(v[mt][j][nt]), ro,
-                  (uint32_t)((((int64_t)split * e.M + row) * e.N + (group * NT + nt) * 32 + ln) * 4), 0, kCpolSC1);
-        }
-      // waves past kWaves of an eight-wave workgroup have left after the reduction
-      partial_norm_tail<ADT, kWaves * 64>(e, S, red);
-    } else {
-      float* out = (float*)e.out + (int64_t)split * e.M * e.N;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int row = mt * 32 + 8 * wave + 4 * g + j;
-          if (row < e.M)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) out[(int64_t)row * e.N + (group * NT + nt) * 32 + ln] = v[mt][j][nt];
-        }
-    }
+          for (int nt = 0; nt < NT; ++nt) out[(int64_t)row * e.N + (group * NT + nt) * 32 + ln] = v[mt][j][nt];
+      }
     return;
   }
   if (S > 1) {
@@ -1659,7 +1523,6 @@ EpiArgs make_epi(int epi, int mc, int N, const void* bias, const void* resid, in
   e.status = nullptr;
   e.amax_keys = nullptr;
   e.amax_groups = 0;
-  e.tail = PeNormTail{};
   return e;
 }
 
@@ -1759,7 +1622,7 @@ int64_t pe_internal_gemm_rope_kv_bytes(int M, int N, int K, int wfmt) {
 // exchange between workgroups, the consumer sums them); one launch, M <= 64.
 int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M, int K,
                                 const void* w, const void* wabs, int N, float* partial, int64_t partial_bytes,
-                                int* splits, hipStream_t st, const PeNormTail* tail) {
+                                int* splits, hipStream_t st) {
   if (M > kMaxChunkRows || !partial || !splits) return PE_ERR_ARG;
   int rc = check_gemm_args(x, M, K, w, N, PE_EPI_STORE, nullptr, partial);
   if (rc != PE_OK) return rc;
@@ -1769,22 +1632,8 @@ int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx,
   const Plan p = make_plan(M, N, K, nf4, kEpiPartial);
   if (partial_bytes < (int64_t)p.S * M * N * 4) return PE_ERR_WORKSPACE;
   EpiArgs e = make_epi(kEpiPartial, M, N, nullptr, nullptr, 0, partial, N);
-  if (tail) {
-    // the rows are normed by the launch's last workgroups, which wait for all
-    // of them: the launch must be one round, resident at once
-    if (!tail->h || !tail->w || !tail->xn || !tail->counters || N % 4 || N > 4 * kTailVT * 2 ||
-        (tail->xn_tiled && N % 128) || (int64_t)p.groups * p.S > cu_count() || p.nl > 0)
-      return PE_ERR_ARG;
-    e.tail = *tail;
-  }
   *splits = p.S;
   return launch_gemm(nf4 ? nf4_fmt(wfmt) : dtype, p, st, (const uint16_t*)x, ldx, x_tiled, K, w, wabs, nullptr, e);
-}
-
-bool pe_internal_partials_tail_ok(int M, int N, int K, int wfmt) {
-  if (M <= 0 || M > kMaxChunkRows || N % 128 || N > 4 * kTailVT * 2 || K % 128) return false;
-  const Plan p = make_plan(M, N, K, pe_wfmt_nf4(wfmt), kEpiPartial);
-  return p.nl == 0 && (int64_t)p.groups * p.S <= cu_count();
 }
 
 int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int wfmt) {

@@ -33,32 +33,10 @@ PE_INTERNAL int pe_internal_linear(int wfmt, int dtype, const void* x, int64_t l
 
 // pe_gemm.hip: Y = X . W^T as split partials partial[S][M][N] fp32 (plain
 // stores, summed by the consumer in split order); *splits receives S. M <= 64.
-// The residual + RMSNorm a split-partial launch can apply itself (see
-// pe_internal_linear_partials): h[m] = round(h[m] + round(sum_s partial[s][m])),
-// then xn / xn_tiled / captures as pe_internal_residual_rmsnorm, with the same
-// arithmetic and summation order (bit-identical results).
-struct PeNormTail {
-  void* h;
-  const void* w;
-  float eps;
-  int mode;
-  void* xn;
-  void* xn_tiled;
-  void* cap_h;
-  int64_t ld_cap_h;
-  void* cap_xn;
-  int64_t ld_cap_xn;
-  int32_t* status;  // PE_ERR_LAUNCH if a waiting workgroup gave up (workgroups not all resident)
-  int* counters;    // two ints, zero before the launch and left zero
-};
 PE_INTERNAL int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M,
                                             int K, const void* w, const void* wabs, int N, float* partial,
-                                            int64_t partial_bytes, int* splits, hipStream_t st,
-                                            const PeNormTail* tail = nullptr);
+                                            int64_t partial_bytes, int* splits, hipStream_t st);
 PE_INTERNAL int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int wfmt);
-// Whether a split-partial launch of this shape can take a PeNormTail (one
-// round of workgroups, resident at once; N within the norm's row size).
-PE_INTERNAL bool pe_internal_partials_tail_ok(int M, int N, int K, int wfmt);
 
 // pe_gemm.hip: the q/k/v epilogue (bias, RoPE, q out, K/V appended at cache rows
 // row0 + row) and the SwiGLU epilogue (N / 2 outputs, A-tiled when out_units)
@@ -121,7 +99,6 @@ PE_INTERNAL int pe_internal_embed_rmsnorm(const int64_t* ids, int M, const void*
 // (head, row tile) pairs use the 1024 ints from kPassAttnCounterInt on, which
 // the last workgroup of each pair also returns to zero.
 constexpr int kGemmCounterInts = 7168;
-constexpr int kTailCounterInt = kGemmCounterInts - 2;  // two ints of the GEMM region: the norm tail's
 constexpr int kPassAttnCounterInt = 7168;
 
 // pe_attn.hip: pe_tree_attention whose output is A-tiled when out_units > 0

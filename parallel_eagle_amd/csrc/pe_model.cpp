@@ -429,26 +429,6 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   // pass 7.9% faster than the in-launch exchange).
   float* part = (float*)(ws + Lo.part);
   int S = 0;
-  // x . W^T as split partials, then the residual add and the RMSNorm that
-  // follows: inside the GEMM launch when its workgroups fit one round (its last
-  // workgroups norm the rows once every partial is stored), else as the
-  // residual + RMSNorm kernel
-  static const bool tail_on = [] {
-    const char* v = getenv("PE_GEMM_NORM_TAIL");
-    return v && atoi(v) != 0;
-  }();
-  auto partials_norm = [&](const void* x, int K, const void* w, const void* ab, const void* nw, int nmode,
-                           void* xt_out, void* cap_h, void* cap_xn) -> int {
-    if (tail_on && pe_internal_partials_tail_ok(M, H, K, wf)) {
-      PeNormTail t{h, nw, m->rms_eps, nmode, xn, xt_out, cap_h, fused_ld, cap_xn, fused_ld, a->status,
-                   (int*)gws + kTailCounterInt};
-      return pe_internal_linear_partials(wf, m->dtype, x, K, tiled, M, K, w, ab, H, part, Lo.part_bytes, &S, st, &t);
-    }
-    int r = pe_internal_linear_partials(wf, m->dtype, x, K, tiled, M, K, w, ab, H, part, Lo.part_bytes, &S, st);
-    if (r != PE_OK) return r;
-    return pe_internal_residual_rmsnorm(part, S, M, h, H, nw, m->rms_eps, nmode, m->dtype, xn, xt_out, cap_h,
-                                        fused_ld, cap_xn, fused_ld, st);
-  };
   for (int l = 0; l < L; ++l) {
     void* kc = (char*)a->k_cache + l * layer_stride;
     void* vc = (char*)a->v_cache + l * layer_stride;
@@ -467,7 +447,10 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
                                         a->tree_bits, a->bits_words, scale, m->dtype, x_attn, qd, attn_units, aws,
                                         Lo.attn_ws_bytes, (int*)gws + kPassAttnCounterInt, st, m->attn_mode));
     const void* a_o = m->a_o ? m->a_o[l] : nullptr;
-    PE_TRY(partials_norm(x_attn, qd, m->w_o[l], a_o, m->mlp_norm[l], m->norm_mode, xn_t, nullptr, nullptr));
+    PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, tiled, M, qd, m->w_o[l], a_o, H, part,
+                                       Lo.part_bytes, &S, st));
+    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, xn_t,
+                                        nullptr, 0, nullptr, 0, st));
     const void* a_gu = m->a_gu ? m->a_gu[l] : nullptr;
     const void* a_down = m->a_down ? m->a_down[l] : nullptr;
     const bool last = l + 1 == L;
@@ -477,8 +460,10 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     const int next_mode = last ? PE_NORM_HF : m->norm_mode;
     PE_TRY(pe_internal_linear(wf, m->dtype, x_norm, H, tiled, M, H, m->w_gu[l], a_gu, 2 * ip, PE_EPI_SWIGLU, nullptr,
                               nullptr, 0, x_act, ip, act_units, gws, gwsb, st));
-    PE_TRY(partials_norm(x_act, ip, m->w_down[l], a_down, next_norm, next_mode, last ? nullptr : xn_t, slot_ptr(fh),
-                         slot_ptr(fx)));
+    PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_act, ip, tiled, M, ip, m->w_down[l], a_down, H, part,
+                                       Lo.part_bytes, &S, st));
+    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn,
+                                        last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
   if (a->logits) PE_TRY(lm_head(m, a, xn, M, gws, gwsb, st));
