@@ -158,21 +158,6 @@ __global__ void dense_repack_kernel(const uint16_t* __restrict__ w, int64_t N, i
   }
 }
 
-// The inverse of dense_repack_kernel: MFMA-tiled 16-bit weights back to
-// row-major [N][K], 16 bytes per thread per step.
-__global__ void dense_untile_kernel(const uint16_t* __restrict__ tiled, int64_t N, int64_t K,
-                                    uint16_t* __restrict__ w) {
-  const int64_t KS = K / 16, total = (N / 32) * KS * 64;
-  int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
-    const int lane = (int)(idx & 63);
-    const int64_t t = idx >> 6;
-    const int64_t nt = t / KS, ks = t % KS;
-    const int64_t n = nt * 32 + (lane & 31);
-    *(u32x4_t*)(w + n * K + 16 * ks + 8 * (lane >> 5)) = *(const u32x4_t*)(tiled + idx * 8);
-  }
-}
-
 __global__ void copy_bytes_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t n) {
   int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
@@ -291,14 +276,6 @@ extern "C" int pe_nf4_dequant_f32abs(const uint8_t* tiled, const float* tiled_ab
   int64_t total = (N / 32) * (K / 128) * 64;
   nf4_dequant_kernel<uint32_t><<<grid_for(total, 256), 256, 0, (hipStream_t)stream>>>(
       tiled, (const uint32_t*)tiled_absmax, N, K, out);
-  PE_CHECK_LAUNCH();
-  return PE_OK;
-}
-
-int pe_internal_dense_untile(const void* tiled, int64_t N, int64_t K, void* out, hipStream_t st) {
-  if (!tiled || !out || N <= 0 || K <= 0 || N % 32 || K % 16) return PE_ERR_ARG;
-  const int64_t total = (N / 32) * (K / 16) * 64;
-  dense_untile_kernel<<<grid_for(total, 256), 256, 0, st>>>((const uint16_t*)tiled, N, K, (uint16_t*)out);
   PE_CHECK_LAUNCH();
   return PE_OK;
 }

@@ -142,5 +142,3 @@ PE_INTERNAL int pe_internal_kv_offsets(const int32_t* seq_row0, const int64_t* s
                                        int64_t seq_stride, int64_t cap, int hd, int64_t max_prefix, int max_rows,
                                        int64_t* off, int32_t* status, hipStream_t st);
 
-// MFMA-tiled 16-bit weights [N][K] back to row-major (the inverse of pe_dense_repack)
-int pe_internal_dense_untile(const void* tiled, int64_t N, int64_t K, void* out, hipStream_t st);

@@ -167,6 +167,22 @@ class Prepared:
                 self.c32 = [(a.float(), b.float()) for a, b in self.o_cache]
 
 
+    def with_prefix(self, P, kv_seed, cache_capacity):
+        """The same model, oracle and fp32 evaluator over another random prefix of P
+        rows (a cache of its own)."""
+        other = Prepared.__new__(Prepared)
+        other.shape, other.tm, other.orc, other.o32, other.P = self.shape, self.tm, self.orc, self.o32, P
+        other.cache = self.tm.make_cache(cache_capacity)
+        g = torch.Generator().manual_seed(kv_seed)
+        kk = torch.randn(other.cache.k[:, :, :P].shape, generator=g).to(self.tm.dtype)
+        vv = torch.randn(other.cache.v[:, :, :P].shape, generator=g).to(self.tm.dtype)
+        other.cache.k[:, :, :P] = kk.to(DEV)
+        other.cache.v[:, :, :P] = vv.to(DEV)
+        other.o_cache = [(kk[li].unsqueeze(0), vv[li].unsqueeze(0)) for li in range(self.shape.num_layers)]
+        other.c32 = [(a.float(), b.float()) for a, b in other.o_cache] if self.o32 is not None else None
+        return other
+
+
 def _run_case(shape, seed, P, depth, widths, top_k, plant, tol, random_kv=False, tm=None, prep=None, details=None):
     """One seed's tree through forward_cached -> accept_tree_cached -> gather_cache
     on the device and through the oracle. ``prep``: a Prepared context (its random
@@ -335,6 +351,22 @@ def test_llama7b_nf4_width_prefill_longer_than_a_chunk(P):
     shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
     v, n, err = _run_case(shape, 7, P, wl.depth, wl.widths, wl.top_k, plant=lambda s: 1 + s % wl.depth, tol=2e-2)
     print(f"P={P}: {v}, accepted {n}, max |dlogit| {err:.3g}")
+
+
+@pytest.mark.timeout(900)
+def test_llama7b_nf4_T64_P8192_full_depth_against_the_oracle(full_7b):
+    """The long-context wide-tree workload at full depth: the 32-layer 7B NF4
+    model, a 64-node depth-6 tree (widths [8,11,11,11,11,12]) over a random
+    8191-row prefix plus the root token (P = 8192), a planted chain to the full
+    depth, against the oracle: logits, features and K/V rows within the parity
+    rule, acceptance exact or a bounded near tie, the compaction bit-exact."""
+    wl = WORKLOADS["llama2-7b-nf4-T64-P8192"]
+    prep = full_7b.with_prefix(8191, 8192, 8192 + 128)
+    det = {}
+    v, n, err = _run_case(LLAMA2_7B_NF4, 4, None, wl.depth, wl.widths, wl.top_k, plant=lambda s: wl.depth, tol=2e-2,
+                          prep=prep, details=det)
+    _report("7b-32layer-T64-P8192", det)
+    assert v == "exact" or v.startswith("near-tie")
 
 
 @pytest.mark.parametrize("case", ["nf4-P2048", "dense-bf16-P300", "dense-fp16-P600"])
