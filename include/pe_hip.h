@@ -236,6 +236,24 @@ int pe_tree_attention(const void* q, const void* k_cache, const void* v_cache, i
                       const uint64_t* bits, int words, float scale, int dtype, void* out,
                       int64_t ld_out, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The same attention for B sequences in one launch, each over its own cache
+ * (per sequence HF sdpa_attention_forward, integrations/sdpa_attention.py:79-154,
+ * with the tree bias of masks.py:127-147, as serve.py:289-297 runs it for one
+ * sequence). Sequence b's nodes are rows [seq_row0[b], seq_row0[b + 1]) of q
+ * [M][nh][128], bits [M][words] and out [M][ld_out]; its keys are its
+ * seq_prefix[b] cached rows (device memory) followed by its node rows, in
+ * k_cache / v_cache + b * seq_stride elements ([nkv][cap][128] per sequence).
+ * max_rows and max_prefix bound every sequence's node count and prefix and
+ * size the launch (a sequence beyond them is skipped). bf16 / fp16, hd = 128.
+ * workspace: pe_attention_batch_workspace_bytes bytes, its first 4 KiB arrival
+ * counters (zero before the first call; every call leaves them zero). */
+int64_t pe_attention_batch_workspace_bytes(int max_rows, int nh, int nkv, int64_t max_kv_len, int batch);
+int pe_tree_attention_batch(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
+                            int64_t seq_stride, int nh, int nkv, int max_rows, int64_t max_prefix, int batch,
+                            const int32_t* seq_row0, const int64_t* seq_prefix, const uint64_t* bits, int words,
+                            float scale, int dtype, void* out, int64_t ld_out, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- acceptance */
 /* Row argmax (first index among equal maxima; NaN counts as the maximum). */
 int pe_argmax_rows(const void* x, int64_t ld, int rows, int64_t V, int dtype, int32_t* out_idx,

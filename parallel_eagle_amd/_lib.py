@@ -129,6 +129,9 @@ SIGNATURES: dict[str, tuple] = {
     "pe_attention_workspace_bytes": (i64, [C.c_int, C.c_int, C.c_int, C.c_int, i64, C.c_int]),
     "pe_tree_attention": (C.c_int, [vp, vp, vp, i64, C.c_int, C.c_int, C.c_int, C.c_int, i64, C.c_int, vp,
                                     C.c_int, f32, C.c_int, vp, i64, vp, i64, vp]),
+    "pe_attention_batch_workspace_bytes": (i64, [C.c_int, C.c_int, C.c_int, i64, C.c_int]),
+    "pe_tree_attention_batch": (C.c_int, [vp, vp, vp, i64, i64, C.c_int, C.c_int, C.c_int, i64, C.c_int, vp, vp,
+                                          vp, C.c_int, f32, C.c_int, vp, i64, vp, i64, vp]),
     "pe_argmax_rows": (C.c_int, [vp, i64, C.c_int, i64, C.c_int, vp, vp]),
     "pe_accept_tree": (C.c_int, [vp, vp, i64, C.c_int, i64, C.c_int, vp, vp, vp, vp, vp]),
     "pe_accept_tree_keys": (C.c_int, [vp, i64, C.c_int, vp, C.c_int, C.c_int, vp, vp, vp, vp, vp]),

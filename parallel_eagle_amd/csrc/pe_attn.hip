@@ -1241,6 +1241,579 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S, int batch = 1) {
   return p;
 }
 
+// Visibility of the 64 keys kb0 .. kb0 + 63 to one query row, as a bit mask
+// (bit j: key kb0 + j), so that each score register tests a bit at an offset
+// fixed at compile time. Built with wave-uniform branches only: a per-lane
+// branch around each score (the tree test nested in the prefix test) was
+// compiled for gfx950 into code that overwrote the first score register with
+// the node index and left that score masked whenever the key was a node key.
+// Tree rows: prefix keys (< P) visible, node key P + u visible when bit u of
+// the row's ancestor bits nb (up to four words) is set.
+__device__ __forceinline__ uint64_t tree_window(int64_t kb0, int64_t P, const uint64_t* nb) {
+  const int64_t off = kb0 - P;  // node index of key kb0
+  if (off <= -64) return ~0ull;
+  if (off < 0) {
+    const int j0 = (int)(-off);  // 1 .. 63: keys below kb0 + j0 are prefix keys
+    return ((1ull << j0) - 1) | (nb[0] << j0);
+  }
+  if (off >= 64 * PE_TREE_MAX_WORDS) return 0ull;
+  const int wi = (int)(off >> 6), sh = (int)(off & 63);
+  static_assert(PE_TREE_MAX_WORDS == 4, "one select per word");
+  const uint64_t a = wi == 0 ? nb[0] : wi == 1 ? nb[1] : wi == 2 ? nb[2] : nb[3];
+  const uint64_t b = wi == 0 ? nb[1] : wi == 1 ? nb[2] : wi == 2 ? nb[3] : 0ull;
+  return sh ? (a >> sh) | (b << (64 - sh)) : a;
+}
+
+// Causal rows: keys up to kvis visible.
+__device__ __forceinline__ uint64_t causal_window(int64_t kb0, int64_t kvis) {
+  const int64_t d = kvis - kb0;  // the last visible key's offset in the step
+  return d >= 63 ? ~0ull : (d < 0 ? 0ull : (2ull << d) - 1);
+}
+
+// Keys at or past kend do not exist: clear their bits.
+__device__ __forceinline__ uint64_t window_limit(uint64_t win, int64_t kb0, int64_t kend) {
+  const int64_t lim = kend - kb0;
+  return lim >= 64 ? win : (lim <= 0 ? 0ull : win & ((1ull << lim) - 1));
+}
+
+// ---------------------------------------------------------------------------
+// Causal attention over many query rows (the prompt prefill)
+// ---------------------------------------------------------------------------
+// A KV head's query rows (T nodes x G query heads, row r = node r / G, query
+// head r % G) are cut into blocks of 128 rows. Causally, block b sees about
+// (b + 1) / nblk of the keys, so one workgroup takes the pair of blocks
+// (nblk - 1 - i, i) in turn and every workgroup does the same work. Eight
+// waves: wave w owns 32-row tile w % 4 of the block and, in key group w / 4,
+// every other 64-key step (group 0 the even steps, group 1 the odd ones), so
+// each SIMD runs two waves on independent work. Each iteration copies the
+// next two steps' K and V (128 keys) once per workgroup into LDS
+// (double-buffered; their global loads are in flight during the current
+// iteration), and every wave multiplies its tile by its step: S^T = K Q^T
+// (A = K from LDS, B = the wave's Q^T, held in registers), the online softmax
+// in base 2 on the S^T accumulators (each lane one row and 16 keys of every
+// 32-key half), O^T += V^T P^T (A = V^T by transposed LDS reads, B = P^T
+// rounded to the compute dtype). At the end of a block group 1 hands its
+// (O, m, l) to group 0 through LDS, which merges the two (group 0 first) and
+// writes out = O / l. The arithmetic is attn_wg_kernel's: scores scaled by
+// scale * log2 e, fp32 maxima and sums, probabilities rounded before PV. Keys
+// past the visible range are masked to -inf (probability exactly zero); key
+// rows past the cache fill (P + T) are read as row P + T - 1, so no
+// uninitialised row reaches the products. Work item w of the nkv x npair grid
+// runs on XCD w / (grid / 8) when the grid is a multiple of eight (workgroup
+// b starts on XCD b % 8), so the row blocks of a KV head share one L2.
+constexpr int kRowsWaves = 8;
+constexpr int kRowsKeys = 64;            // keys per step
+constexpr int kRowsKStride = 128 + 8;    // LDS row stride of K (elements): 272 B
+constexpr int kRowsVStride = 128 + 32;   // LDS row stride of V (elements): 320 B, as kVRow
+constexpr int kRowsKBytes = kRowsKeys * kRowsKStride * 2;
+constexpr int kRowsVBytes = kRowsKeys * kRowsVStride * 2;
+constexpr int kRowsStepBytes = kRowsKBytes + kRowsVBytes;
+constexpr int kRowsSmem = 4 * kRowsStepBytes;  // two buffers of two steps
+// group 1's hand-over: per tile and lane 64 O values, m and l (rows of 68 floats: 16-byte aligned)
+constexpr int kRowsMergeStride = 64 + 4;
+constexpr int kRowsMergeBytes = 4 * 64 * kRowsMergeStride * 4;
+static_assert(kRowsMergeBytes <= kRowsSmem, "the merge reuses the step buffers");
+// causal passes of at least this many nodes take attn_rows_kernel
+constexpr int kRowsMinNodes = 256;
+
+template <int DT>
+__global__ __launch_bounds__(64 * kRowsWaves, 1) void attn_rows_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
+    int nh, int nkv, int T, int64_t P, float scale, int nblk, int npair, void* __restrict__ out, int64_t ld_out,
+    int out_units) {
+  constexpr int HD = 128;
+  __shared__ __align__(16) uint8_t smem[kRowsSmem];
+  const int total = nkv * npair;
+  const int b = blockIdx.x;
+  const int w = (total & 7) ? b : (b & 7) * (total >> 3) + (b >> 3);
+  const int kvh = w / npair, pair = w - kvh * npair;
+  const int G = nh / nkv, rows = T * G;
+  const int64_t S = P + T;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 31, g = lane >> 5;
+  const int tile = wave & 3, kg = wave >> 2;
+  const uint16_t* kh = kc + (int64_t)kvh * cap * HD;
+  const uint16_t* vh = vc + (int64_t)kvh * cap * HD;
+  const float scale2 = scale * 1.44269504088896341f;
+  typedef uint16_t(*KRow)[kRowsKStride];
+  typedef uint16_t(*VRow)[kRowsVStride];
+  // step buffer s (0..3): buffer s / 2 of the double buffer, step s % 2 of the pair
+  auto kbuf = [&](int s) { return (KRow)(smem + s * kRowsStepBytes); };
+  auto vbuf = [&](int s) { return (VRow)(smem + s * kRowsStepBytes + kRowsKBytes); };
+  // two steps' K and V: 128 keys x 16 chunks of 16 bytes each, four of each per thread
+  u32x4_t kr[4], vr[4];
+  auto load_pair = [&](int64_t kb0) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = tid + 512 * s, key = c >> 4, part = c & 15;
+      const int64_t row = min(kb0 + key, S - 1);
+      kr[s] = *(const u32x4_t*)(kh + row * HD + part * 8);
+      vr[s] = *(const u32x4_t*)(vh + row * HD + part * 8);
+    }
+  };
+  auto store_pair = [&](int buf) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = tid + 512 * s, key = c >> 4, part = c & 15;
+      KRow ks = kbuf(2 * buf + (key >> 6));
+      VRow vs = vbuf(2 * buf + (key >> 6));
+      *(u32x4_t*)&ks[key & 63][part * 8] = kr[s];
+      *(u32x4_t*)&vs[key & 63][part * 8] = vr[s];
+    }
+  };
+
+  for (int half = 0; half < 2; ++half) {
+    const int blk = half == 0 ? nblk - 1 - pair : pair;
+    if (half == 1 && blk == nblk - 1 - pair) break;  // the middle block of an odd count, done once
+    const int r0 = blk * 128;
+    // the last node of the block and of this wave's tile: keys up to P + node are visible
+    const int tmax_blk = min(T - 1, (min(r0 + 127, rows - 1)) / G);
+    const int64_t nkeys = P + tmax_blk + 1;
+    const int nsteps = (int)((nkeys + kRowsKeys - 1) / kRowsKeys);
+    const int iters = (nsteps + 1) / 2;
+    const int rt0 = r0 + 32 * tile;
+    const bool tile_live = rt0 < rows;
+    const int64_t tile_last_key = tile_live ? P + min(T - 1, min(rt0 + 31, rows - 1) / G) : -1;
+    const int64_t tile_first_vis = P + (int64_t)(min(rt0, rows - 1) / G);  // keys <= this: every row sees them
+    const int r = rt0 + ln;
+    const int rr = min(r, rows - 1);
+    const int t = rr / G;
+    const int64_t kvis = P + t;  // this lane's row sees keys <= kvis
+    // the row's Q^T operand: k-step j holds dims 16 j + 8 g .. + 7
+    u32x4_t qf[8];
+    {
+      const uint16_t* qrow = q + ((int64_t)t * nh + kvh * G + rr % G) * HD + 8 * g;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qf[j] = *(const u32x4_t*)(qrow + 16 * j);
+    }
+    f32x16_t o[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
+    float m = kInitMax, l = 0.f;
+
+    __syncthreads();  // the previous block's buffers and hand-over are read by every wave
+    load_pair(0);
+    store_pair(0);
+    __syncthreads();
+    for (int it = 0; it < iters; ++it) {
+      if (it + 1 < iters) load_pair((int64_t)(it + 1) * 2 * kRowsKeys);
+      const int step = 2 * it + kg;
+      const int64_t kb0 = (int64_t)step * kRowsKeys;
+      KRow ks = kbuf(2 * (it & 1) + kg);
+      VRow vs = vbuf(2 * (it & 1) + kg);
+      if (tile_live && step < nsteps && kb0 <= tile_last_key) {  // wave-uniform: the tile sees a key of this step
+        f32x16_t sc[2];
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sc[sb][i] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int sb = 0; sb < 2; ++sb) {
+            const u32x4_t kf = *(const u32x4_t*)&ks[32 * sb + ln][16 * j + 8 * g];
+            if constexpr (DT == PE_DTYPE_F16)
+              sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf),
+                                                              __builtin_bit_cast(f16x8_t, qf[j]), sc[sb], 0, 0, 0);
+            else
+              sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
+                                                               __builtin_bit_cast(bf16x8_t, qf[j]), sc[sb], 0, 0, 0);
+          }
+        // sc[sb][i] is key kb0 + 32 sb + 8 (i / 4) + 4 g + i % 4 of row r
+        float bmax = -INFINITY;
+        const bool whole = kb0 + kRowsKeys - 1 <= tile_first_vis;  // visible to every row of the tile
+        const uint64_t win = causal_window(kb0, kvis) >> (4 * g);
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            if (!whole) sc[sb][i] = ((win >> (32 * sb + 8 * (i >> 2) + (i & 3))) & 1ull) ? sc[sb][i] : -INFINITY;
+            bmax = fmaxf(bmax, sc[sb][i]);
+          }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * scale2;
+        const float mnew = fmaxf(m, bmax);
+        const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+        float psum = 0.f;
+        uint32_t pb[2][8];
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int i = 0; i < 16; i += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[sb][i], scale2, -mnew));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[sb][i + 1], scale2, -mnew));
+            psum += p0 + p1;
+            pb[sb][i >> 1] = (DT == PE_DTYPE_F16)
+                                 ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
+                                 : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
+          }
+        psum += __shfl_xor(psum, 32, 64);
+        l = l * alpha + psum;
+        const bool rescale = __builtin_amdgcn_ballot_w64(mnew != m) != 0ull;
+        m = mnew;
+        if (rescale) {
+#pragma unroll
+          for (int h = 0; h < 4; ++h)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[h][i] *= alpha;
+        }
+        // O^T += V^T P^T over the four 16-key quarters of the step
+        const int qg = lane >> 4, jl = lane & 15;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int sb = c >> 1, cq = c & 1;
+          u32x4_t bp;
+          bp[0] = pb[sb][4 * cq + 0];
+          bp[1] = pb[sb][4 * cq + 1];
+          bp[2] = pb[sb][4 * cq + 2];
+          bp[3] = pb[sb][4 * cq + 3];
+          const int kb = 16 * c + 4 * (qg >> 1) + (jl >> 2);
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const int db = 32 * h + 16 * (qg & 1) + 4 * (jl & 3);
+            typedef short s4v_t __attribute__((__vector_size__(4 * sizeof(short))));
+            typedef __attribute__((address_space(3))) s4v_t lds_s4v_t;
+            const s4v_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb][db]);
+            const s4v_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb + 8][db]);
+            const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+            u32x4_t a;
+            a[0] = l2.x;
+            a[1] = l2.y;
+            a[2] = h2.x;
+            a[3] = h2.y;
+            if constexpr (DT == PE_DTYPE_F16)
+              o[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                            __builtin_bit_cast(f16x8_t, bp), o[h], 0, 0, 0);
+            else
+              o[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                             __builtin_bit_cast(bf16x8_t, bp), o[h], 0, 0, 0);
+          }
+        }
+      }
+      if (it + 1 < iters) store_pair((it + 1) & 1);
+      __syncthreads();
+    }
+    // group 1 hands (O, m, l) to group 0 (the loop's last barrier: every wave
+    // is done with the step buffers)
+    float* mo = (float*)smem + (tile * 64 + lane) * kRowsMergeStride;
+    if (kg == 1) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          *(f32x4_t*)&mo[16 * h + 4 * c] = f32x4_t{o[h][4 * c], o[h][4 * c + 1], o[h][4 * c + 2], o[h][4 * c + 3]};
+      mo[64] = m;
+      mo[65] = l;
+    }
+    __syncthreads();
+    if (kg == 0 && tile_live && r < rows) {
+      const float m1 = mo[64], l1 = mo[65];
+      const float mx = fmaxf(m, m1);
+      const float a0 = __builtin_amdgcn_exp2f(m - mx), a1 = __builtin_amdgcn_exp2f(m1 - mx);
+      const float den = a0 * l + a1 * l1;
+      // out = O / l: o[h][4 c .. 4 c + 3] are dims 32 h + 8 c + 4 g + 0..3 of row r
+      const int col0 = (kvh * G + r % G) * HD;
+      typedef typename Elem<DT>::T Te;
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f32x4_t o1 = *(const f32x4_t*)&mo[16 * h + 4 * c];
+          float o4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o4[i] = (a0 * o[h][4 * c + i] + a1 * o1[i]) / den;
+          const int col = col0 + 32 * h + 8 * c + 4 * g;
+          if (out_units)
+            Vec4<DT>::store((Te*)out + xtile_index(t, col, out_units), o4);
+          else if ((ld_out & 3) || ((uintptr_t)out & 7)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Elem<DT>::store((Te*)out, (int64_t)t * ld_out + col + i, o4[i]);
+          } else {
+            Vec4<DT>::store((Te*)out + (int64_t)t * ld_out + col, o4);
+          }
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Batched tree attention with many rows per KV head (GQA batches)
+// ---------------------------------------------------------------------------
+// Sequence b's rows of a KV head are its T_b nodes x G query heads (row r =
+// node r / G, query head r % G), NW = ceil(max rows / 32) tiles of 32 rows,
+// one wave per tile. One workgroup = (key split, KV head, sequence); the
+// sequence's P_b + T_b keys are cut into splits of `kps` keys (a multiple of
+// 64), so a sequence has ceil((P_b + T_b) / kps) splits, every workgroup
+// walks the same number of keys, and the workgroups past a sequence's split
+// count leave at once. A split's keys are walked in 64-key steps, K and V of
+// a step copied once per workgroup into LDS (double-buffered, the next step's
+// global loads in flight during the current one) and multiplied by every
+// tile: the arithmetic of attn_rows_kernel, with the tree mask (prefix keys
+// visible to every node, node key u visible to node t when bit u of the
+// node's ancestor bits is set). A sequence of one split writes its output;
+// otherwise every workgroup publishes its split's (O, m, l) with
+// agent-coherent stores and counts itself on the (sequence, KV head) arrival
+// counter, and the last to arrive combines the splits in split order (running
+// max, rescaled sums) and sets the counter back to zero. Sequences whose
+// device prefix or row count exceed the bounds of the launch are skipped by
+// every workgroup alike (the K/V offsets kernel reports them).
+constexpr int kBRowsMaxWaves = 8;
+constexpr int kBRowsMinWaves = 4;  // fewer tiles: the staging needs 256 threads
+
+template <int DT>
+__global__ __launch_bounds__(64 * kBRowsMaxWaves, 1) void attn_batch_rows_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
+    int nh, int nkv, const uint64_t* __restrict__ bits, int words, float scale, int kps, int max_splits,
+    int rows_pad, float* __restrict__ opart, float* __restrict__ mlpart, int* __restrict__ counters,
+    void* __restrict__ out, int64_t ld_out, int out_units, AttnBatch bt) {
+  constexpr int HD = 128;
+  __shared__ __align__(16) uint8_t smem[2 * kRowsStepBytes];
+  const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int rbase = bt.seq_row0[seq];
+  const int T = bt.seq_row0[seq + 1] - rbase;
+  const int64_t P = bt.seq_prefix[seq];
+  if (T <= 0 || T > bt.max_rows || P < 0 || P > bt.max_prefix) return;
+  const int G = nh / nkv, rows = T * G;
+  const int64_t S = P + T;
+  const int nsplit = (int)((S + kps - 1) / kps);
+  if (split >= nsplit) return;
+  const int64_t k0 = (int64_t)split * kps, k1 = min(S, k0 + kps);
+  const int nsteps = (int)((k1 - k0 + kRowsKeys - 1) / kRowsKeys);
+  const int nthr = blockDim.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 31, g = lane >> 5;
+  const uint16_t* kh = kc + seq * bt.seq_stride + (int64_t)kvh * cap * HD;
+  const uint16_t* vh = vc + seq * bt.seq_stride + (int64_t)kvh * cap * HD;
+  const float scale2 = scale * 1.44269504088896341f;
+  typedef uint16_t(*KRow)[kRowsKStride];
+  typedef uint16_t(*VRow)[kRowsVStride];
+  auto kbuf = [&](int s) { return (KRow)(smem + s * kRowsStepBytes); };
+  auto vbuf = [&](int s) { return (VRow)(smem + s * kRowsStepBytes + kRowsKBytes); };
+  // one step's K and V: 64 keys x 16 chunks of 16 bytes, chunk tid + nthr s (s < 4) per thread
+  u32x4_t kr[4], vr[4];
+  auto load_step = [&](int64_t kb0) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = tid + nthr * s;
+      if (c < 1024) {
+        const int64_t row = min(kb0 + (c >> 4), S - 1);
+        kr[s] = *(const u32x4_t*)(kh + row * HD + (c & 15) * 8);
+        vr[s] = *(const u32x4_t*)(vh + row * HD + (c & 15) * 8);
+      }
+    }
+  };
+  auto store_step = [&](int slot) {
+    KRow ks = kbuf(slot);
+    VRow vs = vbuf(slot);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = tid + nthr * s;
+      if (c < 1024) {
+        *(u32x4_t*)&ks[c >> 4][(c & 15) * 8] = kr[s];
+        *(u32x4_t*)&vs[c >> 4][(c & 15) * 8] = vr[s];
+      }
+    }
+  };
+
+  const int rt0 = 32 * wave;
+  const bool tile_live = rt0 < rows;
+  const int r = rt0 + ln;
+  const int rr = min(r, rows - 1);
+  const int t = rr / G;
+  uint64_t nbits[PE_TREE_MAX_WORDS];
+#pragma unroll
+  for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = bits[(int64_t)(rbase + t) * words + min(w, words - 1)];
+  u32x4_t qf[8];
+  {
+    const uint16_t* qrow = q + ((int64_t)(rbase + t) * nh + kvh * G + rr % G) * HD + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qf[j] = *(const u32x4_t*)(qrow + 16 * j);
+  }
+  f32x16_t o[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
+  float m = kInitMax, l = 0.f;
+
+  load_step(k0);
+  store_step(0);
+  __syncthreads();
+  for (int st = 0; st < nsteps; ++st) {
+    const int64_t kb0 = k0 + (int64_t)st * kRowsKeys;
+    if (st + 1 < nsteps) load_step(kb0 + kRowsKeys);
+    KRow ks = kbuf(st & 1);
+    VRow vs = vbuf(st & 1);
+    if (tile_live) {
+      f32x16_t sc[2];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sc[sb][i] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+          const u32x4_t kf = *(const u32x4_t*)&ks[32 * sb + ln][16 * j + 8 * g];
+          if constexpr (DT == PE_DTYPE_F16)
+            sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf),
+                                                            __builtin_bit_cast(f16x8_t, qf[j]), sc[sb], 0, 0, 0);
+          else
+            sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
+                                                             __builtin_bit_cast(bf16x8_t, qf[j]), sc[sb], 0, 0, 0);
+        }
+      // sc[sb][i] is key kb0 + 32 sb + 8 (i / 4) + 4 g + i % 4 of row r
+      float bmax = -INFINITY;
+      const bool whole = kb0 + kRowsKeys <= min(P, k1);  // prefix keys of the split only: visible to every row
+      const uint64_t win = window_limit(tree_window(kb0, P, nbits), kb0, k1) >> (4 * g);
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (!whole) sc[sb][i] = ((win >> (32 * sb + 8 * (i >> 2) + (i & 3))) & 1ull) ? sc[sb][i] : -INFINITY;
+          bmax = fmaxf(bmax, sc[sb][i]);
+        }
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * scale2;
+      const float mnew = fmaxf(m, bmax);
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+      float psum = 0.f;
+      uint32_t pb[2][8];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[sb][i], scale2, -mnew));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[sb][i + 1], scale2, -mnew));
+          psum += p0 + p1;
+          pb[sb][i >> 1] = (DT == PE_DTYPE_F16)
+                               ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
+                               : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
+        }
+      psum += __shfl_xor(psum, 32, 64);
+      l = l * alpha + psum;
+      const bool rescale = __builtin_amdgcn_ballot_w64(mnew != m) != 0ull;
+      m = mnew;
+      if (rescale) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[h][i] *= alpha;
+      }
+      const int qg = lane >> 4, jl = lane & 15;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int sb = c >> 1, cq = c & 1;
+        u32x4_t bp;
+        bp[0] = pb[sb][4 * cq + 0];
+        bp[1] = pb[sb][4 * cq + 1];
+        bp[2] = pb[sb][4 * cq + 2];
+        bp[3] = pb[sb][4 * cq + 3];
+        const int kb = 16 * c + 4 * (qg >> 1) + (jl >> 2);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const int db = 32 * h + 16 * (qg & 1) + 4 * (jl & 3);
+          typedef short s4v_t __attribute__((__vector_size__(4 * sizeof(short))));
+          typedef __attribute__((address_space(3))) s4v_t lds_s4v_t;
+          const s4v_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb][db]);
+          const s4v_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb + 8][db]);
+          const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+          u32x4_t a;
+          a[0] = l2.x;
+          a[1] = l2.y;
+          a[2] = h2.x;
+          a[3] = h2.y;
+          if constexpr (DT == PE_DTYPE_F16)
+            o[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                          __builtin_bit_cast(f16x8_t, bp), o[h], 0, 0, 0);
+          else
+            o[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                           __builtin_bit_cast(bf16x8_t, bp), o[h], 0, 0, 0);
+        }
+      }
+    }
+    if (st + 1 < nsteps) store_step((st + 1) & 1);
+    __syncthreads();
+  }
+
+  typedef typename Elem<DT>::T Te;
+  // a row's output: 4 consecutive dims at column col of node row rbase + tt
+  auto store4 = [&](int tt, int col, const float (&o4)[4]) {
+    const int64_t row = rbase + tt;
+    if (out_units)
+      Vec4<DT>::store((Te*)out + xtile_index((int)row, col, out_units), o4);
+    else if ((ld_out & 3) || ((uintptr_t)out & 7)) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Elem<DT>::store((Te*)out, row * ld_out + col + i, o4[i]);
+    } else {
+      Vec4<DT>::store((Te*)out + row * ld_out + col, o4);
+    }
+  };
+  // o[h][4 c .. 4 c + 3] are dims 32 h + 8 c + 4 g + 0..3 of row r
+  if (nsplit == 1) {
+    if (tile_live && r < rows) {
+      const int col0 = (kvh * G + r % G) * HD;
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float o4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o4[i] = o[h][4 * c + i] / l;
+          store4(t, col0 + 32 * h + 8 * c + 4 * g, o4);
+        }
+    }
+    return;
+  }
+  const int pair = seq * nkv + kvh;
+  const uint32_t nrows = (uint32_t)(bt.batch * nkv * max_splits * rows_pad);
+  const __amdgpu_buffer_rsrc_t ro = agent_rsrc(opart, nrows * HD * 4), rm = agent_rsrc(mlpart, nrows * 16);
+  auto prow = [&](int sp, int row) -> uint32_t { return (uint32_t)((pair * max_splits + sp) * rows_pad + row); };
+  if (tile_live && r < rows) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        store_agent_x4(ro, (prow(split, r) * HD + 32 * h + 8 * c + 4 * g) * 4,
+                       f32x4_t{o[h][4 * c], o[h][4 * c + 1], o[h][4 * c + 2], o[h][4 * c + 3]});
+    if (g == 0) store_agent_x4(rm, prow(split, r) * 16, f32x4_t{m, l, 0.f, 0.f});
+  }
+  // the stores are acknowledged at agent scope before this workgroup counts itself
+  __builtin_amdgcn_s_waitcnt(0);
+  __shared__ int s_arrived;
+  __syncthreads();
+  if (tid == 0) s_arrived = __hip_atomic_fetch_add(counters + pair, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_arrived + 1 != nsplit) return;
+  // the last to arrive: item = (row, 4-dim chunk), the splits merged in split order
+  for (int item = tid; item < rows * 32; item += nthr) {
+    const int row = item >> 5, d0 = (item & 31) * 4;
+    float Mx = kInitMax, den = 0.f, num[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < nsplit; c0 += 8) {  // up to 8 splits' loads in flight
+      f32x4_t ov[8], mv[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int sp = min(c0 + c, nsplit - 1);
+        ov[c] = load_agent_x4(ro, (prow(sp, row) * HD + d0) * 4);
+        mv[c] = load_agent_x4(rm, prow(sp, row) * 16);
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        if (c0 + c >= nsplit) break;
+        const float mn = fmaxf(Mx, mv[c][0]);
+        const float a = __builtin_amdgcn_exp2f(Mx - mn), wt = __builtin_amdgcn_exp2f(mv[c][0] - mn);
+        Mx = mn;
+        den = den * a + wt * mv[c][1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) num[k] = num[k] * a + wt * ov[c][k];
+      }
+    }
+    float o4[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o4[k] = num[k] / den;
+    store4(row / G, (kvh * G + row % G) * HD + d0, o4);
+  }
+  if (tid == 0) __hip_atomic_store(counters + pair, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
 
 int64_t attention_workspace_bytes(int T, int nh, int nkv, int hd, int64_t kv_len, int dtype, int attn_mode) {
@@ -1273,6 +1846,24 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
   const int eager = attn_mode == PE_ATTN_EAGER;
   if (eager && out_units) return PE_ERR_ARG;
   if (workspace_bytes < attention_workspace_bytes(T, nh, nkv, hd, S, dtype, attn_mode)) return PE_ERR_WORKSPACE;
+  if (dtype != PE_DTYPE_F32 && hd == 128 && !eager && mask_mode == PE_MASK_CAUSAL && T >= kRowsMinNodes) {
+    // many causal rows (a prefill): row blocks in balanced pairs, no key splits
+    if (!(scale > 0.f)) return PE_ERR_ARG;
+    const int nblk = (T * (nh / nkv) + 127) / 128, npair = (nblk + 1) / 2;
+    const dim3 grid(nkv * npair);
+    if (dtype == PE_DTYPE_BF16)
+      attn_rows_kernel<PE_DTYPE_BF16><<<grid, 64 * kRowsWaves, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P, scale,
+          nblk, npair, out, ld_out, out_units);
+    else if (dtype == PE_DTYPE_F16)
+      attn_rows_kernel<PE_DTYPE_F16><<<grid, 64 * kRowsWaves, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, T, P, scale,
+          nblk, npair, out, ld_out, out_units);
+    else
+      return PE_ERR_ARG;
+    PE_CHECK_LAUNCH();
+    return PE_OK;
+  }
   if (dtype != PE_DTYPE_F32 && hd == 128 && !eager) {
     if (!(scale > 0.f) || cache_cap >= kAttnMaxCap) return PE_ERR_ARG;
     AttnPlan p = attn_plan(T, nh, nkv, S);
@@ -1340,9 +1931,48 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
   return PE_OK;
 }
 
+// attn_batch_rows_kernel's plan: keys per split a multiple of 64, sized so
+// that a batch whose prefixes average half the longest fills about two
+// workgroups per CU's worth of splits; sequences take as many splits as their
+// own keys need.
+struct BRowsPlan {
+  bool use;
+  int waves, kps, max_splits, rows_pad;
+  int64_t opart_bytes, ml_bytes;
+};
+
+BRowsPlan brows_plan(int max_rows, int nh, int nkv, int64_t max_kv_len, int batch) {
+  BRowsPlan p{};
+  const int rows = max_rows * (nh / nkv);
+  p.waves = (rows + 31) / 32;
+  // opt-in (PE_ATTN_BATCH_ROWS=1): at the batched workload it measured slower
+  // than attn_pair_kernel (99.5 against 39.1 us per launch), its steps waiting
+  // on their one-step-ahead K/V loads and its combine on 13 rounds of reloads
+  static const bool enabled = [] {
+    const char* v = getenv("PE_ATTN_BATCH_ROWS");
+    return v && v[0] == '1';
+  }();
+  p.use = enabled && p.waves >= kBRowsMinWaves && p.waves <= kBRowsMaxWaves &&
+          (int64_t)batch * nkv * 4 <= kAttnCounterBytes;
+  if (!p.use) return p;
+  int64_t want = (512 + (int64_t)batch * nkv - 1) / ((int64_t)batch * nkv);
+  want = want < 1 ? 1 : (want > 16 ? 16 : want);
+  int64_t kps = (max_kv_len + want - 1) / want;
+  kps = ((kps + kRowsKeys - 1) / kRowsKeys) * kRowsKeys;
+  if (kps < kRowsKeys) kps = kRowsKeys;
+  p.kps = (int)kps;
+  p.max_splits = (int)((max_kv_len + kps - 1) / kps);
+  p.rows_pad = p.waves * 32;
+  p.opart_bytes = (int64_t)batch * nkv * p.max_splits * p.rows_pad * 128 * 4;
+  p.ml_bytes = (int64_t)batch * nkv * p.max_splits * p.rows_pad * 4 * 4;
+  return p;
+}
+
 int64_t pe_internal_attention_batch_bytes(int max_rows, int nh, int nkv, int64_t max_kv_len, int batch) {
   const AttnPlan p = attn_plan(max_rows, nh, nkv, max_kv_len, batch);
-  return kAttnCounterBytes + p.opart_bytes + p.ml_bytes;
+  const BRowsPlan r = brows_plan(max_rows, nh, nkv, max_kv_len, batch);
+  const int64_t a = p.opart_bytes + p.ml_bytes, b = r.use ? r.opart_bytes + r.ml_bytes : 0;
+  return kAttnCounterBytes + (a > b ? a : b);
 }
 
 int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
@@ -1366,6 +1996,23 @@ int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const v
   float* opart = (float*)((char*)workspace + kAttnCounterBytes);
   float* ml = (float*)((char*)workspace + kAttnCounterBytes + p.opart_bytes);
   const AttnBatch bt{batch, p.row_tiles, seq_row0, seq_prefix, seq_stride, max_prefix, max_rows, dyn_split};
+  const BRowsPlan rp = brows_plan(max_rows, nh, nkv, S, batch);
+  if (rp.use) {
+    // K/V of a step staged once per workgroup for every row tile of the (sequence, KV head)
+    float* op = (float*)((char*)workspace + kAttnCounterBytes);
+    float* mp = (float*)((char*)workspace + kAttnCounterBytes + rp.opart_bytes);
+    const dim3 gridr(rp.max_splits, nkv, batch);
+    if (dtype == PE_DTYPE_BF16)
+      attn_batch_rows_kernel<PE_DTYPE_BF16><<<gridr, 64 * rp.waves, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, bits, words,
+          scale, rp.kps, rp.max_splits, rp.rows_pad, op, mp, counters, out, ld_out, out_units, bt);
+    else
+      attn_batch_rows_kernel<PE_DTYPE_F16><<<gridr, 64 * rp.waves, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, bits, words,
+          scale, rp.kps, rp.max_splits, rp.rows_pad, op, mp, counters, out, ld_out, out_units, bt);
+    PE_CHECK_LAUNCH();
+    return PE_OK;
+  }
   const int tpairs = (p.row_tiles + 1) / 2;
   if (p.row_tiles >= 2 && (int64_t)batch * nkv * tpairs >= 128) {
     // two row tiles per wave: each K/V block read once for both
@@ -1394,6 +2041,23 @@ int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const v
         out, ld_out, out_units, bt);
   PE_CHECK_LAUNCH();
   return PE_OK;
+}
+
+extern "C" int64_t pe_attention_batch_workspace_bytes(int max_rows, int nh, int nkv, int64_t max_kv_len,
+                                                      int batch) {
+  if (max_rows <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || batch <= 0 || max_kv_len <= 0) return 0;
+  return pe_internal_attention_batch_bytes(max_rows, nh, nkv, max_kv_len, batch);
+}
+
+extern "C" int pe_tree_attention_batch(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
+                                       int64_t seq_stride, int nh, int nkv, int max_rows, int64_t max_prefix,
+                                       int batch, const int32_t* seq_row0, const int64_t* seq_prefix,
+                                       const uint64_t* bits, int words, float scale, int dtype, void* out,
+                                       int64_t ld_out, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (ld_out < (int64_t)nh * 128 || seq_stride < 0) return PE_ERR_ARG;
+  return pe_internal_tree_attention_batch(q, k_cache, v_cache, cache_cap, seq_stride, nh, nkv, max_rows, max_prefix,
+                                          batch, seq_row0, seq_prefix, bits, words, scale, dtype, out, ld_out, 0,
+                                          workspace, workspace_bytes, nullptr, (hipStream_t)stream, 0);
 }
 
 extern "C" int pe_tree_attention(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap, int nh,

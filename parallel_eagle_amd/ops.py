@@ -290,6 +290,26 @@ def tree_attention(q, k_cache, v_cache, prefix_len, mask_mode, bits, scale, work
     return out
 
 
+def tree_attention_batch(q, k_cache, v_cache, seq_row0, seq_prefix, bits, scale, max_rows, max_prefix,
+                         workspace=None):
+    """q [M][nh][128]; caches [B][nkv][cap][128] (one layer per sequence);
+    seq_row0 int32 [B + 1], seq_prefix int64 [B] and bits int64 [M][words] on
+    the device."""
+    m, nh, hd = q.shape
+    b, nkv, cap, _ = k_cache.shape
+    _req(hd == 128 and q.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous(),
+         "q and the caches must be contiguous with 128-dim heads")
+    need = int(lib().pe_attention_batch_workspace_bytes(max_rows, nh, nkv, max_prefix + max_rows, b))
+    if workspace is None:
+        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
+    out = torch.empty((m, nh * hd), dtype=q.dtype, device=q.device)
+    check(lib().pe_tree_attention_batch(ptr(q), ptr(k_cache), ptr(v_cache), cap, nkv * cap * hd, nh, nkv, max_rows,
+                                        max_prefix, b, ptr(seq_row0), ptr(seq_prefix), ptr(bits), bits.shape[1],
+                                        scale, dcode(q.dtype), ptr(out), out.stride(0), ptr(workspace),
+                                        workspace.numel(), stream_ptr()), "pe_tree_attention_batch")
+    return out
+
+
 # ------------------------------------------------------------------ acceptance / cache
 def argmax_rows(x: torch.Tensor) -> torch.Tensor:
     _req(x.dim() == 2 and x.stride(1) == 1, "x must be [rows][V]")

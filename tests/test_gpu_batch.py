@@ -156,6 +156,20 @@ def test_batched_ragged_tree_sizes_7b_width():
     print("verdicts", verdicts, "accepted", [len(r[0]) for r in c["res"]])
 
 
+def test_batched_ragged_gqa_tree_sizes():
+    """GQA rows of different counts in one batch at the 14B width (trees of 26, 7
+    and 40 nodes: 130, 35 and 200 rows per KV head, seven row tiles of which the
+    short tree fills two) over prefixes of 0, 900 and 2500 rows: the first
+    sequence attends to its own node keys only, the others over several key
+    splits combined by the last workgroup to arrive."""
+    shape = QWEN25_14B_NF4.reduced(1, feature_layers=(0, 1, 1), vocab=16384)
+    spec = [(5, (4, 5, 5, 6, 6), 4), (3, (2, 2, 3), 2), (5, (8, 8, 8, 8, 8), 8)]
+    c = _batch_case(shape, 11, [0, 900, 2500], spec, plant=lambda b: (2, 1, 3)[b])
+    assert c["trees"].rows == [26, 7, 40]
+    verdicts = _check_sequences(shape, c)
+    print("verdicts", verdicts, "accepted", [len(r[0]) for r in c["res"]])
+
+
 def _graph_replays_equal_eager(c, prefixes):
     cache, tm = c["cache"], c["tm"]
     want = c["res"]

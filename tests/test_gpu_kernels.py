@@ -368,6 +368,94 @@ def test_multi_tile_attention_with_key_splits_matches_sdpa(dtype, nh, nkv, T, P)
     assert torch.allclose(causal.float(), ref_c.float(), rtol=2e-2, atol=2e-2)
 
 
+@pytest.mark.parametrize("dtype,nh,nkv,T,P", [
+    (torch.bfloat16, 4, 4, 2048, 0),    # a prefill from an empty cache: 16 row blocks, 8 balanced pairs
+    (torch.float16, 10, 2, 300, 77),    # GQA rows (node, query head), 12 row blocks, after a prefix
+    (torch.bfloat16, 2, 2, 320, 5),     # 3 row blocks: the middle block is a pair of its own
+    (torch.bfloat16, 4, 1, 257, 1000),  # four query heads per KV head, a long prefix, a ragged last tile
+])
+def test_causal_attention_over_many_rows_matches_sdpa(dtype, nh, nkv, T, P):
+    """Causal passes of 256 nodes or more (prompt prefills) run attn_rows_kernel:
+    against SDPA with the reference's causal additive bias, every element within
+    2e-2; cache rows past P + T hold NaN, which no output may see."""
+    hd = 128
+    S = P + T
+    cap = S + 70  # the last 64-key step reaches past the fill
+    q = torch.from_numpy(synth.normal(7, 63, T * nh * hd).reshape(T, nh, hd)).to(dtype)
+    k = torch.from_numpy(synth.normal(8, 64, nkv * S * hd).reshape(nkv, S, hd)).to(dtype)
+    v = torch.from_numpy(synth.normal(9, 65, nkv * S * hd).reshape(nkv, S, hd)).to(dtype)
+    kc = torch.full((nkv, cap, hd), float("nan"), dtype=dtype)
+    vc = torch.full((nkv, cap, hd), float("nan"), dtype=dtype)
+    kc[:, :S], vc[:, :S] = k, v
+    scale = hd ** -0.5
+    out = ops.tree_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), P, _lib.PE_MASK_CAUSAL, None, scale).cpu()
+    assert torch.isfinite(out.float()).all()
+    ref = _attn_ref(q, k, v, P, None, True, scale, dtype)
+    err = (out.float() - ref.float()).abs()
+    assert torch.allclose(out.float(), ref.float(), rtol=2e-2, atol=2e-2), err.max()
+
+
+@pytest.mark.parametrize("dtype,nh,nkv,trees,prefixes", [
+    # five query heads per KV head, 26-node trees: one wave per 32-row tile, 1-8 key splits per sequence
+    (torch.bfloat16, 40, 8, [26] * 8, [812, 3000, 512, 4096, 1500, 700, 2222, 64]),
+    (torch.float16, 40, 8, [26] * 3, [100, 513, 1024]),
+    # ragged trees: 130, 35 and 200 rows per KV head (seven tiles, the short tree fills two), no prefix
+    (torch.bfloat16, 40, 8, [26, 7, 40], [0, 900, 2500]),
+    # one query head per KV head: two row tiles
+    (torch.bfloat16, 4, 4, [26, 64], [100, 2048]),
+])
+def test_batched_tree_attention_matches_sdpa_per_sequence(dtype, nh, nkv, trees, prefixes):
+    """pe_tree_attention_batch against SDPA per sequence (its own prefix, tree
+    bias and cache): for every (sequence, query head) the relative L2 distance
+    from an fp32 evaluation is at most twice that of torch's own reduced-precision
+    SDPA, plus 1e-3; every element within 2e-2. Cache rows past each sequence's
+    fill hold NaN, which no output may see."""
+    hd = 128
+    B = len(trees)
+    rng = np.random.default_rng(sum(prefixes) + len(trees))
+    parents = [[-1] + [int(rng.integers(-1, t)) for t in range(1, T)] for T in trees]
+    cap = max(p + t for p, t in zip(prefixes, trees)) + 70
+    kc = torch.full((B, nkv, cap, hd), float("nan"), dtype=dtype)
+    vc = torch.full((B, nkv, cap, hd), float("nan"), dtype=dtype)
+    qs, ks, vs = [], [], []
+    for b, (T, P) in enumerate(zip(trees, prefixes)):
+        S = P + T
+        q = torch.from_numpy(synth.normal(20 + b, 70, T * nh * hd).reshape(T, nh, hd)).to(dtype)
+        k = torch.from_numpy(synth.normal(40 + b, 71, nkv * S * hd).reshape(nkv, S, hd)).to(dtype)
+        v = torch.from_numpy(synth.normal(60 + b, 72, nkv * S * hd).reshape(nkv, S, hd)).to(dtype)
+        kc[b, :, :S], vc[b, :, :S] = k, v
+        qs.append(q)
+        ks.append(k)
+        vs.append(v)
+    row0 = np.concatenate([[0], np.cumsum(trees)]).astype(np.int32)
+    words = (max(trees) + 63) // 64
+    bits = np.zeros((int(row0[-1]), words), dtype=np.uint64)
+    for b, par in enumerate(parents):
+        for t, a in enumerate(om.ancestor_bits(par)):
+            for w in range(words):
+                bits[row0[b] + t, w] = np.uint64((a >> (64 * w)) & ((1 << 64) - 1))
+    scale = hd ** -0.5
+    out = ops.tree_attention_batch(torch.cat(qs).to(DEV), kc.to(DEV), vc.to(DEV),
+                                   torch.from_numpy(row0).to(DEV), torch.tensor(prefixes, dtype=torch.int64).to(DEV),
+                                   torch.from_numpy(bits.view(np.int64)).to(DEV), scale, max(trees),
+                                   max(prefixes)).cpu()
+    assert torch.isfinite(out.float()).all()
+    worst = []
+    for b, (T, P) in enumerate(zip(trees, prefixes)):
+        got = out[row0[b]: row0[b + 1]].float()
+        ref = _attn_ref(qs[b], ks[b], vs[b], P, parents[b], False, scale, dtype).float()
+        r32 = _attn_ref(qs[b].float(), ks[b].float(), vs[b].float(), P, parents[b], False, scale, torch.float32)
+        assert torch.allclose(got, ref, rtol=2e-2, atol=2e-2), (b, (got - ref).abs().max())
+        for h in range(nh):
+            cols = slice(h * hd, (h + 1) * hd)
+            n32 = r32[:, cols].norm()
+            e_dev = float((got[:, cols] - r32[:, cols]).norm() / n32)
+            e_ref = float((ref[:, cols] - r32[:, cols]).norm() / n32)
+            worst.append((e_dev - 2 * e_ref, b, h, e_dev, e_ref))
+    worst.sort(reverse=True)
+    assert worst[0][0] <= 1e-3, f"(excess, sequence, head, device relL2, torch relL2): {worst[:4]}"
+
+
 # ------------------------------------------------------------------ acceptance and compaction
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("seed", range(6))
