@@ -1241,6 +1241,27 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S, int batch = 1) {
   return p;
 }
 
+__device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 256 + ((chunk ^ (row & 15)) << 4)); }
+
+// 16 bytes per lane from global memory straight into LDS at lds_base + 16 *
+// lane (lds_base wave-uniform, through M0). Issued as inline assembly so that
+// the compiler, which cannot tell these LDS writes from the ring slot being
+// read, adds no wait for them in front of every LDS read; the kernel orders
+// them itself (an explicit vmcnt wait and a workgroup barrier per step).
+// A pointer that is the same in every lane, held in scalar registers.
+__device__ __forceinline__ const uint16_t* uniform_ptr(const uint16_t* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint16_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// The source is a wave-uniform base (SGPRs) plus a per-lane 32-bit byte
+// offset (a head's cache rows span less than 2^24 x 256 bytes).
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_base)
+               : "memory", "m0");
+}
+
 // Visibility of the 64 keys kb0 .. kb0 + 63 to one query row, as a bit mask
 // (bit j: key kb0 + j), so that each score register tests a bit at an offset
 // fixed at compile time. Built with wave-uniform branches only: a per-lane
@@ -1285,10 +1306,11 @@ __device__ __forceinline__ uint64_t window_limit(uint64_t win, int64_t kb0, int6
 // (nblk - 1 - i, i) in turn and every workgroup does the same work. Eight
 // waves: wave w owns 32-row tile w % 4 of the block and, in key group w / 4,
 // every other 64-key step (group 0 the even steps, group 1 the odd ones), so
-// each SIMD runs two waves on independent work. Each iteration copies the
-// next two steps' K and V (128 keys) once per workgroup into LDS
-// (double-buffered; their global loads are in flight during the current
-// iteration), and every wave multiplies its tile by its step: S^T = K Q^T
+// each SIMD runs two waves on independent work. The next iteration's two
+// steps of K and V (128 keys) go straight from global memory into the other
+// half of a four-step LDS ring (global_load_lds_dwordx4, rows unpadded, their
+// 16-byte chunks swizzled by row as in attn_batch_rows_kernel) while every
+// wave multiplies its tile by its step of this iteration: S^T = K Q^T
 // (A = K from LDS, B = the wave's Q^T, held in registers), the online softmax
 // in base 2 on the S^T accumulators (each lane one row and 16 keys of every
 // 32-key half), O^T += V^T P^T (A = V^T by transposed LDS reads, B = P^T
@@ -1303,12 +1325,8 @@ __device__ __forceinline__ uint64_t window_limit(uint64_t win, int64_t kb0, int6
 // b starts on XCD b % 8), so the row blocks of a KV head share one L2.
 constexpr int kRowsWaves = 8;
 constexpr int kRowsKeys = 64;            // keys per step
-constexpr int kRowsKStride = 128 + 8;    // LDS row stride of K (elements): 272 B
-constexpr int kRowsVStride = 128 + 32;   // LDS row stride of V (elements): 320 B, as kVRow
-constexpr int kRowsKBytes = kRowsKeys * kRowsKStride * 2;
-constexpr int kRowsVBytes = kRowsKeys * kRowsVStride * 2;
-constexpr int kRowsStepBytes = kRowsKBytes + kRowsVBytes;
-constexpr int kRowsSmem = 4 * kRowsStepBytes;  // two buffers of two steps
+constexpr int kRowsStepBytes = 2 * kRowsKeys * 256;  // one step's K and V rows, unpadded (swizzled chunks)
+constexpr int kRowsSmem = 4 * kRowsStepBytes;         // two iterations of two steps
 // group 1's hand-over: per tile and lane 64 O values, m and l (rows of 68 floats: 16-byte aligned)
 constexpr int kRowsMergeStride = 64 + 4;
 constexpr int kRowsMergeBytes = 4 * 64 * kRowsMergeStride * 4;
@@ -1322,7 +1340,7 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void attn_rows_kernel(
     int nh, int nkv, int T, int64_t P, float scale, int nblk, int npair, void* __restrict__ out, int64_t ld_out,
     int out_units) {
   constexpr int HD = 128;
-  __shared__ __align__(16) uint8_t smem[kRowsSmem];
+  __shared__ __align__(1024) uint8_t smem[kRowsSmem];
   const int total = nkv * npair;
   const int b = blockIdx.x;
   const int w = (total & 7) ? b : (b & 7) * (total >> 3) + (b >> 3);
@@ -1334,30 +1352,22 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void attn_rows_kernel(
   const uint16_t* kh = kc + (int64_t)kvh * cap * HD;
   const uint16_t* vh = vc + (int64_t)kvh * cap * HD;
   const float scale2 = scale * 1.44269504088896341f;
-  typedef uint16_t(*KRow)[kRowsKStride];
-  typedef uint16_t(*VRow)[kRowsVStride];
-  // step buffer s (0..3): buffer s / 2 of the double buffer, step s % 2 of the pair
-  auto kbuf = [&](int s) { return (KRow)(smem + s * kRowsStepBytes); };
-  auto vbuf = [&](int s) { return (VRow)(smem + s * kRowsStepBytes + kRowsKBytes); };
-  // two steps' K and V: 128 keys x 16 chunks of 16 bytes each, four of each per thread
-  u32x4_t kr[4], vr[4];
-  auto load_pair = [&](int64_t kb0) {
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  // iteration it's two steps (2 it + group) go to step buffers 2 (it % 2) + group:
+  // wave w loads step 2 it + w / 4, its loads 8 (w % 4) .. + 7 of the step's
+  // 32 (K rows 4 i .. 4 i + 3 for i < 16, else V rows 4 (i - 16) ..), each
+  // lane one 16-byte chunk, swizzled by row
+  const int dsp = wave >> 2, dq = wave & 3;
+  const uint16_t* dsrc = uniform_ptr(dq < 2 ? kh : vh);
+  auto issue_pair = [&](int it) {
+    const int64_t kb0 = (int64_t)(2 * it + dsp) * kRowsKeys;
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_base + (2 * (it & 1) + dsp) * kRowsStepBytes +
+                                                        (dq < 2 ? 0 : 16384) + (dq & 1) * 8192);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int c = tid + 512 * s, key = c >> 4, part = c & 15;
-      const int64_t row = min(kb0 + key, S - 1);
-      kr[s] = *(const u32x4_t*)(kh + row * HD + part * 8);
-      vr[s] = *(const u32x4_t*)(vh + row * HD + part * 8);
-    }
-  };
-  auto store_pair = [&](int buf) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int c = tid + 512 * s, key = c >> 4, part = c & 15;
-      KRow ks = kbuf(2 * buf + (key >> 6));
-      VRow vs = vbuf(2 * buf + (key >> 6));
-      *(u32x4_t*)&ks[key & 63][part * 8] = kr[s];
-      *(u32x4_t*)&vs[key & 63][part * 8] = vr[s];
+    for (int k = 0; k < 8; ++k) {
+      const int row = 32 * (dq & 1) + 4 * k + (lane >> 4);
+      const uint32_t key = (uint32_t)min(kb0 + row, S - 1);
+      lds_dma16(dsrc, key * (HD * 2) + (((lane & 15) ^ (row & 15)) << 4), dst + k * 1024);
     }
   };
 
@@ -1393,15 +1403,16 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void attn_rows_kernel(
     float m = kInitMax, l = 0.f;
 
     __syncthreads();  // the previous block's buffers and hand-over are read by every wave
-    load_pair(0);
-    store_pair(0);
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);  // Q has landed: no wait of the compiler's covers the ring's loads
+    issue_pair(0);
     for (int it = 0; it < iters; ++it) {
-      if (it + 1 < iters) load_pair((int64_t)(it + 1) * 2 * kRowsKeys);
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of iteration it have landed
+      __syncthreads();                // everyone's have, and iteration it - 1's buffers are free
+      if (it + 1 < iters) issue_pair(it + 1);
       const int step = 2 * it + kg;
       const int64_t kb0 = (int64_t)step * kRowsKeys;
-      KRow ks = kbuf(2 * (it & 1) + kg);
-      VRow vs = vbuf(2 * (it & 1) + kg);
+      const uint8_t* kbp = smem + (2 * (it & 1) + kg) * kRowsStepBytes;
+      const uint8_t* vbp = kbp + 16384;
       if (tile_live && step < nsteps && kb0 <= tile_last_key) {  // wave-uniform: the tile sees a key of this step
         f32x16_t sc[2];
 #pragma unroll
@@ -1412,7 +1423,7 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void attn_rows_kernel(
         for (int j = 0; j < 8; ++j)
 #pragma unroll
           for (int sb = 0; sb < 2; ++sb) {
-            const u32x4_t kf = *(const u32x4_t*)&ks[32 * sb + ln][16 * j + 8 * g];
+            const u32x4_t kf = *(const u32x4_t*)(kbp + swz(32 * sb + ln, 2 * j + g));
             if constexpr (DT == PE_DTYPE_F16)
               sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf),
                                                               __builtin_bit_cast(f16x8_t, qf[j]), sc[sb], 0, 0, 0);
@@ -1473,8 +1484,10 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void attn_rows_kernel(
             const int db = 32 * h + 16 * (qg & 1) + 4 * (jl & 3);
             typedef short s4v_t __attribute__((__vector_size__(4 * sizeof(short))));
             typedef __attribute__((address_space(3))) s4v_t lds_s4v_t;
-            const s4v_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb][db]);
-            const s4v_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb + 8][db]);
+            const s4v_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s4v_t*)(vbp + swz(kb, db >> 3) + (db & 7) * 2));
+            const s4v_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s4v_t*)(vbp + swz(kb + 8, db >> 3) + (db & 7) * 2));
             const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
             u32x4_t a;
             a[0] = l2.x;
@@ -1490,11 +1503,9 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void attn_rows_kernel(
           }
         }
       }
-      if (it + 1 < iters) store_pair((it + 1) & 1);
-      __syncthreads();
     }
-    // group 1 hands (O, m, l) to group 0 (the loop's last barrier: every wave
-    // is done with the step buffers)
+    __syncthreads();  // every wave is done with the step buffers
+    // group 1 hands (O, m, l) to group 0
     float* mo = (float*)smem + (tile * 64 + lane) * kRowsMergeStride;
     if (kg == 1) {
 #pragma unroll
@@ -1540,34 +1551,42 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void attn_rows_kernel(
 // Batched tree attention with many rows per KV head (GQA batches)
 // ---------------------------------------------------------------------------
 // Sequence b's rows of a KV head are its T_b nodes x G query heads (row r =
-// node r / G, query head r % G), NW = ceil(max rows / 32) tiles of 32 rows,
-// one wave per tile. One workgroup = (key split, KV head, sequence); the
-// sequence's P_b + T_b keys are cut into splits of `kps` keys (a multiple of
-// 64), so a sequence has ceil((P_b + T_b) / kps) splits, every workgroup
-// walks the same number of keys, and the workgroups past a sequence's split
-// count leave at once. A split's keys are walked in 64-key steps, K and V of
-// a step copied once per workgroup into LDS (double-buffered, the next step's
-// global loads in flight during the current one) and multiplied by every
-// tile: the arithmetic of attn_rows_kernel, with the tree mask (prefix keys
-// visible to every node, node key u visible to node t when bit u of the
-// node's ancestor bits is set). A sequence of one split writes its output;
-// otherwise every workgroup publishes its split's (O, m, l) with
-// agent-coherent stores and counts itself on the (sequence, KV head) arrival
-// counter, and the last to arrive combines the splits in split order (running
-// max, rescaled sums) and sets the counter back to zero. Sequences whose
-// device prefix or row count exceed the bounds of the launch are skipped by
-// every workgroup alike (the K/V offsets kernel reports them).
-constexpr int kBRowsMaxWaves = 8;
-constexpr int kBRowsMinWaves = 4;  // fewer tiles: the staging needs 256 threads
+// node r / G, query head r % G): up to eight tiles of 32 rows, tile w on wave
+// w of an eight-wave workgroup. One workgroup = (key split, KV head,
+// sequence); the sequence's P_b + T_b keys are cut into splits of `kps` keys
+// (a multiple of 64), so a sequence has ceil((P_b + T_b) / kps) splits, every
+// workgroup walks the same number of keys, and those past a sequence's split
+// count leave at once. A split's keys are walked in 64-key steps through a
+// ring of four LDS step buffers filled by direct global-to-LDS loads
+// (global_load_lds_dwordx4: no registers, three steps in flight while one is
+// multiplied); each step is 32 loads of 1 KiB (wave w the four of K rows
+// 16 (w % 4) .. + 15 for w < 4, of V rows for w >= 4), one wait for this
+// wave's loads of the step and one barrier. K and V rows are stored unpadded
+// (256 bytes), their 16-byte chunks swizzled by row (chunk c of key row k at
+// c ^ (k % 16)), so the K fragment and transposed V reads of 16 consecutive
+// rows fall on different banks. The arithmetic is attn_rows_kernel's, with
+// the tree mask as a bit window. A sequence of one split writes its output;
+// otherwise each tile stores its split's (O, m, l) and attn_combine_kernel
+// (a second launch, one thread per row and 4-dim chunk) merges the splits in
+// split order. Sequences whose device prefix or row count exceed the bounds
+// of the launch are skipped by every workgroup alike (the K/V offsets kernel
+// reports them).
+constexpr int kBRowsWaves = 8;
+constexpr int kBRowsMinWaves = 4;  // fewer row tiles: attn_pair_kernel / attn_wg_kernel
+constexpr int kBRowsStep = 32 * 1024;  // one step's K and V, 64 keys x 256 bytes each
+constexpr int kBRowsRing = 4;          // step buffers; three steps in flight
+// s_waitcnt with vmcnt = 8 (expcnt and lgkmcnt left at their maxima): this
+// wave's loads of the two later steps in flight may still be outstanding
+constexpr int kWaitVm8 = 0x0F78;
 
 template <int DT>
-__global__ __launch_bounds__(64 * kBRowsMaxWaves, 1) void attn_batch_rows_kernel(
+__global__ __launch_bounds__(64 * kBRowsWaves, 1) void attn_batch_rows_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t cap,
     int nh, int nkv, const uint64_t* __restrict__ bits, int words, float scale, int kps, int max_splits,
-    int rows_pad, float* __restrict__ opart, float* __restrict__ mlpart, int* __restrict__ counters,
-    void* __restrict__ out, int64_t ld_out, int out_units, AttnBatch bt) {
+    int rows_pad, float* __restrict__ opart, float* __restrict__ mlpart, void* __restrict__ out, int64_t ld_out,
+    int out_units, AttnBatch bt) {
   constexpr int HD = 128;
-  __shared__ __align__(16) uint8_t smem[2 * kRowsStepBytes];
+  __shared__ __align__(1024) uint8_t smem[kBRowsRing * kBRowsStep];
   const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
   const int rbase = bt.seq_row0[seq];
   const int T = bt.seq_row0[seq + 1] - rbase;
@@ -1579,51 +1598,34 @@ __global__ __launch_bounds__(64 * kBRowsMaxWaves, 1) void attn_batch_rows_kernel
   if (split >= nsplit) return;
   const int64_t k0 = (int64_t)split * kps, k1 = min(S, k0 + kps);
   const int nsteps = (int)((k1 - k0 + kRowsKeys - 1) / kRowsKeys);
-  const int nthr = blockDim.x;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, ln = lane & 31, g = lane >> 5;
-  const uint16_t* kh = kc + seq * bt.seq_stride + (int64_t)kvh * cap * HD;
-  const uint16_t* vh = vc + seq * bt.seq_stride + (int64_t)kvh * cap * HD;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int ln = lane & 31, g = lane >> 5;
   const float scale2 = scale * 1.44269504088896341f;
-  typedef uint16_t(*KRow)[kRowsKStride];
-  typedef uint16_t(*VRow)[kRowsVStride];
-  auto kbuf = [&](int s) { return (KRow)(smem + s * kRowsStepBytes); };
-  auto vbuf = [&](int s) { return (VRow)(smem + s * kRowsStepBytes + kRowsKBytes); };
-  // one step's K and V: 64 keys x 16 chunks of 16 bytes, chunk tid + nthr s (s < 4) per thread
-  u32x4_t kr[4], vr[4];
-  auto load_step = [&](int64_t kb0) {
+  const uint16_t* kvbase = uniform_ptr((wave < 4 ? kc : vc) + seq * bt.seq_stride + (int64_t)kvh * cap * HD);
+  // this wave's four loads of a step: rows 16 (wave % 4) + 4 i + lane / 16, physical chunk lane % 16
+  const int prow0 = 16 * (wave & 3) + (lane >> 4), pch = lane & 15;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  auto issue = [&](int step) {
+    const int64_t kb0 = k0 + (int64_t)step * kRowsKeys;
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(
+        lds_base + (step % kBRowsRing) * kBRowsStep + (wave >= 4 ? 16384 : 0) + (wave & 3) * 4096);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int c = tid + nthr * s;
-      if (c < 1024) {
-        const int64_t row = min(kb0 + (c >> 4), S - 1);
-        kr[s] = *(const u32x4_t*)(kh + row * HD + (c & 15) * 8);
-        vr[s] = *(const u32x4_t*)(vh + row * HD + (c & 15) * 8);
-      }
-    }
-  };
-  auto store_step = [&](int slot) {
-    KRow ks = kbuf(slot);
-    VRow vs = vbuf(slot);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int c = tid + nthr * s;
-      if (c < 1024) {
-        *(u32x4_t*)&ks[c >> 4][(c & 15) * 8] = kr[s];
-        *(u32x4_t*)&vs[c >> 4][(c & 15) * 8] = vr[s];
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int row = prow0 + 4 * i;
+      const uint32_t key = (uint32_t)min(kb0 + row, S - 1);
+      lds_dma16(kvbase, key * (HD * 2) + ((pch ^ (row & 15)) << 4), dst + i * 1024);
     }
   };
 
-  const int rt0 = 32 * wave;
-  const bool tile_live = rt0 < rows;
-  const int r = rt0 + ln;
+  const bool tile_live = wave * 32 < rows;
+  const int r = wave * 32 + ln;
   const int rr = min(r, rows - 1);
   const int t = rr / G;
   uint64_t nbits[PE_TREE_MAX_WORDS];
-#pragma unroll
-  for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = bits[(int64_t)(rbase + t) * words + min(w, words - 1)];
   u32x4_t qf[8];
-  {
+  if (tile_live) {
+#pragma unroll
+    for (int w = 0; w < PE_TREE_MAX_WORDS; ++w) nbits[w] = bits[(int64_t)(rbase + t) * words + min(w, words - 1)];
     const uint16_t* qrow = q + ((int64_t)(rbase + t) * nh + kvh * G + rr % G) * HD + 8 * g;
 #pragma unroll
     for (int j = 0; j < 8; ++j) qf[j] = *(const u32x4_t*)(qrow + 16 * j);
@@ -1635,14 +1637,21 @@ __global__ __launch_bounds__(64 * kBRowsMaxWaves, 1) void attn_batch_rows_kernel
     for (int i = 0; i < 16; ++i) o[h][i] = 0.f;
   float m = kInitMax, l = 0.f;
 
-  load_step(k0);
-  store_step(0);
-  __syncthreads();
+  // Q and the bits have landed before the ring starts, so no wait of the
+  // compiler's for them covers the ring's loads; then three steps in flight
+  // ahead of the one multiplied (past the split's end the loads repeat its
+  // last key row into buffers nobody reads)
+  __builtin_amdgcn_s_waitcnt(0);
+  issue(0);
+  issue(1);
+  issue(2);
   for (int st = 0; st < nsteps; ++st) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm8);  // this wave's loads of step st have landed
+    __syncthreads();
+    issue(st + 3);
     const int64_t kb0 = k0 + (int64_t)st * kRowsKeys;
-    if (st + 1 < nsteps) load_step(kb0 + kRowsKeys);
-    KRow ks = kbuf(st & 1);
-    VRow vs = vbuf(st & 1);
+    const uint8_t* kb = smem + (st % kBRowsRing) * kBRowsStep;
+    const uint8_t* vb = kb + 16384;
     if (tile_live) {
       f32x16_t sc[2];
 #pragma unroll
@@ -1653,7 +1662,7 @@ __global__ __launch_bounds__(64 * kBRowsMaxWaves, 1) void attn_batch_rows_kernel
       for (int j = 0; j < 8; ++j)
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
-          const u32x4_t kf = *(const u32x4_t*)&ks[32 * sb + ln][16 * j + 8 * g];
+          const u32x4_t kf = *(const u32x4_t*)(kb + swz(32 * sb + ln, 2 * j + g));
           if constexpr (DT == PE_DTYPE_F16)
             sc[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, kf),
                                                             __builtin_bit_cast(f16x8_t, qf[j]), sc[sb], 0, 0, 0);
@@ -1698,6 +1707,7 @@ __global__ __launch_bounds__(64 * kBRowsMaxWaves, 1) void attn_batch_rows_kernel
 #pragma unroll
           for (int i = 0; i < 16; ++i) o[h][i] *= alpha;
       }
+      // O^T += V^T P^T; lane (qg, jl) reads 8 bytes of key row kbr, dims db .. db + 3
       const int qg = lane >> 4, jl = lane & 15;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -1707,14 +1717,16 @@ __global__ __launch_bounds__(64 * kBRowsMaxWaves, 1) void attn_batch_rows_kernel
         bp[1] = pb[sb][4 * cq + 1];
         bp[2] = pb[sb][4 * cq + 2];
         bp[3] = pb[sb][4 * cq + 3];
-        const int kb = 16 * c + 4 * (qg >> 1) + (jl >> 2);
+        const int kbr = 16 * c + 4 * (qg >> 1) + (jl >> 2);
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
           const int db = 32 * h + 16 * (qg & 1) + 4 * (jl & 3);
           typedef short s4v_t __attribute__((__vector_size__(4 * sizeof(short))));
           typedef __attribute__((address_space(3))) s4v_t lds_s4v_t;
-          const s4v_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb][db]);
-          const s4v_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4v_t*)&vs[kb + 8][db]);
+          const s4v_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s4v_t*)(vb + swz(kbr, db >> 3) + (db & 7) * 2));
+          const s4v_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s4v_t*)(vb + swz(kbr + 8, db >> 3) + (db & 7) * 2));
           const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
           u32x4_t a;
           a[0] = l2.x;
@@ -1730,88 +1742,105 @@ __global__ __launch_bounds__(64 * kBRowsMaxWaves, 1) void attn_batch_rows_kernel
         }
       }
     }
-    if (st + 1 < nsteps) store_step((st + 1) & 1);
-    __syncthreads();
   }
-
+  // the ring's last loads land before the workgroup ends
+  __builtin_amdgcn_s_waitcnt(0);
+  if (!tile_live || r >= rows) return;
   typedef typename Elem<DT>::T Te;
-  // a row's output: 4 consecutive dims at column col of node row rbase + tt
-  auto store4 = [&](int tt, int col, const float (&o4)[4]) {
-    const int64_t row = rbase + tt;
-    if (out_units)
-      Vec4<DT>::store((Te*)out + xtile_index((int)row, col, out_units), o4);
-    else if ((ld_out & 3) || ((uintptr_t)out & 7)) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Elem<DT>::store((Te*)out, row * ld_out + col + i, o4[i]);
-    } else {
-      Vec4<DT>::store((Te*)out + row * ld_out + col, o4);
-    }
-  };
   // o[h][4 c .. 4 c + 3] are dims 32 h + 8 c + 4 g + 0..3 of row r
   if (nsplit == 1) {
-    if (tile_live && r < rows) {
-      const int col0 = (kvh * G + r % G) * HD;
-#pragma unroll
-      for (int h = 0; h < 4; ++h)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          float o4[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o4[i] = o[h][4 * c + i] / l;
-          store4(t, col0 + 32 * h + 8 * c + 4 * g, o4);
-        }
-    }
-    return;
-  }
-  const int pair = seq * nkv + kvh;
-  const uint32_t nrows = (uint32_t)(bt.batch * nkv * max_splits * rows_pad);
-  const __amdgpu_buffer_rsrc_t ro = agent_rsrc(opart, nrows * HD * 4), rm = agent_rsrc(mlpart, nrows * 16);
-  auto prow = [&](int sp, int row) -> uint32_t { return (uint32_t)((pair * max_splits + sp) * rows_pad + row); };
-  if (tile_live && r < rows) {
+    const int col0 = (kvh * G + r % G) * HD;
+    const int64_t orow = rbase + t;
 #pragma unroll
     for (int h = 0; h < 4; ++h)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        store_agent_x4(ro, (prow(split, r) * HD + 32 * h + 8 * c + 4 * g) * 4,
-                       f32x4_t{o[h][4 * c], o[h][4 * c + 1], o[h][4 * c + 2], o[h][4 * c + 3]});
-    if (g == 0) store_agent_x4(rm, prow(split, r) * 16, f32x4_t{m, l, 0.f, 0.f});
+      for (int c = 0; c < 4; ++c) {
+        float o4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o4[i] = o[h][4 * c + i] / l;
+        const int col = col0 + 32 * h + 8 * c + 4 * g;
+        if (out_units)
+          Vec4<DT>::store((Te*)out + xtile_index((int)orow, col, out_units), o4);
+        else if ((ld_out & 3) || ((uintptr_t)out & 7)) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Elem<DT>::store((Te*)out, orow * ld_out + col + i, o4[i]);
+        } else {
+          Vec4<DT>::store((Te*)out + orow * ld_out + col, o4);
+        }
+      }
+    return;
   }
-  // the stores are acknowledged at agent scope before this workgroup counts itself
-  __builtin_amdgcn_s_waitcnt(0);
-  __shared__ int s_arrived;
-  __syncthreads();
-  if (tid == 0) s_arrived = __hip_atomic_fetch_add(counters + pair, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (s_arrived + 1 != nsplit) return;
-  // the last to arrive: item = (row, 4-dim chunk), the splits merged in split order
-  for (int item = tid; item < rows * 32; item += nthr) {
-    const int row = item >> 5, d0 = (item & 31) * 4;
-    float Mx = kInitMax, den = 0.f, num[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int c0 = 0; c0 < nsplit; c0 += 8) {  // up to 8 splits' loads in flight
-      f32x4_t ov[8], mv[8];
+  const int64_t prow = ((int64_t)(seq * nkv + kvh) * max_splits + split) * rows_pad + r;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int sp = min(c0 + c, nsplit - 1);
-        ov[c] = load_agent_x4(ro, (prow(sp, row) * HD + d0) * 4);
-        mv[c] = load_agent_x4(rm, prow(sp, row) * 16);
-      }
+  for (int h = 0; h < 4; ++h)
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        if (c0 + c >= nsplit) break;
-        const float mn = fmaxf(Mx, mv[c][0]);
-        const float a = __builtin_amdgcn_exp2f(Mx - mn), wt = __builtin_amdgcn_exp2f(mv[c][0] - mn);
-        Mx = mn;
-        den = den * a + wt * mv[c][1];
+    for (int c = 0; c < 4; ++c)
+      *(f32x4_t*)(opart + prow * HD + 32 * h + 8 * c + 4 * g) =
+          f32x4_t{o[h][4 * c], o[h][4 * c + 1], o[h][4 * c + 2], o[h][4 * c + 3]};
+  if (g == 0) *(float2*)(mlpart + prow * 2) = float2{m, l};
+}
+
+// The split merge of attn_batch_rows_kernel: one thread per (sequence, KV
+// head, row, 4-dim chunk), every split's partial requested at once (up to
+// eight per round), merged in split order (running max, rescaled sums).
+template <int DT>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ opart,
+                                                           const float* __restrict__ mlpart, int nh, int nkv,
+                                                           int kps, int max_splits, int rows_pad,
+                                                           void* __restrict__ out, int64_t ld_out, int out_units,
+                                                           AttnBatch bt) {
+  constexpr int HD = 128;
+  const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int chunk = (int)(item & 31);
+  const int64_t rowid = item >> 5;  // (seq * nkv + kvh) * rows_pad + row
+  const int row = (int)(rowid % rows_pad);
+  const int pair = (int)(rowid / rows_pad);
+  if (pair >= bt.batch * nkv) return;
+  const int seq = pair / nkv, kvh = pair - seq * nkv;
+  const int rbase = bt.seq_row0[seq];
+  const int T = bt.seq_row0[seq + 1] - rbase;
+  const int64_t P = bt.seq_prefix[seq];
+  if (T <= 0 || T > bt.max_rows || P < 0 || P > bt.max_prefix) return;
+  const int G = nh / nkv;
+  if (row >= T * G) return;
+  const int nsplit = (int)((P + T + kps - 1) / kps);
+  if (nsplit <= 1) return;
+  float Mx = kInitMax, den = 0.f, num[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < nsplit; c0 += 8) {
+    f32x4_t ov[8];
+    float2 mv[8];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) num[k] = num[k] * a + wt * ov[c][k];
-      }
+    for (int c = 0; c < 8; ++c) {
+      const int sp = min(c0 + c, nsplit - 1);
+      const int64_t prow = ((int64_t)pair * max_splits + sp) * rows_pad + row;
+      ov[c] = *(const f32x4_t*)(opart + prow * HD + chunk * 4);
+      mv[c] = *(const float2*)(mlpart + prow * 2);
     }
-    float o4[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) o4[k] = num[k] / den;
-    store4(row / G, (kvh * G + row % G) * HD + d0, o4);
+    for (int c = 0; c < 8; ++c) {
+      if (c0 + c >= nsplit) break;
+      const float mn = fmaxf(Mx, mv[c].x);
+      const float a = __builtin_amdgcn_exp2f(Mx - mn), wt = __builtin_amdgcn_exp2f(mv[c].x - mn);
+      Mx = mn;
+      den = den * a + wt * mv[c].y;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) num[k] = num[k] * a + wt * ov[c][k];
+    }
   }
-  if (tid == 0) __hip_atomic_store(counters + pair, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float o4[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o4[k] = num[k] / den;
+  typedef typename Elem<DT>::T Te;
+  const int64_t orow = rbase + row / G;
+  const int col = (kvh * G + row % G) * HD + chunk * 4;
+  if (out_units)
+    Vec4<DT>::store((Te*)out + xtile_index((int)orow, col, out_units), o4);
+  else if ((ld_out & 3) || ((uintptr_t)out & 7)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Elem<DT>::store((Te*)out, orow * ld_out + col + i, o4[i]);
+  } else {
+    Vec4<DT>::store((Te*)out + orow * ld_out + col, o4);
+  }
 }
 
 }  // namespace
@@ -1848,7 +1877,7 @@ int pe_internal_tree_attention(const void* q, const void* k_cache, const void* v
   if (workspace_bytes < attention_workspace_bytes(T, nh, nkv, hd, S, dtype, attn_mode)) return PE_ERR_WORKSPACE;
   if (dtype != PE_DTYPE_F32 && hd == 128 && !eager && mask_mode == PE_MASK_CAUSAL && T >= kRowsMinNodes) {
     // many causal rows (a prefill): row blocks in balanced pairs, no key splits
-    if (!(scale > 0.f)) return PE_ERR_ARG;
+    if (!(scale > 0.f) || cache_cap >= kAttnMaxCap) return PE_ERR_ARG;
     const int nblk = (T * (nh / nkv) + 127) / 128, npair = (nblk + 1) / 2;
     const dim3 grid(nkv * npair);
     if (dtype == PE_DTYPE_BF16)
@@ -1945,15 +1974,15 @@ BRowsPlan brows_plan(int max_rows, int nh, int nkv, int64_t max_kv_len, int batc
   BRowsPlan p{};
   const int rows = max_rows * (nh / nkv);
   p.waves = (rows + 31) / 32;
-  // opt-in (PE_ATTN_BATCH_ROWS=1): at the batched workload it measured slower
-  // than attn_pair_kernel (99.5 against 39.1 us per launch), its steps waiting
-  // on their one-step-ahead K/V loads and its combine on 13 rounds of reloads
+  // opt-in (PE_ATTN_BATCH_ROWS=1): at the batched workload the kernel matches
+  // attn_pair_kernel (39.2 against 39.1 us per launch) but its split combine
+  // (a second launch, 8.2 us) and a partly filled second round of workgroups
+  // leave the pass 0.3 ms slower
   static const bool enabled = [] {
     const char* v = getenv("PE_ATTN_BATCH_ROWS");
     return v && v[0] == '1';
   }();
-  p.use = enabled && p.waves >= kBRowsMinWaves && p.waves <= kBRowsMaxWaves &&
-          (int64_t)batch * nkv * 4 <= kAttnCounterBytes;
+  p.use = enabled && p.waves >= kBRowsMinWaves && p.waves <= kBRowsWaves;
   if (!p.use) return p;
   int64_t want = (512 + (int64_t)batch * nkv - 1) / ((int64_t)batch * nkv);
   want = want < 1 ? 1 : (want > 16 ? 16 : want);
@@ -1964,7 +1993,7 @@ BRowsPlan brows_plan(int max_rows, int nh, int nkv, int64_t max_kv_len, int batc
   p.max_splits = (int)((max_kv_len + kps - 1) / kps);
   p.rows_pad = p.waves * 32;
   p.opart_bytes = (int64_t)batch * nkv * p.max_splits * p.rows_pad * 128 * 4;
-  p.ml_bytes = (int64_t)batch * nkv * p.max_splits * p.rows_pad * 4 * 4;
+  p.ml_bytes = (int64_t)batch * nkv * p.max_splits * p.rows_pad * 2 * 4;
   return p;
 }
 
@@ -2002,14 +2031,23 @@ int pe_internal_tree_attention_batch(const void* q, const void* k_cache, const v
     float* op = (float*)((char*)workspace + kAttnCounterBytes);
     float* mp = (float*)((char*)workspace + kAttnCounterBytes + rp.opart_bytes);
     const dim3 gridr(rp.max_splits, nkv, batch);
-    if (dtype == PE_DTYPE_BF16)
-      attn_batch_rows_kernel<PE_DTYPE_BF16><<<gridr, 64 * rp.waves, 0, st>>>(
+    const int64_t items = (int64_t)batch * nkv * rp.rows_pad * 32;
+    const dim3 gridc((unsigned)((items + 255) / 256));
+    if (dtype == PE_DTYPE_BF16) {
+      attn_batch_rows_kernel<PE_DTYPE_BF16><<<gridr, 64 * kBRowsWaves, 0, st>>>(
           (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, bits, words,
-          scale, rp.kps, rp.max_splits, rp.rows_pad, op, mp, counters, out, ld_out, out_units, bt);
-    else
-      attn_batch_rows_kernel<PE_DTYPE_F16><<<gridr, 64 * rp.waves, 0, st>>>(
+          scale, rp.kps, rp.max_splits, rp.rows_pad, op, mp, out, ld_out, out_units, bt);
+      if (rp.max_splits > 1)
+        attn_combine_kernel<PE_DTYPE_BF16><<<gridc, 256, 0, st>>>(op, mp, nh, nkv, rp.kps, rp.max_splits, rp.rows_pad,
+                                                                  out, ld_out, out_units, bt);
+    } else {
+      attn_batch_rows_kernel<PE_DTYPE_F16><<<gridr, 64 * kBRowsWaves, 0, st>>>(
           (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, cache_cap, nh, nkv, bits, words,
-          scale, rp.kps, rp.max_splits, rp.rows_pad, op, mp, counters, out, ld_out, out_units, bt);
+          scale, rp.kps, rp.max_splits, rp.rows_pad, op, mp, out, ld_out, out_units, bt);
+      if (rp.max_splits > 1)
+        attn_combine_kernel<PE_DTYPE_F16><<<gridc, 256, 0, st>>>(op, mp, nh, nkv, rp.kps, rp.max_splits, rp.rows_pad,
+                                                                 out, ld_out, out_units, bt);
+    }
     PE_CHECK_LAUNCH();
     return PE_OK;
   }
