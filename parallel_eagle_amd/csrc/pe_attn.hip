@@ -1241,26 +1241,10 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S, int batch = 1) {
   return p;
 }
 
+// Byte offset of 16-byte chunk `chunk` of a 256-byte K / V row in an LDS step
+// buffer: chunks swizzled by row, so that 16 consecutive rows' reads of one
+// chunk fall on different banks.
 __device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 256 + ((chunk ^ (row & 15)) << 4)); }
-
-// 16 bytes per lane from global memory straight into LDS at lds_base + 16 *
-// lane (lds_base wave-uniform, through M0). Issued as inline assembly so that
-// the compiler, which cannot tell these LDS writes from the ring slot being
-// read, adds no wait for them in front of every LDS read; the kernel orders
-// them itself (an explicit vmcnt wait and a workgroup barrier per step).
-// A pointer that is the same in every lane, held in scalar registers.
-__device__ __forceinline__ const uint16_t* uniform_ptr(const uint16_t* p) {
-  const uint64_t v = (uint64_t)(uintptr_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const uint16_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-
-// The source is a wave-uniform base (SGPRs) plus a per-lane 32-bit byte
-// offset (a head's cache rows span less than 2^24 x 256 bytes).
-__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_base)
-               : "memory", "m0");
-}
 
 // Visibility of the 64 keys kb0 .. kb0 + 63 to one query row, as a bit mask
 // (bit j: key kb0 + j), so that each score register tests a bit at an offset

@@ -164,6 +164,26 @@ __device__ __forceinline__ f32x4_t load_agent_x4(__amdgpu_buffer_rsrc_t r, uint3
   return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSC1));
 }
 
+// 16 bytes per lane from global memory straight into LDS at lds_base + 16 *
+// lane (lds_base wave-uniform, through M0), for rings of LDS buffers.
+//
+// A pointer that is the same in every lane, held in scalar registers.
+__device__ __forceinline__ const uint16_t* uniform_ptr(const uint16_t* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint16_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// The source is a wave-uniform base (SGPRs) plus a per-lane 32-bit byte
+// offset (callers keep every source within 4 GiB of the base). Issued as
+// inline assembly so that the compiler, which cannot tell these LDS writes
+// from the LDS being read, adds no wait for them in front of every LDS read;
+// callers order them with an explicit vmcnt wait and a workgroup barrier.
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_base)
+               : "memory", "m0");
+}
+
 #define PE_CHECK_LAUNCH()                                   \
   do {                                                      \
     hipError_t _e = hipGetLastError();                      \

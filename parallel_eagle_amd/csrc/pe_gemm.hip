@@ -1087,6 +1087,124 @@ __global__ __launch_bounds__(kWaves * 64, 2) void dense_gemm_bigm_kernel(const u
 }
 
 // ---------------------------------------------------------------------------
+// Dense 16-bit GEMM over many rows: 256 x 256 output tiles
+// ---------------------------------------------------------------------------
+// One workgroup = 4 waves = 256 rows (eight 32-row tiles of the A-tiled X) x
+// 256 columns (eight 32-column weight tiles); wave w owns rows 128 (w / 2) ..
+// + 127 and columns 128 (w % 2) .. + 127: 4 x 4 MFMA tiles, 256 fp32
+// accumulators. K is walked in stages of two MFMA k-steps. A stage's 16 A
+// fragments (8 M tiles x 2 k-steps) and 16 B fragments (8 N tiles x 2
+// k-steps), 1 KiB each, go straight from global memory into a four-stage LDS
+// ring (global_load_lds_dwordx4: three stages in flight while one is
+// multiplied); wave w loads fragments 8 w .. 8 w + 7 of the stage (A for
+// w < 2, B otherwise). A fragments are copied as stored (the A-tiled layout is
+// MFMA fragment order). The B fragment for k-step s of unit p is gathered lane
+// by lane from weight k-step 8 p + 4 g + s / 2, lane n + 32 (s % 2) of the
+// tiled weights, so that both operands hold the same k in the same place. Per
+// stage a wave reads its 4 + 4 fragments of each k-step (ds_read_b128 at the
+// lane's 16 bytes: conflict-free) and issues 32 MFMAs. One vmcnt wait and one
+// barrier per stage; loads past the split's last stage repeat its last unit
+// into buffers nobody reads. Work item w of the grid (column tile w / mblocks,
+// row block w % mblocks) runs on XCD w / (grid / 8) when the grid is a
+// multiple of eight, so the row blocks of a column tile share its weights in
+// one L2. grid.y: K splits (fp32 partials out[split][row][col]).
+constexpr int kT256Stage = 32 * 1024;
+constexpr int kT256Ring = 4;
+// s_waitcnt with vmcnt = 16 (expcnt and lgkmcnt at their maxima): this wave's
+// loads of the two later stages in flight may still be outstanding
+constexpr int kWaitVm16 = (16 & 15) | (7 << 4) | (15 << 8) | ((16 >> 4) << 14);
+
+template <int DT, bool F32OUT>
+__global__ __launch_bounds__(256, 1) void dense_gemm_t256_kernel(const uint16_t* __restrict__ X,
+                                                                 const uint16_t* __restrict__ W, int units,
+                                                                 int ups, int mtiles, int mblocks, int M,
+                                                                 void* __restrict__ out, int64_t ld, int64_t N) {
+  __shared__ __align__(1024) uint8_t smem[kT256Ring * kT256Stage];
+  const int total = gridDim.x;
+  const int b = blockIdx.x;
+  const int w = (total & 7) ? b : (b & 7) * (total >> 3) + (b >> 3);
+  const int ntile = w / mblocks, mblock = w - ntile * mblocks;
+  const int split = blockIdx.y;
+  const int u0 = split * ups, u1 = min(units, u0 + ups);
+  if (u0 >= u1) return;
+  const int nstages = (u1 - u0) * 4;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int ln = lane & 31, g = lane >> 5;
+  const int KS = units * 8;  // weight k-steps
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  const uint16_t* xb = uniform_ptr(X);
+  const uint16_t* wb = uniform_ptr(W);
+  // this wave's eight fragments of a stage
+  auto issue = [&](int t) {
+    const int tc = min(t, nstages - 1);
+    const int p = u0 + tc / 4, s0 = 2 * (tc % 4);
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_base + (t % kT256Ring) * kT256Stage + wave * 8192);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int f = 8 * (wave & 1) + i;  // fragment of the operand: tile f / 2, k-step s0 + f % 2
+      const int s = s0 + (f & 1);
+      uint32_t off;
+      if (wave < 2) {
+        const int mt = min(mblock * 8 + (f >> 1), mtiles - 1);
+        off = (uint32_t)((((mt * units + p) * 8 + s) * 64 + lane) * 16);
+      } else {
+        const int nt = ntile * 8 + (f >> 1);
+        off = (uint32_t)((((int64_t)nt * KS + 8 * p + 4 * g + (s >> 1)) * 64 + ln + 32 * (s & 1)) * 16);
+      }
+      lds_dma16(wave < 2 ? (const void*)xb : (const void*)wb, off, dst + i * 1024);
+    }
+  };
+  const int wm = wave >> 1, wn = wave & 1;
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
+  issue(0);
+  issue(1);
+  issue(2);
+  for (int t = 0; t < nstages; ++t) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm16);  // this wave's loads of stage t have landed
+    __syncthreads();                        // everyone's have; stage t - 1's buffer is free
+    issue(t + 3);
+    const uint8_t* st = smem + (t % kT256Ring) * kT256Stage + lane * 16;
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      u32x4_t a[4], bf[4];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) a[mi] = *(const u32x4_t*)(st + ((4 * wm + mi) * 2 + sl) * 1024);
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) bf[ni] = *(const u32x4_t*)(st + 16384 + ((4 * wn + ni) * 2 + sl) * 1024);
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma16<DT>(a[mi], bf[ni], acc[mi][ni]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the ring's last loads land before the workgroup ends
+  typedef typename Elem<DT>::T Te;
+  const int64_t base = F32OUT ? (int64_t)split * M * ld : 0;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = mblock * 256 + 128 * wm + 32 * mi + 8 * (r >> 2) + 4 * g + (r & 3);
+      if (row >= M) continue;
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        const int64_t o = base + (int64_t)row * ld + ntile * 256 + 128 * wn + 32 * ni + ln;
+        if constexpr (F32OUT)
+          ((float*)out)[o] = acc[mi][ni][r];
+        else
+          Elem<DT>::store((Te*)out, o, acc[mi][ni][r]);
+      }
+    }
+  (void)N;
+}
+
+// ---------------------------------------------------------------------------
 // Dense 16-bit GEMM: one iteration = 4 MFMA k-steps (64 along K) of NT tiles.
 // Same pipeline as the NF4 kernel; a padded iteration multiplies a zero X.
 // ---------------------------------------------------------------------------
@@ -1726,6 +1844,34 @@ int64_t pe_internal_nf4_bigm_partials_bytes(int M, int N, int K) {
 int pe_internal_dense_bigm(const void* x_tiled, int M, int K, const void* w, int dtype, int N, void* out,
                            int64_t ld_out, hipStream_t st, bool f32_out) {
   if (!x_tiled || !w || !out || M <= 0 || K % 128 || N % (32 * kBigNT) || ld_out < N) return PE_ERR_ARG;
+  const int mtiles0 = (M + 31) / 32;
+  // 256 x 256 tiles from an LDS ring when the tiles fill at least two rounds
+  // of one workgroup per CU (offsets within X and W below 4 GiB). With fewer
+  // tiles the 128-column kernel, two workgroups per CU, measured faster (a
+  // 2047-row drafter context: q/k/v 226 against 258 us, the 4096-column
+  // linears 212 against 285; gate/up, 688 tiles, 403 against 442)
+  const int mblocks0 = (M + 255) / 256;
+  if (M > 256 && N % 256 == 0 && (int64_t)(N / 256) * mblocks0 >= 512 && (int64_t)N * K * 2 < (int64_t(1) << 32) &&
+      (int64_t)mtiles0 * 32 * K * 2 < (int64_t(1) << 32)) {
+    const int units = K / 128, mblocks = mblocks0;
+    const dim3 grid((unsigned)(N / 256 * mblocks), 1);
+#define PE_T256_LAUNCH(D, F)                                                                                   \
+  dense_gemm_t256_kernel<D, F><<<grid, 256, 0, st>>>((const uint16_t*)x_tiled, (const uint16_t*)w, units, units, \
+                                                     mtiles0, mblocks, M, out, ld_out, N)
+    if (dtype == PE_DTYPE_BF16 && f32_out)
+      PE_T256_LAUNCH(PE_DTYPE_BF16, true);
+    else if (dtype == PE_DTYPE_BF16)
+      PE_T256_LAUNCH(PE_DTYPE_BF16, false);
+    else if (dtype == PE_DTYPE_F16 && f32_out)
+      PE_T256_LAUNCH(PE_DTYPE_F16, true);
+    else if (dtype == PE_DTYPE_F16)
+      PE_T256_LAUNCH(PE_DTYPE_F16, false);
+    else
+      return PE_ERR_ARG;
+#undef PE_T256_LAUNCH
+    PE_CHECK_LAUNCH();
+    return PE_OK;
+  }
   const int np = K / 128;
   const int mtiles = (M + 31) / 32;
   const dim3 grid(N / (32 * kBigNT), (mtiles + 7) / 8);

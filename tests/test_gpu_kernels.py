@@ -207,6 +207,31 @@ def test_dense_linear_epilogues(dtype, epi):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,k,n", [(300, 1024, 512), (513, 1152, 768), (2047, 4096, 4096),
+                                   (2048, 1024, 16384), (1025, 512, 26624)])
+def test_dense_linear_over_many_rows(dtype, m, k, n):
+    """pe_dense_gemm over more than 256 rows (prefill and drafter-context
+    linears: 128-column workgroups, or, from 512 tiles on, 256 x 256 tiles with
+    both operands through an LDS ring; last row blocks partly filled) against
+    the fp32 product rounded once: outputs of
+    at least 1e-3 of the largest within one step of the dtype, at most 0.5% of
+    them one step away (another fp32 summation order alone moves 0.15% of fp16
+    outputs by a step); every output within 1e-5 of the largest (near zero a
+    step of fp16 is far below the summation-order noise of fp32)."""
+    w = torch.from_numpy(synth.normal(5, 44, n * k, 0.02).reshape(n, k)).to(dtype)
+    x = torch.from_numpy(synth.normal(6, 45, m * k, 1.0).reshape(m, k)).to(dtype)
+    y = ops.linear(x.to(DEV), n, dense=ops.dense_repack(w.to(DEV))).cpu()
+    r32 = x.float() @ w.float().t()
+    ref = r32.to(dtype)
+    top = float(r32.abs().max())
+    big = r32.abs() >= 1e-3 * top
+    steps = (y.view(torch.int16).int() - ref.view(torch.int16).int()).abs()[big]
+    assert int(steps.max()) <= 1, int(steps.max())
+    assert int((steps == 1).sum()) <= m * n // 200, int((steps == 1).sum())
+    assert float((y.float() - r32).abs().max()) <= 1e-5 * top + float((ref.float() - r32).abs().max())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m", [26, 40])
 def test_dense_swiglu_at_the_14b_shape(dtype, m):
     """The dense gate/up at the Qwen2.5-14B shape (K = 5120, 2 x 13824 columns:
