@@ -969,8 +969,8 @@ __global__ __launch_bounds__(kWsWaves * 64, 1) void nf4_gemm_bigws_kernel(const 
 // once and stored in the dtype, row-major with leading dimension ld.
 template <int DT, int NMT, int WV, bool F32OUT>
 __device__ __forceinline__ void dense_bigm_wave(uint8_t* smem, const uint16_t* __restrict__ X,
-                                                const uint16_t* __restrict__ W, int NP, int group, int mt0, int M,
-                                                void* __restrict__ out, int64_t ld) {
+                                                const uint16_t* __restrict__ W, int NP, int p0, int p1, int group,
+                                                int mt0, int M, void* __restrict__ out, int64_t ld) {
   constexpr int MA = NMT > 0 ? NMT : 1;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 5, ln = lane & 31;
@@ -982,7 +982,7 @@ __device__ __forceinline__ void dense_bigm_wave(uint8_t* smem, const uint16_t* _
   // fragment from k-step 8 p + 4 g + s / 2, lane n + 32 (s % 2) of the tile:
   // two 512-byte contiguous runs per load instruction.
   auto load_b = [&](u32x4_t (&b)[8], int p) {
-    const int pc = min(p, NP - 1);
+    const int pc = min(p, p1 - 1);
     const u32x4_t* src = (const u32x4_t*)(W + ((tile * NP * 8 + 8 * pc + 4 * g) * 64 + ln) * 8);
 #pragma unroll
     for (int s = 0; s < 8; ++s) b[s] = __builtin_nontemporal_load(src + (s >> 1) * 64 + 32 * (s & 1));
@@ -1019,16 +1019,16 @@ __device__ __forceinline__ void dense_bigm_wave(uint8_t* smem, const uint16_t* _
     }
   };
   u32x4_t ba[8], bb[8];
-  load_b(ba, 0);
-  load_b(bb, 1);
-  for (int p = 0; p < NP; p += 2) {
+  load_b(ba, p0);
+  load_b(bb, p0 + 1);
+  for (int p = p0; p < p1; p += 2) {
     load_x(p, 0);
     load_x(p, 1);
     store_b(ba, p);
     load_b(ba, p + 2);
     lds_barrier();  // unit p's fragments are complete; the other slot is free
     multiply(p);
-    if (p + 1 < NP) {  // the same for every wave of the workgroup
+    if (p + 1 < p1) {  // the same for every wave of the workgroup
       load_x(p + 1, 0);
       load_x(p + 1, 1);
       store_b(bb, p + 1);
@@ -1050,15 +1050,17 @@ __device__ __forceinline__ void dense_bigm_wave(uint8_t* smem, const uint16_t* _
           for (int nt = 0; nt < kBigNT; ++nt) {
             const int64_t o = (int64_t)row * ld + (group * kBigNT + nt) * 32 + ln;
             if constexpr (F32OUT)
-              ((float*)out)[o] = acc[nt][mt][4 * q4 + j];
+              ((float*)out)[(int64_t)blockIdx.z * M * ld + o] = acc[nt][mt][4 * q4 + j];
             else
               Elem<DT>::store((Te*)out, o, acc[nt][mt][4 * q4 + j]);
           }
       }
 }
 
-// F32OUT: the fp32 sums are stored as they are (one split of partials, for the
-// prefill's epilogue kernels); grid.y runs over blocks of eight 32-row tiles.
+// F32OUT: the fp32 sums are stored as they are, split partials
+// out[split][row][col] for the prefill's epilogue kernels (grid.z: K splits of
+// ceil(NP / splits) units, each non-empty); grid.y runs over blocks of eight
+// 32-row tiles.
 template <int DT, bool F32OUT>
 __global__ __launch_bounds__(kWaves * 64, 2) void dense_gemm_bigm_kernel(const uint16_t* __restrict__ X,
                                                                         const uint16_t* __restrict__ W, int NP,
@@ -1069,12 +1071,14 @@ __global__ __launch_bounds__(kWaves * 64, 2) void dense_gemm_bigm_kernel(const u
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int mt0 = blockIdx.y * 8 + wave * 2;
   const int nmt = max(0, min(2, mtiles - mt0));
-#define PE_DBIGM_WAVE(N)                                                                            \
-  switch (wave) {                                                                                   \
-    case 0: dense_bigm_wave<DT, N, 0, F32OUT>(smem, X, W, NP, group, mt0, M, out, ld); break;       \
-    case 1: dense_bigm_wave<DT, N, 1, F32OUT>(smem, X, W, NP, group, mt0, M, out, ld); break;       \
-    case 2: dense_bigm_wave<DT, N, 2, F32OUT>(smem, X, W, NP, group, mt0, M, out, ld); break;       \
-    default: dense_bigm_wave<DT, N, 3, F32OUT>(smem, X, W, NP, group, mt0, M, out, ld); break;      \
+  const int ups = (NP + gridDim.z - 1) / gridDim.z;
+  const int p0 = blockIdx.z * ups, p1 = min(NP, p0 + ups);
+#define PE_DBIGM_WAVE(N)                                                                                  \
+  switch (wave) {                                                                                         \
+    case 0: dense_bigm_wave<DT, N, 0, F32OUT>(smem, X, W, NP, p0, p1, group, mt0, M, out, ld); break;     \
+    case 1: dense_bigm_wave<DT, N, 1, F32OUT>(smem, X, W, NP, p0, p1, group, mt0, M, out, ld); break;     \
+    case 2: dense_bigm_wave<DT, N, 2, F32OUT>(smem, X, W, NP, p0, p1, group, mt0, M, out, ld); break;     \
+    default: dense_bigm_wave<DT, N, 3, F32OUT>(smem, X, W, NP, p0, p1, group, mt0, M, out, ld); break;    \
   }
   if (nmt == 2) {
     PE_DBIGM_WAVE(2)
@@ -1842,8 +1846,9 @@ int64_t pe_internal_nf4_bigm_partials_bytes(int M, int N, int K) {
 }
 
 int pe_internal_dense_bigm(const void* x_tiled, int M, int K, const void* w, int dtype, int N, void* out,
-                           int64_t ld_out, hipStream_t st, bool f32_out) {
+                           int64_t ld_out, hipStream_t st, bool f32_out, int* splits) {
   if (!x_tiled || !w || !out || M <= 0 || K % 128 || N % (32 * kBigNT) || ld_out < N) return PE_ERR_ARG;
+  if (splits) *splits = 1;
   const int mtiles0 = (M + 31) / 32;
   // 256 x 256 tiles from an LDS ring when the tiles fill at least two rounds
   // of one workgroup per CU (offsets within X and W below 4 GiB). With fewer
@@ -1874,7 +1879,12 @@ int pe_internal_dense_bigm(const void* x_tiled, int M, int K, const void* w, int
   }
   const int np = K / 128;
   const int mtiles = (M + 31) / 32;
-  const dim3 grid(N / (32 * kBigNT), (mtiles + 7) / 8);
+  // fp32 partials for a caller that sums splits: two K splits when the column
+  // groups x row blocks would fill fewer than two workgroups per CU
+  int S = 1;
+  if (f32_out && splits && (int64_t)(N / (32 * kBigNT)) * ((mtiles + 7) / 8) < 512 && np >= 4) S = 2;
+  if (splits) *splits = S;
+  const dim3 grid(N / (32 * kBigNT), (mtiles + 7) / 8, S);
 #define PE_DBIGM_LAUNCH(D, F)                                                                             \
   dense_gemm_bigm_kernel<D, F><<<grid, kWaves * 64, 0, st>>>((const uint16_t*)x_tiled, (const uint16_t*)w, np, \
                                                              mtiles, M, out, ld_out)

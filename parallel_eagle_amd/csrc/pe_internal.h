@@ -54,9 +54,12 @@ PE_INTERNAL int pe_internal_rope_kv_partials(const float* partial, int S, int M,
 // MFMA-tiled layout, K % 128 == 0, N % 128 == 0), one workgroup per 128
 // columns and block of 256 rows, each weight read once per row block; Y
 // row-major (leading dimension ld_out) in the dtype, or the fp32 sums as they
-// are (f32_out: one split of partials for the prefill's epilogue kernels).
+// are (f32_out: split partials [S][M][ld_out] for the prefill's epilogue
+// kernels; with `splits` given the launch may take S = 2 K splits and reports
+// S there, else S = 1).
 PE_INTERNAL int pe_internal_dense_bigm(const void* x_tiled, int M, int K, const void* w, int dtype, int N, void* out,
-                                       int64_t ld_out, hipStream_t st, bool f32_out = false);
+                                       int64_t ld_out, hipStream_t st, bool f32_out = false,
+                                       int* splits = nullptr);
 // The prefill's NF4 linear over all M rows (A-tiled X, blocks of 256 rows, one
 // K split): fp32 sums y[M][N], or with out_units > 0 (the interleaved gate/up
 // weight, N = 2 * 128 * out_units) the SwiGLU activation stored A-tiled.

@@ -203,7 +203,7 @@ PrefillLayout make_prefill_layout(const pe_model_desc* m, int M, int64_t kv_len)
   int64_t ny = nqkv;
   if (2 * ip > ny) ny = 2 * ip;
   if (H > ny) ny = H;
-  L.y = take(M * ny * 4);
+  L.y = take(M * ny * 4 * 2);  // up to two K splits of fp32 partials
   L.wdeq = L.wtile = 0;
   if (m->weight_format == PE_WFMT_NF4_F32ABS) {  // one linear dequantised, then tiled
     int64_t nw = nqkv * H;
@@ -273,8 +273,10 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
     }
     return PE_OK;
   };
-  // y[M][N] (fp32) = x (A-tiled) . W^T over all rows
+  // y[ys][M][N] (fp32 split partials) = x (A-tiled) . W^T over all rows
+  int ys = 1;
   auto linear = [&](const void* xt, int K, const void* w, const void* ab, int N) -> int {
+    ys = 1;
     if (nf4) return pe_internal_nf4_prefill(xt, M, K, w, ab, N, y, nullptr, 0, st);
     const void* wt = w;
     if (m->weight_format == PE_WFMT_NF4_F32ABS) {
@@ -284,7 +286,7 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
       if (r != PE_OK) return r;
       wt = ws + Lp.wtile;
     }
-    return pe_internal_dense_bigm(xt, M, K, wt, m->dtype, N, y, N, st, true);
+    return pe_internal_dense_bigm(xt, M, K, wt, m->dtype, N, y, N, st, true, &ys);
   };
 
   {
@@ -299,7 +301,7 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
     void* kc = (char*)a->k_cache + l * layer_stride;
     void* vc = (char*)a->v_cache + l * layer_stride;
     PE_TRY(linear(xn_t, H, m->w_qkv[l], m->a_qkv ? m->a_qkv[l] : nullptr, nqkv));
-    PE_TRY(pe_internal_rope_kv_partials(y, 1, M, nh, nkv, hd, m->b_qkv ? m->b_qkv[l] : nullptr, a->positions,
+    PE_TRY(pe_internal_rope_kv_partials(y, ys, M, nh, nkv, hd, m->b_qkv ? m->b_qkv[l] : nullptr, a->positions,
                                         m->rope_cos_sin, m->max_positions, q, kc, vc, a->cache_capacity,
                                         a->prefix_len, a->status, m->dtype, st));
     PE_TRY(pe_internal_tree_attention(q, kc, vc, a->cache_capacity, nh, nkv, hd, M, a->prefix_len, PE_MASK_CAUSAL,
@@ -308,13 +310,13 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
                                       st, m->attn_mode));
     if (eager) PE_TRY(pe_internal_to_xtile(attn, qd, M, qd, attn_t, st));
     PE_TRY(linear(attn_t, qd, m->w_o[l], m->a_o ? m->a_o[l] : nullptr, H));
-    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, xn_t,
+    PE_TRY(pe_internal_residual_rmsnorm(y, ys, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, xn_t,
                                         nullptr, 0, nullptr, 0, st));
     if (nf4) {
       PE_TRY(pe_internal_nf4_prefill(xn_t, M, H, m->w_gu[l], m->a_gu[l], 2 * ip, nullptr, act_t, ip / 128, st));
     } else {
       PE_TRY(linear(xn_t, H, m->w_gu[l], m->a_gu ? m->a_gu[l] : nullptr, 2 * ip));
-      PE_TRY(pe_internal_swiglu_partials(y, 1, M, 2 * ip, act_t, ip, ip / 128, m->dtype, st));
+      PE_TRY(pe_internal_swiglu_partials(y, ys, M, 2 * ip, act_t, ip, ip / 128, m->dtype, st));
     }
     PE_TRY(linear(act_t, ip, m->w_down[l], m->a_down ? m->a_down[l] : nullptr, H));
     const bool last = l + 1 == L;
@@ -322,7 +324,7 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
     const int fx = last ? slot_of(L) : -1;
     const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
     const int next_mode = last ? PE_NORM_HF : m->norm_mode;
-    PE_TRY(pe_internal_residual_rmsnorm(y, 1, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn, xn_t,
+    PE_TRY(pe_internal_residual_rmsnorm(y, ys, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn, xn_t,
                                         slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
