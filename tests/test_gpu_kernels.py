@@ -389,6 +389,13 @@ def test_multi_tile_attention_with_key_splits_matches_sdpa(dtype, nh, nkv, T, P)
     assert torch.equal(out, again)
     ref = _attn_ref(q, k, v, P, parents, False, scale, dtype)
     assert torch.allclose(out.float(), ref.float(), rtol=2e-2, atol=2e-2), (out.float() - ref.float()).abs().max()
+    r32 = _attn_ref(q.float(), k.float(), v.float(), P, parents, False, scale, torch.float32)
+    for h in range(nh):  # per query head: as close to fp32 as torch's own reduced-precision SDPA
+        cols = slice(h * hd, (h + 1) * hd)
+        n32 = r32[:, cols].norm()
+        e_dev = float((out[:, cols].float() - r32[:, cols]).norm() / n32)
+        e_ref = float((ref[:, cols].float() - r32[:, cols]).norm() / n32)
+        assert e_dev <= 2 * e_ref + 1e-3, (h, e_dev, e_ref)
     ref_c = _attn_ref(q, k, v, P, None, True, scale, dtype)
     assert torch.allclose(causal.float(), ref_c.float(), rtol=2e-2, atol=2e-2)
 
