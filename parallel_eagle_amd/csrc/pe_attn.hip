@@ -702,8 +702,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(
       const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[i], scale2, -mnew));
       const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[i + 1], scale2, -mnew));
       psum += p0 + p1;
-      pb[i >> 1] = (DT == PE_DTYPE_F16) ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
-                                        : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
+      pb[i >> 1] = pack2_16<DT>(p0, p1);
     }
     psum += __shfl_xor(psum, 32, 64);
     l = l * alpha + psum;
@@ -1051,8 +1050,7 @@ __global__ __launch_bounds__(64 * kAttnWaves, 1) void attn_eager_kernel(
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
       const float p0 = E::round(expf(s[i] - M) * invL), p1 = E::round(expf(s[i + 1] - M) * invL);
-      pb[i >> 1] = (DT == PE_DTYPE_F16) ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
-                                        : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
+      pb[i >> 1] = pack2_16<DT>(p0, p1);
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c) *(u32x4_t*)&vs[4 * c + (lane >> 4)][(lane & 15) * 8] = vf[c];
@@ -1677,9 +1675,7 @@ __global__ __launch_bounds__(64 * kBRowsWaves, 1) void attn_batch_rows_kernel(
           const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[sb][i], scale2, -mnew));
           const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[sb][i + 1], scale2, -mnew));
           psum += p0 + p1;
-          pb[sb][i >> 1] = (DT == PE_DTYPE_F16)
-                               ? ((uint32_t)f32_to_f16_bits(p0) | ((uint32_t)f32_to_f16_bits(p1) << 16))
-                               : ((uint32_t)f32_to_bf16_bits(p0) | ((uint32_t)f32_to_bf16_bits(p1) << 16));
+          pb[sb][i >> 1] = pack2_16<DT>(p0, p1);
         }
       psum += __shfl_xor(psum, 32, 64);
       l = l * alpha + psum;

@@ -34,6 +34,21 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, h);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats rounded (nearest even) to the 16-bit type DT and packed, lo in
+// the low half: one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 instead of two
+// conversions and a pack; the same bits as f32_to_bf16_bits / f32_to_f16_bits.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2_16(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  if constexpr (DT == PE_DTYPE_F16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 // Element access by storage type: dtype codes follow PE_DTYPE_* in pe_hip.h.
 template <int DT> struct Elem;
 template <> struct Elem<PE_DTYPE_F32> {

@@ -256,8 +256,6 @@ __device__ __forceinline__ void nf4_read8(const uint8_t* smem, const uint32_t (&
 
 __device__ __forceinline__ uint32_t pack16(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
 // The lane's 16 table entries for two block pairs at once: entry c (at lane
 // base + 256 c + OFF) holds bf16_rne(NF4[c] * scale0) in its low half and
 // bf16_rne(NF4[c] * scale1) in its high half.
