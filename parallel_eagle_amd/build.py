@@ -51,11 +51,22 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP library cannot be built")
 
 
+# Per-file code generation options. attn_pair_kernel holds two row tiles' O
+# accumulators per wave (more than the 256 architectural VGPRs); with the
+# MFMA results in VGPR form the compiler spills 88 values to the accumulation
+# registers instead of 254, and copies far fewer of them per round (the other
+# kernels of the file compile to the same code either way).
+FILE_FLAGS = {
+    "pe_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: str) -> Path:
     obj = BUILD_DIR / (Path(src).stem + ".o")
-    cmd = [hipcc(), *COMMON, "-c", str(CSRC / src), "-o", str(obj)]
+    extra = FILE_FLAGS.get(src, [])
+    cmd = [hipcc(), *COMMON, *extra, "-c", str(CSRC / src), "-o", str(obj)]
     if src.endswith(".cpp"):
-        cmd = [hipcc(), *COMMON, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [hipcc(), *COMMON, *extra, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr[-6000:]}")

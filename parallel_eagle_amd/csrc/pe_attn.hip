@@ -1239,10 +1239,22 @@ AttnPlan attn_plan(int T, int nh, int nkv, int64_t S, int batch = 1) {
   return p;
 }
 
+// The chunk permutation of K / V row `row` in an LDS step buffer (physical
+// chunk = logical chunk ^ swz_row(row)). With i = row % 4 and j = row / 4 % 4
+// it is (2i ^ 4i ^ j) % 16: a bijection on 16 consecutive rows (so the K
+// fragment reads, 16 bytes of one chunk from each of 16 consecutive rows, fall
+// on distinct banks), and for four rows 4k .. 4k + 3 it moves bits 1-3 of the
+// chunk differently per row, so that the transposed V reads (8 bytes from each
+// of two or four neighbouring chunks of those four rows) do as well. Plain
+// row % 16 left those V reads two- to four-way conflicted.
+__device__ __forceinline__ int swz_row(int row) {
+  const int i = row & 3, j = (row >> 2) & 3;
+  return ((i << 1) ^ (i << 2) ^ j) & 15;
+}
+
 // Byte offset of 16-byte chunk `chunk` of a 256-byte K / V row in an LDS step
-// buffer: chunks swizzled by row, so that 16 consecutive rows' reads of one
-// chunk fall on different banks.
-__device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 256 + ((chunk ^ (row & 15)) << 4)); }
+// buffer.
+__device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 256 + ((chunk ^ swz_row(row)) << 4)); }
 
 // Visibility of the 64 keys kb0 .. kb0 + 63 to one query row, as a bit mask
 // (bit j: key kb0 + j), so that each score register tests a bit at an offset
@@ -1349,7 +1361,7 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void attn_rows_kernel(
     for (int k = 0; k < 8; ++k) {
       const int row = 32 * (dq & 1) + 4 * k + (lane >> 4);
       const uint32_t key = (uint32_t)min(kb0 + row, S - 1);
-      lds_dma16(dsrc, key * (HD * 2) + (((lane & 15) ^ (row & 15)) << 4), dst + k * 1024);
+      lds_dma16(dsrc, key * (HD * 2) + (((lane & 15) ^ swz_row(row)) << 4), dst + k * 1024);
     }
   };
 
@@ -1544,9 +1556,9 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void attn_rows_kernel(
 // multiplied); each step is 32 loads of 1 KiB (wave w the four of K rows
 // 16 (w % 4) .. + 15 for w < 4, of V rows for w >= 4), one wait for this
 // wave's loads of the step and one barrier. K and V rows are stored unpadded
-// (256 bytes), their 16-byte chunks swizzled by row (chunk c of key row k at
-// c ^ (k % 16)), so the K fragment and transposed V reads of 16 consecutive
-// rows fall on different banks. The arithmetic is attn_rows_kernel's, with
+// (256 bytes), their 16-byte chunks permuted by row (chunk c of key row k at
+// c ^ swz_row(k)), so that the K fragment and transposed V reads fall on
+// distinct banks. The arithmetic is attn_rows_kernel's, with
 // the tree mask as a bit window. A sequence of one split writes its output;
 // otherwise each tile stores its split's (O, m, l) and attn_combine_kernel
 // (a second launch, one thread per row and 4-dim chunk) merges the splits in
@@ -1595,7 +1607,7 @@ __global__ __launch_bounds__(64 * kBRowsWaves, 1) void attn_batch_rows_kernel(
     for (int i = 0; i < 4; ++i) {
       const int row = prow0 + 4 * i;
       const uint32_t key = (uint32_t)min(kb0 + row, S - 1);
-      lds_dma16(kvbase, key * (HD * 2) + ((pch ^ (row & 15)) << 4), dst + i * 1024);
+      lds_dma16(kvbase, key * (HD * 2) + ((pch ^ swz_row(row)) << 4), dst + i * 1024);
     }
   };
 
