@@ -427,7 +427,7 @@ def test_causal_attention_over_many_rows_matches_sdpa(dtype, nh, nkv, T, P):
     assert torch.allclose(out.float(), ref.float(), rtol=2e-2, atol=2e-2), err.max()
 
 
-@pytest.mark.parametrize("dtype,nh,nkv,trees,prefixes", [
+BATCHED_ATTENTION_CASES = [
     # five query heads per KV head, 26-node trees: one wave per 32-row tile, 1-8 key splits per sequence
     (torch.bfloat16, 40, 8, [26] * 8, [812, 3000, 512, 4096, 1500, 700, 2222, 64]),
     (torch.float16, 40, 8, [26] * 3, [100, 513, 1024]),
@@ -435,8 +435,10 @@ def test_causal_attention_over_many_rows_matches_sdpa(dtype, nh, nkv, T, P):
     (torch.bfloat16, 40, 8, [26, 7, 40], [0, 900, 2500]),
     # one query head per KV head: two row tiles
     (torch.bfloat16, 4, 4, [26, 64], [100, 2048]),
-])
-def test_batched_tree_attention_matches_sdpa_per_sequence(dtype, nh, nkv, trees, prefixes):
+]
+
+
+def check_batched_attention(dtype, nh, nkv, trees, prefixes):
     """pe_tree_attention_batch against SDPA per sequence (its own prefix, tree
     bias and cache): for every (sequence, query head) the relative L2 distance
     from an fp32 evaluation is at most twice that of torch's own reduced-precision
@@ -486,6 +488,30 @@ def test_batched_tree_attention_matches_sdpa_per_sequence(dtype, nh, nkv, trees,
             worst.append((e_dev - 2 * e_ref, b, h, e_dev, e_ref))
     worst.sort(reverse=True)
     assert worst[0][0] <= 1e-3, f"(excess, sequence, head, device relL2, torch relL2): {worst[:4]}"
+
+
+@pytest.mark.parametrize("dtype,nh,nkv,trees,prefixes", BATCHED_ATTENTION_CASES)
+def test_batched_tree_attention_matches_sdpa_per_sequence(dtype, nh, nkv, trees, prefixes):
+    """The default batched kernels (check_batched_attention)."""
+    check_batched_attention(dtype, nh, nkv, trees, prefixes)
+
+
+def test_batched_tree_attention_on_the_opt_in_rows_kernel():
+    """The same cases with PE_ATTN_BATCH_ROWS=1 (attn_batch_rows_kernel and its
+    split combine for four to eight row tiles per sequence and KV head). The
+    switch is read once per process, so the cases run in one child process."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("import sys; sys.path[:0] = [{r!r}, {t!r}]\n"
+            "import test_gpu_kernels as t\n"
+            "for c in t.BATCHED_ATTENTION_CASES: t.check_batched_attention(*c)\n"
+            "print('rows kernel cases passed')\n").format(r=root, t=os.path.join(root, "tests"))
+    env = dict(os.environ, PE_ATTN_BATCH_ROWS="1")
+    res = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-4000:]
+    assert "rows kernel cases passed" in res.stdout
 
 
 # ------------------------------------------------------------------ acceptance and compaction
