@@ -1209,8 +1209,13 @@ __global__ __launch_bounds__(256, 1) void dense_gemm_t256_kernel(const uint16_t*
 // ---------------------------------------------------------------------------
 // Dense 16-bit GEMM: one iteration = 4 MFMA k-steps (64 along K) of NT tiles.
 // Same pipeline as the NF4 kernel; a padded iteration multiplies a zero X.
+// XT: X is A-tiled (xtile_index). Weight k-step 4u + j holds, in lane half
+// g, k = 64u + 16j + 8g .. + 7; in the A-tiled X those eight elements of row
+// 32 mt + ln are chunk 2j + g of 128-column unit u / 2 at lane ln + 32 (u % 2),
+// so each X load reads two 512-byte runs (whole cache lines) instead of
+// 32 bytes from each of 32 rows.
 // ---------------------------------------------------------------------------
-template <int FMT, int MT, int NT>
+template <int FMT, int MT, int NT, bool XT>
 __global__ __launch_bounds__(kWaves * 64, 3) void dense_gemm_kernel(const uint16_t* __restrict__ X, int64_t ldx,
                                                                     int K, const uint16_t* __restrict__ W, int S,
                                                                     int ups, float* __restrict__ partial,
@@ -1237,8 +1242,11 @@ __global__ __launch_bounds__(kWaves * 64, 3) void dense_gemm_kernel(const uint16
   const int n = w1 - w0;
   if (n > 0) {
     const uint16_t* xrow[MT];
+    const int xunits = K >> 7;  // XT: 128-column units of a tiled row block
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (int64_t)min(mt * 32 + ln, e.M - 1) * ldx + 8 * g;
+    for (int mt = 0; mt < MT; ++mt)
+      xrow[mt] = XT ? X + ((int64_t)mt * xunits * 8 + g) * 512 + ln * 8
+                    : X + (int64_t)min(mt * 32 + ln, e.M - 1) * ldx + 8 * g;
     u32x4_t ba[NT][4], bb[NT][4], x[MT][4];
     auto load_w = [&](u32x4_t (&b)[NT][4], int u) {
       const int uc = min(u, w1 - 1);
@@ -1251,7 +1259,9 @@ __global__ __launch_bounds__(kWaves * 64, 3) void dense_gemm_kernel(const uint16
     auto load_x = [&](int j, int u) {
       const int uc = min(u, w1 - 1);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) x[mt][j] = *(const u32x4_t*)(xrow[mt] + 64 * uc + 16 * j);
+      for (int mt = 0; mt < MT; ++mt)
+        x[mt][j] = XT ? *(const u32x4_t*)(xrow[mt] + (((int64_t)(uc >> 1) * 8 + 2 * j) * 64 + 32 * (uc & 1)) * 8)
+                      : *(const u32x4_t*)(xrow[mt] + 64 * uc + 16 * j);
     };
     auto iter = [&](const u32x4_t (&b)[NT][4], int u) {
       const uint32_t keep = u < w1 ? 0xffffffffu : 0u;
@@ -1596,10 +1606,16 @@ int launch_gemm(int fmt, const Plan& p, hipStream_t st, const uint16_t* x, int64
     else
       launch_nf4<false>(p, grid, st, x, ldx, x_tiled, w, wabs, partial, counters, e);
   } else {
-    if (x_tiled) return PE_ERR_ARG;
-#define PE_DENSE(F, MT_, NT_)                                                                                      \
-  dense_gemm_kernel<F, MT_, NT_><<<grid, kWaves * 64, 0, st>>>(x, ldx, K, (const uint16_t*)w, p.S, p.per_split, \
-                                                               partial, counters, e)
+    if (x_tiled && K % 128) return PE_ERR_ARG;
+#define PE_DENSE(F, MT_, NT_)                                                                                         \
+  do {                                                                                                               \
+    if (x_tiled)                                                                                                     \
+      dense_gemm_kernel<F, MT_, NT_, true><<<grid, kWaves * 64, 0, st>>>(x, ldx, K, (const uint16_t*)w, p.S,        \
+                                                                         p.per_split, partial, counters, e);       \
+    else                                                                                                             \
+      dense_gemm_kernel<F, MT_, NT_, false><<<grid, kWaves * 64, 0, st>>>(x, ldx, K, (const uint16_t*)w, p.S,       \
+                                                                          p.per_split, partial, counters, e);      \
+  } while (0)
     if (fmt == PE_DTYPE_F16) {
       if (p.NT == 2) { if (p.MT == 1) PE_DENSE(PE_DTYPE_F16, 1, 2); else PE_DENSE(PE_DTYPE_F16, 2, 2); }
       else { if (p.MT == 1) PE_DENSE(PE_DTYPE_F16, 1, 1); else PE_DENSE(PE_DTYPE_F16, 2, 1); }
@@ -1748,7 +1764,6 @@ int pe_internal_linear_partials(int wfmt, int dtype, const void* x, int64_t ldx,
   if (rc != PE_OK) return rc;
   const bool nf4 = pe_wfmt_nf4(wfmt);
   if (nf4 ? !wabs : (dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16)) return PE_ERR_ARG;
-  if (x_tiled && !nf4) return PE_ERR_ARG;
   const Plan p = make_plan(M, N, K, nf4, kEpiPartial);
   if (partial_bytes < (int64_t)p.S * M * N * 4) return PE_ERR_WORKSPACE;
   EpiArgs e = make_epi(kEpiPartial, M, N, nullptr, nullptr, 0, partial, N);

@@ -40,7 +40,7 @@ struct Layout {
   int64_t gemm;  // GEMM arrival counters, then split-K partials
   int64_t gemm_bytes;
   int64_t h, xn, qkv, q, attn, act, attn_ws, attn_ws_bytes;
-  int64_t xn_t, attn_t, act_t;  // A-tiled GEMM inputs of the fused NF4 pass
+  int64_t xn_t, attn_t, act_t;  // A-tiled GEMM inputs of the fused pass
   int64_t part, part_bytes;      // split partials of the fused NF4 pass's GEMMs
   int64_t kvoff;                 // per-row K/V slots of a pass whose prefix is read on the device
   int64_t total;
@@ -52,9 +52,13 @@ bool fused_path(const pe_model_desc* m, int M) {
   return m->dtype != PE_DTYPE_F32 && m->qkv_layout == PE_QKV_ROPE_PAIRED && m->head_dim == 128 && M <= 64;
 }
 
-// The fused NF4 pass hands the GEMMs their X A-tiled (see xtile_index).
+// The fused pass hands the GEMMs their X A-tiled (see xtile_index): NF4 and
+// dense 16-bit weights alike (the dense kernel's X loads then read whole
+// cache lines), except with eager attention (the drafter's), whose output is
+// row-major.
 bool tiled_path(const pe_model_desc* m, int M) {
-  return fused_path(m, M) && pe_wfmt_nf4(m->weight_format) && m->hidden % 128 == 0 &&
+  return fused_path(m, M) && (pe_wfmt_nf4(m->weight_format) || m->weight_format == PE_WFMT_DENSE) &&
+         m->attn_mode != PE_ATTN_EAGER && m->hidden % 128 == 0 &&
          (m->num_heads * m->head_dim) % 128 == 0 && m->intermediate_padded % 128 == 0;
 }
 
@@ -374,7 +378,7 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   void* attn = ws + Lo.attn;
   void* act = ws + Lo.act;
   void* aws = ws + Lo.attn_ws;
-  // A-tiled GEMM inputs (NF4): x_* is what the GEMMs read, *_units the tiled output widths
+  // A-tiled GEMM inputs: x_* is what the GEMMs read, *_units the tiled output widths
   const bool tiled = tiled_path(m, M);
   void* xn_t = tiled ? ws + Lo.xn_t : nullptr;
   void* x_norm = tiled ? xn_t : xn;
@@ -705,7 +709,8 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
   if (m->intermediate_padded % 32 || m->intermediate_padded < m->intermediate) return PE_ERR_ARG;
   if (m->norm_mode != PE_NORM_HF && m->norm_mode != PE_NORM_FP32_WEIGHT) return PE_ERR_ARG;
   if (m->attn_mode != PE_ATTN_SDPA && m->attn_mode != PE_ATTN_EAGER) return PE_ERR_ARG;
-  // eager attention writes row-major output: not the A-tiled NF4 pass
+  // eager attention writes row-major output: not the A-tiled NF4 pass (dense
+  // models with eager attention run the fused pass on row-major activations)
   if (m->attn_mode == PE_ATTN_EAGER && pe_wfmt_nf4(m->weight_format)) return PE_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   if (a->batch < 0) return PE_ERR_ARG;
