@@ -23,7 +23,7 @@ PE_INTERNAL int pe_internal_gemm_rope_kv(int wfmt, int dtype, const void* x, int
                                          int64_t row0, int32_t* status, void* ws, int64_t ws_bytes, bool x_tiled,
                                          hipStream_t st, const int64_t* kv_off = nullptr);
 PE_INTERNAL int64_t pe_internal_gemm_rope_kv_bytes(int M, int N, int K, int wfmt);
-// pe_nf4_gemm / pe_dense_gemm with A-tiled X (x_tiled, NF4 only, M <= 64)
+// pe_nf4_gemm / pe_dense_gemm with A-tiled X (x_tiled, M <= 64, K % 128 == 0)
 // and/or an A-tiled output (out_units = N_out / 128, not with the residual
 // epilogue).
 PE_INTERNAL int pe_internal_linear(int wfmt, int dtype, const void* x, int64_t ldx, bool x_tiled, int M, int K,
