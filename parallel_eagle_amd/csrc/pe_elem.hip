@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
 #pragma unroll
   for (int i = 0; i < kNormThreads / 64; ++i) tot += part[i];
   const float inv = 1.0f / sqrtf(tot / (float)H + eps);
-  T* orow = xn + (int64_t)m * H;
+  T* orow = xn ? xn + (int64_t)m * H : nullptr;  // null: the A-tiled rows only
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
     const int c = threadIdx.x + k * kNormThreads;
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
     RW::cvt(wraw[k], wv);
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = norm_out<E>(mode, v[k][e], inv, wv[e]);
-    V::store(orow + 4 * c, o);
+    if (orow) V::store(orow + 4 * c, o);
     // four consecutive columns are consecutive in the A-tiled layout too
     if (xt) V::store(xt + xtile_index(m, 4 * c, H >> 7), o);
     if (cap_xn) V::store(cap_xn + (int64_t)m * ld_cap_xn + 4 * c, o);
@@ -446,7 +446,7 @@ void launch_norm(int smax, const NormArgs<typename Elem<DT>::T>& a, hipStream_t 
 int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, int H, const void* w, float eps,
                                  int mode, int dtype, void* xn, void* xn_tiled, void* cap_h, int64_t ld_cap_h, void* cap_xn,
                                  int64_t ld_cap_xn, hipStream_t st) {
-  if (!h || !w || !xn || M <= 0 || H <= 0 || S < 0 || (S > 0 && !partial)) return PE_ERR_ARG;
+  if (!h || !w || !(xn || xn_tiled) || M <= 0 || H <= 0 || S < 0 || (S > 0 && !partial)) return PE_ERR_ARG;
   if (H % 4 || H > 4 * kNormThreads * kNormChunks || S > kNormMaxSplits) return PE_ERR_ARG;
   if (xn_tiled && (H % 128 || dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
   const int ch = (H >> 2) > kNormThreads ? 2 : 1;
@@ -467,7 +467,7 @@ int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, in
 int pe_internal_embed_rmsnorm(const int64_t* ids, int M, const void* table, int64_t V, void* h, int H, const void* w,
                               float eps, int mode, int dtype, void* xn, void* xn_tiled, void* cap_h, int64_t ld_cap_h,
                               void* cap_xn, int64_t ld_cap_xn, int32_t* status, hipStream_t st) {
-  if (!ids || !table || !h || !w || !xn || M <= 0 || H <= 0 || V <= 0) return PE_ERR_ARG;
+  if (!ids || !table || !h || !w || !(xn || xn_tiled) || M <= 0 || H <= 0 || V <= 0) return PE_ERR_ARG;
   if (H % 4 || H > 4 * kNormThreads * kNormChunks) return PE_ERR_ARG;
   if (xn_tiled && (H % 128 || dtype == PE_DTYPE_F32)) return PE_ERR_ARG;
   const int ch = (H >> 2) > kNormThreads ? 2 : 1;

@@ -84,8 +84,8 @@ PE_INTERNAL int pe_internal_swiglu_partials(const float* partial, int S, int M, 
 
 // pe_elem.hip: h = round(h + round(sum_s partial[s])) (S == 0: h unchanged),
 // xn = the RMSNorm of h rounded as `mode` (PE_NORM_*), also A-tiled into xn_tiled when
-// given; optional copies of the new h (cap_h) and of xn (cap_xn) into the
-// fused-feature rows.
+// given (xn may then be null: the tiled rows only); optional copies of the new
+// h (cap_h) and of xn (cap_xn) into the fused-feature rows.
 PE_INTERNAL int pe_internal_residual_rmsnorm(const float* partial, int S, int M, void* h, int H, const void* w,
                                              float eps, int mode, int dtype, void* xn, void* xn_tiled, void* cap_h,
                                              int64_t ld_cap_h, void* cap_xn, int64_t ld_cap_xn, hipStream_t st);

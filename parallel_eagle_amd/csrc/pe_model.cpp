@@ -296,8 +296,8 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
   {
     const int f0 = slot_of(0);
     PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, embed_rows(m), h, H, m->attn_norm[0], m->rms_eps,
-                                     m->norm_mode, m->dtype, xn, xn_t, slot_ptr(f0), fused_ld, nullptr, 0, a->status,
-                                     st));
+                                     m->norm_mode, m->dtype, nullptr, xn_t, slot_ptr(f0), fused_ld, nullptr, 0,
+                                     a->status, st));
     PE_TRY(copy_repeats(0, f0));
   }
   const bool eager = m->attn_mode == PE_ATTN_EAGER;  // writes row-major output, packed afterwards
@@ -314,7 +314,7 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
                                       st, m->attn_mode));
     if (eager) PE_TRY(pe_internal_to_xtile(attn, qd, M, qd, attn_t, st));
     PE_TRY(linear(attn_t, qd, m->w_o[l], m->a_o ? m->a_o[l] : nullptr, H));
-    PE_TRY(pe_internal_residual_rmsnorm(y, ys, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, xn_t,
+    PE_TRY(pe_internal_residual_rmsnorm(y, ys, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, nullptr, xn_t,
                                         nullptr, 0, nullptr, 0, st));
     if (nf4) {
       PE_TRY(pe_internal_nf4_prefill(xn_t, M, H, m->w_gu[l], m->a_gu[l], 2 * ip, nullptr, act_t, ip / 128, st));
@@ -328,7 +328,7 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
     const int fx = last ? slot_of(L) : -1;
     const void* next_norm = last ? m->final_norm : m->attn_norm[l + 1];
     const int next_mode = last ? PE_NORM_HF : m->norm_mode;
-    PE_TRY(pe_internal_residual_rmsnorm(y, ys, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn, xn_t,
+    PE_TRY(pe_internal_residual_rmsnorm(y, ys, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, nullptr, xn_t,
                                         slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
@@ -382,6 +382,7 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   const bool tiled = tiled_path(m, M);
   void* xn_t = tiled ? ws + Lo.xn_t : nullptr;
   void* x_norm = tiled ? xn_t : xn;
+  void* xn_rm = tiled ? nullptr : xn;  // row-major norm rows: read only by the lm_head (last norm) when tiled
   void* x_attn = tiled ? ws + Lo.attn_t : attn;
   void* x_act = tiled ? ws + Lo.act_t : act;
   const int attn_units = tiled ? qd / 128 : 0, act_units = tiled ? ip / 128 : 0;
@@ -424,7 +425,8 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   {
     const int f0 = slot_of(0);
     PE_TRY(pe_internal_embed_rmsnorm(a->input_ids, M, m->embed, embed_rows(m), h, H, m->attn_norm[0], m->rms_eps,
-                                     m->norm_mode, m->dtype, xn, xn_t, slot_ptr(f0), fused_ld, nullptr, 0, a->status, st));
+                                     m->norm_mode, m->dtype, xn_rm, xn_t, slot_ptr(f0), fused_ld, nullptr, 0, a->status,
+                                     st));
     PE_TRY(copy_repeats(0, f0));
   }
   // q/k/v and gate/up run with their RoPE + KV append / SwiGLU epilogues in
@@ -455,7 +457,7 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
     const void* a_o = m->a_o ? m->a_o[l] : nullptr;
     PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_attn, qd, tiled, M, qd, m->w_o[l], a_o, H, part,
                                        Lo.part_bytes, &S, st));
-    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn, xn_t,
+    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, m->mlp_norm[l], m->rms_eps, m->norm_mode, m->dtype, xn_rm, xn_t,
                                         nullptr, 0, nullptr, 0, st));
     const void* a_gu = m->a_gu ? m->a_gu[l] : nullptr;
     const void* a_down = m->a_down ? m->a_down[l] : nullptr;
@@ -468,8 +470,9 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
                               nullptr, 0, x_act, ip, act_units, gws, gwsb, st));
     PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_act, ip, tiled, M, ip, m->w_down[l], a_down, H, part,
                                        Lo.part_bytes, &S, st));
-    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn,
-                                        last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
+    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype,
+                                        last ? xn : xn_rm, last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx),
+                                        fused_ld, st));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
   if (a->logits) PE_TRY(lm_head(m, a, xn, M, gws, gwsb, st));
