@@ -946,6 +946,9 @@ __global__ __launch_bounds__(kWsWaves * 64, 1) void nf4_gemm_bigws_kernel(const 
     }
     return;
   }
+  // the consumers (the critical path) win issue arbitration over the
+  // producers of their SIMD
+  __builtin_amdgcn_s_setprio(2);
   // grid.z: blocks of eight 32-row tiles (a prefill of more than 256 rows)
   const int mt0 = blockIdx.z * 8 + (wave - kWaves) * 2;
   const int nmt = max(0, min(2, mtiles - mt0));
