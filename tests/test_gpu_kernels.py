@@ -146,7 +146,8 @@ def test_nf4_partials_sum_to_the_product(m, n, k, tiled):
     assert torch.all(err <= 1e-4 * (1 + ref32.abs()) * (k / 1024)), err.max()
 
 
-@pytest.mark.parametrize("m,n,k", [(208, 27648, 5120), (97, 22016, 4096), (130, 5120, 4096)])
+@pytest.mark.parametrize("m,n,k", [(208, 27648, 5120), (97, 22016, 4096), (130, 5120, 4096), (65, 22016, 4096),
+                                   (161, 22016, 4096), (150, 22016, 4096), (256, 22016, 4096)])
 def test_many_row_swiglu_equals_the_swiglu_of_the_split_partials(m, n, k):
     """pe_nf4_gemm_tiled with 64 < M <= 256 rows and the SwiGLU epilogue (the
     batched pass's gate/up linear) against the SwiGLU of the same kernel's fp32

@@ -74,6 +74,9 @@ def _key_sets(m, k):
     ("rowmajor-m64", 64, 4096, 4096),         # two M tiles, split-K exchange
     ("bigm-partials", 208, 7168, 5120),       # the batched pass's many-row kernel (seven M tiles, four waves)
     ("bigm-partials", 97, 4096, 4096),        # ragged: four M tiles, one wave without any
+    ("bigm-partials", 65, 4096, 4096),        # three M tiles, one row in the third
+    ("bigm-partials", 161, 4096, 4096),       # six M tiles, one row in the sixth
+    ("bigm-partials", 256, 4096, 4096),       # eight M tiles: every consumer two
     ("rowmajor-m1", 1, 1024, 2048),
 ])
 def test_nf4_gemm_reads_back_the_exact_bf16_weights(plan, m, n, k):
