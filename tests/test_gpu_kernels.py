@@ -361,6 +361,8 @@ def test_tree_attention_matches_sdpa(dtype, hd, nh, nkv, P, parents, causal):
     (10, 2, 26, 1000),  # five row tiles per KV head, the last with two rows
     (2, 1, 26, 5000),   # two row tiles in 16 key splits
     (8, 8, 40, 0),      # node keys only, one split, the second tile 8 rows
+    (32, 32, 26, 2047),  # the 7B shape: eight key splits per head, a multiple of eight KV heads
+    (16, 8, 40, 3000),  # eight KV heads, two row tiles of grouped rows in key splits
 ])
 def test_multi_tile_attention_with_key_splits_matches_sdpa(dtype, nh, nkv, T, P):
     """Tree attention over more than 32 query rows per KV head (several row
