@@ -274,10 +274,15 @@ __global__ __launch_bounds__(kArgThreads) void accept_kernel(const typename Elem
                                         : row_argmax<DT>(x, V, nullptr);
   __shared__ int s_last;
   if (threadIdx.x == 0) {
+    // The row's argmax is stored at agent scope (past this die's L2) and
+    // acknowledged before the block counts itself, and the last block reads
+    // every argmax at agent scope, so it sees all of them. (An acquire-release
+    // count would write back and invalidate the whole L2 in every block.)
     __hip_atomic_store(amax + r, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // release: this row's argmax is visible before the count; acquire: the
-    // last block sees every row's
-    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = old == T;
     if (old == T) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
