@@ -19,7 +19,7 @@ module's full-size model is held at the same time.
 import pytest
 
 from parallel_eagle_amd.config import QWEN25_14B_FP16, WORKLOADS
-from test_gpu_target import Prepared, _report, _run_case
+from tests.test_gpu_target import Prepared, _report, _run_case
 
 pytestmark = pytest.mark.gpu
 
