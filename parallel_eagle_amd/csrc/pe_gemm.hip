@@ -2066,6 +2066,15 @@ extern "C" int pe_dense_gemm_argmax_groups(int M, int N, int K) {
   return make_plan(M > kMaxChunkRows ? kMaxChunkRows : M, N, K, false, kEpiArgmax).groups;
 }
 
+// The lm_head of the fused pass over its A-tiled final norm rows (M <= 64):
+// the logits stored in the dtype and, with keys, each row's argmax keys.
+int pe_internal_dense_gemm_tiled(const void* x_tiled, int M, int K, const void* w, int dtype, int N, void* out,
+                                 int64_t ld_out, uint64_t* keys, void* ws, int64_t ws_bytes, hipStream_t st) {
+  if (dtype != PE_DTYPE_BF16 && dtype != PE_DTYPE_F16) return PE_ERR_ARG;
+  return mfma_gemm(dtype, x_tiled, 0, M, K, w, nullptr, N, PE_EPI_STORE, nullptr, nullptr, 0, out, ld_out, ws,
+                   ws_bytes, st, true, 0, keys);
+}
+
 extern "C" int pe_dense_gemm_argmax(const void* x, int64_t ldx, int M, int K, const void* w, int dtype, int N,
                                     void* out, int64_t ld_out, uint64_t* keys, void* workspace,
                                     int64_t workspace_bytes, void* stream) {

@@ -38,6 +38,12 @@ PE_INTERNAL int pe_internal_linear_partials(int wfmt, int dtype, const void* x, 
                                             int64_t partial_bytes, int* splits, hipStream_t st);
 PE_INTERNAL int64_t pe_internal_linear_partials_bytes(int M, int N, int K, int wfmt);
 
+// pe_gemm.hip: the dense 16-bit lm_head over A-tiled rows (M <= 64), logits in
+// the dtype and, with keys, each row's per-column-group argmax keys.
+PE_INTERNAL int pe_internal_dense_gemm_tiled(const void* x_tiled, int M, int K, const void* w, int dtype, int N,
+                                             void* out, int64_t ld_out, uint64_t* keys, void* ws, int64_t ws_bytes,
+                                             hipStream_t st);
+
 // pe_gemm.hip: the q/k/v epilogue (bias, RoPE, q out, K/V appended at cache rows
 // row0 + row) and the SwiGLU epilogue (N / 2 outputs, A-tiled when out_units)
 // applied to the S split partials of their projections (the head-paired /

@@ -224,11 +224,15 @@ PrefillLayout make_prefill_layout(const pe_model_desc* m, int M, int64_t kv_len)
   return L;
 }
 
-// The lm_head over the final normed rows (row-major xn); with a->node_keys
-// (single-sequence 16-bit passes) the GEMM also writes each row's argmax keys.
-int lm_head(const pe_model_desc* m, const pe_pass_args* a, const void* xn, int M, void* ws, int64_t wsb,
-            hipStream_t st) {
+// The lm_head over the final normed rows (row-major xn, or A-tiled in the
+// tiled fused pass); with a->node_keys (single-sequence 16-bit passes) the
+// GEMM also writes each row's argmax keys.
+int lm_head(const pe_model_desc* m, const pe_pass_args* a, const void* xn, bool x_tiled, int M, void* ws,
+            int64_t wsb, hipStream_t st) {
   const int H = m->hidden;
+  if (x_tiled)
+    return pe_internal_dense_gemm_tiled(xn, M, H, m->lm_head, m->dtype, m->vocab, a->logits, m->vocab, a->node_keys,
+                                        ws, wsb, st);
   if (a->node_keys)
     return pe_dense_gemm_argmax(xn, H, M, H, m->lm_head, m->dtype, m->vocab, a->logits, m->vocab, a->node_keys, ws,
                                 wsb, st);
@@ -382,7 +386,7 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
   const bool tiled = tiled_path(m, M);
   void* xn_t = tiled ? ws + Lo.xn_t : nullptr;
   void* x_norm = tiled ? xn_t : xn;
-  void* xn_rm = tiled ? nullptr : xn;  // row-major norm rows: read only by the lm_head (last norm) when tiled
+  void* xn_rm = tiled ? nullptr : xn;  // row-major norm rows: none when tiled (the lm_head reads A-tiled rows too)
   void* x_attn = tiled ? ws + Lo.attn_t : attn;
   void* x_act = tiled ? ws + Lo.act_t : act;
   const int attn_units = tiled ? qd / 128 : 0, act_units = tiled ? ip / 128 : 0;
@@ -470,12 +474,11 @@ int forward_fused(const pe_model_desc* m, const pe_pass_args* a, const Layout& L
                               nullptr, 0, x_act, ip, act_units, gws, gwsb, st));
     PE_TRY(pe_internal_linear_partials(wf, m->dtype, x_act, ip, tiled, M, ip, m->w_down[l], a_down, H, part,
                                        Lo.part_bytes, &S, st));
-    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype,
-                                        last ? xn : xn_rm, last ? nullptr : xn_t, slot_ptr(fh), fused_ld, slot_ptr(fx),
-                                        fused_ld, st));
+    PE_TRY(pe_internal_residual_rmsnorm(part, S, M, h, H, next_norm, m->rms_eps, next_mode, m->dtype, xn_rm, xn_t,
+                                        slot_ptr(fh), fused_ld, slot_ptr(fx), fused_ld, st));
     PE_TRY(copy_repeats(last ? L : l + 1, last ? fx : fh));
   }
-  if (a->logits) PE_TRY(lm_head(m, a, xn, M, gws, gwsb, st));
+  if (a->logits) PE_TRY(lm_head(m, a, tiled ? xn_t : xn, tiled, M, gws, gwsb, st));
 #undef PE_TRY
   return PE_OK;
 }
@@ -833,7 +836,7 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
   }
   PE_TRY(pe_rmsnorm(h, H, M, H, m->final_norm, m->rms_eps, m->dtype, xn, H, st));
   PE_TRY(capture(m->num_layers, xn));
-  if (a->logits) PE_TRY(lm_head(m, a, xn, M, gws, gwsb, st));
+  if (a->logits) PE_TRY(lm_head(m, a, xn, false, M, gws, gwsb, st));
 #undef PE_TRY
   return PE_OK;
 }
