@@ -471,7 +471,10 @@ int64_t pe_forward_batch_workspace_bytes(const pe_model_desc* m, int M, int max_
  * or dense (a prefill), runs every linear once over all rows in blocks of 256
  * rows on the matrix cores (each NF4 weight dequantised once per block inside
  * the GEMM) and attention once over all rows. Set PE_PREFILL_GEMM=0 to run such
- * passes in 64-row chunks of the fused pass instead. */
+ * passes in 64-row chunks of the fused pass instead.
+ * A tree pass (batch 0) of 65 to 64 * PE_TREE_MAX_WORDS nodes on such a model
+ * runs as a batch of one sequence (its sequence table written into the
+ * workspace, which pe_forward_workspace_bytes covers); node_keys must be NULL. */
 int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* stream);
 
 #ifdef __cplusplus

@@ -343,6 +343,20 @@ int pe_internal_to_xtile(const void* x, int64_t ld, int M, int K, void* out, hip
   return PE_OK;
 }
 
+// The sequence table of a batch of one: rows [0, M) over a prefix of P rows.
+__global__ void one_sequence_kernel(int32_t* seq_row0, int64_t* seq_prefix, int M, int64_t P) {
+  seq_row0[0] = 0;
+  seq_row0[1] = M;
+  seq_prefix[0] = P;
+}
+
+int pe_internal_one_sequence(int32_t* seq_row0, int64_t* seq_prefix, int M, int64_t P, hipStream_t st) {
+  if (!seq_row0 || !seq_prefix || M <= 0 || P < 0) return PE_ERR_ARG;
+  one_sequence_kernel<<<1, 1, 0, st>>>(seq_row0, seq_prefix, M, P);
+  PE_CHECK_LAUNCH();
+  return PE_OK;
+}
+
 int pe_internal_kv_offsets(const int32_t* seq_row0, const int64_t* seq_prefix, int batch, int M, int64_t seq_stride,
                            int64_t cap, int hd, int64_t max_prefix, int max_rows, int64_t* off, int32_t* status,
                            hipStream_t st) {

@@ -147,6 +147,9 @@ PE_INTERNAL int pe_internal_tree_attention_batch(const void* q, const void* k_ca
 // or when seq_prefix[b] exceeds max_prefix (the bound the launches were sized
 // for); a sequence of more than max_rows rows sets PE_ERR_TREE and drops its
 // rows' K/V.
+// pe_elem.hip: the device sequence table of a batch of one (seq_row0 = {0, M},
+// seq_prefix = {P}), written by a kernel so that a recorded pass can hold it.
+PE_INTERNAL int pe_internal_one_sequence(int32_t* seq_row0, int64_t* seq_prefix, int M, int64_t P, hipStream_t st);
 PE_INTERNAL int pe_internal_kv_offsets(const int32_t* seq_row0, const int64_t* seq_prefix, int batch, int M,
                                        int64_t seq_stride, int64_t cap, int hd, int64_t max_prefix, int max_rows,
                                        int64_t* off, int32_t* status, hipStream_t st);

@@ -52,6 +52,16 @@ bool fused_path(const pe_model_desc* m, int M) {
   return m->dtype != PE_DTYPE_F32 && m->qkv_layout == PE_QKV_ROPE_PAIRED && m->head_dim == 128 && M <= 64;
 }
 
+// A tree pass of more nodes than one fused chunk (65 up to the bitmask limit):
+// it runs as a batch of one sequence on the batched pass's kernels (each NF4
+// weight dequantised once for all rows), its sequence table written into the
+// workspace after the batch layout.
+bool wide_tree_path(const pe_model_desc* m, int M) {
+  return m->dtype != PE_DTYPE_F32 && m->qkv_layout == PE_QKV_ROPE_PAIRED && m->head_dim == 128 &&
+         m->attn_mode == PE_ATTN_SDPA && M > 64 && M <= 64 * PE_TREE_MAX_WORDS;
+}
+constexpr int64_t kOneSeqBytes = 256;  // seq_row0 {0, M} at +0, seq_prefix {P} at +16
+
 // The fused pass hands the GEMMs their X A-tiled (see xtile_index): NF4 and
 // dense 16-bit weights alike (the dense kernel's X loads then read whole
 // cache lines), except with eager attention (the drafter's), whose output is
@@ -342,6 +352,8 @@ int forward_prefill(const pe_model_desc* m, const pe_pass_args* a, const Prefill
   return PE_OK;
 }
 
+int64_t batch_layout_total(const pe_model_desc* m, int M, int max_rows, int64_t max_kv_len, int batch);
+
 extern "C" int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int64_t kv_len) {
   if (!m || M <= 0 || kv_len <= 0) return 0;
   // a causal pass of more than one chunk may take the prefill path
@@ -356,6 +368,10 @@ extern "C" int64_t pe_forward_workspace_bytes(const pe_model_desc* m, int M, int
     }
   } else {
     fused = make_layout(m, M, kv_len).total;
+  }
+  if (wide_tree_path(m, M)) {
+    const int64_t wide = batch_layout_total(m, M, M, kv_len, 1) + kOneSeqBytes;
+    if (wide > fused) fused = wide;
   }
   return pre > fused ? pre : fused;
 }
@@ -554,6 +570,10 @@ BatchLayout make_batch_layout(const pe_model_desc* m, int M, int max_rows, int64
   return L;
 }
 
+int64_t batch_layout_total(const pe_model_desc* m, int M, int max_rows, int64_t max_kv_len, int batch) {
+  return make_batch_layout(m, M, max_rows, max_kv_len, batch).total;
+}
+
 int forward_batched(const pe_model_desc* m, const pe_pass_args* a, const BatchLayout& Lb, hipStream_t st) {
   const int M = a->M;
   char* ws = (char*)a->workspace;
@@ -748,6 +768,22 @@ extern "C" int pe_forward(const pe_model_desc* m, const pe_pass_args* a, void* s
     return forward_batched(m, a, Lb, st);
   }
   const int64_t kv_len = a->prefix_len + M;
+  if (a->mask_mode == PE_MASK_TREE && wide_tree_path(m, M)) {
+    if (a->bits_words <= 0 || a->bits_words > PE_TREE_MAX_WORDS || M > 64 * a->bits_words) return PE_ERR_TREE;
+    const BatchLayout Lb = make_batch_layout(m, M, M, kv_len, 1);
+    if (a->workspace_bytes < Lb.total + kOneSeqBytes) return PE_ERR_WORKSPACE;
+    int32_t* row0 = (int32_t*)((char*)a->workspace + Lb.total);
+    int64_t* prefix = (int64_t*)((char*)row0 + 16);
+    pe_pass_args b = *a;
+    b.batch = 1;
+    b.max_seq_rows = M;
+    b.seq_row0 = row0;
+    b.seq_prefix = prefix;
+    b.cache_seq_stride = (int64_t)m->num_layers * m->num_kv_heads * a->cache_capacity * m->head_dim;
+    const int rc = pe_internal_one_sequence(row0, prefix, M, a->prefix_len, st);
+    if (rc != PE_OK) return rc;
+    return forward_batched(m, &b, Lb, st);
+  }
   if (prefill_path(m, M, a->mask_mode)) {
     const PrefillLayout Lp = make_prefill_layout(m, M, kv_len);
     if (a->workspace_bytes < Lp.total) return PE_ERR_WORKSPACE;

@@ -437,7 +437,8 @@ class VerifyStep:
         self.ws = torch.zeros(target.model.workspace_bytes(self.T, self.P + self.T), dtype=torch.uint8,
                               device=dev)
         # the lm_head's per-row argmax keys (16-bit models): [T][groups] uint64
-        self.key_groups = 0 if target.dtype == torch.float32 else int(
+        # (trees of more than 64 nodes run as a batch of one and walk the rows)
+        self.key_groups = 0 if (target.dtype == torch.float32 or self.T > 64) else int(
             _lib.load().pe_dense_gemm_argmax_groups(self.T, s.vocab, s.hidden))
         self.node_keys = (torch.zeros((self.T, self.key_groups), dtype=torch.int64, device=dev)
                           if self.key_groups > 0 else None)

@@ -422,6 +422,73 @@ def test_llama7b_nf4_width_wide_tree():
     print(f"T=64: {v}, accepted {n}, max |dlogit| {err:.3g}")
 
 
+@pytest.mark.parametrize("case", ["nf4-T100", "nf4-T200", "fp16-gqa-T100"])
+def test_trees_wider_than_one_chunk(case):
+    """Trees of more than 64 nodes (up to the 256 the bitmasks hold) through
+    forward_cached: the pass runs as a batch of one sequence on the batched
+    kernels (the many-row NF4 GEMM, the tree attention over row-tile pairs).
+    Logits, features and K/V rows against the oracle, acceptance and the
+    compaction as for every other case."""
+    if case.startswith("nf4"):
+        shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
+    else:
+        shape = QWEN25_14B_FP16.reduced(1, feature_layers=(0, 1, 1), vocab=16384)
+    if case.endswith("T200"):
+        depth, widths, top_k = 6, [8, 32, 40, 40, 40, 40], 8
+    else:
+        depth, widths, top_k = 5, [8, 16, 24, 26, 26], 8
+    det = {}
+    v, n, err = _run_case(shape, 3, 300, depth, widths, top_k, plant=lambda s: depth, tol=2e-2, random_kv=True,
+                          details=det)
+    _report(f"wide-tree-{case}", det)
+    assert v == "exact" or v.startswith("near-tie")
+
+
+def test_verify_step_with_a_wide_tree_replays_the_eager_api():
+    """VerifyStep over a 100-node tree (the pass as a batch of one, the walk
+    from the node rows): eager and three graph replays, with eager work in
+    between, equal forward_cached -> accept_tree_cached -> gather_cache bit for
+    bit, a planted greedy chain accepted to full depth."""
+    shape = LLAMA2_7B_NF4.reduced(2, feature_layers=(1, 2, 2))
+    P, depth, widths, top_k = 300, 5, [8, 16, 24, 26, 26], 8
+    tm = TargetModel.synthetic(shape, seed=4, device=DEV, cache_capacity=P + 128)
+    V = shape.vocab
+    prompt = synth.uniform_int(4, synth.STREAM_PROMPT, P, V).tolist()
+    cache = tm.make_cache()
+    pl, _, cache = tm.forward_cached(torch.tensor([prompt]), cache, torch.arange(P).unsqueeze(0))
+    root = pl[0, -1].clone()
+    tokens, parents = synth.tree_for_seed(4, V, depth, widths, top_k)
+    chain = synth.chain_nodes(parents, synth.deepest_first_leaf(parents))
+    pos = [P + d for d in om.tree_depths(parents)]
+    row = root
+    for node in chain:
+        synth.set_token(tokens, parents, node, int(row.float().argmax()), V)
+        lg, _, cache = tm.forward_cached(torch.tensor([tokens]), cache, torch.tensor([pos]), parents=parents)
+        cache.crop(P)
+        row = lg[0, node]
+    k0, v0 = cache.k.clone(), cache.v.clone()
+    lg_e, fu_e, cache = tm.forward_cached(torch.tensor([tokens]), cache, torch.tensor([pos]), parents=parents)
+    path_e, bonus_e = accept_tree_cached(root, lg_e[0], tokens, parents)
+    assert path_e == chain
+    tm.gather_cache(cache, torch.tensor(list(range(P)) + [P + t for t in path_e], device=DEV))
+    n = cache.seq_len
+    k_e, v_e = cache.k[:, :, :n].clone(), cache.v[:, :, :n].clone()
+    cache.k.copy_(k0)
+    cache.v.copy_(v0)
+    cache.seq_len = P
+    step = tm.verify_step(cache, len(tokens))
+    step.load_tree(tokens, parents, root)
+    step.capture()
+    for rep in range(3):
+        step.run()
+        assert step.result() == (path_e, bonus_e), rep
+        assert torch.equal(step.logits, lg_e[0]) and torch.equal(step.fused, fu_e[0])
+        assert torch.equal(cache.k[:, :, :n], k_e) and torch.equal(cache.v[:, :, :n], v_e)
+        cache.k[:, :, P:P + len(tokens)].normal_()
+        step.logits.zero_()
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("shape", [QWEN25_14B_FP16.reduced(1, feature_layers=(0, 1, 1), vocab=16384),
                                    QWEN25_14B_NF4.reduced(1, feature_layers=(0, 1, 1), vocab=16384)],
                          ids=["fp16", "nf4"])
