@@ -227,8 +227,8 @@ class SpeculativeDecoder:
     and one with ``sync_status`` / ``status`` lets the loop fold its status word
     into the step's one read. The tree is the reference's constant-width beam:
     width max(1, min(tree_top_k, tree_max_nodes // k)) at each of k depths.
-    ``use_graphs``: replay recorded steps (16-bit models with 128-dim heads and
-    trees of at most 64 nodes); otherwise the kernels are launched each step.
+    ``use_graphs``: replay recorded steps (16-bit models with 128-dim heads);
+    otherwise the kernels are launched each step.
     """
 
     def __init__(self, target: TargetModel, drafter, *, k: int, tree_top_k: int = 3, tree_max_nodes: int = 24,
@@ -241,8 +241,11 @@ class SpeculativeDecoder:
         if self.T > 64 * _lib.PE_TREE_MAX_WORDS:
             raise ValueError(f"a tree of {self.T} nodes exceeds {64 * _lib.PE_TREE_MAX_WORDS}")
         s = target.shape
+        # argmax keys from the lm_head for trees of one chunk; wider trees run as
+        # a batch of one and their walk reads the node rows
         self.keys = target.dtype != torch.float32 and self.T <= 64
-        self.device_prefix = bool(use_graphs) and self.keys and s.head_dim == 128 and target.model.qkv_paired
+        self.device_prefix = (bool(use_graphs) and target.dtype != torch.float32 and s.head_dim == 128
+                              and target.model.qkv_paired)
 
     # ------------------------------------------------------------ set-up per generate call
     def _allocate(self, capacity: int) -> None:

@@ -177,7 +177,8 @@ def _near_tie_or_equal(tm, prompt, ref_tokens, got_tokens, bound=0.0625):
     return f"near tie at token {j} (margin {margin:.3g})"
 
 
-def test_speculative_loop_at_the_7b_width_bf16():
+@pytest.mark.parametrize("tree_top_k,tree_max_nodes", [(4, 26), (20, 100)], ids=["26-nodes", "100-nodes"])
+def test_speculative_loop_at_the_7b_width_bf16(tree_top_k, tree_max_nodes):
     """Two 7B-width NF4 layers in bf16, recorded steps with P read on the device.
     The tree pass and the one-token pass that greedy decoding uses compute the
     same logits in different row blocks, so a bf16 rounding can flip a near
@@ -191,18 +192,18 @@ def test_speculative_loop_at_the_7b_width_bf16():
     prompt = list(range(100, 140))
     n = 64
     ref = greedy_decode(tm, prompt, n)
-    graph = SpeculativeDecoder(tm, PeekingDrafter(dr, prompt + ref.tokens, 0.8, seed=3), k=5, tree_top_k=4,
-                               tree_max_nodes=26)
+    graph = SpeculativeDecoder(tm, PeekingDrafter(dr, prompt + ref.tokens, 0.8, seed=3), k=5, tree_top_k=tree_top_k,
+                               tree_max_nodes=tree_max_nodes)
     assert graph.device_prefix
     res = graph.generate(prompt, n)
-    eager = SpeculativeDecoder(tm, PeekingDrafter(dr, prompt + ref.tokens, 0.8, seed=3), k=5, tree_top_k=4,
-                               tree_max_nodes=26, use_graphs=False).generate(prompt, n)
+    eager = SpeculativeDecoder(tm, PeekingDrafter(dr, prompt + ref.tokens, 0.8, seed=3), k=5, tree_top_k=tree_top_k,
+                               tree_max_nodes=tree_max_nodes, use_graphs=False).generate(prompt, n)
     assert res.tokens == eager.tokens  # one key split either way at these lengths: the same roundings
     assert res.steps <= res.host_reads <= res.steps + 1
     verdict = _near_tie_or_equal(tm, prompt, ref.tokens, res.tokens)
-    print(f"7B width: tokens per step {res.tokens_per_step:.2f}, steps {res.steps}, {verdict}")
+    print(f"7B width, {tree_max_nodes} nodes: tokens per step {res.tokens_per_step:.2f}, steps {res.steps}, {verdict}")
     # an untrained drafter: every step misses and runs the one-token pass
-    miss = SpeculativeDecoder(tm, dr, k=5, tree_top_k=4, tree_max_nodes=26).generate(prompt, 24)
+    miss = SpeculativeDecoder(tm, dr, k=5, tree_top_k=tree_top_k, tree_max_nodes=tree_max_nodes).generate(prompt, 24)
     print("miss path:", _near_tie_or_equal(tm, prompt, ref.tokens[:24], miss.tokens))
 
 
