@@ -108,3 +108,42 @@ def test_nf4_split_partials_fill_one_round(lib, m, n, k):
         assert s == max(1, min(256 // groups, units // 8))
     else:
         assert 1 <= s <= 16
+
+
+def _desc_7b_nf4() -> _lib.ModelDesc:
+    """A 7B-shaped NF4 model description (dimensions only: no weight is read
+    by the checks below)."""
+    d = _lib.ModelDesc()
+    d.num_layers, d.hidden, d.num_heads, d.num_kv_heads, d.head_dim = 2, 4096, 32, 32, 128
+    d.intermediate, d.intermediate_padded, d.vocab = 11008, 11008, 32000
+    d.dtype, d.weight_format, d.qkv_layout = _lib.PE_DTYPE_BF16, _lib.PE_WFMT_NF4, _lib.PE_QKV_ROPE_PAIRED
+    d.rms_eps, d.norm_mode, d.attn_mode, d.max_positions = 1e-5, _lib.PE_NORM_HF, _lib.PE_ATTN_SDPA, 4096
+    return d
+
+
+def _wide_tree_args(M: int, P: int, words: int, ws_bytes: int) -> _lib.PassArgs:
+    a = _lib.PassArgs()
+    a.input_ids = a.positions = a.tree_bits = a.k_cache = a.v_cache = a.workspace = 8
+    a.M, a.mask_mode, a.prefix_len, a.bits_words = M, _lib.PE_MASK_TREE, P, words
+    a.cache_capacity, a.workspace_bytes = P + M + 64, ws_bytes
+    return a
+
+
+def test_wide_tree_passes_are_validated_before_any_launch(lib):
+    """A tree pass of 65-256 nodes runs as a batch of one sequence: its workspace
+    (pe_forward_workspace_bytes) covers the batched layout plus the sequence
+    table, and argument errors are refused before anything is launched."""
+    d = _desc_7b_nf4()
+    M, P = 100, 300
+    need = lib.pe_forward_workspace_bytes(C.byref(d), M, P + M)
+    batch = lib.pe_forward_batch_workspace_bytes(C.byref(d), M, M, P + M, 1)
+    assert batch > 0 and need >= batch + 256
+    a = _wide_tree_args(M, P, 2, need)
+    a.node_keys = 8  # argmax keys are for passes of one chunk
+    assert lib.pe_forward(C.byref(d), C.byref(a), None) == _lib.PE_ERR_ARG
+    a = _wide_tree_args(M, P, 1, need)  # one word of ancestor bits cannot name 100 nodes
+    assert lib.pe_forward(C.byref(d), C.byref(a), None) == _lib.PE_ERR_TREE
+    a = _wide_tree_args(M, P, 2, batch)  # no room for the sequence table
+    assert lib.pe_forward(C.byref(d), C.byref(a), None) == _lib.PE_ERR_WORKSPACE
+    a = _wide_tree_args(300, P, 4, need)  # beyond the 256 nodes the bitmasks hold
+    assert lib.pe_forward(C.byref(d), C.byref(a), None) == _lib.PE_ERR_TREE
